@@ -1,0 +1,355 @@
+"""Benchmark: headshot's aggregator fused-op pass on one MI355X.
+
+A step is one aggregator pass of the per-layer ops at S frames x 1374 tokens
+x 1024 (f16 storage, f32 math): patch-token assembly, then 24 frame blocks
+(QK-norm + 2D RoPE, prefix 5, 37x37 grid) and 24 global blocks (QK-norm, no
+RoPE, one sequence of S*1374 tokens), each block running
+
+    LN1 -> QK-norm(+RoPE) on q -> on k -> proj bias + LayerScale + residual
+        -> LN2 -> fc1 bias + GELU (hidden 4096) -> fc2 bias + LayerScale + residual
+
+(model/block.rs:118-159 with the GEMMs and attention out of scope: their
+outputs are synthetic resident buffers). Inputs are synthetic and already in
+HBM when timing starts. ``value`` is algorithmic bytes of the whole pass /
+pass time (GB/s); per-op times come from HIP events on the launch stream.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames S]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "fused-layer-op HBM GB/s (% of peak) + ms/aggregator pass at S=32 f16"
+PEAK_GBS = 8000.0  # MI355X HBM3E
+DIM, HEADS, HEAD_DIM, HIDDEN = 1024, 16, 64, 4096
+GRID = (37, 37)
+PREFIX = 5  # 1 camera + 4 register tokens
+N_REG = 4
+EPS = 1e-6
+N_FRAME_BLOCKS = N_GLOBAL_BLOCKS = 24
+OPS = ["assemble", "layernorm", "qknorm_rope", "bias_ls_residual", "bias_gelu"]
+
+
+def op_bytes(rows: int, esz: int, patch_esz: int = 4, n_patch_rows: int = 0,
+             n_pos_rows: int = 0) -> dict:
+    """Algorithmic (minimal) HBM bytes per launch of each fused op."""
+    return {
+        "layernorm": rows * DIM * esz * 2,                   # read x, write out
+        "qknorm_rope": rows * DIM * esz * 2,                 # one of q / k
+        "bias_ls_residual": rows * DIM * esz * 3,            # read res, x; write out
+        "bias_gelu": rows * HIDDEN * esz * 2,                # read h, write act
+        "assemble": (n_patch_rows * DIM * patch_esz          # read patches (f32)
+                     + n_pos_rows * DIM * 4                  # pos-embed once
+                     + rows * DIM * esz),                    # write tokens
+    }
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--frames", type=int, default=32)
+    ap.add_argument("--dtype", choices=["f16", "f32"], default="f16")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="target CPU work for the oracle baseline sample")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=512,
+                    help="size of a plain torch copy launched once (HBM counter calibration)")
+    return ap.parse_args()
+
+
+class Pass:
+    """Buffers and launch sequence of one aggregator fused-op pass."""
+
+    def __init__(self, ctx, frames: int, dtype):
+        import numpy as np
+        import torch
+        from headshot_amd import rope
+
+        self.ctx, self.frames, self.dtype = ctx, frames, dtype
+        dev = ctx.device
+        p = GRID[0] * GRID[1]
+        self.p, self.t = p, p + 1 + N_REG
+        self.rows = frames * self.t
+        g = torch.Generator(device=dev)
+        g.manual_seed(42)
+
+        def normal(shape, mean=0.0, std=1.0, dt=torch.float32):
+            return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std
+                    + mean).to(dt)
+
+        rows = self.rows
+        # stage inputs (DINO patch tokens are f32)
+        self.patches = normal((frames * p, DIM))
+        self.pos = normal((p, DIM), 0.0, 0.02)
+        self.patch_bias = normal((DIM,), 0.0, 0.02)
+        self.cam = normal((2, DIM), dt=dtype)
+        self.reg = normal((2 * N_REG, DIM), dt=dtype)
+        # synthetic GEMM outputs (raw, biases applied by the fused ops)
+        self.q_raw = normal((rows, DIM), dt=dtype)
+        self.k_raw = normal((rows, DIM), dt=dtype)
+        self.proj_raw = normal((rows, DIM), dt=dtype)
+        self.fc1_raw = normal((rows, HIDDEN), dt=dtype)
+        self.fc2_raw = normal((rows, DIM), dt=dtype)
+        # outputs / residual stream
+        e = lambda *s: torch.empty(s, device=dev, dtype=dtype)  # noqa: E731
+        self.x = [e(rows, DIM), e(rows, DIM)]
+        self.x1 = e(rows, DIM)
+        self.normed = e(rows, DIM)
+        self.normed2 = e(rows, DIM)
+        self.q_head = e(rows * DIM)
+        self.k_head = e(rows * DIM)
+        self.act = e(rows, HIDDEN)
+        sin, cos = rope.tables(rope.periods(), *GRID)
+        self.sin = torch.from_numpy(sin).to(dev)
+        self.cos = torch.from_numpy(cos).to(dev)
+        # per-block parameters (f32), random init as in the reference configs
+        self.blocks = []
+        for _ in range(N_FRAME_BLOCKS + N_GLOBAL_BLOCKS):
+            self.blocks.append(dict(
+                ln1=(normal((DIM,), 1.0, 0.02), normal((DIM,), 0.0, 0.02)),
+                ln2=(normal((DIM,), 1.0, 0.02), normal((DIM,), 0.0, 0.02)),
+                qn=(normal((HEAD_DIM,), 1.0, 0.02), normal((HEAD_DIM,), 0.0, 0.02)),
+                kn=(normal((HEAD_DIM,), 1.0, 0.02), normal((HEAD_DIM,), 0.0, 0.02)),
+                proj_b=normal((DIM,), 0.0, 0.02), ls1=torch.full((DIM,), 1e-5, device=dev),
+                fc1_b=normal((HIDDEN,), 0.0, 0.02), fc2_b=normal((DIM,), 0.0, 0.02),
+                ls2=torch.full((DIM,), 1e-5, device=dev)))
+        esz = 2 if dtype == torch.float16 else 4
+        self.bytes = op_bytes(rows, esz, 4, frames * p, p)
+        self.pass_bytes = (self.bytes["assemble"]
+                           + len(self.blocks) * (2 * self.bytes["layernorm"]
+                                                 + 2 * self.bytes["qknorm_rope"]
+                                                 + 2 * self.bytes["bias_ls_residual"]
+                                                 + self.bytes["bias_gelu"]))
+        self.launches = {"assemble": 1}
+        for k in OPS[1:]:
+            self.launches[k] = len(self.blocks) * (1 if k == "bias_gelu" else 2)
+        _ = np  # numpy is used by the CPU leg
+
+    def run(self, timer=None):
+        """Enqueue one pass on the current stream. ``timer(op)`` returns a
+        context manager recording events around a launch."""
+        c = self.ctx
+        nullctx = _Null()
+        tm = timer or (lambda op: nullctx)
+        x = self.x[0]
+        with tm("assemble"):
+            c.assemble_tokens(self.patches, self.frames, self.p, self.cam, self.reg,
+                              patch_bias=self.patch_bias, pos=self.pos, out_dtype=self.dtype,
+                              out=x)
+        for i, b in enumerate(self.blocks):
+            frame_block = i % 2 == 0  # frame / global alternate (model/trunk.rs:92-143)
+            if frame_block:
+                s, t, rope = self.frames, self.t, (self.sin, self.cos, PREFIX)
+            else:
+                s, t, rope = 1, self.rows, None
+            x_out = self.x[1] if x is self.x[0] else self.x[0]
+            with tm("layernorm"):
+                c.layernorm(x, *b["ln1"], eps=EPS, out=self.normed)
+            with tm("qknorm_rope"):
+                c.qknorm_rope(self.q_raw, s, t, HEADS, HEAD_DIM, norm=b["qn"], rope=rope, eps=EPS,
+                              out=self.q_head)
+            with tm("qknorm_rope"):
+                c.qknorm_rope(self.k_raw, s, t, HEADS, HEAD_DIM, norm=b["kn"], rope=rope, eps=EPS,
+                              out=self.k_head)
+            with tm("bias_ls_residual"):
+                c.bias_ls_residual(x, self.proj_raw, b["ls1"], b["proj_b"], out=self.x1)
+            with tm("layernorm"):
+                c.layernorm(self.x1, *b["ln2"], eps=EPS, out=self.normed2)
+            with tm("bias_gelu"):
+                c.bias_gelu(self.fc1_raw, b["fc1_b"], out=self.act)
+            with tm("bias_ls_residual"):
+                c.bias_ls_residual(self.x1, self.fc2_raw, b["ls2"], b["fc2_b"], out=x_out)
+            x = x_out
+
+
+class _Null:
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        return False
+
+
+class EventTimer:
+    """Per-op HIP event pairs on the current (launch) stream."""
+
+    def __init__(self):
+        self.pairs = {op: [] for op in OPS}
+
+    def __call__(self, op):
+        import torch
+        timer = self
+
+        class _Ctx:
+            def __enter__(self_inner):
+                self_inner.a = torch.cuda.Event(enable_timing=True)
+                self_inner.b = torch.cuda.Event(enable_timing=True)
+                self_inner.a.record()
+                return self_inner
+
+            def __exit__(self_inner, *exc):
+                self_inner.b.record()
+                timer.pairs[op].append((self_inner.a, self_inner.b))
+                return False
+
+        return _Ctx()
+
+    def mean_ms(self):
+        return {op: (sum(a.elapsed_time(b) for a, b in v) / len(v)) if v else None
+                for op, v in self.pairs.items()}
+
+
+def cpu_baseline(bench: Pass, target_s: float):
+    """Time the oracle (C restatement of the reference's f32-math kernels, run
+    with the reference's unfused dispatch sequence and f16 storage rounding)
+    on the host cores over a bounded sample of the same pass."""
+    import numpy as np
+    import torch
+
+    from oracle import oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    O.set_num_threads(threads)
+    dt = O.F16 if bench.dtype == torch.float16 else O.F32
+    h = lambda t: t.cpu().numpy()  # noqa: E731
+    rows, frames = bench.rows, bench.frames
+    x = h(bench.x[0])
+    q, k = h(bench.q_raw), h(bench.k_raw)
+    proj, fc1, fc2 = h(bench.proj_raw), h(bench.fc1_raw), h(bench.fc2_raw)
+    sin, cos = h(bench.sin), h(bench.cos)
+    npdt = x.dtype
+    out = dict(normed=np.empty_like(x), q_head=np.empty_like(q), k_head=np.empty_like(k),
+               x1=np.empty_like(x), normed2=np.empty_like(x), act=np.empty_like(fc1),
+               x_out=np.empty_like(x))
+    patches, pos, pb = h(bench.patches), h(bench.pos), h(bench.patch_bias)
+    cam, reg = h(bench.cam), h(bench.reg)
+
+    done_bytes = 0
+    blocks_done = 0
+    t0 = time.perf_counter()
+    O.assemble_tokens(patches, pb, pos, cam, reg, frames, bench.p, N_REG, npdt)
+    done_bytes += bench.bytes["assemble"]
+    block_bytes = (2 * bench.bytes["layernorm"] + 2 * bench.bytes["qknorm_rope"]
+                   + 2 * bench.bytes["bias_ls_residual"] + bench.bytes["bias_gelu"])
+    for i, b in enumerate(bench.blocks):
+        p = {kk: tuple(h(t) for t in v) if isinstance(v, tuple) else h(v) for kk, v in b.items()}
+        frame_block = i % 2 == 0
+        s, t = (frames, bench.t) if frame_block else (1, rows)
+        O.block_ops(dt, x, *p["ln1"], q, k, *p["qn"], *p["kn"],
+                    sin if frame_block else None, cos if frame_block else None, PREFIX,
+                    proj, p["proj_b"], p["ls1"], *p["ln2"], fc1, p["fc1_b"], fc2, p["fc2_b"],
+                    p["ls2"], out, s, t, DIM, HEADS, HIDDEN, EPS)
+        done_bytes += block_bytes
+        blocks_done += 1
+        if time.perf_counter() - t0 >= target_s and blocks_done >= 2:
+            break
+    elapsed = time.perf_counter() - t0
+    return {
+        "value": round(done_bytes / elapsed / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle/hs_oracle.c (C restatement of the reference's WGSL kernels, unfused "
+                   f"reference dispatch order, {'f16' if dt == O.F16 else 'f32'} storage) over "
+                   f"assembly + {blocks_done} of 48 blocks at S={frames}: "
+                   f"{done_bytes / 1e9:.2f} GB algorithmic in {elapsed:.1f} s, "
+                   f"{threads} OpenMP threads"),
+        "ms_per_block": round(elapsed * 1e3 / max(blocks_done, 1), 1),
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU: the fused per-layer ops are "
+                                   "row-local and shard by frames with no exchange; run with "
+                                   "--gpus 1"}))
+        sys.exit(2)
+    import torch
+
+    from headshot_amd.context import HipContext
+
+    dtype = torch.float16 if args.dtype == "f16" else torch.float32
+    ctx = HipContext("cuda:0")
+    bench = Pass(ctx, args.frames, dtype)
+    torch.cuda.synchronize()
+
+    # HBM counter calibration: one plain copy of known size (outside timing).
+    if args.calibrate_copy_mib > 0:
+        n = args.calibrate_copy_mib * (1 << 20) // 4
+        a = torch.empty(n, device=ctx.device, dtype=torch.float32).fill_(1.0)
+        b_ = torch.empty_like(a)
+        b_.copy_(a)
+        torch.cuda.synchronize()
+        del a, b_
+
+    for _ in range(args.warmup):
+        bench.run()
+    torch.cuda.synchronize()
+
+    timer = EventTimer()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(args.steps):
+        bench.run(timer)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+
+    per_op = {}
+    mean = timer.mean_ms()
+    for op in OPS:
+        us = mean[op] * 1e3
+        gbs = bench.bytes[op] / (us * 1e-6) / 1e9
+        per_op[op] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                      "bytes": bench.bytes[op], "launches_per_pass": bench.launches[op]}
+    ops_ms = sum(per_op[op]["us"] * bench.launches[op] for op in OPS) / 1e3
+    dominant = max(OPS, key=lambda op: per_op[op]["us"] * bench.launches[op])
+    value = bench.pass_bytes / (ms * 1e-3) / 1e9
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.dtype,
+        "data": "synthetic: torch seeded N(0,1) activations/GEMM outputs, random-init params "
+                "(LN gamma N(1,.02), beta/biases/pos N(0,.02), LayerScale 1e-5)",
+        "config": {"workload": f"aggregator fused-op pass: assembly + {N_FRAME_BLOCKS} frame + "
+                               f"{N_GLOBAL_BLOCKS} global blocks",
+                   "frames": args.frames, "tokens_per_frame": bench.t, "dim": DIM,
+                   "heads": HEADS, "head_dim": HEAD_DIM, "hidden": HIDDEN, "prefix": PREFIX,
+                   "grid": f"{GRID[0]}x{GRID[1]}", "eps": EPS},
+        "frac_of_peak": round(value / PEAK_GBS, 4),
+        "pass_bytes": bench.pass_bytes,
+        "tokens_per_s": round(bench.rows / (ms * 1e-3), 1),
+        "ops_ms_per_step": round(ops_ms, 3),
+        "ops": per_op,
+        "roofline": {"bound": "hbm", "kernel": dominant,
+                     "achieved": per_op[dominant]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": per_op[dominant]["frac"], "traffic": None},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,252 @@
+"""``HipContext``: headshot-server's op-dispatch surface over libheadshot_hip.
+
+Mirrors ``impl GpuContext`` (crates/headshot-server/src/engine/ops.rs,
+engine/tensor.rs) for the per-layer op path: same method names, argument
+meaning and error behaviour. Tensors are torch tensors in device memory
+(torch supplies allocation and streams only; every op runs a HIP kernel of
+libheadshot_hip through its C ABI on the current stream). Storage is
+float32 or float16; norm weights, biases, gammas and RoPE tables must be
+float32 (engine/ops.rs:5-8). Contract violations raise AssertionError, as the
+reference's ``assert!`` panics.
+
+Like the reference, every op except ``rope_apply`` and ``copy_rows`` returns
+a new output tensor; the fused ops also accept ``out=`` to write into a
+caller buffer (no allocation).
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from . import _lib
+
+F32 = torch.float32
+F16 = torch.float16
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == F32:
+        return _lib.HS_F32
+    if t.dtype == F16:
+        return _lib.HS_F16
+    raise AssertionError(f"storage must be f32 or f16, got {t.dtype}")
+
+
+def _dev(t: torch.Tensor, what: str) -> int:
+    assert t.is_cuda, f"{what} must live in device memory"
+    assert t.is_contiguous(), f"{what} must be contiguous"
+    return t.data_ptr()
+
+
+def _param(t, n: int, what: str) -> int:
+    assert t.dtype == F32, f"{what} must be f32"
+    assert t.numel() == n, f"{what} len {t.numel()} != {n}"
+    return _dev(t, what)
+
+
+def _opt(t, n: int, what: str):
+    return None if t is None else _param(t, n, what)
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+class HipContext:
+    """One device's op surface. ``device`` is a torch device (default cuda:0)."""
+
+    def __init__(self, device: str | torch.device = "cuda"):
+        self.lib = _lib.load()
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise AssertionError("HipContext needs a HIP device")
+        if not torch.cuda.is_available():
+            raise RuntimeError("no HIP device visible (torch.cuda.is_available() is False)")
+
+    # ------------------------------------------------------------------ tensors
+
+    def empty_typed(self, shape, dtype: torch.dtype = F32) -> torch.Tensor:
+        """engine/tensor.rs:132-141 (uninitialised device tensor)."""
+        return torch.empty(tuple(shape), dtype=dtype, device=self.device)
+
+    def empty(self, shape) -> torch.Tensor:
+        return self.empty_typed(shape, F32)
+
+    def tensor_from_f32(self, shape, data, dtype: torch.dtype = F32) -> torch.Tensor:
+        """engine/tensor.rs:71-91: upload f32 data as ``dtype`` storage (f16 by
+        round-to-nearest-even)."""
+        arr = np.asarray(data, dtype=np.float32)
+        assert arr.size == int(np.prod(shape)), "shape/data mismatch"
+        host = torch.from_numpy(np.ascontiguousarray(arr).reshape(tuple(shape)))
+        return host.to(device=self.device, dtype=dtype)
+
+    def tensor_from_slice(self, shape, data) -> torch.Tensor:
+        return self.tensor_from_f32(shape, data, F32)
+
+    def download(self, t: torch.Tensor) -> np.ndarray:
+        """engine/tensor.rs:162-198: flush, read back as f32."""
+        torch.cuda.current_stream().synchronize()
+        return t.detach().to("cpu").to(F32).numpy()
+
+    def sync(self) -> None:
+        torch.cuda.current_stream().synchronize()
+
+    # ----------------------------------------------------------- reference ops
+
+    def layernorm(self, x, weight, bias, eps: float = 1e-5, out=None) -> torch.Tensor:
+        """engine/ops.rs:130-153 (eps is 1e-5 there; pass it explicitly here)."""
+        dim = x.shape[-1]
+        rows = x.numel() // dim if dim else 0
+        w = _param(weight, dim, "norm weight")
+        b = _param(bias, dim, "norm bias")
+        if out is None:
+            out = self.empty_typed(x.shape, x.dtype)
+        assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
+        _lib.check(self.lib.hs_layernorm(_stream(), _dt(x), _dev(x, "x"), w, b, _dev(out, "out"),
+                                         rows, dim, eps), "layernorm")
+        return out
+
+    def gelu(self, x, out=None) -> torch.Tensor:
+        """engine/ops.rs:155-165."""
+        if out is None:
+            out = self.empty_typed(x.shape, x.dtype)
+        assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
+        _lib.check(self.lib.hs_gelu(_stream(), _dt(x), _dev(x, "x"), _dev(out, "out"), x.numel()),
+                   "gelu")
+        return out
+
+    def residual_ls(self, res, x, gamma, out=None) -> torch.Tensor:
+        """engine/ops.rs:167-183: ``res + gamma ⊙ x``."""
+        assert res.numel() == x.numel(), "res/x length"
+        assert res.dtype == x.dtype, "res/x dtype"
+        assert gamma.dtype == F32, "gamma must be f32"
+        dim = gamma.numel()
+        assert dim > 0 and x.numel() % dim == 0, "gamma must tile x"
+        if out is None:
+            out = self.empty_typed(res.shape, x.dtype)
+        _lib.check(self.lib.hs_residual_ls(_stream(), _dt(x), _dev(res, "res"), _dev(x, "x"),
+                                           _dev(gamma, "gamma"), _dev(out, "out"), x.numel(), dim),
+                   "residual_ls")
+        return out
+
+    def split_heads(self, x, s: int, t: int, h: int, d: int) -> torch.Tensor:
+        """engine/ops.rs:185-200: (S·T, H·D) → (S, H, T, D)."""
+        assert x.numel() == s * t * h * d, "split_heads size"
+        out = self.empty_typed((s, h, t, d), x.dtype)
+        _lib.check(self.lib.hs_split_heads(_stream(), _dt(x), _dev(x, "x"), _dev(out, "out"),
+                                           s, t, h, d), "split_heads")
+        return out
+
+    def rope_apply(self, x, sin, cos, prefix: int) -> None:
+        """engine/ops.rs:202-223: in place on (S, H, T, D); tables (T−prefix, D)."""
+        assert x.dim() == 4, "rope_apply wants (S,H,T,D)"
+        s, h, t, d = x.shape
+        assert 0 <= prefix <= t, "prefix"
+        assert sin.numel() == (t - prefix) * d, "table size"
+        assert sin.dtype == F32 and cos.dtype == F32, "rope tables must be f32"
+        assert cos.numel() == sin.numel(), "table size"
+        _lib.check(self.lib.hs_rope_apply(_stream(), _dt(x), _dev(x, "x"), _dev(sin, "sin"),
+                                          _dev(cos, "cos"), s, h, t, d, prefix), "rope_apply")
+
+    def cast_to_f16(self, x) -> torch.Tensor:
+        """engine/ops.rs:336-348."""
+        assert x.dtype == F32, "cast_to_f16 wants f32"
+        out = self.empty_typed(x.shape, F16)
+        _lib.check(self.lib.hs_cast_f32_to_f16(_stream(), _dev(x, "x"), _dev(out, "out"),
+                                               x.numel()), "cast_to_f16")
+        return out
+
+    def copy_rows(self, src, src_row: int, dst, dst_row: int, n_rows: int) -> None:
+        """engine/tensor.rs:146-160: rows of the last dimension."""
+        assert src.dtype == dst.dtype, "copy_rows dtype"
+        row_bytes = src.shape[-1] * src.element_size()
+        assert row_bytes == dst.shape[-1] * dst.element_size(), "copy_rows row width"
+        assert (src_row + n_rows) * row_bytes <= src.numel() * src.element_size(), "src rows"
+        assert (dst_row + n_rows) * row_bytes <= dst.numel() * dst.element_size(), "dst rows"
+        _lib.check(self.lib.hs_copy_rows(_stream(), _dev(src, "src"), src_row, _dev(dst, "dst"),
+                                         dst_row, n_rows, row_bytes), "copy_rows")
+
+    def tiled_add(self, x, table) -> torch.Tensor:
+        """engine/ops.rs:374-389 (f32 only)."""
+        assert x.dtype == F32 and table.dtype == F32, "tiled_add is f32"
+        assert table.numel() > 0 and x.numel() % table.numel() == 0, "table must tile x"
+        out = self.empty(x.shape)
+        _lib.check(self.lib.hs_tiled_add(_stream(), _dev(x, "x"), _dev(table, "table"),
+                                         _dev(out, "out"), x.numel(), table.numel()), "tiled_add")
+        return out
+
+    # --------------------------------------------------------------- fused ops
+
+    def qknorm_rope(self, x_tok, s: int, t: int, h: int, d: int, norm=None, rope=None,
+                    eps: float = 1e-5, out=None) -> torch.Tensor:
+        """split_heads + QK-norm + RoPE (model/block.rs:130-146) in one pass.
+
+        ``norm`` = (weight, bias) f32 (d) or None; ``rope`` = (sin, cos, prefix)
+        with f32 tables (t − prefix, d) or None (global blocks)."""
+        assert x_tok.numel() == s * t * h * d, "qknorm_rope size"
+        nw = nb = sn = cs = None
+        prefix = 0
+        if norm is not None:
+            nw = _param(norm[0], d, "qk-norm weight")
+            nb = _param(norm[1], d, "qk-norm bias")
+        if rope is not None:
+            sin, cos, prefix = rope
+            assert 0 <= prefix <= t, "prefix"
+            sn = _param(sin, (t - prefix) * d, "rope sin table")
+            cs = _param(cos, (t - prefix) * d, "rope cos table")
+        if out is None:
+            out = self.empty_typed((s, h, t, d), x_tok.dtype)
+        assert out.dtype == x_tok.dtype and out.numel() == x_tok.numel(), "out shape/dtype"
+        _lib.check(self.lib.hs_qknorm_rope(_stream(), _dt(x_tok), _dev(x_tok, "x"), nw, nb, sn, cs,
+                                           _dev(out, "out"), s, t, h, d, prefix, eps),
+                   "qknorm_rope")
+        return out
+
+    def bias_gelu(self, x, bias=None, out=None) -> torch.Tensor:
+        """fc1 bias epilogue + GELU (model/block.rs:173-174)."""
+        cols = x.shape[-1]
+        rows = x.numel() // cols if cols else 0
+        b = _opt(bias, cols, "fc1 bias")
+        if out is None:
+            out = self.empty_typed(x.shape, x.dtype)
+        assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
+        _lib.check(self.lib.hs_bias_gelu(_stream(), _dt(x), _dev(x, "x"), b, _dev(out, "out"),
+                                         rows, cols), "bias_gelu")
+        return out
+
+    def bias_ls_residual(self, res, x, gamma, bias=None, out=None) -> torch.Tensor:
+        """proj/fc2 bias epilogue + LayerScale + residual (model/block.rs:150-155)."""
+        assert res.numel() == x.numel() and res.dtype == x.dtype, "res/x shape or dtype"
+        dim = x.shape[-1]
+        rows = x.numel() // dim if dim else 0
+        g = _param(gamma, dim, "gamma")
+        b = _opt(bias, dim, "bias")
+        if out is None:
+            out = self.empty_typed(res.shape, x.dtype)
+        assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
+        _lib.check(self.lib.hs_bias_ls_residual(_stream(), _dt(x), _dev(res, "res"), _dev(x, "x"),
+                                                b, g, _dev(out, "out"), rows, dim),
+                   "bias_ls_residual")
+        return out
+
+    def assemble_tokens(self, patches, s: int, p: int, cam, reg, patch_bias=None, pos=None,
+                        out_dtype: torch.dtype = F16, n_var: int = 2, out=None) -> torch.Tensor:
+        """Token assembly (model/trunk.rs:68-85): per frame
+        ``[cam[v], reg[v·R .. v·R+R), patches + bias + pos]`` → (S·T, D)."""
+        d = patches.shape[-1]
+        assert patches.numel() == s * p * d, "patches shape"
+        assert cam.dtype == out_dtype and cam.numel() == n_var * d, "camera token shape/dtype"
+        r = reg.numel() // (n_var * d) if reg is not None else 0
+        if reg is not None:
+            assert reg.dtype == out_dtype and reg.numel() == n_var * r * d, "register token shape"
+        b = _opt(patch_bias, d, "patch bias")
+        ps = _opt(pos, p * d, "pos embed")
+        t = 1 + r + p
+        if out is None:
+            out = self.empty_typed((s * t, d), out_dtype)
+        assert out.dtype == out_dtype and out.numel() == s * t * d, "out shape/dtype"
+        _lib.check(self.lib.hs_assemble_tokens(
+            _stream(), _dt(out), _dev(patches, "patches"), _dt(patches), b, ps, _dev(cam, "cam"),
+            None if reg is None else _dev(reg, "reg"), _dev(out, "out"), s, p, r, d, n_var),
+            "assemble_tokens")
+        return out

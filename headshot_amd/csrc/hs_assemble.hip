@@ -1,0 +1,210 @@
+// Patch-token assembly for gfx950: one pass that builds the (S*T, D) token
+// matrix the first block reads (model/trunk.rs:68-85: per frame a camera
+// token variant, R register token variants and the P patch tokens; the
+// reference issues 3*S buffer copies plus a full f32 -> f16 cast pass, and
+// DINO adds the patch-embed bias in its GEMM epilogue, model/dino.rs:76-93).
+// Patch rows fold the patch bias and the positional-embedding add (the
+// tiled_add.wesl semantics, out[i] = x[i] + table[i % block]) into the cast,
+// so each patch element is read once in its input dtype and written once.
+//
+// One wave64 per output row (persistent); each lane moves 4 consecutive
+// channels per step, CHUNKS steps per row. Rows are independent; the
+// camera/register gather is row-granular, so no LDS staging is needed.
+#include "hs_common.hpp"
+
+namespace hs {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / 64;
+constexpr int kBlocksPerCu = 8;
+
+__device__ __forceinline__ void load4(const float* p, float (&f)[4]) {
+    float4 v = ld_f32x4(p);
+    f[0] = v.x, f[1] = v.y, f[2] = v.z, f[3] = v.w;
+}
+__device__ __forceinline__ void load4(const f16* p, float (&f)[4]) {
+    u32x2 v = *reinterpret_cast<const u32x2*>(p);
+    const f16x2 a = u2h2(v[0]), b = u2h2(v[1]);
+    f[0] = static_cast<float>(a.x), f[1] = static_cast<float>(a.y);
+    f[2] = static_cast<float>(b.x), f[3] = static_cast<float>(b.y);
+}
+__device__ __forceinline__ void store4(float* p, const float (&f)[4]) {
+    *reinterpret_cast<float4*>(p) = make_float4(f[0], f[1], f[2], f[3]);
+}
+__device__ __forceinline__ void store4(f16* p, const float (&f)[4]) {
+    f16x2 a, b;
+    a.x = static_cast<f16>(f[0]), a.y = static_cast<f16>(f[1]);
+    b.x = static_cast<f16>(f[2]), b.y = static_cast<f16>(f[3]);
+    u32x2 v;
+    v[0] = h22u(a), v[1] = h22u(b);
+    *reinterpret_cast<u32x2*>(p) = v;
+}
+
+// Patch-row value as the reference sequence stores it: the GEMM epilogue
+// stores (x + bias) in the patch dtype, then tiled_add adds pos.
+template <typename TP>
+__device__ __forceinline__ float patch_value(float x, float b, float p, bool has_b, bool has_p) {
+    if (has_b) x = storage_round(x + b, TP{});
+    if (has_p) x = storage_round(x + p, TP{});
+    return x;
+}
+
+template <typename TO, typename TP, int CHUNKS>
+__global__ __launch_bounds__(kBlock) void assemble_kernel(
+    const TP* __restrict__ patches, const float* __restrict__ pbias, const float* __restrict__ pos,
+    const TO* __restrict__ cam, const TO* __restrict__ reg, TO* __restrict__ out, int64_t out_rows,
+    int seq, int np, int nr, int n_var) {
+    constexpr int D = 256 * CHUNKS;
+    const int lane = lane_id();
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    const bool has_b = pbias != nullptr, has_p = pos != nullptr;
+    float bv[CHUNKS][4];
+    if (has_b) {
+#pragma unroll
+        for (int c = 0; c < CHUNKS; c++) load4(pbias + c * 256 + lane * 4, bv[c]);
+    }
+    for (int64_t row = wave; row < out_rows; row += nwaves) {
+        const uint32_t f = static_cast<uint32_t>(row) / static_cast<uint32_t>(seq);
+        const int t = static_cast<int>(static_cast<uint32_t>(row) - f * static_cast<uint32_t>(seq));
+        const int v = (n_var == 2 && f != 0) ? 1 : 0;
+        TO* orow = out + row * D + lane * 4;
+        if (t <= nr) {
+            const TO* src = t == 0 ? cam + static_cast<int64_t>(v) * D
+                                   : reg + (static_cast<int64_t>(v) * nr + (t - 1)) * D;
+            float vals[CHUNKS][4];
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) load4(src + c * 256 + lane * 4, vals[c]);
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) store4(orow + c * 256, vals[c]);
+        } else {
+            const int p = t - 1 - nr;
+            const TP* src = patches + (static_cast<int64_t>(f) * np + p) * D + lane * 4;
+            const float* prow = has_p ? pos + static_cast<int64_t>(p) * D + lane * 4 : nullptr;
+            float x[CHUNKS][4], pe[CHUNKS][4];
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) load4(src + c * 256, x[c]);
+            if (has_p) {
+#pragma unroll
+                for (int c = 0; c < CHUNKS; c++) load4(prow + c * 256, pe[c]);
+            }
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) {
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    x[c][k] = patch_value<TP>(x[c][k], has_b ? bv[c][k] : 0.0f,
+                                              has_p ? pe[c][k] : 0.0f, has_b, has_p);
+                store4(orow + c * 256, x[c]);
+            }
+        }
+    }
+}
+
+// Any D, any alignment: lanes strided over the row.
+template <typename TO, typename TP>
+__global__ __launch_bounds__(kBlock) void assemble_generic_kernel(
+    const TP* patches, const float* pbias, const float* pos, const TO* cam, const TO* reg, TO* out,
+    int64_t out_rows, int seq, int np, int nr, int d, int n_var) {
+    const int lane = lane_id();
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    const bool has_b = pbias != nullptr, has_p = pos != nullptr;
+    for (int64_t row = wave; row < out_rows; row += nwaves) {
+        const int64_t f = row / seq;
+        const int t = static_cast<int>(row - f * seq);
+        const int64_t v = (n_var == 2 && f != 0) ? 1 : 0;
+        TO* orow = out + row * d;
+        if (t <= nr) {
+            const TO* src = t == 0 ? cam + v * d : reg + (v * nr + (t - 1)) * d;
+            for (int j = lane; j < d; j += 64) orow[j] = src[j];
+        } else {
+            const int64_t p = t - 1 - nr;
+            const TP* src = patches + (f * np + p) * d;
+            for (int j = lane; j < d; j += 64) {
+                float x = load_elem(src + j);
+                x = patch_value<TP>(x, has_b ? pbias[j] : 0.0f, has_p ? pos[p * d + j] : 0.0f,
+                                    has_b, has_p);
+                store_elem(orow + j, x);
+            }
+        }
+    }
+}
+
+int64_t persistent_blocks(int64_t work_waves) {
+    const int64_t cap = static_cast<int64_t>(num_cus()) * kBlocksPerCu;
+    const int64_t blocks = ceil_div(work_waves, kWavesPerBlock);
+    return blocks < cap ? blocks : cap;
+}
+
+template <typename TO, typename TP>
+hs_status launch(hipStream_t st, const void* patches, const float* pbias, const float* pos,
+                 const void* cam, const void* reg, void* out, int s, int np, int nr, int d,
+                 int n_var) {
+    const int seq = 1 + nr + np;
+    const int64_t out_rows = static_cast<int64_t>(s) * seq;
+    const dim3 grid(static_cast<uint32_t>(persistent_blocks(out_rows)));
+    const auto* P = static_cast<const TP*>(patches);
+    const auto* C = static_cast<const TO*>(cam);
+    const auto* R = static_cast<const TO*>(reg);
+    auto* O = static_cast<TO*>(out);
+    const bool vec_ok = d % 256 == 0 && aligned16(patches) && aligned16(out) && aligned16(cam) &&
+                        (nr == 0 || aligned16(reg)) && (!pbias || aligned16(pbias)) &&
+                        (!pos || aligned16(pos));
+    if (vec_ok) {
+        switch (d / 256) {
+            case 1:
+                assemble_kernel<TO, TP, 1><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows, seq, np, nr, n_var);
+                return check_launch("assemble_tokens");
+            case 2:
+                assemble_kernel<TO, TP, 2><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows, seq, np, nr, n_var);
+                return check_launch("assemble_tokens");
+            case 4:
+                assemble_kernel<TO, TP, 4><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows, seq, np, nr, n_var);
+                return check_launch("assemble_tokens");
+            case 8:
+                assemble_kernel<TO, TP, 8><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows, seq, np, nr, n_var);
+                return check_launch("assemble_tokens");
+            default: break;
+        }
+    }
+    assemble_generic_kernel<TO, TP><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows,
+                                                                   seq, np, nr, d, n_var);
+    return check_launch("assemble_tokens");
+}
+
+}  // namespace
+}  // namespace hs
+
+extern "C" hs_status hs_assemble_tokens(hs_stream_t stream, hs_dtype out_dt, const void* patches,
+                                        hs_dtype patch_dt, const float* patch_bias,
+                                        const float* pos, const void* cam, const void* reg,
+                                        void* out, int32_t s, int32_t p, int32_t r, int32_t d,
+                                        int32_t n_var) {
+    using namespace hs;
+    if (!valid_dtype(out_dt) || !valid_dtype(patch_dt))
+        return fail(HS_EINVAL, "assemble_tokens: unknown dtype");
+    if (s < 0 || p < 0 || r < 0 || d <= 0)
+        return fail(HS_EINVAL, "assemble_tokens: shape S=%d P=%d R=%d D=%d", s, p, r, d);
+    if (n_var != 1 && n_var != 2) return fail(HS_EINVAL, "assemble_tokens: n_var must be 1 or 2");
+    const int64_t seq = int64_t{1} + r + p;
+    const int64_t out_rows = static_cast<int64_t>(s) * seq;
+    if (out_rows >= (int64_t{1} << 31) || seq >= (int64_t{1} << 31))
+        return fail(HS_EINVAL, "assemble_tokens: S*T must be below 2^31");
+    if (s == 0) return HS_OK;
+    if (!out || !cam || (r > 0 && !reg) || (p > 0 && !patches))
+        return fail(HS_EINVAL, "assemble_tokens: null buffer");
+    const int64_t out_bytes = out_rows * d * dtype_size(out_dt);
+    if (overlaps(out, out_bytes, patches, static_cast<int64_t>(s) * p * d * dtype_size(patch_dt)) ||
+        overlaps(out, out_bytes, cam, n_var * d * dtype_size(out_dt)) ||
+        overlaps(out, out_bytes, reg, static_cast<int64_t>(n_var) * r * d * dtype_size(out_dt)))
+        return fail(HS_EINVAL, "assemble_tokens: out overlaps an input");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (out_dt == HS_F16)
+        return patch_dt == HS_F32
+                   ? launch<f16, float>(st, patches, patch_bias, pos, cam, reg, out, s, p, r, d, n_var)
+                   : launch<f16, f16>(st, patches, patch_bias, pos, cam, reg, out, s, p, r, d, n_var);
+    return patch_dt == HS_F32
+               ? launch<float, float>(st, patches, patch_bias, pos, cam, reg, out, s, p, r, d, n_var)
+               : launch<float, f16>(st, patches, patch_bias, pos, cam, reg, out, s, p, r, d, n_var);
+}

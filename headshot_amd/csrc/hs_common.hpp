@@ -1,0 +1,191 @@
+// Shared device and host helpers for the gfx950 kernels of libheadshot_hip.
+//
+// Device side: 16-byte vector loads/stores, f16 <-> f32 conversion (round to
+// nearest even), and wave64 reductions built on DPP lane permutes (no LDS).
+// Host side: error reporting for the C ABI and launch-shape helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "headshot_hip.h"
+
+namespace hs {
+
+// ---------------------------------------------------------------------------
+// host: errors
+
+// Records a message for hs_last_error() and returns `code`.
+hs_status fail(hs_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// HS_EHIP with the pending launch error if the last launch failed, else HS_OK.
+hs_status check_launch(const char* what);
+// Number of compute units of the current device (cached per device).
+int num_cus();
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// [a, a+na) and [b, b+nb) byte ranges overlap.
+inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
+    auto pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+    return na > 0 && nb > 0 && pa < pb + static_cast<uintptr_t>(nb) &&
+           pb < pa + static_cast<uintptr_t>(na);
+}
+
+inline int64_t dtype_size(hs_dtype dt) { return dt == HS_F16 ? 2 : 4; }
+
+inline bool valid_dtype(hs_dtype dt) { return dt == HS_F32 || dt == HS_F16; }
+
+// ---------------------------------------------------------------------------
+// device: storage types and 16-byte vectors
+
+using f16 = _Float16;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+
+// Elements of T in one 16-byte vector.
+template <typename T>
+struct Vec {
+    static constexpr int N = 16 / sizeof(T);
+};
+
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Streaming variants: data touched once (non-temporal hint).
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void st16_nt(void* p, u32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+__device__ __forceinline__ float4 ld_f32x4(const float* p) {
+    return *reinterpret_cast<const float4*>(p);
+}
+
+// Scalar reinterpretation, always of a value. Bit-casting a vector element
+// expression such as v[k] in place reads element 0 with this compiler, so
+// elements are passed through these by-value helpers.
+__device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ f16x2 u2h2(uint32_t u) { return __builtin_bit_cast(f16x2, u); }
+__device__ __forceinline__ uint32_t h22u(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// Unpack a 16-byte vector of T into f32.
+__device__ __forceinline__ void unpack(u32x4 v, float (&f)[8], f16) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const f16x2 h = u2h2(v[k]);
+        f[2 * k] = static_cast<float>(h.x);
+        f[2 * k + 1] = static_cast<float>(h.y);
+    }
+}
+__device__ __forceinline__ void unpack(u32x4 v, float (&f)[4], float) {
+#pragma unroll
+    for (int k = 0; k < 4; k++) f[k] = u2f(v[k]);
+}
+
+// Pack f32 values into a 16-byte vector of T (f16: round to nearest even).
+__device__ __forceinline__ u32x4 pack(const float (&f)[8], f16) {
+    u32x4 v;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        f16x2 h;
+        h.x = static_cast<f16>(f[2 * k]);
+        h.y = static_cast<f16>(f[2 * k + 1]);
+        v[k] = h22u(h);
+    }
+    return v;
+}
+__device__ __forceinline__ u32x4 pack(const float (&f)[4], float) {
+    u32x4 v;
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = f2u(f[k]);
+    return v;
+}
+
+// The value a later dispatch would read back after storing v as T: the
+// reference rounds to its storage type after every dispatch, and the fused
+// kernels reproduce those rounding points in registers.
+__device__ __forceinline__ float storage_round(float v, f16) {
+    return static_cast<float>(static_cast<f16>(v));
+}
+__device__ __forceinline__ float storage_round(float v, float) { return v; }
+
+template <typename T>
+__device__ __forceinline__ float load_elem(const T* p) {
+    return static_cast<float>(*p);
+}
+template <typename T>
+__device__ __forceinline__ void store_elem(T* p, float v) {
+    *p = static_cast<T>(v);
+}
+
+// ---------------------------------------------------------------------------
+// device: wave64 lane permutes (DPP) and reductions
+
+// dpp_ctrl encodings (GFX9 DPP).
+constexpr int kQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;  // lane i <- lane 7-i within each 8 lanes
+constexpr int kRowMirror = 0x140;      // lane i <- lane 15-i within each 16 lanes
+constexpr int kRowBcast15 = 0x142;     // lane 15 of each row -> next row
+constexpr int kRowBcast31 = 0x143;     // lane 31 -> rows 2 and 3
+
+template <int CTRL, int ROW_MASK = 0xF, int BANK_MASK = 0xF>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                           BANK_MASK, false));
+}
+
+// Sum over each aligned group of 8 lanes; every lane receives its group's sum.
+__device__ __forceinline__ float sum8(float v) {
+    v += dpp<kQuadXor1>(v);
+    v += dpp<kQuadXor2>(v);
+    v += dpp<kRowHalfMirror>(v);
+    return v;
+}
+
+// Sum over each aligned group of 16 lanes; every lane receives the sum.
+__device__ __forceinline__ float sum16(float v) {
+    v = sum8(v);
+    v += dpp<kRowMirror>(v);
+    return v;
+}
+
+// Sum over the whole wave64, returned wave-uniform (scalar register).
+__device__ __forceinline__ float wave_sum(float v) {
+    v = sum16(v);
+    v += dpp<kRowBcast15, 0xA>(v);
+    v += dpp<kRowBcast31, 0xC>(v);
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Sum over lane groups of G (8, 16 or 64) lanes.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G == 8 || G == 16 || G == 64, "group of 8, 16 or 64 lanes");
+    if constexpr (G == 8) return sum8(v);
+    if constexpr (G == 16) return sum16(v);
+    if constexpr (G == 64) return wave_sum(v);
+}
+
+// Value held by the mirror-partner lane within a group of G lanes
+// (lane i <-> G-1-i).
+template <int G>
+__device__ __forceinline__ float group_mirror(float v) {
+    static_assert(G == 8 || G == 16, "mirror within 8 or 16 lanes");
+    if constexpr (G == 8) return dpp<kRowHalfMirror>(v);
+    if constexpr (G == 16) return dpp<kRowMirror>(v);
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+}  // namespace hs

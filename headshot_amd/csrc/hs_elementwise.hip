@@ -1,0 +1,347 @@
+// Elementwise per-layer ops for gfx950:
+//   bias + erf-GELU        (fc1 epilogue, linear_wmma.wgsl:69-74, + gelu.wesl)
+//   bias + LayerScale + residual (proj/fc2 epilogue + residual_ls.wesl)
+//   f32 -> f16 cast        (cast_f32_to_f16.wesl)
+//   tiled add              (tiled_add.wesl)
+//
+// The bias/GELU and LayerScale kernels are column-stationary and persistent:
+// the grid's stride through the flat (rows, cols) tensor is a multiple of
+// cols, so each thread owns the same V consecutive columns (one 16-byte
+// vector) for every row it visits and keeps their bias/gamma in registers.
+// Each thread issues U independent 16-byte loads per tensor before it
+// computes, so a wave keeps U KiB per input stream in flight.
+#include "hs_common.hpp"
+
+namespace hs {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kBlocksPerCu = 8;
+
+// erf by Abramowitz & Stegun 7.1.26 (gelu.wesl:18-27), f32. The
+// reciprocal and exponential use the hardware v_rcp_f32 / v_exp_f32.
+__device__ __forceinline__ float erf_as(float v) {
+    const float a = fabsf(v);
+    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
+    float p = fmaf(1.061405429f, t, -1.453152027f);
+    p = fmaf(p, t, 1.421413741f);
+    p = fmaf(p, t, -0.284496736f);
+    p = fmaf(p, t, 0.254829592f);
+    p = p * t;
+    // exp(-a^2) = 2^(-a^2 * log2(e))
+    const float e = __builtin_amdgcn_exp2f((a * a) * -1.4426950408889634f);
+    return copysignf(fmaf(-p, e, 1.0f), v);
+}
+
+// gelu.wesl:36-38: 0.5 * v * (1 + erf(v / sqrt(2)))
+__device__ __forceinline__ float gelu_f(float v) {
+    const float h = 0.5f * v;
+    return fmaf(h, erf_as(v * 0.7071067811865475f), h);
+}
+
+// Grid size (in blocks) for a column-stationary launch: the stride
+// blocks*kBlock*V must be a multiple of cols. Returns 0 if no such grid of
+// useful size exists.
+int64_t column_stationary_blocks(int64_t total, int64_t cols, int V, int U) {
+    const int64_t per_block = static_cast<int64_t>(kBlock) * V;
+    int64_t a = per_block, b = cols;
+    while (b) {
+        int64_t r = a % b;
+        a = b;
+        b = r;
+    }
+    const int64_t step = cols / a;  // blocks must be a multiple of this
+    const int64_t want = ceil_div(total, per_block * U);
+    const int64_t cap = static_cast<int64_t>(num_cus()) * kBlocksPerCu;
+    int64_t blocks = want < cap ? want : cap;
+    blocks = ceil_div(blocks, step) * step;
+    if (blocks > 4 * cap) return 0;
+    return blocks;
+}
+
+template <typename T, bool BIAS, int U>
+__global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const float* __restrict__ bias,
+                                                           T* out, int64_t total, int cols) {
+    constexpr int V = Vec<T>::N;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * V;
+    const int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * V;
+    float bv[V];
+    if constexpr (BIAS) {
+        const int c0 = static_cast<int>(e0 % cols);
+#pragma unroll
+        for (int k = 0; k < V; k += 4) {
+            float4 b4 = ld_f32x4(bias + c0 + k);
+            bv[k] = b4.x, bv[k + 1] = b4.y, bv[k + 2] = b4.z, bv[k + 3] = b4.w;
+        }
+    }
+    for (int64_t base = e0; base < total; base += stride * U) {
+        u32x4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (base + u * stride < total) raw[u] = ld16(x + base + u * stride);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (base + u * stride >= total) break;
+            float f[V];
+            unpack(raw[u], f, T{});
+#pragma unroll
+            for (int k = 0; k < V; k++) {
+                float v = f[k];
+                if constexpr (BIAS) v = storage_round(v + bv[k], T{});
+                f[k] = gelu_f(v);
+            }
+            st16(out + base + u * stride, pack(f, T{}));
+        }
+    }
+}
+
+template <typename T, bool BIAS, int U>
+__global__ __launch_bounds__(kBlock) void bias_ls_kernel(const T* res, const T* x,
+                                                         const float* __restrict__ bias,
+                                                         const float* __restrict__ gamma, T* out,
+                                                         int64_t total, int cols) {
+    constexpr int V = Vec<T>::N;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * V;
+    const int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * V;
+    const int c0 = static_cast<int>(e0 % cols);
+    float gv[V], bv[V];
+#pragma unroll
+    for (int k = 0; k < V; k += 4) {
+        float4 g4 = ld_f32x4(gamma + c0 + k);
+        gv[k] = g4.x, gv[k + 1] = g4.y, gv[k + 2] = g4.z, gv[k + 3] = g4.w;
+        if constexpr (BIAS) {
+            float4 b4 = ld_f32x4(bias + c0 + k);
+            bv[k] = b4.x, bv[k + 1] = b4.y, bv[k + 2] = b4.z, bv[k + 3] = b4.w;
+        }
+    }
+    for (int64_t base = e0; base < total; base += stride * U) {
+        u32x4 rr[U], xr[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (base + u * stride < total) {
+                rr[u] = ld16(res + base + u * stride);
+                xr[u] = ld16(x + base + u * stride);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (base + u * stride >= total) break;
+            float fr[V], fx[V];
+            unpack(rr[u], fr, T{});
+            unpack(xr[u], fx, T{});
+#pragma unroll
+            for (int k = 0; k < V; k++) {
+                float v = fx[k];
+                if constexpr (BIAS) v = storage_round(v + bv[k], T{});
+                fr[k] = fr[k] + gv[k] * v;  // residual_ls.wesl:28
+            }
+            st16(out + base + u * stride, pack(fr, T{}));
+        }
+    }
+}
+
+// Scalar fallbacks for shapes or pointers the vector kernels do not cover.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void bias_gelu_scalar_kernel(const T* x, const float* bias,
+                                                                  T* out, int64_t total, int cols) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+        float v = load_elem(x + i);
+        if (bias) v = storage_round(v + bias[i % cols], T{});
+        store_elem(out + i, gelu_f(v));
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void bias_ls_scalar_kernel(const T* res, const T* x,
+                                                                const float* bias,
+                                                                const float* gamma, T* out,
+                                                                int64_t total, int cols) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+        const int c = static_cast<int>(i % cols);
+        float v = load_elem(x + i);
+        if (bias) v = storage_round(v + bias[c], T{});
+        store_elem(out + i, load_elem(res + i) + gamma[c] * v);
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void cast_f32_f16_kernel(const float* x, f16* out, int64_t total) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * 8;
+    const int64_t nvec = total / 8 * 8;
+    for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8; i < nvec;
+         i += stride) {
+        float f[8], g[4];
+        unpack(ld16(x + i), g, float{});
+        f[0] = g[0], f[1] = g[1], f[2] = g[2], f[3] = g[3];
+        unpack(ld16(x + i + 4), g, float{});
+        f[4] = g[0], f[5] = g[1], f[6] = g[2], f[7] = g[3];
+        st16(out + i, pack(f, f16{}));
+    }
+    if (blockIdx.x == 0 && threadIdx.x < total - nvec)
+        out[nvec + threadIdx.x] = static_cast<f16>(x[nvec + threadIdx.x]);
+}
+
+__global__ __launch_bounds__(kBlock) void cast_f32_f16_scalar_kernel(const float* x, f16* out,
+                                                                     int64_t total) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride)
+        out[i] = static_cast<f16>(x[i]);
+}
+
+__global__ __launch_bounds__(kBlock) void tiled_add_kernel(const float* x, const float* table,
+                                                           float* out, int64_t total, int64_t block) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride)
+        out[i] = x[i] + table[i % block];
+}
+
+int64_t flat_blocks(int64_t items) {
+    const int64_t cap = static_cast<int64_t>(num_cus()) * kBlocksPerCu;
+    const int64_t want = ceil_div(items, kBlock);
+    return want < 1 ? 1 : (want < cap ? want : cap);
+}
+
+template <typename T>
+hs_status launch_gelu(hipStream_t st, const void* x, const float* bias, void* out, int64_t rows,
+                      int cols) {
+    constexpr int V = Vec<T>::N;
+    constexpr int U = 4;
+    const int64_t total = rows * cols;
+    const bool vec_ok = cols % V == 0 && aligned16(x) && aligned16(out) && (!bias || aligned16(bias));
+    const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U) : 0;
+    if (blocks > 0) {
+        if (bias)
+            bias_gelu_kernel<T, true, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                static_cast<const T*>(x), bias, static_cast<T*>(out), total, cols);
+        else
+            bias_gelu_kernel<T, false, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                static_cast<const T*>(x), bias, static_cast<T*>(out), total, cols);
+    } else {
+        bias_gelu_scalar_kernel<T><<<dim3(static_cast<uint32_t>(flat_blocks(total))), dim3(kBlock), 0, st>>>(
+            static_cast<const T*>(x), bias, static_cast<T*>(out), total, cols);
+    }
+    return check_launch("bias_gelu");
+}
+
+template <typename T>
+hs_status launch_ls(hipStream_t st, const void* res, const void* x, const float* bias,
+                    const float* gamma, void* out, int64_t rows, int cols) {
+    constexpr int V = Vec<T>::N;
+    constexpr int U = 2;
+    const int64_t total = rows * cols;
+    const bool vec_ok = cols % V == 0 && aligned16(res) && aligned16(x) && aligned16(out) &&
+                        aligned16(gamma) && (!bias || aligned16(bias));
+    const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U) : 0;
+    if (blocks > 0) {
+        if (bias)
+            bias_ls_kernel<T, true, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                static_cast<const T*>(res), static_cast<const T*>(x), bias, gamma,
+                static_cast<T*>(out), total, cols);
+        else
+            bias_ls_kernel<T, false, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                static_cast<const T*>(res), static_cast<const T*>(x), bias, gamma,
+                static_cast<T*>(out), total, cols);
+    } else {
+        bias_ls_scalar_kernel<T><<<dim3(static_cast<uint32_t>(flat_blocks(total))), dim3(kBlock), 0, st>>>(
+            static_cast<const T*>(res), static_cast<const T*>(x), bias, gamma,
+            static_cast<T*>(out), total, cols);
+    }
+    return check_launch("bias_ls_residual");
+}
+
+// In-place is allowed only as exact aliasing of whole tensors.
+bool bad_alias(const void* a, const void* out, int64_t bytes) {
+    return a != out && overlaps(a, bytes, out, bytes);
+}
+
+}  // namespace
+}  // namespace hs
+
+extern "C" {
+
+hs_status hs_bias_gelu(hs_stream_t stream, hs_dtype dt, const void* x, const float* bias,
+                       void* out, int64_t rows, int32_t cols) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "bias_gelu: unknown dtype %d", (int)dt);
+    if (rows < 0 || cols <= 0)
+        return fail(HS_EINVAL, "bias_gelu: rows %lld / cols %d", (long long)rows, cols);
+    if (rows == 0) return HS_OK;
+    if (!x || !out) return fail(HS_EINVAL, "bias_gelu: null buffer");
+    if (bad_alias(x, out, rows * cols * dtype_size(dt)))
+        return fail(HS_EINVAL, "bias_gelu: out partially overlaps x");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return dt == HS_F16 ? launch_gelu<f16>(st, x, bias, out, rows, cols)
+                        : launch_gelu<float>(st, x, bias, out, rows, cols);
+}
+
+hs_status hs_gelu(hs_stream_t stream, hs_dtype dt, const void* x, void* out, int64_t total) {
+    if (total < 0) return hs::fail(HS_EINVAL, "gelu: negative length %lld", (long long)total);
+    if (total == 0) return HS_OK;
+    // Without a bias the column split is arbitrary: rows of 8 elements keep
+    // the vector path for any length that is a multiple of 8.
+    if (total % 8 == 0) return hs_bias_gelu(stream, dt, x, nullptr, out, total / 8, 8);
+    return hs_bias_gelu(stream, dt, x, nullptr, out, total, 1);
+}
+
+hs_status hs_bias_ls_residual(hs_stream_t stream, hs_dtype dt, const void* res, const void* x,
+                              const float* bias, const float* gamma, void* out, int64_t rows,
+                              int32_t dim) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "bias_ls_residual: unknown dtype %d", (int)dt);
+    if (rows < 0 || dim <= 0)
+        return fail(HS_EINVAL, "bias_ls_residual: rows %lld / dim %d", (long long)rows, dim);
+    if (rows == 0) return HS_OK;
+    if (!res || !x || !gamma || !out) return fail(HS_EINVAL, "bias_ls_residual: null buffer");
+    const int64_t bytes = rows * dim * dtype_size(dt);
+    if (bad_alias(res, out, bytes) || bad_alias(x, out, bytes))
+        return fail(HS_EINVAL, "bias_ls_residual: out partially overlaps an input");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return dt == HS_F16 ? launch_ls<f16>(st, res, x, bias, gamma, out, rows, dim)
+                        : launch_ls<float>(st, res, x, bias, gamma, out, rows, dim);
+}
+
+hs_status hs_residual_ls(hs_stream_t stream, hs_dtype dt, const void* res, const void* x,
+                         const float* gamma, void* out, int64_t total, int32_t dim) {
+    if (total < 0 || dim <= 0)
+        return hs::fail(HS_EINVAL, "residual_ls: total %lld / dim %d", (long long)total, dim);
+    if (total % dim != 0)
+        return hs::fail(HS_EINVAL, "residual_ls: total %lld is not a multiple of dim %d",
+                        (long long)total, dim);
+    return hs_bias_ls_residual(stream, dt, res, x, nullptr, gamma, out, total / dim, dim);
+}
+
+hs_status hs_cast_f32_to_f16(hs_stream_t stream, const float* x, void* out, int64_t total) {
+    using namespace hs;
+    if (total < 0) return fail(HS_EINVAL, "cast_f32_to_f16: negative length");
+    if (total == 0) return HS_OK;
+    if (!x || !out) return fail(HS_EINVAL, "cast_f32_to_f16: null buffer");
+    if (overlaps(x, total * 4, out, total * 2))
+        return fail(HS_EINVAL, "cast_f32_to_f16: out overlaps x");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (aligned16(x) && aligned16(out))
+        cast_f32_f16_kernel<<<dim3(static_cast<uint32_t>(flat_blocks(ceil_div(total, 8)))), dim3(kBlock), 0, st>>>(
+            x, static_cast<f16*>(out), total);
+    else
+        cast_f32_f16_scalar_kernel<<<dim3(static_cast<uint32_t>(flat_blocks(total))), dim3(kBlock), 0, st>>>(
+            x, static_cast<f16*>(out), total);
+    return check_launch("cast_f32_to_f16");
+}
+
+hs_status hs_tiled_add(hs_stream_t stream, const float* x, const float* table, float* out,
+                       int64_t total, int64_t block) {
+    using namespace hs;
+    if (total < 0 || block <= 0) return fail(HS_EINVAL, "tiled_add: total / block");
+    if (total % block != 0)
+        return fail(HS_EINVAL, "tiled_add: table of %lld does not tile %lld elements",
+                    (long long)block, (long long)total);
+    if (total == 0) return HS_OK;
+    if (!x || !table || !out) return fail(HS_EINVAL, "tiled_add: null buffer");
+    if (bad_alias(x, out, total * 4)) return fail(HS_EINVAL, "tiled_add: out partially overlaps x");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    tiled_add_kernel<<<dim3(static_cast<uint32_t>(flat_blocks(total))), dim3(kBlock), 0, st>>>(
+        x, table, out, total, block);
+    return check_launch("tiled_add");
+}
+
+}  // extern "C"

@@ -1,0 +1,170 @@
+// Row LayerNorm for gfx950 (replaces shaders/layernorm.wesl, dispatched by
+// GpuContext::layernorm, engine/ops.rs:130-153).
+//
+// Fast path: one wave64 per row with the whole row held in registers — each
+// lane loads CHUNKS 16-byte vectors (a 1024-wide f16 row is 2 loads per
+// lane, each load instruction a contiguous 1 KiB), mean and variance are
+// reduced across the wave with DPP lane permutes (no LDS, no barrier), and
+// the row is written back with 16-byte stores. Waves are persistent: each
+// keeps the weight and bias slices it needs in registers and walks rows in
+// groups of U, issuing all U*CHUNKS loads before it reduces, so every wave
+// has U*2 KiB of HBM reads in flight.
+//
+// Generic path: any dim, one wave per row, strided over the row three
+// times (mean, variance, output) with the second and third reads served by
+// the cache.
+#include "hs_common.hpp"
+
+namespace hs {
+namespace {
+
+constexpr int kBlock = 256;  // 4 waves per workgroup
+constexpr int kWavesPerBlock = kBlock / 64;
+constexpr int kBlocksPerCu = 8;
+
+template <typename T, int CHUNKS, int U>
+__global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float* __restrict__ w,
+                                                        const float* __restrict__ b, T* out,
+                                                        int64_t rows, float eps) {
+    constexpr int V = Vec<T>::N;
+    constexpr int DIM = 64 * V * CHUNKS;
+    const int lane = lane_id();
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+
+    float wr[CHUNKS][V], br[CHUNKS][V];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) {
+        const int col = c * 64 * V + lane * V;
+#pragma unroll
+        for (int k = 0; k < V; k += 4) {
+            float4 w4 = ld_f32x4(w + col + k), b4 = ld_f32x4(b + col + k);
+            wr[c][k] = w4.x, wr[c][k + 1] = w4.y, wr[c][k + 2] = w4.z, wr[c][k + 3] = w4.w;
+            br[c][k] = b4.x, br[c][k + 1] = b4.y, br[c][k + 2] = b4.z, br[c][k + 3] = b4.w;
+        }
+    }
+
+    for (int64_t r0 = wave * U; r0 < rows; r0 += nwaves * U) {
+        u32x4 raw[U][CHUNKS];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (r0 + u < rows) {
+                const T* xr = x + (r0 + u) * DIM + lane * V;
+#pragma unroll
+                for (int c = 0; c < CHUNKS; c++) raw[u][c] = ld16(xr + c * 64 * V);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (r0 + u >= rows) break;
+            float f[CHUNKS][V];
+            float s = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) {
+                unpack(raw[u][c], f[c], T{});
+#pragma unroll
+                for (int k = 0; k < V; k++) s += f[c][k];
+            }
+            const float mean = wave_sum(s) / static_cast<float>(DIM);
+            float q = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++)
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    const float d = f[c][k] - mean;
+                    q += d * d;
+                }
+            const float var = wave_sum(q) / static_cast<float>(DIM);
+            const float inv = rsqrtf(var + eps);
+            T* orow = out + (r0 + u) * DIM + lane * V;
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) {
+                float y[V];
+#pragma unroll
+                for (int k = 0; k < V; k++) y[k] = (f[c][k] - mean) * inv * wr[c][k] + br[c][k];
+                st16(orow + c * 64 * V, pack(y, T{}));
+            }
+        }
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void ln_generic_kernel(const T* x, const float* __restrict__ w,
+                                                            const float* __restrict__ b, T* out,
+                                                            int64_t rows, int dim, float eps) {
+    const int lane = lane_id();
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    for (int64_t row = wave; row < rows; row += nwaves) {
+        const T* xr = x + row * dim;
+        T* orow = out + row * dim;
+        float s = 0.0f;
+        for (int j = lane; j < dim; j += 64) s += load_elem(xr + j);
+        const float mean = wave_sum(s) / static_cast<float>(dim);
+        float q = 0.0f;
+        for (int j = lane; j < dim; j += 64) {
+            const float d = load_elem(xr + j) - mean;
+            q += d * d;
+        }
+        const float var = wave_sum(q) / static_cast<float>(dim);
+        const float inv = rsqrtf(var + eps);
+        for (int j = lane; j < dim; j += 64)
+            store_elem(orow + j, (load_elem(xr + j) - mean) * inv * w[j] + b[j]);
+    }
+}
+
+int64_t persistent_blocks(int64_t work_waves) {
+    const int64_t cap = static_cast<int64_t>(num_cus()) * kBlocksPerCu;
+    int64_t blocks = ceil_div(work_waves, kWavesPerBlock);
+    return blocks < cap ? blocks : cap;
+}
+
+template <typename T, int CHUNKS>
+hs_status launch_vec(hipStream_t st, const void* x, const float* w, const float* b, void* out,
+                     int64_t rows, float eps) {
+    constexpr int U = 2;
+    const int64_t blocks = persistent_blocks(ceil_div(rows, U));
+    ln_vec_kernel<T, CHUNKS, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+        static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, eps);
+    return check_launch("layernorm");
+}
+
+template <typename T>
+hs_status launch(hipStream_t st, const void* x, const float* w, const float* b, void* out,
+                 int64_t rows, int dim, float eps) {
+    constexpr int V = Vec<T>::N;
+    const bool vec_ok = aligned16(x) && aligned16(out) && aligned16(w) && aligned16(b) &&
+                        dim % (64 * V) == 0;
+    if (vec_ok) {
+        switch (dim / (64 * V)) {
+            case 1: return launch_vec<T, 1>(st, x, w, b, out, rows, eps);
+            case 2: return launch_vec<T, 2>(st, x, w, b, out, rows, eps);
+            case 4: return launch_vec<T, 4>(st, x, w, b, out, rows, eps);
+            default: break;
+        }
+    }
+    const int64_t blocks = persistent_blocks(rows);
+    ln_generic_kernel<T><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+        static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, dim, eps);
+    return check_launch("layernorm");
+}
+
+}  // namespace
+}  // namespace hs
+
+extern "C" hs_status hs_layernorm(hs_stream_t stream, hs_dtype dt, const void* x, const float* w,
+                                  const float* b, void* out, int64_t rows, int32_t dim,
+                                  float eps) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "layernorm: unknown dtype %d", (int)dt);
+    if (rows < 0 || dim <= 0)
+        return fail(HS_EINVAL, "layernorm: rows %lld / dim %d", (long long)rows, dim);
+    if (rows == 0) return HS_OK;
+    if (!x || !w || !b || !out) return fail(HS_EINVAL, "layernorm: null buffer");
+    const int64_t bytes = rows * dim * dtype_size(dt);
+    if (x != out && overlaps(x, bytes, out, bytes))
+        return fail(HS_EINVAL, "layernorm: out partially overlaps x");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return dt == HS_F16 ? launch<f16>(st, x, w, b, out, rows, dim, eps)
+                        : launch<float>(st, x, w, b, out, rows, dim, eps);
+}

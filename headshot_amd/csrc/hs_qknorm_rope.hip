@@ -1,0 +1,337 @@
+// split_heads + QK-norm + 2D RoPE for gfx950 (replaces the reference's
+// split_heads.wesl, layernorm.wesl at dim 64 and rope_apply.wesl, dispatched
+// in sequence by model/block.rs:130-146), plus the stand-alone split_heads
+// and in-place rope_apply surface ops.
+//
+// Fast path (head_dim 64, H a multiple of the heads one load covers): one
+// wave64 per token row of the token-major projection (S*T, H*64). A 64-wide
+// head vector is spread over a group of G lanes (8 for f16, 16 for f32), each
+// holding one 16-byte vector, so a single load instruction reads 1 KiB of
+// the row and LN(64) is a G-lane DPP reduction. Rotate-half RoPE pairs
+// channel i with i+32; the lane holding channels [i, i+V) is placed opposite
+// the lane holding [32+i, 32+i+V) under the DPP row mirror (lane j <-> G-1-j),
+// so each lane gets its partner's values with one permute per element.
+// Norm, rotation and the reference's intermediate storage rounding all stay
+// in registers; each element crosses HBM once each way. Output goes straight
+// to the head-major (S, H, T, 64) layout that attention consumes.
+//
+// Generic path (any head_dim, either input layout): one wave per head vector,
+// lanes strided over the vector; used for rope_apply on head-major tensors
+// and for shapes the fast path does not cover.
+#include "hs_common.hpp"
+
+namespace hs {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kWavesPerBlock = kBlock / 64;
+constexpr int kBlocksPerCu = 8;
+
+int64_t persistent_blocks(int64_t work_waves) {
+    const int64_t cap = static_cast<int64_t>(num_cus()) * kBlocksPerCu;
+    const int64_t blocks = ceil_div(work_waves, kWavesPerBlock);
+    return blocks < cap ? blocks : cap;
+}
+
+template <typename T, int CHUNKS, bool NORM, bool ROPE, int U>
+__global__ __launch_bounds__(kBlock) void qkn_tok_kernel(
+    const T* __restrict__ x, const float* __restrict__ nw, const float* __restrict__ nb,
+    const float* __restrict__ sin_tab, const float* __restrict__ cos_tab, T* __restrict__ out,
+    int64_t tokens, int seq, int prefix, float eps) {
+    constexpr int D = 64;
+    constexpr int V = Vec<T>::N;   // elements per lane per head
+    constexpr int G = D / V;       // lanes per head
+    constexpr int HPI = 64 / G;    // heads per load instruction
+    constexpr int H = CHUNKS * HPI;
+    const int lane = lane_id();
+    const int piece = lane % G;
+    const int hsub = lane / G;
+    // Channels held by this lane: lower-half pieces hold [piece*V, +V), the
+    // mirrored upper-half pieces hold the matching [32 + (G-1-piece)*V, +V).
+    const bool upper = piece >= G / 2;
+    const int ch = upper ? 32 + (G - 1 - piece) * V : piece * V;
+
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+
+    float wr[V], br[V];
+    if constexpr (NORM) {
+#pragma unroll
+        for (int k = 0; k < V; k += 4) {
+            float4 w4 = ld_f32x4(nw + ch + k), b4 = ld_f32x4(nb + ch + k);
+            wr[k] = w4.x, wr[k + 1] = w4.y, wr[k + 2] = w4.z, wr[k + 3] = w4.w;
+            br[k] = b4.x, br[k + 1] = b4.y, br[k + 2] = b4.z, br[k + 3] = b4.w;
+        }
+    }
+
+    for (int64_t tok0 = wave * U; tok0 < tokens; tok0 += nwaves * U) {
+        u32x4 raw[U][CHUNKS];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (tok0 + u < tokens) {
+                const T* xr = x + (tok0 + u) * (H * D) + hsub * D + ch;
+#pragma unroll
+                for (int c = 0; c < CHUNKS; c++) raw[u][c] = ld16(xr + c * HPI * D);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t tok = tok0 + u;
+            if (tok >= tokens) break;
+            // tokens < 2^31 (checked on the host): 32-bit wave-uniform divide
+            const uint32_t s = static_cast<uint32_t>(tok) / static_cast<uint32_t>(seq);
+            const int t = static_cast<int>(static_cast<uint32_t>(tok) - s * static_cast<uint32_t>(seq));
+            const bool rot = ROPE && t >= prefix;
+            float cs[V], sn[V];
+            if (rot) {
+                const float* crow = cos_tab + static_cast<int64_t>(t - prefix) * D + ch;
+                const float* srow = sin_tab + static_cast<int64_t>(t - prefix) * D + ch;
+#pragma unroll
+                for (int k = 0; k < V; k += 4) {
+                    float4 c4 = ld_f32x4(crow + k), s4 = ld_f32x4(srow + k);
+                    cs[k] = c4.x, cs[k + 1] = c4.y, cs[k + 2] = c4.z, cs[k + 3] = c4.w;
+                    sn[k] = s4.x, sn[k + 1] = s4.y, sn[k + 2] = s4.z, sn[k + 3] = s4.w;
+                }
+            }
+            T* obase = out + (static_cast<int64_t>(s) * H + hsub) * static_cast<int64_t>(seq) * D +
+                       static_cast<int64_t>(t) * D + ch;
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) {
+                float f[V];
+                unpack(raw[u][c], f, T{});
+                if constexpr (NORM) {
+                    float sum = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < V; k++) sum += f[k];
+                    const float mean = group_sum<G>(sum) / static_cast<float>(D);
+                    float q = 0.0f;
+#pragma unroll
+                    for (int k = 0; k < V; k++) {
+                        const float d = f[k] - mean;
+                        q += d * d;
+                    }
+                    const float var = group_sum<G>(q) / static_cast<float>(D);
+                    const float inv = rsqrtf(var + eps);
+#pragma unroll
+                    for (int k = 0; k < V; k++)
+                        f[k] = storage_round((f[k] - mean) * inv * wr[k] + br[k], T{});
+                }
+                if (rot) {
+#pragma unroll
+                    for (int k = 0; k < V; k++) {
+                        const float partner = group_mirror<G>(f[k]);
+                        // lower: lo*cos - hi*sin; upper: hi*cos + lo*sin
+                        const float signed_partner = upper ? partner : -partner;
+                        f[k] = f[k] * cs[k] + signed_partner * sn[k];
+                    }
+                }
+                st16(obase + static_cast<int64_t>(c) * HPI * seq * D, pack(f, T{}));
+            }
+        }
+    }
+}
+
+// One wave per head vector. in_head_major selects the input layout:
+// false = token-major (S*T, H*D), true = head-major (S, H, T, D). The output
+// is head-major and may equal the input when the input is head-major.
+template <typename T>
+__global__ __launch_bounds__(kBlock) void qkn_generic_kernel(
+    const T* x, bool in_head_major, const float* __restrict__ nw, const float* __restrict__ nb,
+    const float* __restrict__ sin_tab, const float* __restrict__ cos_tab, T* out, int nseq,
+    int seq, int heads, int d, int prefix, float eps) {
+    const int lane = lane_id();
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    const int64_t nvec = static_cast<int64_t>(nseq) * seq * heads;
+    const bool norm = nw != nullptr;
+    const int half = d / 2;
+    for (int64_t v = wave; v < nvec; v += nwaves) {
+        int64_t s, h, t;
+        if (in_head_major) {
+            t = v % seq;
+            const int64_t sh = v / seq;
+            h = sh % heads;
+            s = sh / heads;
+        } else {
+            h = v % heads;
+            const int64_t tok = v / heads;
+            t = tok % seq;
+            s = tok / seq;
+        }
+        const T* xin = in_head_major ? x + v * d : x + (s * seq + t) * heads * d + h * d;
+        T* o = out + ((s * heads + h) * seq + t) * d;
+        float mean = 0.0f, inv = 1.0f;
+        if (norm) {
+            float sum = 0.0f;
+            for (int j = lane; j < d; j += 64) sum += load_elem(xin + j);
+            mean = wave_sum(sum) / static_cast<float>(d);
+            float q = 0.0f;
+            for (int j = lane; j < d; j += 64) {
+                const float dd = load_elem(xin + j) - mean;
+                q += dd * dd;
+            }
+            inv = rsqrtf(wave_sum(q) / static_cast<float>(d) + eps);
+        }
+        const bool rot = sin_tab != nullptr && t >= prefix;
+        if (rot) {
+            const int64_t row = (t - prefix) * d;
+            for (int dp = lane; dp < half; dp += 64) {
+                float lo = load_elem(xin + dp), hi = load_elem(xin + dp + half);
+                if (norm) {
+                    lo = storage_round((lo - mean) * inv * nw[dp] + nb[dp], T{});
+                    hi = storage_round((hi - mean) * inv * nw[dp + half] + nb[dp + half], T{});
+                }
+                store_elem(o + dp, lo * cos_tab[row + dp] - hi * sin_tab[row + dp]);
+                store_elem(o + dp + half,
+                           hi * cos_tab[row + half + dp] + lo * sin_tab[row + half + dp]);
+            }
+        } else {
+            for (int j = lane; j < d; j += 64) {
+                float val = load_elem(xin + j);
+                if (norm) val = (val - mean) * inv * nw[j] + nb[j];
+                store_elem(o + j, val);
+            }
+        }
+    }
+}
+
+template <typename T, int CHUNKS, bool NORM, bool ROPE>
+hs_status launch_tok(hipStream_t st, const void* x, const float* nw, const float* nb,
+                     const float* sn, const float* cs, void* out, int64_t tokens, int seq,
+                     int prefix, float eps) {
+    constexpr int U = 2;
+    const int64_t blocks = persistent_blocks(ceil_div(tokens, U));
+    qkn_tok_kernel<T, CHUNKS, NORM, ROPE, U>
+        <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+            static_cast<const T*>(x), nw, nb, sn, cs, static_cast<T*>(out), tokens, seq, prefix,
+            eps);
+    return check_launch("qknorm_rope");
+}
+
+template <typename T, int CHUNKS>
+hs_status launch_tok_flags(hipStream_t st, const void* x, const float* nw, const float* nb,
+                           const float* sn, const float* cs, void* out, int64_t tokens, int seq,
+                           int prefix, float eps) {
+    const bool norm = nw != nullptr, rope = sn != nullptr && prefix < seq;
+    if (norm && rope)
+        return launch_tok<T, CHUNKS, true, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix,
+                                                 eps);
+    if (norm)
+        return launch_tok<T, CHUNKS, true, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix,
+                                                  eps);
+    if (rope)
+        return launch_tok<T, CHUNKS, false, true>(st, x, nw, nb, sn, cs, out, tokens, seq,
+                                                  prefix, eps);
+    return launch_tok<T, CHUNKS, false, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix,
+                                               eps);
+}
+
+template <typename T>
+hs_status launch_generic(hipStream_t st, const void* x, bool in_head_major, const float* nw,
+                         const float* nb, const float* sn, const float* cs, void* out, int s,
+                         int t, int h, int d, int prefix, float eps) {
+    const int64_t nvec = static_cast<int64_t>(s) * t * h;
+    const int64_t blocks = persistent_blocks(nvec);
+    qkn_generic_kernel<T><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+        static_cast<const T*>(x), in_head_major, nw, nb, sn, cs, static_cast<T*>(out), s, t, h, d,
+        prefix, eps);
+    return check_launch("qknorm_rope");
+}
+
+// Token-major input: fast path when head_dim is 64, H fills whole load
+// instructions and every pointer is 16-byte aligned.
+template <typename T>
+hs_status dispatch_tok(hipStream_t st, const void* x, const float* nw, const float* nb,
+                       const float* sn, const float* cs, void* out, int s, int t, int h, int d,
+                       int prefix, float eps) {
+    constexpr int HPI = 64 / (64 / Vec<T>::N);
+    const bool ptrs_ok = aligned16(x) && aligned16(out) && (!nw || (aligned16(nw) && aligned16(nb))) &&
+                         (!sn || (aligned16(sn) && aligned16(cs)));
+    if (d == 64 && ptrs_ok && h % HPI == 0) {
+        const int64_t tokens = static_cast<int64_t>(s) * t;
+        switch (h / HPI) {
+            case 1: return launch_tok_flags<T, 1>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+            case 2: return launch_tok_flags<T, 2>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+            case 4: return launch_tok_flags<T, 4>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+            default: break;
+        }
+    }
+    return launch_generic<T>(st, x, false, nw, nb, sn, cs, out, s, t, h, d, prefix, eps);
+}
+
+hs_status check_shape(const char* op, int32_t s, int32_t t, int32_t h, int32_t d) {
+    if (s < 0 || t < 0 || h < 0 || d < 0)
+        return fail(HS_EINVAL, "%s: negative shape (%d, %d, %d, %d)", op, s, t, h, d);
+    const int64_t n = static_cast<int64_t>(s) * t * h * d;
+    if (n > (int64_t{1} << 40)) return fail(HS_EINVAL, "%s: tensor too large", op);
+    if (static_cast<int64_t>(s) * t * h >= (int64_t{1} << 31))
+        return fail(HS_EINVAL, "%s: S*T*H must be below 2^31", op);
+    return HS_OK;
+}
+
+}  // namespace
+}  // namespace hs
+
+extern "C" {
+
+hs_status hs_qknorm_rope(hs_stream_t stream, hs_dtype dt, const void* x_tok, const float* nw,
+                         const float* nb, const float* sin_tab, const float* cos_tab,
+                         void* out_head, int32_t s, int32_t t, int32_t h, int32_t d,
+                         int32_t prefix, float eps) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "qknorm_rope: unknown dtype %d", (int)dt);
+    if (hs_status e = check_shape("qknorm_rope", s, t, h, d)) return e;
+    if ((nw == nullptr) != (nb == nullptr))
+        return fail(HS_EINVAL, "qknorm_rope: norm weight and bias must both be given or both NULL");
+    if ((sin_tab == nullptr) != (cos_tab == nullptr))
+        return fail(HS_EINVAL, "qknorm_rope: sin and cos tables must both be given or both NULL");
+    if (sin_tab && (prefix < 0 || prefix > t))
+        return fail(HS_EINVAL, "qknorm_rope: prefix %d outside [0, T=%d]", prefix, t);
+    if (sin_tab && d % 2 != 0) return fail(HS_EINVAL, "qknorm_rope: RoPE needs an even head_dim");
+    const int64_t n = static_cast<int64_t>(s) * t * h * d;
+    if (n == 0) return HS_OK;
+    if (!x_tok || !out_head) return fail(HS_EINVAL, "qknorm_rope: null buffer");
+    const int64_t bytes = n * dtype_size(dt);
+    if (overlaps(x_tok, bytes, out_head, bytes))
+        return fail(HS_EINVAL, "qknorm_rope: out_head overlaps x_tok");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return dt == HS_F16
+               ? dispatch_tok<f16>(st, x_tok, nw, nb, sin_tab, cos_tab, out_head, s, t, h, d, prefix, eps)
+               : dispatch_tok<float>(st, x_tok, nw, nb, sin_tab, cos_tab, out_head, s, t, h, d, prefix, eps);
+}
+
+hs_status hs_split_heads(hs_stream_t stream, hs_dtype dt, const void* x, void* out, int32_t s,
+                         int32_t t, int32_t h, int32_t d) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "split_heads: unknown dtype %d", (int)dt);
+    if (hs_status e = check_shape("split_heads", s, t, h, d)) return e;
+    const int64_t n = static_cast<int64_t>(s) * t * h * d;
+    if (n == 0) return HS_OK;
+    if (!x || !out) return fail(HS_EINVAL, "split_heads: null buffer");
+    const int64_t bytes = n * dtype_size(dt);
+    if (overlaps(x, bytes, out, bytes)) return fail(HS_EINVAL, "split_heads: out overlaps x");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return dt == HS_F16
+               ? dispatch_tok<f16>(st, x, nullptr, nullptr, nullptr, nullptr, out, s, t, h, d, 0, 0.0f)
+               : dispatch_tok<float>(st, x, nullptr, nullptr, nullptr, nullptr, out, s, t, h, d, 0, 0.0f);
+}
+
+hs_status hs_rope_apply(hs_stream_t stream, hs_dtype dt, void* x, const float* sin_tab,
+                        const float* cos_tab, int32_t s, int32_t h, int32_t t, int32_t d,
+                        int32_t prefix) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "rope_apply: unknown dtype %d", (int)dt);
+    if (hs_status e = check_shape("rope_apply", s, t, h, d)) return e;
+    if (prefix < 0 || prefix > t)
+        return fail(HS_EINVAL, "rope_apply: prefix %d outside [0, T=%d]", prefix, t);
+    if (d % 2 != 0) return fail(HS_EINVAL, "rope_apply: head_dim %d is odd", d);
+    const int64_t n = static_cast<int64_t>(s) * t * h * d;
+    if (n == 0 || prefix == t) return HS_OK;
+    if (!x || !sin_tab || !cos_tab) return fail(HS_EINVAL, "rope_apply: null buffer");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return dt == HS_F16
+               ? launch_generic<f16>(st, x, true, nullptr, nullptr, sin_tab, cos_tab, x, s, t, h, d, prefix, 0.0f)
+               : launch_generic<float>(st, x, true, nullptr, nullptr, sin_tab, cos_tab, x, s, t, h, d, prefix, 0.0f);
+}
+
+}  // extern "C"

@@ -1,0 +1,175 @@
+/*
+ * headshot_hip.h — C ABI of libheadshot_hip.so: headshot's fused per-layer
+ * ops (LayerNorm, QK-norm + 2D RoPE, bias + erf-GELU, bias + LayerScale +
+ * residual, patch-token assembly) as hand-written HIP kernels for gfx950.
+ *
+ * The entry points replace the op-dispatch methods of the reference's
+ * `GpuContext` (crates/headshot-server/src/engine/ops.rs, engine/tensor.rs,
+ * engine/rope.rs); each declaration names the method it stands in for. The
+ * reference has no FFI layer: its string-keyed `dispatch(name, params,
+ * buffers, grid)` registry (engine/mod.rs:216-258) is what these exports
+ * replace, one function per kernel family.
+ *
+ * Conventions (all entry points):
+ *  - Device pointers are caller-owned; the library never allocates device
+ *    memory and keeps no per-call state. Work is enqueued on `stream` (a
+ *    hipStream_t; NULL is the default stream) and is stream-ordered.
+ *  - Activations are row-major. Token matrices are (rows, channels); the
+ *    attention layout is head-major (S, H, T, D) (engine/ops.rs:1-3).
+ *  - `dt` selects the storage type of activations (HS_F32 or HS_F16, the
+ *    reference's `Elem`); norm weights, biases, LayerScale gammas,
+ *    positional tables and RoPE tables are always f32 (engine/ops.rs:5-8).
+ *    Arithmetic is f32 in both variants; f16 results are rounded to nearest
+ *    even once, when stored.
+ *  - Returns HS_OK, or HS_EINVAL for a contract violation (the reference
+ *    panics on these: engine/ops.rs:134-137, 169-173, 206-208), HS_EHIP when
+ *    a HIP call or kernel launch fails, HS_EUNSUPPORTED for a shape the
+ *    library does not implement. hs_last_error() gives the message. Nothing
+ *    is enqueued when a call fails validation.
+ *  - Zero-sized work (rows == 0, S == 0, ...) is a valid no-op.
+ *  - Calls are reentrant; calls on one stream execute in order.
+ */
+#ifndef HEADSHOT_HIP_H
+#define HEADSHOT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* hs_stream_t; /* hipStream_t */
+
+typedef enum { HS_F32 = 0, HS_F16 = 1 } hs_dtype;
+
+typedef int32_t hs_status;
+#define HS_OK 0
+#define HS_EINVAL (-1)
+#define HS_EHIP (-2)
+#define HS_EUNSUPPORTED (-3)
+
+#define HS_ABI_VERSION 1
+
+/* ABI version of the loaded library (HS_ABI_VERSION it was built with). */
+int32_t hs_abi_version(void);
+/* Static name of a status code. */
+const char* hs_status_string(hs_status status);
+/* Message of the last failing call on this thread ("" if none). */
+const char* hs_last_error(void);
+
+/* ---------------------------------------------------------------------- */
+/* Reference op surface (one export per GpuContext method on the path)      */
+
+/* GpuContext::layernorm (engine/ops.rs:130-153; shaders/layernorm.wesl).
+ * out[r, :] = (x[r, :] - mean) * rsqrt(var + eps) * w + b over `dim`, with
+ * f32 statistics. The reference hardcodes eps = 1e-5 (engine/ops.rs:139);
+ * here the caller passes it. out may equal x. Serves the block pre-norm
+ * (dim 1024) and the head-major QK-norm (dim 64, rows S*H*T). */
+hs_status hs_layernorm(hs_stream_t stream, hs_dtype dt, const void* x, const float* w,
+                       const float* b, void* out, int64_t rows, int32_t dim, float eps);
+
+/* GpuContext::gelu (engine/ops.rs:155-165; shaders/gelu.wesl): exact-erf
+ * GELU 0.5*v*(1 + erf(v/sqrt(2))), erf by Abramowitz & Stegun 7.1.26.
+ * out may equal x. */
+hs_status hs_gelu(hs_stream_t stream, hs_dtype dt, const void* x, void* out, int64_t total);
+
+/* GpuContext::residual_ls (engine/ops.rs:167-183; shaders/residual_ls.wesl):
+ * out[i] = res[i] + gamma[i % dim] * x[i]. total must be a multiple of dim.
+ * out may equal res or x. */
+hs_status hs_residual_ls(hs_stream_t stream, hs_dtype dt, const void* res, const void* x,
+                         const float* gamma, void* out, int64_t total, int32_t dim);
+
+/* GpuContext::split_heads (engine/ops.rs:185-200; shaders/split_heads.wesl):
+ * (S*T, H*D) token-major -> (S, H, T, D) head-major, an exact copy.
+ * out must not overlap x. */
+hs_status hs_split_heads(hs_stream_t stream, hs_dtype dt, const void* x, void* out, int32_t s,
+                         int32_t t, int32_t h, int32_t d);
+
+/* GpuContext::rope_apply (engine/ops.rs:202-223; shaders/rope_apply.wesl),
+ * in place on head-major x (S, H, T, D), D even. Tables are f32
+ * (T - prefix, D); token t >= prefix uses table row t - prefix:
+ *   x[dp]     = x[dp] * cos[dp] - x[dp+D/2] * sin[dp]
+ *   x[dp+D/2] = x[dp+D/2] * cos[D/2+dp] + x[dp] * sin[D/2+dp]
+ * The first `prefix` tokens of every sequence are left untouched. */
+hs_status hs_rope_apply(hs_stream_t stream, hs_dtype dt, void* x, const float* sin_tab,
+                        const float* cos_tab, int32_t s, int32_t h, int32_t t, int32_t d,
+                        int32_t prefix);
+
+/* GpuContext::cast_to_f16 (engine/ops.rs:336-348; cast_f32_to_f16.wesl):
+ * f32 -> f16, round to nearest even. out (f16) must not overlap x. */
+hs_status hs_cast_f32_to_f16(hs_stream_t stream, const float* x, void* out, int64_t total);
+
+/* GpuContext::copy_rows (engine/tensor.rs:146-160): copy n_rows rows of
+ * row_bytes bytes from src row src_row to dst row dst_row (stream-ordered
+ * device-to-device copy). Source and destination ranges must not overlap. */
+hs_status hs_copy_rows(hs_stream_t stream, const void* src, int64_t src_row, void* dst,
+                       int64_t dst_row, int64_t n_rows, int64_t row_bytes);
+
+/* GpuContext::tiled_add (engine/ops.rs:374-389; shaders/tiled_add.wesl),
+ * f32 only: out[i] = x[i] + table[i % block]; total a multiple of block.
+ * out may equal x. */
+hs_status hs_tiled_add(hs_stream_t stream, const float* x, const float* table, float* out,
+                       int64_t total, int64_t block);
+
+/* ---------------------------------------------------------------------- */
+/* Fused per-layer ops (each replaces a run of reference dispatches)        */
+
+/* split_heads + QK-norm + RoPE in one pass (model/block.rs:130-146:
+ * split_heads, layernorm(q|k) over head_dim, rope_apply). Reads token-major
+ * x_tok (S*T, H*D), writes head-major out_head (S, H, T, D). nw/nb (D) are
+ * the QK-norm weight and bias; both NULL skips the norm (DINO blocks).
+ * sin_tab/cos_tab (T - prefix, D) apply RoPE to tokens t >= prefix; both
+ * NULL skips it (global-attention blocks, model/trunk.rs:123-125). With
+ * norm and RoPE both off this is exactly hs_split_heads. out_head must not
+ * overlap x_tok. */
+hs_status hs_qknorm_rope(hs_stream_t stream, hs_dtype dt, const void* x_tok, const float* nw,
+                         const float* nb, const float* sin_tab, const float* cos_tab,
+                         void* out_head, int32_t s, int32_t t, int32_t h, int32_t d,
+                         int32_t prefix, float eps);
+
+/* fc1 bias epilogue + GELU (shaders/linear_wmma.wgsl:69-74 then
+ * engine/ops.rs:155-165): out[r, c] = gelu(x[r, c] + bias[c]) over
+ * (rows, cols); bias NULL is plain GELU. out may equal x. */
+hs_status hs_bias_gelu(hs_stream_t stream, hs_dtype dt, const void* x, const float* bias,
+                       void* out, int64_t rows, int32_t cols);
+
+/* proj/fc2 bias epilogue + LayerScale + residual (linear_wmma.wgsl:69-74
+ * then engine/ops.rs:167-183): out[r, c] = res[r, c] + gamma[c] * (x[r, c]
+ * + bias[c]); bias NULL is plain residual_ls. out may equal res or x. */
+hs_status hs_bias_ls_residual(hs_stream_t stream, hs_dtype dt, const void* res, const void* x,
+                              const float* bias, const float* gamma, void* out, int64_t rows,
+                              int32_t dim);
+
+/* Patch-token assembly (model/trunk.rs:68-85 with engine/ops.rs:337-348,
+ * model/dino.rs:76-93; pos-embed add as shaders/tiled_add.wesl:23). Output
+ * (S*T, D) in out_dt with T = 1 + R + P; for frame f and v = (f != 0 && n_var
+ * == 2) ? 1 : 0:
+ *   row f*T          = cam[v]                  (cam: (n_var, D), out_dt)
+ *   rows f*T+1..+R   = reg[v*R .. v*R+R-1]     (reg: (n_var*R, D), out_dt)
+ *   row f*T+1+R+p    = out_dt((patches[f*P+p] + patch_bias) + pos[p])
+ * patches (S*P, D) are in patch_dt; patch_bias (D) and pos (P, D) are f32
+ * and each may be NULL. The sums run in f32 in that order and round once.
+ * cam/reg may be NULL only when R == 0 / never for cam. n_var is 1 or 2. */
+hs_status hs_assemble_tokens(hs_stream_t stream, hs_dtype out_dt, const void* patches,
+                             hs_dtype patch_dt, const float* patch_bias, const float* pos,
+                             const void* cam, const void* reg, void* out, int32_t s, int32_t p,
+                             int32_t r, int32_t d, int32_t n_var);
+
+/* ---------------------------------------------------------------------- */
+/* Host-side RoPE tables (computed once per session, as the reference does) */
+
+/* rope::periods (engine/rope.rs:5-10): out16[i] = 100^(2i/32) in f32. */
+void hs_rope_periods(float* out16);
+
+/* rope::tables (engine/rope.rs:12-43), bit-exact: sin_out/cos_out are host
+ * arrays of (h_p*w_p, 64) f32, rows in h-outer/w-inner patch order.
+ * Channels [0,16) carry h-angles, [16,32) w-angles, [32,64) repeat [0,32);
+ * angle = (2*pi * (2*((i+0.5)/max(h_p,w_p)) - 1)) / periods16[k]. */
+hs_status hs_rope_tables(const float* periods16, int32_t h_p, int32_t w_p, float* sin_out,
+                         float* cos_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HEADSHOT_HIP_H */

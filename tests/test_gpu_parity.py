@@ -1,0 +1,261 @@
+"""HIP kernels vs the CPU oracle on identical seeded inputs (small shapes).
+
+Bars: f32 within |a-e| <= 1e-5 + 1e-5|e|; f16 within 2e-3*max(1,|e|) and,
+because the fused kernels reproduce the reference's storage rounding points,
+within one f16 ulp everywhere; permutations, copies and RoPE passthrough
+bit-exact.
+"""
+import numpy as np
+import pytest
+import torch
+
+from headshot_amd import rope
+from headshot_amd.parity import assert_bit_exact, assert_close, f16_close, ulp_diff_f16
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NP = {torch.float32: np.float32, torch.float16: np.float16}
+DTYPES = [torch.float32, torch.float16]
+
+
+def host(a: np.ndarray, dtype) -> np.ndarray:
+    """Storage-typed host copy (f16 by the oracle's RNE)."""
+    return O.to_f16(a) if dtype == torch.float16 else np.ascontiguousarray(a, np.float32)
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def back(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def check(got: np.ndarray, want: np.ndarray, what: str, max_ulp: int = 1,
+          stages: int = 1):
+    """f32: 1e-5 (abs + rel). f16: the 2e-3 gate, plus at most `max_ulp` f16
+    ulps wherever |want| >= 1/64 (below that an f16 ulp, <= 2^-16, is close
+    to the f32 noise of values that cancel to near zero). With two rounding
+    stages (QK-norm stored as f16, then rotated) a 1-ulp flip of the stored
+    norm output can move a cancelling rotation by more, so there at most
+    0.1% of elements may exceed `max_ulp`."""
+    assert got.dtype == want.dtype, f"{what}: dtype {got.dtype} vs {want.dtype}"
+    if got.dtype == np.float32:
+        assert_close(got, want, 1e-5, what)
+    else:
+        f16_close(got.astype(np.float32), want.astype(np.float32), what)
+        u = ulp_diff_f16(got, want)
+        big = np.abs(want.astype(np.float32)) >= 1.0 / 64
+        bad = (u > max_ulp) & big
+        allowed = 0 if stages == 1 else max(1, big.sum() // 1000)
+        assert bad.sum() <= allowed, f"{what}: {int(bad.sum())} elements > {max_ulp} ulp"
+
+
+# ---------------------------------------------------------------- layernorm
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,dim", [(1, 1024), (19, 1024), (257, 1024), (19, 300), (33, 64),
+                                      (7, 512), (5, 2048), (3, 4096), (11, 100)])
+def test_layernorm(ctx, dtype, rows, dim):
+    x = host(O.normal(11, (rows, dim)), dtype)
+    w = O.normal(12, (dim,), 1.0, 0.02)
+    b = O.normal(13, (dim,), 0.0, 0.02)
+    for eps in (1e-5, 1e-6):
+        got = back(ctx.layernorm(dev(x), dev(w), dev(b), eps=eps))
+        check(got, O.layernorm(x, w, b, eps), f"layernorm {dtype} {rows}x{dim} eps={eps}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_layernorm_in_place_and_empty(ctx, dtype):
+    x = host(O.normal(14, (9, 1024)), dtype)
+    w, b = O.normal(15, (1024,), 1.0, 0.02), O.normal(16, (1024,), 0.0, 0.02)
+    t = dev(x)
+    ctx.layernorm(t, dev(w), dev(b), eps=1e-6, out=t)
+    check(back(t), O.layernorm(x, w, b, 1e-6), "layernorm in place")
+    empty = torch.empty((0, 1024), dtype=dtype, device="cuda:0")
+    assert ctx.layernorm(empty, dev(w), dev(b)).shape == (0, 1024)
+
+
+# ------------------------------------------------------ qk-norm + rope (fused)
+
+QK_CASES = [
+    # s, t, h, d, prefix, grid (h_p, w_p)
+    (2, 11, 16, 64, 5, (2, 3)),
+    (2, 21, 16, 64, 5, (4, 4)),
+    (3, 37, 8, 64, 17, (4, 5)),
+    (1, 9, 4, 64, 3, (2, 3)),
+    (2, 11, 3, 64, 5, (2, 3)),    # H not a multiple of a load's heads: generic path
+    (2, 10, 2, 32, 4, (2, 3)),    # head_dim 32: generic path (tables cut to 32 channels)
+]
+
+
+def _tables(t, prefix, grid, d):
+    sin, cos = rope.tables(rope.periods(), *grid)
+    assert sin.shape[0] == t - prefix
+    if d != 64:
+        sin, cos = np.ascontiguousarray(sin[:, :d]), np.ascontiguousarray(cos[:, :d])
+    return sin, cos
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", QK_CASES)
+@pytest.mark.parametrize("norm,use_rope", [(True, True), (True, False), (False, True),
+                                           (False, False)])
+def test_qknorm_rope(ctx, dtype, case, norm, use_rope):
+    s, t, h, d, prefix, grid = case
+    x = host(O.normal(21, (s * t, h * d)), dtype)
+    nw, nb = O.normal(22, (d,), 1.0, 0.02), O.normal(23, (d,), 0.0, 0.02)
+    sin, cos = _tables(t, prefix, grid, d)
+    got = back(ctx.qknorm_rope(dev(x), s, t, h, d,
+                               norm=(dev(nw), dev(nb)) if norm else None,
+                               rope=(dev(sin), dev(cos), prefix) if use_rope else None, eps=1e-6))
+    want = O.qknorm_rope(x, nw if norm else None, nb if norm else None,
+                         sin if use_rope else None, cos if use_rope else None,
+                         s, t, h, d, prefix, 1e-6)
+    what = f"qknorm_rope {dtype} {case} norm={norm} rope={use_rope}"
+    if not norm and not use_rope:
+        assert_bit_exact(got, want, what)  # pure split_heads
+        return
+    check(got, want, what, stages=2 if (norm and use_rope) else 1)
+    if use_rope and not norm:
+        # prefix tokens pass through untouched
+        xs = x.reshape(s, t, h, d).transpose(0, 2, 1, 3)
+        assert_bit_exact(got[:, :, :prefix], np.ascontiguousarray(xs[:, :, :prefix]), what + " prefix")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_qknorm_rope_prefix_equals_t(ctx, dtype):
+    s, t, h, d = 2, 5, 16, 64
+    x = host(O.normal(24, (s * t, h * d)), dtype)
+    nw, nb = O.normal(25, (d,), 1.0, 0.02), O.normal(26, (d,), 0.0, 0.02)
+    dummy = torch.zeros(0, dtype=torch.float32, device="cuda:0")
+    got = back(ctx.qknorm_rope(dev(x), s, t, h, d, norm=(dev(nw), dev(nb)),
+                               rope=(dummy, dummy, t), eps=1e-5))
+    want = O.qknorm_rope(x, nw, nb, None, None, s, t, h, d, t, 1e-5)
+    check(got, want, "qknorm_rope prefix == T")
+
+
+# ---------------------------------------------------------- split / rope ops
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 5, 4, 8), (2, 11, 16, 64), (1, 7, 3, 64), (3, 4, 5, 6)])
+def test_split_heads(ctx, dtype, shape):
+    s, t, h, d = shape
+    x = host(O.normal(31, (s * t, h * d)), dtype)
+    got = back(ctx.split_heads(dev(x), s, t, h, d))
+    assert_bit_exact(got, np.ascontiguousarray(x.reshape(s, t, h, d).transpose(0, 2, 1, 3)),
+                     f"split_heads {shape}")
+    assert_bit_exact(got, O.split_heads(x, s, t, h, d), f"split_heads {shape} oracle")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", [(2, 3, 11, 64, 5, (2, 3)), (2, 4, 21, 64, 5, (4, 4)),
+                                  (1, 2, 23, 64, 17, (2, 3)), (2, 2, 7, 64, 7, (2, 3))])
+def test_rope_apply(ctx, dtype, case):
+    s, h, t, d, prefix, grid = case
+    sin, cos = rope.tables(rope.periods(), *grid)
+    if t - prefix != sin.shape[0]:
+        sin, cos = sin[: t - prefix].copy(), cos[: t - prefix].copy()
+    x = host(O.normal(41, (s, h, t, d)), dtype)
+    g = dev(x)
+    ctx.rope_apply(g, dev(sin), dev(cos), prefix)
+    got = back(g)
+    want = O.rope_apply(x, sin, cos, prefix)
+    check(got, want, f"rope_apply {case}")
+    assert_bit_exact(got[:, :, :prefix], x[:, :, :prefix], "rope prefix passthrough")
+
+
+# ------------------------------------------------------------- elementwise
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,cols", [(37, 4096), (5, 1000), (3, 30), (64, 1024), (1, 8)])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_bias_gelu(ctx, dtype, rows, cols, with_bias):
+    x = host(O.normal(51, (rows, cols)) * np.float32(2.0), dtype)
+    b = O.normal(52, (cols,), 0.0, 0.02) if with_bias else None
+    got = back(ctx.bias_gelu(dev(x), None if b is None else dev(b)))
+    check(got, O.bias_gelu(x, b), f"bias_gelu {dtype} {rows}x{cols} bias={with_bias}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gelu_surface_and_in_place(ctx, dtype):
+    for n in (1000, 999, 8, 3):
+        x = host(O.normal(53 + n, (n,)) * np.float32(3.0), dtype)
+        check(back(ctx.gelu(dev(x))), O.gelu(x), f"gelu n={n}")
+    x = host(O.normal(54, (64, 4096)), dtype)
+    b = O.normal(55, (4096,), 0.0, 0.02)
+    t = dev(x)
+    ctx.bias_gelu(t, dev(b), out=t)
+    check(back(t), O.bias_gelu(x, b), "bias_gelu in place")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,dim", [(37, 1024), (5, 300), (3, 30), (64, 4096), (2, 6)])
+@pytest.mark.parametrize("with_bias", [True, False])
+@pytest.mark.parametrize("gamma_kind", ["init", "normal"])
+def test_bias_ls_residual(ctx, dtype, rows, dim, with_bias, gamma_kind):
+    res = host(O.normal(61, (rows, dim)), dtype)
+    x = host(O.normal(62, (rows, dim)), dtype)
+    b = O.normal(63, (dim,), 0.0, 0.02) if with_bias else None
+    g = np.full(dim, 1e-5, np.float32) if gamma_kind == "init" else O.normal(64, (dim,))
+    got = back(ctx.bias_ls_residual(dev(res), dev(x), dev(g), None if b is None else dev(b)))
+    check(got, O.bias_ls_residual(res, x, b, g), f"bias_ls_residual {dtype} {rows}x{dim}")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_residual_ls_surface_in_place(ctx, dtype):
+    res = host(O.normal(65, (40, 1024)), dtype)
+    x = host(O.normal(66, (40, 1024)), dtype)
+    g = O.normal(67, (1024,))
+    check(back(ctx.residual_ls(dev(res), dev(x), dev(g))), O.residual_ls(res, x, g), "residual_ls")
+    t = dev(res)
+    ctx.bias_ls_residual(t, dev(x), dev(g), out=t)
+    check(back(t), O.residual_ls(res, x, g), "residual_ls in place on res")
+
+
+def test_cast_to_f16(ctx):
+    for n in (1 << 16, 1001, 7):
+        x = O.normal(71, (n,)) * np.float32(300.0)
+        assert_bit_exact(back(ctx.cast_to_f16(dev(x))), O.cast_to_f16(x), f"cast n={n}")
+    edge = np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, -7e4, 6.0e-8, 2.98e-8, 1e-10,
+                     np.inf, -np.inf, 0.1, 1.0 / 3], np.float32)
+    assert_bit_exact(back(ctx.cast_to_f16(dev(edge))), edge.astype(np.float16), "cast edges")
+
+
+def test_tiled_add_and_copy_rows(ctx):
+    x = O.normal(81, (6, 10, 4))
+    table = O.normal(82, (10, 4))
+    assert_bit_exact(back(ctx.tiled_add(dev(x), dev(table))), O.tiled_add(x, table), "tiled_add")
+    src = dev(O.normal(83, (10, 24)))
+    dst = torch.zeros((7, 24), dtype=torch.float32, device="cuda:0")
+    ctx.copy_rows(src, 3, dst, 2, 4)
+    want = np.zeros((7, 24), np.float32)
+    want[2:6] = back(src)[3:7]
+    assert_bit_exact(back(dst), want, "copy_rows")
+
+
+# ----------------------------------------------------------------- assembly
+
+@pytest.mark.parametrize("out_dtype", DTYPES)
+@pytest.mark.parametrize("patch_dtype", DTYPES)
+@pytest.mark.parametrize("s,grid,r,d,n_var", [(3, (2, 3), 4, 1024, 2), (2, (2, 3), 16, 256, 2),
+                                              (2, (3, 2), 4, 96, 1), (1, (1, 4), 0, 512, 2)])
+@pytest.mark.parametrize("bias,pos", [(True, True), (False, False), (True, False)])
+def test_assemble_tokens(ctx, out_dtype, patch_dtype, s, grid, r, d, n_var, bias, pos):
+    p = grid[0] * grid[1]
+    patches = host(O.normal(91, (s * p, d)), patch_dtype)
+    nout = NP[out_dtype]
+    cam = host(O.normal(92, (n_var, d)), out_dtype)
+    reg = host(O.normal(93, (n_var * r, d)), out_dtype) if r else None
+    pb = O.normal(94, (d,), 0.0, 0.02) if bias else None
+    pe = O.normal(95, (p, d), 0.0, 0.02) if pos else None
+    got = back(ctx.assemble_tokens(dev(patches), s, p, dev(cam), None if reg is None else dev(reg),
+                                   patch_bias=None if pb is None else dev(pb),
+                                   pos=None if pe is None else dev(pe), out_dtype=out_dtype,
+                                   n_var=n_var))
+    want = O.assemble_tokens(patches, pb, pe, cam, reg if reg is not None else np.zeros((0, d), nout),
+                             s, p, r, nout, n_var)
+    what = f"assemble {out_dtype}<-{patch_dtype} s={s} p={p} r={r} d={d}"
+    assert_bit_exact(got, want, what)
