@@ -10,8 +10,14 @@ RoPE, one sequence of S*1374 tokens), each block running
 
 (model/block.rs:118-159 with the GEMMs and attention out of scope: their
 outputs are synthetic resident buffers). Inputs are synthetic and already in
-HBM when timing starts. ``value`` is algorithmic bytes of the whole pass /
-pass time (GB/s); per-op times come from HIP events on the launch stream.
+HBM when timing starts.
+
+Timed region: K replays of a HIP graph holding one pass (launch overhead
+removed, as a serving loop would run it), bracketed by synchronisation and
+HIP events. ``value`` = algorithmic bytes of the pass / pass time (GB/s).
+Per-op kernel durations: every op of one more pass launched eagerly behind a
+GPU busy-wait head start, with a HIP event pair around each launch on the
+launch stream, averaged over ``--op-passes`` passes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames S]
 """
@@ -37,15 +43,14 @@ N_FRAME_BLOCKS = N_GLOBAL_BLOCKS = 24
 OPS = ["assemble", "layernorm", "qknorm_rope", "bias_ls_residual", "bias_gelu"]
 
 
-def op_bytes(rows: int, esz: int, patch_esz: int = 4, n_patch_rows: int = 0,
-             n_pos_rows: int = 0) -> dict:
+def op_bytes(rows: int, esz: int, n_patch_rows: int, n_pos_rows: int) -> dict:
     """Algorithmic (minimal) HBM bytes per launch of each fused op."""
     return {
         "layernorm": rows * DIM * esz * 2,                   # read x, write out
         "qknorm_rope": rows * DIM * esz * 2,                 # one of q / k
         "bias_ls_residual": rows * DIM * esz * 3,            # read res, x; write out
         "bias_gelu": rows * HIDDEN * esz * 2,                # read h, write act
-        "assemble": (n_patch_rows * DIM * patch_esz          # read patches (f32)
+        "assemble": (n_patch_rows * DIM * 4                  # read f32 patches
                      + n_pos_rows * DIM * 4                  # pos-embed once
                      + rows * DIM * esz),                    # write tokens
     }
@@ -54,23 +59,25 @@ def op_bytes(rows: int, esz: int, patch_esz: int = 4, n_patch_rows: int = 0,
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--frames", type=int, default=32)
     ap.add_argument("--dtype", choices=["f16", "f32"], default="f16")
+    ap.add_argument("--op-passes", type=int, default=3)
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="target CPU work for the oracle baseline sample")
     ap.add_argument("--calibrate-copy-mib", type=int, default=512,
-                    help="size of a plain torch copy launched once (HBM counter calibration)")
+                    help="size of one plain torch copy launched before timing (HBM counter "
+                         "calibration for rocprofv3 --pmc runs)")
     return ap.parse_args()
 
 
 class Pass:
-    """Buffers and launch sequence of one aggregator fused-op pass."""
+    """Buffers and the launch sequence of one aggregator fused-op pass."""
 
     def __init__(self, ctx, frames: int, dtype):
-        import numpy as np
         import torch
         from headshot_amd import rope
 
@@ -78,7 +85,7 @@ class Pass:
         dev = ctx.device
         p = GRID[0] * GRID[1]
         self.p, self.t = p, p + 1 + N_REG
-        self.rows = frames * self.t
+        self.rows = rows = frames * self.t
         g = torch.Generator(device=dev)
         g.manual_seed(42)
 
@@ -86,14 +93,13 @@ class Pass:
             return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std
                     + mean).to(dt)
 
-        rows = self.rows
         # stage inputs (DINO patch tokens are f32)
         self.patches = normal((frames * p, DIM))
         self.pos = normal((p, DIM), 0.0, 0.02)
         self.patch_bias = normal((DIM,), 0.0, 0.02)
         self.cam = normal((2, DIM), dt=dtype)
         self.reg = normal((2 * N_REG, DIM), dt=dtype)
-        # synthetic GEMM outputs (raw, biases applied by the fused ops)
+        # synthetic GEMM outputs (raw: their biases are applied by the fused ops)
         self.q_raw = normal((rows, DIM), dt=dtype)
         self.k_raw = normal((rows, DIM), dt=dtype)
         self.proj_raw = normal((rows, DIM), dt=dtype)
@@ -123,89 +129,76 @@ class Pass:
                 fc1_b=normal((HIDDEN,), 0.0, 0.02), fc2_b=normal((DIM,), 0.0, 0.02),
                 ls2=torch.full((DIM,), 1e-5, device=dev)))
         esz = 2 if dtype == torch.float16 else 4
-        self.bytes = op_bytes(rows, esz, 4, frames * p, p)
-        self.pass_bytes = (self.bytes["assemble"]
-                           + len(self.blocks) * (2 * self.bytes["layernorm"]
-                                                 + 2 * self.bytes["qknorm_rope"]
-                                                 + 2 * self.bytes["bias_ls_residual"]
-                                                 + self.bytes["bias_gelu"]))
+        self.bytes = op_bytes(rows, esz, frames * p, p)
         self.launches = {"assemble": 1}
         for k in OPS[1:]:
             self.launches[k] = len(self.blocks) * (1 if k == "bias_gelu" else 2)
-        _ = np  # numpy is used by the CPU leg
+        self.pass_bytes = sum(self.bytes[k] * self.launches[k] for k in OPS)
+        self.seq = self._launch_sequence()
 
-    def run(self, timer=None):
-        """Enqueue one pass on the current stream. ``timer(op)`` returns a
-        context manager recording events around a launch."""
+    def _launch_sequence(self):
+        """[(op, thunk)]: each thunk re-issues one validated C-ABI call on the
+        current stream (the HipContext checks ran once, here)."""
         c = self.ctx
-        nullctx = _Null()
-        tm = timer or (lambda op: nullctx)
+        seq = []
+
+        def rec(op, fn, *args, **kw):
+            # run once through HipContext (validation + first launch), then
+            # keep the raw call for the timed loops
+            fn(*args, **kw)
+            seq.append((op, c.last_launch))
+
         x = self.x[0]
-        with tm("assemble"):
-            c.assemble_tokens(self.patches, self.frames, self.p, self.cam, self.reg,
-                              patch_bias=self.patch_bias, pos=self.pos, out_dtype=self.dtype,
-                              out=x)
+        rec("assemble", c.assemble_tokens, self.patches, self.frames, self.p, self.cam, self.reg,
+            patch_bias=self.patch_bias, pos=self.pos, out_dtype=self.dtype, out=x)
         for i, b in enumerate(self.blocks):
             frame_block = i % 2 == 0  # frame / global alternate (model/trunk.rs:92-143)
             if frame_block:
-                s, t, rope = self.frames, self.t, (self.sin, self.cos, PREFIX)
+                s, t, rp = self.frames, self.t, (self.sin, self.cos, PREFIX)
             else:
-                s, t, rope = 1, self.rows, None
+                s, t, rp = 1, self.rows, None
             x_out = self.x[1] if x is self.x[0] else self.x[0]
-            with tm("layernorm"):
-                c.layernorm(x, *b["ln1"], eps=EPS, out=self.normed)
-            with tm("qknorm_rope"):
-                c.qknorm_rope(self.q_raw, s, t, HEADS, HEAD_DIM, norm=b["qn"], rope=rope, eps=EPS,
-                              out=self.q_head)
-            with tm("qknorm_rope"):
-                c.qknorm_rope(self.k_raw, s, t, HEADS, HEAD_DIM, norm=b["kn"], rope=rope, eps=EPS,
-                              out=self.k_head)
-            with tm("bias_ls_residual"):
-                c.bias_ls_residual(x, self.proj_raw, b["ls1"], b["proj_b"], out=self.x1)
-            with tm("layernorm"):
-                c.layernorm(self.x1, *b["ln2"], eps=EPS, out=self.normed2)
-            with tm("bias_gelu"):
-                c.bias_gelu(self.fc1_raw, b["fc1_b"], out=self.act)
-            with tm("bias_ls_residual"):
-                c.bias_ls_residual(self.x1, self.fc2_raw, b["ls2"], b["fc2_b"], out=x_out)
+            rec("layernorm", c.layernorm, x, *b["ln1"], eps=EPS, out=self.normed)
+            rec("qknorm_rope", c.qknorm_rope, self.q_raw, s, t, HEADS, HEAD_DIM, norm=b["qn"],
+                rope=rp, eps=EPS, out=self.q_head)
+            rec("qknorm_rope", c.qknorm_rope, self.k_raw, s, t, HEADS, HEAD_DIM, norm=b["kn"],
+                rope=rp, eps=EPS, out=self.k_head)
+            rec("bias_ls_residual", c.bias_ls_residual, x, self.proj_raw, b["ls1"], b["proj_b"],
+                out=self.x1)
+            rec("layernorm", c.layernorm, self.x1, *b["ln2"], eps=EPS, out=self.normed2)
+            rec("bias_gelu", c.bias_gelu, self.fc1_raw, b["fc1_b"], out=self.act)
+            rec("bias_ls_residual", c.bias_ls_residual, self.x1, self.fc2_raw, b["ls2"],
+                b["fc2_b"], out=x_out)
             x = x_out
+        return seq
+
+    def run(self):
+        for _, thunk in self.seq:
+            thunk()
 
 
-class _Null:
-    def __enter__(self):
-        return self
+def per_op_times(bench: Pass, passes: int) -> dict:
+    """Mean kernel duration per op (ms) from HIP event pairs on the launch
+    stream. A GPU busy-wait ahead of each pass lets the host enqueue the
+    whole pass first, so the kernels run back to back as in the timed loop."""
+    import torch
 
-    def __exit__(self, *a):
-        return False
-
-
-class EventTimer:
-    """Per-op HIP event pairs on the current (launch) stream."""
-
-    def __init__(self):
-        self.pairs = {op: [] for op in OPS}
-
-    def __call__(self, op):
-        import torch
-        timer = self
-
-        class _Ctx:
-            def __enter__(self_inner):
-                self_inner.a = torch.cuda.Event(enable_timing=True)
-                self_inner.b = torch.cuda.Event(enable_timing=True)
-                self_inner.a.record()
-                return self_inner
-
-            def __exit__(self_inner, *exc):
-                self_inner.b.record()
-                timer.pairs[op].append((self_inner.a, self_inner.b))
-                return False
-
-        return _Ctx()
-
-    def mean_ms(self):
-        return {op: (sum(a.elapsed_time(b) for a, b in v) / len(v)) if v else None
-                for op, v in self.pairs.items()}
+    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+             for _ in bench.seq]
+    sums = {op: 0.0 for op in OPS}
+    counts = {op: 0 for op in OPS}
+    for _ in range(passes):
+        torch.cuda.synchronize()
+        torch.cuda._sleep(100_000_000)  # ~40 ms head start
+        for (op, thunk), (a, b) in zip(bench.seq, pairs):
+            a.record()
+            thunk()
+            b.record()
+        torch.cuda.synchronize()
+        for (op, _), (a, b) in zip(bench.seq, pairs):
+            sums[op] += a.elapsed_time(b)
+            counts[op] += 1
+    return {op: sums[op] / counts[op] for op in OPS}
 
 
 def cpu_baseline(bench: Pass, target_s: float):
@@ -226,7 +219,6 @@ def cpu_baseline(bench: Pass, target_s: float):
     q, k = h(bench.q_raw), h(bench.k_raw)
     proj, fc1, fc2 = h(bench.proj_raw), h(bench.fc1_raw), h(bench.fc2_raw)
     sin, cos = h(bench.sin), h(bench.cos)
-    npdt = x.dtype
     out = dict(normed=np.empty_like(x), q_head=np.empty_like(q), k_head=np.empty_like(k),
                x1=np.empty_like(x), normed2=np.empty_like(x), act=np.empty_like(fc1),
                x_out=np.empty_like(x))
@@ -236,7 +228,7 @@ def cpu_baseline(bench: Pass, target_s: float):
     done_bytes = 0
     blocks_done = 0
     t0 = time.perf_counter()
-    O.assemble_tokens(patches, pb, pos, cam, reg, frames, bench.p, N_REG, npdt)
+    O.assemble_tokens(patches, pb, pos, cam, reg, frames, bench.p, N_REG, x.dtype)
     done_bytes += bench.bytes["assemble"]
     block_bytes = (2 * bench.bytes["layernorm"] + 2 * bench.bytes["qknorm_rope"]
                    + 2 * bench.bytes["bias_ls_residual"] + bench.bytes["bias_gelu"])
@@ -271,8 +263,8 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU: the fused per-layer ops are "
-                                   "row-local and shard by frames with no exchange; run with "
-                                   "--gpus 1"}))
+                                   "row-local and shard by frames with no exchange, so the "
+                                   "figure that matters is one GPU's; run with --gpus 1"}))
         sys.exit(2)
     import torch
 
@@ -286,7 +278,7 @@ def main():
     # HBM counter calibration: one plain copy of known size (outside timing).
     if args.calibrate_copy_mib > 0:
         n = args.calibrate_copy_mib * (1 << 20) // 4
-        a = torch.empty(n, device=ctx.device, dtype=torch.float32).fill_(1.0)
+        a = torch.ones(n, device=ctx.device, dtype=torch.float32)
         b_ = torch.empty_like(a)
         b_.copy_(a)
         torch.cuda.synchronize()
@@ -296,19 +288,36 @@ def main():
         bench.run()
     torch.cuda.synchronize()
 
-    timer = EventTimer()
+    launch = "eager"
+    graph = None
+    if not args.eager:
+        try:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                bench.run()
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            launch = "hip_graph"
+        except Exception as exc:  # capture unsupported: time eager launches
+            print(f"graph capture failed ({exc}); timing eager launches", file=sys.stderr)
+            graph = None
+
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record()
     for _ in range(args.steps):
-        bench.run(timer)
+        if graph is not None:
+            graph.replay()
+        else:
+            bench.run()
     end.record()
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
 
+    mean = per_op_times(bench, args.op_passes)
     per_op = {}
-    mean = timer.mean_ms()
     for op in OPS:
         us = mean[op] * 1e3
         gbs = bench.bytes[op] / (us * 1e-6) / 1e9
@@ -336,7 +345,7 @@ def main():
                                f"{N_GLOBAL_BLOCKS} global blocks",
                    "frames": args.frames, "tokens_per_frame": bench.t, "dim": DIM,
                    "heads": HEADS, "head_dim": HEAD_DIM, "hidden": HIDDEN, "prefix": PREFIX,
-                   "grid": f"{GRID[0]}x{GRID[1]}", "eps": EPS},
+                   "grid": f"{GRID[0]}x{GRID[1]}", "eps": EPS, "launch": launch},
         "frac_of_peak": round(value / PEAK_GBS, 4),
         "pass_bytes": bench.pass_bytes,
         "tokens_per_s": round(bench.rows / (ms * 1e-3), 1),

@@ -10,7 +10,9 @@ import os
 import re
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libheadshot_hip.so")
+# HEADSHOT_HIP_LIB points at another build of the same library (e.g. one
+# compiled with different launch-shape constants).
+LIB_PATH = os.environ.get("HEADSHOT_HIP_LIB") or os.path.join(HERE, "libheadshot_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "headshot_hip.h")
 
 HS_F32, HS_F16 = 0, 1

@@ -58,14 +58,17 @@ def _run(cmd):
     return err
 
 
-def build(verbose: bool = False) -> str:
-    os.makedirs(BUILD, exist_ok=True)
+def build(verbose: bool = False, defines=(), lib_path: str = LIB, build_dir: str = BUILD) -> str:
+    """Compile every source and link ``lib_path``. ``defines`` (``NAME=VALUE``
+    strings) override the kernels' launch-shape constants."""
+    os.makedirs(build_dir, exist_ok=True)
+    dflags = [f"-D{d}" for d in defines]
     jobs = []
     for src in HIP_SOURCES:
-        obj = os.path.join(BUILD, src.replace(".hip", ".o"))
-        jobs.append([HIPCC, *HIP_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
+        jobs.append([HIPCC, *HIP_FLAGS, *dflags, "-c", os.path.join(CSRC, src), "-o", obj])
     for src in CXX_SOURCES:
-        obj = os.path.join(BUILD, src.replace(".cpp", ".o"))
+        obj = os.path.join(build_dir, src.replace(".cpp", ".o"))
         jobs.append(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
     workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(workers) as pool:
@@ -73,10 +76,10 @@ def build(verbose: bool = False) -> str:
             if msg and verbose:
                 print(msg, file=sys.stderr)
     objs = [j[-1] for j in jobs]
-    tmp = LIB + ".tmp"
+    tmp = lib_path + ".tmp"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib_path)
+    return lib_path
 
 
 if __name__ == "__main__":

@@ -11,7 +11,9 @@ reference's ``assert!`` panics.
 
 Like the reference, every op except ``rope_apply`` and ``copy_rows`` returns
 a new output tensor; the fused ops also accept ``out=`` to write into a
-caller buffer (no allocation).
+caller buffer (no allocation). After each op, ``last_launch`` holds a
+callable that re-issues the same validated C call on the then-current
+stream (for launch loops and graph capture without per-call Python checks).
 """
 from __future__ import annotations
 
@@ -48,10 +50,6 @@ def _opt(t, n: int, what: str):
     return None if t is None else _param(t, n, what)
 
 
-def _stream() -> int:
-    return torch.cuda.current_stream().cuda_stream
-
-
 class HipContext:
     """One device's op surface. ``device`` is a torch device (default cuda:0)."""
 
@@ -62,6 +60,14 @@ class HipContext:
             raise AssertionError("HipContext needs a HIP device")
         if not torch.cuda.is_available():
             raise RuntimeError("no HIP device visible (torch.cuda.is_available() is False)")
+        self.last_launch = None
+
+    def _launch(self, name: str, fn, *args) -> None:
+        def call():
+            _lib.check(fn(torch.cuda.current_stream().cuda_stream, *args), name)
+
+        call()
+        self.last_launch = call
 
     # ------------------------------------------------------------------ tensors
 
@@ -102,8 +108,8 @@ class HipContext:
         if out is None:
             out = self.empty_typed(x.shape, x.dtype)
         assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
-        _lib.check(self.lib.hs_layernorm(_stream(), _dt(x), _dev(x, "x"), w, b, _dev(out, "out"),
-                                         rows, dim, eps), "layernorm")
+        self._launch("layernorm", self.lib.hs_layernorm, _dt(x), _dev(x, "x"), w, b,
+                     _dev(out, "out"), rows, dim, eps)
         return out
 
     def gelu(self, x, out=None) -> torch.Tensor:
@@ -111,8 +117,7 @@ class HipContext:
         if out is None:
             out = self.empty_typed(x.shape, x.dtype)
         assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
-        _lib.check(self.lib.hs_gelu(_stream(), _dt(x), _dev(x, "x"), _dev(out, "out"), x.numel()),
-                   "gelu")
+        self._launch("gelu", self.lib.hs_gelu, _dt(x), _dev(x, "x"), _dev(out, "out"), x.numel())
         return out
 
     def residual_ls(self, res, x, gamma, out=None) -> torch.Tensor:
@@ -124,17 +129,16 @@ class HipContext:
         assert dim > 0 and x.numel() % dim == 0, "gamma must tile x"
         if out is None:
             out = self.empty_typed(res.shape, x.dtype)
-        _lib.check(self.lib.hs_residual_ls(_stream(), _dt(x), _dev(res, "res"), _dev(x, "x"),
-                                           _dev(gamma, "gamma"), _dev(out, "out"), x.numel(), dim),
-                   "residual_ls")
+        self._launch("residual_ls", self.lib.hs_residual_ls, _dt(x), _dev(res, "res"),
+                     _dev(x, "x"), _dev(gamma, "gamma"), _dev(out, "out"), x.numel(), dim)
         return out
 
     def split_heads(self, x, s: int, t: int, h: int, d: int) -> torch.Tensor:
         """engine/ops.rs:185-200: (S·T, H·D) → (S, H, T, D)."""
         assert x.numel() == s * t * h * d, "split_heads size"
         out = self.empty_typed((s, h, t, d), x.dtype)
-        _lib.check(self.lib.hs_split_heads(_stream(), _dt(x), _dev(x, "x"), _dev(out, "out"),
-                                           s, t, h, d), "split_heads")
+        self._launch("split_heads", self.lib.hs_split_heads, _dt(x), _dev(x, "x"),
+                     _dev(out, "out"), s, t, h, d)
         return out
 
     def rope_apply(self, x, sin, cos, prefix: int) -> None:
@@ -145,15 +149,15 @@ class HipContext:
         assert sin.numel() == (t - prefix) * d, "table size"
         assert sin.dtype == F32 and cos.dtype == F32, "rope tables must be f32"
         assert cos.numel() == sin.numel(), "table size"
-        _lib.check(self.lib.hs_rope_apply(_stream(), _dt(x), _dev(x, "x"), _dev(sin, "sin"),
-                                          _dev(cos, "cos"), s, h, t, d, prefix), "rope_apply")
+        self._launch("rope_apply", self.lib.hs_rope_apply, _dt(x), _dev(x, "x"),
+                     _dev(sin, "sin"), _dev(cos, "cos"), s, h, t, d, prefix)
 
     def cast_to_f16(self, x) -> torch.Tensor:
         """engine/ops.rs:336-348."""
         assert x.dtype == F32, "cast_to_f16 wants f32"
         out = self.empty_typed(x.shape, F16)
-        _lib.check(self.lib.hs_cast_f32_to_f16(_stream(), _dev(x, "x"), _dev(out, "out"),
-                                               x.numel()), "cast_to_f16")
+        self._launch("cast_to_f16", self.lib.hs_cast_f32_to_f16, _dev(x, "x"), _dev(out, "out"),
+                     x.numel())
         return out
 
     def copy_rows(self, src, src_row: int, dst, dst_row: int, n_rows: int) -> None:
@@ -163,16 +167,16 @@ class HipContext:
         assert row_bytes == dst.shape[-1] * dst.element_size(), "copy_rows row width"
         assert (src_row + n_rows) * row_bytes <= src.numel() * src.element_size(), "src rows"
         assert (dst_row + n_rows) * row_bytes <= dst.numel() * dst.element_size(), "dst rows"
-        _lib.check(self.lib.hs_copy_rows(_stream(), _dev(src, "src"), src_row, _dev(dst, "dst"),
-                                         dst_row, n_rows, row_bytes), "copy_rows")
+        self._launch("copy_rows", self.lib.hs_copy_rows, _dev(src, "src"), src_row,
+                     _dev(dst, "dst"), dst_row, n_rows, row_bytes)
 
     def tiled_add(self, x, table) -> torch.Tensor:
         """engine/ops.rs:374-389 (f32 only)."""
         assert x.dtype == F32 and table.dtype == F32, "tiled_add is f32"
         assert table.numel() > 0 and x.numel() % table.numel() == 0, "table must tile x"
         out = self.empty(x.shape)
-        _lib.check(self.lib.hs_tiled_add(_stream(), _dev(x, "x"), _dev(table, "table"),
-                                         _dev(out, "out"), x.numel(), table.numel()), "tiled_add")
+        self._launch("tiled_add", self.lib.hs_tiled_add, _dev(x, "x"), _dev(table, "table"),
+                     _dev(out, "out"), x.numel(), table.numel())
         return out
 
     # --------------------------------------------------------------- fused ops
@@ -197,9 +201,8 @@ class HipContext:
         if out is None:
             out = self.empty_typed((s, h, t, d), x_tok.dtype)
         assert out.dtype == x_tok.dtype and out.numel() == x_tok.numel(), "out shape/dtype"
-        _lib.check(self.lib.hs_qknorm_rope(_stream(), _dt(x_tok), _dev(x_tok, "x"), nw, nb, sn, cs,
-                                           _dev(out, "out"), s, t, h, d, prefix, eps),
-                   "qknorm_rope")
+        self._launch("qknorm_rope", self.lib.hs_qknorm_rope, _dt(x_tok), _dev(x_tok, "x"), nw, nb,
+                     sn, cs, _dev(out, "out"), s, t, h, d, prefix, eps)
         return out
 
     def bias_gelu(self, x, bias=None, out=None) -> torch.Tensor:
@@ -210,8 +213,8 @@ class HipContext:
         if out is None:
             out = self.empty_typed(x.shape, x.dtype)
         assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
-        _lib.check(self.lib.hs_bias_gelu(_stream(), _dt(x), _dev(x, "x"), b, _dev(out, "out"),
-                                         rows, cols), "bias_gelu")
+        self._launch("bias_gelu", self.lib.hs_bias_gelu, _dt(x), _dev(x, "x"), b,
+                     _dev(out, "out"), rows, cols)
         return out
 
     def bias_ls_residual(self, res, x, gamma, bias=None, out=None) -> torch.Tensor:
@@ -224,9 +227,8 @@ class HipContext:
         if out is None:
             out = self.empty_typed(res.shape, x.dtype)
         assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
-        _lib.check(self.lib.hs_bias_ls_residual(_stream(), _dt(x), _dev(res, "res"), _dev(x, "x"),
-                                                b, g, _dev(out, "out"), rows, dim),
-                   "bias_ls_residual")
+        self._launch("bias_ls_residual", self.lib.hs_bias_ls_residual, _dt(x), _dev(res, "res"),
+                     _dev(x, "x"), b, g, _dev(out, "out"), rows, dim)
         return out
 
     def assemble_tokens(self, patches, s: int, p: int, cam, reg, patch_bias=None, pos=None,
@@ -245,8 +247,8 @@ class HipContext:
         if out is None:
             out = self.empty_typed((s * t, d), out_dtype)
         assert out.dtype == out_dtype and out.numel() == s * t * d, "out shape/dtype"
-        _lib.check(self.lib.hs_assemble_tokens(
-            _stream(), _dt(out), _dev(patches, "patches"), _dt(patches), b, ps, _dev(cam, "cam"),
-            None if reg is None else _dev(reg, "reg"), _dev(out, "out"), s, p, r, d, n_var),
-            "assemble_tokens")
+        self._launch("assemble_tokens", self.lib.hs_assemble_tokens, _dt(out),
+                     _dev(patches, "patches"), _dt(patches), b, ps, _dev(cam, "cam"),
+                     None if reg is None else _dev(reg, "reg"), _dev(out, "out"), s, p, r, d,
+                     n_var)
         return out

@@ -17,7 +17,11 @@ namespace {
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / 64;
-constexpr int kBlocksPerCu = 8;
+// Launch shape (overridable at build time for tuning sweeps).
+#ifndef HS_AS_BPC
+#define HS_AS_BPC 8  // resident workgroups per CU
+#endif
+constexpr int kBlocksPerCu = HS_AS_BPC;
 
 __device__ __forceinline__ void load4(const float* p, float (&f)[4]) {
     float4 v = ld_f32x4(p);
@@ -29,8 +33,22 @@ __device__ __forceinline__ void load4(const f16* p, float (&f)[4]) {
     f[0] = static_cast<float>(a.x), f[1] = static_cast<float>(a.y);
     f[2] = static_cast<float>(b.x), f[3] = static_cast<float>(b.y);
 }
+// Patch loads and token stores stream (non-temporal); camera/register rows
+// and the positional table are reread across frames and stay cached.
+__device__ __forceinline__ void load4_stream(const float* p, float (&f)[4]) {
+    const u32x4 v = ld_stream(p);
+    f[0] = u2f(v[0]), f[1] = u2f(v[1]), f[2] = u2f(v[2]), f[3] = u2f(v[3]);
+}
+__device__ __forceinline__ void load4_stream(const f16* p, float (&f)[4]) {
+    const u32x2 v = ld_stream_as(reinterpret_cast<const u32x2*>(p));
+    const f16x2 a = u2h2(v[0]), b = u2h2(v[1]);
+    f[0] = static_cast<float>(a.x), f[1] = static_cast<float>(a.y);
+    f[2] = static_cast<float>(b.x), f[3] = static_cast<float>(b.y);
+}
 __device__ __forceinline__ void store4(float* p, const float (&f)[4]) {
-    *reinterpret_cast<float4*>(p) = make_float4(f[0], f[1], f[2], f[3]);
+    u32x4 v;
+    v[0] = f2u(f[0]), v[1] = f2u(f[1]), v[2] = f2u(f[2]), v[3] = f2u(f[3]);
+    st_stream(p, v);
 }
 __device__ __forceinline__ void store4(f16* p, const float (&f)[4]) {
     f16x2 a, b;
@@ -38,7 +56,7 @@ __device__ __forceinline__ void store4(f16* p, const float (&f)[4]) {
     b.x = static_cast<f16>(f[2]), b.y = static_cast<f16>(f[3]);
     u32x2 v;
     v[0] = h22u(a), v[1] = h22u(b);
-    *reinterpret_cast<u32x2*>(p) = v;
+    st_stream_as(reinterpret_cast<u32x2*>(p), v);
 }
 
 // Patch-row value as the reference sequence stores it: the GEMM epilogue
@@ -84,7 +102,7 @@ __global__ __launch_bounds__(kBlock) void assemble_kernel(
             const float* prow = has_p ? pos + static_cast<int64_t>(p) * D + lane * 4 : nullptr;
             float x[CHUNKS][4], pe[CHUNKS][4];
 #pragma unroll
-            for (int c = 0; c < CHUNKS; c++) load4(src + c * 256, x[c]);
+            for (int c = 0; c < CHUNKS; c++) load4_stream(src + c * 256, x[c]);
             if (has_p) {
 #pragma unroll
                 for (int c = 0; c < CHUNKS; c++) load4(prow + c * 256, pe[c]);

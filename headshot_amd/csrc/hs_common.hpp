@@ -24,7 +24,7 @@ int num_cus();
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // [a, a+na) and [b, b+nb) byte ranges overlap.
 inline bool overlaps(const void* a, int64_t na, const void* b, int64_t nb) {
@@ -56,12 +56,46 @@ __device__ __forceinline__ u32x4 ld16(const void* p) {
 }
 __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
-// Streaming variants: data touched once (non-temporal hint).
+// Streaming variants for activations, which every op touches exactly once:
+// non-temporal loads and stores. On MI355X these sustain ~6.2 TB/s for a
+// 1:1 read/write stream against ~4.3-5.0 TB/s for plain accesses in the
+// same launch shapes. Parameters (weights, biases, tables) use the cached
+// ld16/ld_f32x4 paths because every wave rereads them.
+#ifndef HS_NT
+#define HS_NT 1
+#endif
+
 __device__ __forceinline__ u32x4 ld16_nt(const void* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 __device__ __forceinline__ void st16_nt(void* p, u32x4 v) {
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+template <bool NT = (HS_NT != 0)>
+__device__ __forceinline__ u32x4 ld_stream(const void* p) {
+    if constexpr (NT) return ld16_nt(p);
+    return ld16(p);
+}
+template <bool NT = (HS_NT != 0)>
+__device__ __forceinline__ void st_stream(void* p, u32x4 v) {
+    if constexpr (NT)
+        st16_nt(p, v);
+    else
+        st16(p, v);
+}
+
+template <typename V>
+__device__ __forceinline__ V ld_stream_as(const V* p) {
+    if constexpr (HS_NT) return __builtin_nontemporal_load(p);
+    return *p;
+}
+template <typename V>
+__device__ __forceinline__ void st_stream_as(V* p, V v) {
+    if constexpr (HS_NT)
+        __builtin_nontemporal_store(v, p);
+    else
+        *p = v;
 }
 
 __device__ __forceinline__ float4 ld_f32x4(const float* p) {

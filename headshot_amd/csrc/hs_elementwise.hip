@@ -15,34 +15,66 @@
 namespace hs {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kBlocksPerCu = 8;
+// Launch shape (overridable at build time for tuning sweeps).
+// U: 16-byte vectors per input stream per thread per iteration; BPC:
+// workgroups launched per CU. Chosen by timing the whole aggregator pass,
+// not the op alone: with U = 1 GELU itself runs ~8% faster but the kernels
+// after it (LayerNorm most) lose more than that.
+#ifndef HS_GELU_U
+#define HS_GELU_U 2
+#endif
+#ifndef HS_GELU_BPC
+#define HS_GELU_BPC 16
+#endif
+#ifndef HS_GELU_NTL
+#define HS_GELU_NTL (HS_NT != 0)  // non-temporal loads of the fc1 output
+#endif
+#ifndef HS_GELU_NTS
+#define HS_GELU_NTS (HS_NT != 0)  // non-temporal stores of the activation
+#endif
+#ifndef HS_LS_U
+#define HS_LS_U 2
+#endif
+#ifndef HS_LS_BPC
+#define HS_LS_BPC 8
+#endif
+#ifndef HS_EW_BPC
+#define HS_EW_BPC 4  // cast and tiled add
+#endif
 
-// erf by Abramowitz & Stegun 7.1.26 (gelu.wesl:18-27), f32. The
-// reciprocal and exponential use the hardware v_rcp_f32 / v_exp_f32.
-__device__ __forceinline__ float erf_as(float v) {
-    const float a = fabsf(v);
-    const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
+constexpr int kBlock = 256;
+constexpr int kBlocksPerCu = HS_EW_BPC;
+
+// Exact-erf GELU, gelu.wesl:18-38: 0.5*v*(1 + erf(v/sqrt(2))) with erf by
+// Abramowitz & Stegun 7.1.26, erf(z) = sign(z)*(1 - P(t)*t*exp(-z^2)),
+// t = 1/(1 + p*|z|). Evaluated in f32 with the scale folded into the
+// constants (z = v/sqrt(2) is never formed) and the sign folded into the
+// final multiply-add, since 0.5*v*sign(v) = |0.5*v|:
+//   gelu(v) = h + |h| * (1 - P(t)*t*2^(-(v*k)^2)),   h = v/2,
+//   t = 1/(1 + (p/sqrt(2))*|v|),  k = sqrt(log2(e)/2).
+// That is 13 VALU operations per element including one v_rcp_f32 and one
+// v_exp_f32 (both ~1 ulp); the folded constants move the result by a few
+// f32 ulps against the shader's operand order, far inside the parity bars.
+constexpr float kAsP = 0.3275911f * 0.70710678118654752f;  // p / sqrt(2)
+constexpr float kExpK = 0.84932180028801904f;               // sqrt(log2(e) / 2)
+
+__device__ __forceinline__ float gelu_f(float v) {
+    const float h = 0.5f * v;
+    const float t = __builtin_amdgcn_rcpf(fmaf(kAsP, fabsf(v), 1.0f));
     float p = fmaf(1.061405429f, t, -1.453152027f);
     p = fmaf(p, t, 1.421413741f);
     p = fmaf(p, t, -0.284496736f);
     p = fmaf(p, t, 0.254829592f);
     p = p * t;
-    // exp(-a^2) = 2^(-a^2 * log2(e))
-    const float e = __builtin_amdgcn_exp2f((a * a) * -1.4426950408889634f);
-    return copysignf(fmaf(-p, e, 1.0f), v);
-}
-
-// gelu.wesl:36-38: 0.5 * v * (1 + erf(v / sqrt(2)))
-__device__ __forceinline__ float gelu_f(float v) {
-    const float h = 0.5f * v;
-    return fmaf(h, erf_as(v * 0.7071067811865475f), h);
+    const float w = v * kExpK;
+    const float e = __builtin_amdgcn_exp2f(-(w * w));  // exp(-v^2/2)
+    return fmaf(fabsf(h), fmaf(-p, e, 1.0f), h);
 }
 
 // Grid size (in blocks) for a column-stationary launch: the stride
 // blocks*kBlock*V must be a multiple of cols. Returns 0 if no such grid of
 // useful size exists.
-int64_t column_stationary_blocks(int64_t total, int64_t cols, int V, int U) {
+int64_t column_stationary_blocks(int64_t total, int64_t cols, int V, int U, int bpc) {
     const int64_t per_block = static_cast<int64_t>(kBlock) * V;
     int64_t a = per_block, b = cols;
     while (b) {
@@ -52,7 +84,7 @@ int64_t column_stationary_blocks(int64_t total, int64_t cols, int V, int U) {
     }
     const int64_t step = cols / a;  // blocks must be a multiple of this
     const int64_t want = ceil_div(total, per_block * U);
-    const int64_t cap = static_cast<int64_t>(num_cus()) * kBlocksPerCu;
+    const int64_t cap = static_cast<int64_t>(num_cus()) * bpc;
     int64_t blocks = want < cap ? want : cap;
     blocks = ceil_div(blocks, step) * step;
     if (blocks > 4 * cap) return 0;
@@ -78,7 +110,7 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
         u32x4 raw[U];
 #pragma unroll
         for (int u = 0; u < U; u++)
-            if (base + u * stride < total) raw[u] = ld16(x + base + u * stride);
+            if (base + u * stride < total) raw[u] = ld_stream<HS_GELU_NTL>(x + base + u * stride);
 #pragma unroll
         for (int u = 0; u < U; u++) {
             if (base + u * stride >= total) break;
@@ -86,11 +118,14 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
             unpack(raw[u], f, T{});
 #pragma unroll
             for (int k = 0; k < V; k++) {
+                // The fc1 bias joins in f32; the reference's GEMM epilogue
+                // would have stored x + bias as f16 first (one extra
+                // rounding this fused op leaves out).
                 float v = f[k];
-                if constexpr (BIAS) v = storage_round(v + bv[k], T{});
+                if constexpr (BIAS) v = v + bv[k];
                 f[k] = gelu_f(v);
             }
-            st16(out + base + u * stride, pack(f, T{}));
+            st_stream<HS_GELU_NTS>(out + base + u * stride, pack(f, T{}));
         }
     }
 }
@@ -119,8 +154,8 @@ __global__ __launch_bounds__(kBlock) void bias_ls_kernel(const T* res, const T* 
 #pragma unroll
         for (int u = 0; u < U; u++) {
             if (base + u * stride < total) {
-                rr[u] = ld16(res + base + u * stride);
-                xr[u] = ld16(x + base + u * stride);
+                rr[u] = ld_stream(res + base + u * stride);
+                xr[u] = ld_stream(x + base + u * stride);
             }
         }
 #pragma unroll
@@ -135,7 +170,7 @@ __global__ __launch_bounds__(kBlock) void bias_ls_kernel(const T* res, const T* 
                 if constexpr (BIAS) v = storage_round(v + bv[k], T{});
                 fr[k] = fr[k] + gv[k] * v;  // residual_ls.wesl:28
             }
-            st16(out + base + u * stride, pack(fr, T{}));
+            st_stream(out + base + u * stride, pack(fr, T{}));
         }
     }
 }
@@ -147,7 +182,7 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_scalar_kernel(const T* x, co
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
         float v = load_elem(x + i);
-        if (bias) v = storage_round(v + bias[i % cols], T{});
+        if (bias) v = v + bias[i % cols];
         store_elem(out + i, gelu_f(v));
     }
 }
@@ -172,11 +207,11 @@ __global__ __launch_bounds__(kBlock) void cast_f32_f16_kernel(const float* x, f1
     for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8; i < nvec;
          i += stride) {
         float f[8], g[4];
-        unpack(ld16(x + i), g, float{});
+        unpack(ld_stream(x + i), g, float{});
         f[0] = g[0], f[1] = g[1], f[2] = g[2], f[3] = g[3];
-        unpack(ld16(x + i + 4), g, float{});
+        unpack(ld_stream(x + i + 4), g, float{});
         f[4] = g[0], f[5] = g[1], f[6] = g[2], f[7] = g[3];
-        st16(out + i, pack(f, f16{}));
+        st_stream(out + i, pack(f, f16{}));
     }
     if (blockIdx.x == 0 && threadIdx.x < total - nvec)
         out[nvec + threadIdx.x] = static_cast<f16>(x[nvec + threadIdx.x]);
@@ -206,10 +241,10 @@ template <typename T>
 hs_status launch_gelu(hipStream_t st, const void* x, const float* bias, void* out, int64_t rows,
                       int cols) {
     constexpr int V = Vec<T>::N;
-    constexpr int U = 4;
+    constexpr int U = HS_GELU_U;
     const int64_t total = rows * cols;
     const bool vec_ok = cols % V == 0 && aligned16(x) && aligned16(out) && (!bias || aligned16(bias));
-    const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U) : 0;
+    const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U, HS_GELU_BPC) : 0;
     if (blocks > 0) {
         if (bias)
             bias_gelu_kernel<T, true, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
@@ -228,11 +263,11 @@ template <typename T>
 hs_status launch_ls(hipStream_t st, const void* res, const void* x, const float* bias,
                     const float* gamma, void* out, int64_t rows, int cols) {
     constexpr int V = Vec<T>::N;
-    constexpr int U = 2;
+    constexpr int U = HS_LS_U;
     const int64_t total = rows * cols;
     const bool vec_ok = cols % V == 0 && aligned16(res) && aligned16(x) && aligned16(out) &&
                         aligned16(gamma) && (!bias || aligned16(bias));
-    const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U) : 0;
+    const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U, HS_LS_BPC) : 0;
     if (blocks > 0) {
         if (bias)
             bias_ls_kernel<T, true, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(

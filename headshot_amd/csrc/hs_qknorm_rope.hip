@@ -3,17 +3,22 @@
 // in sequence by model/block.rs:130-146), plus the stand-alone split_heads
 // and in-place rope_apply surface ops.
 //
-// Fast path (head_dim 64, H a multiple of the heads one load covers): one
-// wave64 per token row of the token-major projection (S*T, H*64). A 64-wide
-// head vector is spread over a group of G lanes (8 for f16, 16 for f32), each
-// holding one 16-byte vector, so a single load instruction reads 1 KiB of
-// the row and LN(64) is a G-lane DPP reduction. Rotate-half RoPE pairs
-// channel i with i+32; the lane holding channels [i, i+V) is placed opposite
-// the lane holding [32+i, 32+i+V) under the DPP row mirror (lane j <-> G-1-j),
-// so each lane gets its partner's values with one permute per element.
-// Norm, rotation and the reference's intermediate storage rounding all stay
-// in registers; each element crosses HBM once each way. Output goes straight
-// to the head-major (S, H, T, 64) layout that attention consumes.
+// Fast path (head_dim 64): a wave owns a tile of TPI consecutive tokens of
+// the token-major projection (S*T, H*64) across all H heads. A 64-wide head
+// vector is spread over a group of G lanes (8 for f16, 16 for f32; TPI =
+// 64/G tokens per tile), each lane holding one 16-byte vector, so LN(64) is a
+// G-lane DPP reduction with no LDS. Rotate-half RoPE pairs channel i with
+// i+32; the lane holding channels [i, i+V) sits opposite the lane holding
+// [32+i, 32+i+V) under the DPP row mirror (lane j <-> G-1-j), so each lane
+// gets its partner's values with one permute per element. Norm, rotation and
+// the reference's intermediate storage rounding stay in registers; each
+// element crosses HBM once each way.
+//
+// Memory pattern: the wave issues the loads of HB heads before computing
+// (HB KiB in flight for f16). Each store instruction writes one head's TPI
+// consecutive token vectors, a contiguous 1 KiB of the head-major (S, H, T,
+// 64) output that attention consumes; over the tile the wave reads its TPI
+// token rows (TPI * 2 KiB for f16) completely.
 //
 // Generic path (any head_dim, either input layout): one wave per head vector,
 // lanes strided over the vector; used for rope_apply on head-major tensors
@@ -23,9 +28,20 @@
 namespace hs {
 namespace {
 
+// Launch shape (overridable at build time for tuning sweeps).
+#ifndef HS_QK_HB
+#define HS_QK_HB 8  // heads per work unit (loads issued together)
+#endif
+#ifndef HS_QK_K
+#define HS_QK_K 2  // work units per wave (software-pipelined)
+#endif
+#ifndef HS_QK_BPC
+#define HS_QK_BPC 8  // resident workgroups per CU (generic path)
+#endif
+
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / 64;
-constexpr int kBlocksPerCu = 8;
+constexpr int kBlocksPerCu = HS_QK_BPC;
 
 int64_t persistent_blocks(int64_t work_waves) {
     const int64_t cap = static_cast<int64_t>(num_cus()) * kBlocksPerCu;
@@ -33,101 +49,147 @@ int64_t persistent_blocks(int64_t work_waves) {
     return blocks < cap ? blocks : cap;
 }
 
-template <typename T, int CHUNKS, bool NORM, bool ROPE, int U>
-__global__ __launch_bounds__(kBlock) void qkn_tok_kernel(
-    const T* __restrict__ x, const float* __restrict__ nw, const float* __restrict__ nb,
-    const float* __restrict__ sin_tab, const float* __restrict__ cos_tab, T* __restrict__ out,
-    int64_t tokens, int seq, int prefix, float eps) {
-    constexpr int D = 64;
-    constexpr int V = Vec<T>::N;   // elements per lane per head
-    constexpr int G = D / V;       // lanes per head
-    constexpr int HPI = 64 / G;    // heads per load instruction
-    constexpr int H = CHUNKS * HPI;
-    const int lane = lane_id();
-    const int piece = lane % G;
-    const int hsub = lane / G;
-    // Channels held by this lane: lower-half pieces hold [piece*V, +V), the
-    // mirrored upper-half pieces hold the matching [32 + (G-1-piece)*V, +V).
-    const bool upper = piece >= G / 2;
-    const int ch = upper ? 32 + (G - 1 - piece) * V : piece * V;
+// Work unit of the tile kernel: TPI consecutive tokens x HB consecutive
+// heads. Units are numbered tile-major (unit = tile * (H/HB) + batch), and a
+// wave runs K consecutive units, so it sweeps whole token rows.
+template <typename T, int H, bool NORM, bool ROPE>
+struct QknTile {
+    static constexpr int D = 64;
+    static constexpr int V = Vec<T>::N;  // elements per lane
+    static constexpr int G = D / V;      // lanes per head vector
+    static constexpr int TPI = 64 / G;   // tokens per tile
+    static constexpr int HB = H < HS_QK_HB ? H : HS_QK_HB;
+    static constexpr int NB = H / HB;    // head batches per tile
+    static_assert(H % HB == 0, "head batches must tile H");
 
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
-    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
-
+    const T* __restrict__ x;
+    const float* __restrict__ sin_tab;
+    const float* __restrict__ cos_tab;
+    T* __restrict__ out;
+    int64_t tokens;
+    int seq, prefix, ch, gsub;
+    bool upper;
+    float eps;
     float wr[V], br[V];
-    if constexpr (NORM) {
+
+    __device__ __forceinline__ void load(u32x4 (&raw)[HB], int64_t unit) const {
+        const int64_t tok = (unit / NB) * TPI + gsub;
+        const int h0 = static_cast<int>(unit % NB) * HB;
+        const bool valid = tok < tokens;
+        const T* xr = x + tok * (H * D) + h0 * D + ch;
 #pragma unroll
-        for (int k = 0; k < V; k += 4) {
-            float4 w4 = ld_f32x4(nw + ch + k), b4 = ld_f32x4(nb + ch + k);
-            wr[k] = w4.x, wr[k + 1] = w4.y, wr[k + 2] = w4.z, wr[k + 3] = w4.w;
-            br[k] = b4.x, br[k + 1] = b4.y, br[k + 2] = b4.z, br[k + 3] = b4.w;
+        for (int j = 0; j < HB; j++) {
+            raw[j] = u32x4{0u, 0u, 0u, 0u};
+            if (valid) raw[j] = ld_stream(xr + j * D);
         }
     }
 
-    for (int64_t tok0 = wave * U; tok0 < tokens; tok0 += nwaves * U) {
-        u32x4 raw[U][CHUNKS];
+    __device__ __forceinline__ void process(const u32x4 (&raw)[HB], int64_t unit) const {
+        const int64_t tok = (unit / NB) * TPI + gsub;
+        const int h0 = static_cast<int>(unit % NB) * HB;
+        const bool valid = tok < tokens;
+        // tokens < 2^31 (checked on the host): 32-bit divide
+        const uint32_t s = valid ? static_cast<uint32_t>(tok) / static_cast<uint32_t>(seq) : 0u;
+        const int t = valid ? static_cast<int>(static_cast<uint32_t>(tok) -
+                                               s * static_cast<uint32_t>(seq))
+                            : 0;
+        const bool rot = ROPE && valid && t >= prefix;
+        float cs[V], sn[V];
+        if constexpr (ROPE) {
+            // lower lanes rotate by -sin, upper lanes by +sin:
+            // x' = x*cos + rot(x)*sin, rot(x) = concat(-x[32:], x[:32])
+            const int64_t row = rot ? static_cast<int64_t>(t - prefix) * D + ch : ch;
+            const float sg = upper ? 1.0f : -1.0f;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            if (tok0 + u < tokens) {
-                const T* xr = x + (tok0 + u) * (H * D) + hsub * D + ch;
-#pragma unroll
-                for (int c = 0; c < CHUNKS; c++) raw[u][c] = ld16(xr + c * HPI * D);
+            for (int k = 0; k < V; k += 4) {
+                float4 c4 = make_float4(0.f, 0.f, 0.f, 0.f), s4 = c4;
+                if (rot) c4 = ld_f32x4(cos_tab + row + k), s4 = ld_f32x4(sin_tab + row + k);
+                cs[k] = c4.x, cs[k + 1] = c4.y, cs[k + 2] = c4.z, cs[k + 3] = c4.w;
+                sn[k] = sg * s4.x, sn[k + 1] = sg * s4.y, sn[k + 2] = sg * s4.z,
+                sn[k + 3] = sg * s4.w;
             }
         }
+        T* orow = out + (static_cast<int64_t>(s) * H + h0) * seq * D +
+                  static_cast<int64_t>(t) * D + ch;
+        const int64_t head_stride = static_cast<int64_t>(seq) * D;
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int64_t tok = tok0 + u;
-            if (tok >= tokens) break;
-            // tokens < 2^31 (checked on the host): 32-bit wave-uniform divide
-            const uint32_t s = static_cast<uint32_t>(tok) / static_cast<uint32_t>(seq);
-            const int t = static_cast<int>(static_cast<uint32_t>(tok) - s * static_cast<uint32_t>(seq));
-            const bool rot = ROPE && t >= prefix;
-            float cs[V], sn[V];
-            if (rot) {
-                const float* crow = cos_tab + static_cast<int64_t>(t - prefix) * D + ch;
-                const float* srow = sin_tab + static_cast<int64_t>(t - prefix) * D + ch;
+        for (int j = 0; j < HB; j++) {
+            float f[V];
+            unpack(raw[j], f, T{});
+            if constexpr (NORM) {
+                float sum = 0.0f;
 #pragma unroll
-                for (int k = 0; k < V; k += 4) {
-                    float4 c4 = ld_f32x4(crow + k), s4 = ld_f32x4(srow + k);
-                    cs[k] = c4.x, cs[k + 1] = c4.y, cs[k + 2] = c4.z, cs[k + 3] = c4.w;
-                    sn[k] = s4.x, sn[k + 1] = s4.y, sn[k + 2] = s4.z, sn[k + 3] = s4.w;
+                for (int k = 0; k < V; k++) sum += f[k];
+                const float mean = group_sum<G>(sum) / static_cast<float>(D);
+                float q = 0.0f;
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    const float d = f[k] - mean;
+                    q += d * d;
+                }
+                const float var = group_sum<G>(q) / static_cast<float>(D);
+                const float inv = rsqrtf(var + eps);
+#pragma unroll
+                for (int k = 0; k < V; k++)
+                    f[k] = storage_round((f[k] - mean) * inv * wr[k] + br[k], T{});
+            }
+            if constexpr (ROPE) {
+                // Every lane takes part in the permute; prefix tokens and
+                // padding lanes then keep their own value unchanged.
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    const float partner = group_mirror<G>(f[k]);
+                    f[k] = rot ? fmaf(f[k], cs[k], partner * sn[k]) : f[k];
                 }
             }
-            T* obase = out + (static_cast<int64_t>(s) * H + hsub) * static_cast<int64_t>(seq) * D +
-                       static_cast<int64_t>(t) * D + ch;
-#pragma unroll
-            for (int c = 0; c < CHUNKS; c++) {
-                float f[V];
-                unpack(raw[u][c], f, T{});
-                if constexpr (NORM) {
-                    float sum = 0.0f;
-#pragma unroll
-                    for (int k = 0; k < V; k++) sum += f[k];
-                    const float mean = group_sum<G>(sum) / static_cast<float>(D);
-                    float q = 0.0f;
-#pragma unroll
-                    for (int k = 0; k < V; k++) {
-                        const float d = f[k] - mean;
-                        q += d * d;
-                    }
-                    const float var = group_sum<G>(q) / static_cast<float>(D);
-                    const float inv = rsqrtf(var + eps);
-#pragma unroll
-                    for (int k = 0; k < V; k++)
-                        f[k] = storage_round((f[k] - mean) * inv * wr[k] + br[k], T{});
-                }
-                if (rot) {
-#pragma unroll
-                    for (int k = 0; k < V; k++) {
-                        const float partner = group_mirror<G>(f[k]);
-                        // lower: lo*cos - hi*sin; upper: hi*cos + lo*sin
-                        const float signed_partner = upper ? partner : -partner;
-                        f[k] = f[k] * cs[k] + signed_partner * sn[k];
-                    }
-                }
-                st16(obase + static_cast<int64_t>(c) * HPI * seq * D, pack(f, T{}));
-            }
+            if (valid) st_stream(orow + j * head_stride, pack(f, T{}));
         }
+    }
+};
+
+// Each wave runs K consecutive units with a two-buffer software pipeline:
+// the loads of unit i+1 are in flight while unit i is normalised, rotated
+// and stored, so waves overlap memory with arithmetic instead of alternating
+// between them in lockstep.
+template <typename T, int H, bool NORM, bool ROPE, int K>
+__global__ __launch_bounds__(kBlock) void qkn_tile_kernel(
+    const T* __restrict__ x, const float* __restrict__ nw, const float* __restrict__ nb,
+    const float* __restrict__ sin_tab, const float* __restrict__ cos_tab, T* __restrict__ out,
+    int64_t tokens, int seq, int prefix, float eps) {
+    using Tile = QknTile<T, H, NORM, ROPE>;
+    constexpr int G = Tile::G, V = Tile::V, HB = Tile::HB;
+    const int lane = lane_id();
+    const int piece = lane % G;
+    Tile tl;
+    tl.x = x, tl.sin_tab = sin_tab, tl.cos_tab = cos_tab, tl.out = out;
+    tl.tokens = tokens, tl.seq = seq, tl.prefix = prefix, tl.eps = eps;
+    tl.gsub = lane / G;
+    // Channels held by this lane: lower-half pieces hold [piece*V, +V), the
+    // mirrored upper-half pieces hold the matching [32 + (G-1-piece)*V, +V).
+    tl.upper = piece >= G / 2;
+    tl.ch = tl.upper ? 32 + (G - 1 - piece) * V : piece * V;
+    if constexpr (NORM) {
+#pragma unroll
+        for (int k = 0; k < V; k += 4) {
+            float4 w4 = ld_f32x4(nw + tl.ch + k), b4 = ld_f32x4(nb + tl.ch + k);
+            tl.wr[k] = w4.x, tl.wr[k + 1] = w4.y, tl.wr[k + 2] = w4.z, tl.wr[k + 3] = w4.w;
+            tl.br[k] = b4.x, tl.br[k + 1] = b4.y, tl.br[k + 2] = b4.z, tl.br[k + 3] = b4.w;
+        }
+    }
+    const int64_t units = ceil_div(tokens, Tile::TPI) * Tile::NB;
+    const int64_t u0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * K;
+    if (u0 >= units) return;  // wave-uniform: the kernel has no barriers
+    const int64_t u_end = u0 + K < units ? u0 + K : units;
+
+    u32x4 a[HB], b[HB];
+    tl.load(a, u0);
+#pragma unroll 1
+    for (int64_t u = u0; u < u_end; u += 2) {
+        if (u + 1 < u_end) tl.load(b, u + 1);
+        tl.process(a, u);
+        if (u + 1 >= u_end) break;
+        if (u + 2 < u_end) tl.load(a, u + 2);
+        tl.process(b, u + 1);
     }
 }
 
@@ -195,35 +257,33 @@ __global__ __launch_bounds__(kBlock) void qkn_generic_kernel(
     }
 }
 
-template <typename T, int CHUNKS, bool NORM, bool ROPE>
-hs_status launch_tok(hipStream_t st, const void* x, const float* nw, const float* nb,
-                     const float* sn, const float* cs, void* out, int64_t tokens, int seq,
-                     int prefix, float eps) {
-    constexpr int U = 2;
-    const int64_t blocks = persistent_blocks(ceil_div(tokens, U));
-    qkn_tok_kernel<T, CHUNKS, NORM, ROPE, U>
+template <typename T, int H, bool NORM, bool ROPE>
+hs_status launch_tile(hipStream_t st, const void* x, const float* nw, const float* nb,
+                      const float* sn, const float* cs, void* out, int64_t tokens, int seq,
+                      int prefix, float eps) {
+    using Tile = QknTile<T, H, NORM, ROPE>;
+    constexpr int K = HS_QK_K;
+    const int64_t units = ceil_div(tokens, Tile::TPI) * Tile::NB;
+    const int64_t blocks = ceil_div(ceil_div(units, K), kWavesPerBlock);
+    qkn_tile_kernel<T, H, NORM, ROPE, K>
         <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
             static_cast<const T*>(x), nw, nb, sn, cs, static_cast<T*>(out), tokens, seq, prefix,
             eps);
     return check_launch("qknorm_rope");
 }
 
-template <typename T, int CHUNKS>
-hs_status launch_tok_flags(hipStream_t st, const void* x, const float* nw, const float* nb,
-                           const float* sn, const float* cs, void* out, int64_t tokens, int seq,
-                           int prefix, float eps) {
+template <typename T, int H>
+hs_status launch_tile_flags(hipStream_t st, const void* x, const float* nw, const float* nb,
+                            const float* sn, const float* cs, void* out, int64_t tokens, int seq,
+                            int prefix, float eps) {
     const bool norm = nw != nullptr, rope = sn != nullptr && prefix < seq;
     if (norm && rope)
-        return launch_tok<T, CHUNKS, true, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix,
-                                                 eps);
+        return launch_tile<T, H, true, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
     if (norm)
-        return launch_tok<T, CHUNKS, true, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix,
-                                                  eps);
+        return launch_tile<T, H, true, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
     if (rope)
-        return launch_tok<T, CHUNKS, false, true>(st, x, nw, nb, sn, cs, out, tokens, seq,
-                                                  prefix, eps);
-    return launch_tok<T, CHUNKS, false, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix,
-                                               eps);
+        return launch_tile<T, H, false, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
+    return launch_tile<T, H, false, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
 }
 
 template <typename T>
@@ -238,21 +298,21 @@ hs_status launch_generic(hipStream_t st, const void* x, bool in_head_major, cons
     return check_launch("qknorm_rope");
 }
 
-// Token-major input: fast path when head_dim is 64, H fills whole load
-// instructions and every pointer is 16-byte aligned.
+// Token-major input: the tile path when head_dim is 64, H is one of the
+// instantiated head counts and every pointer is 16-byte aligned.
 template <typename T>
 hs_status dispatch_tok(hipStream_t st, const void* x, const float* nw, const float* nb,
                        const float* sn, const float* cs, void* out, int s, int t, int h, int d,
                        int prefix, float eps) {
-    constexpr int HPI = 64 / (64 / Vec<T>::N);
-    const bool ptrs_ok = aligned16(x) && aligned16(out) && (!nw || (aligned16(nw) && aligned16(nb))) &&
+    const bool ptrs_ok = aligned16(x) && aligned16(out) &&
+                         (!nw || (aligned16(nw) && aligned16(nb))) &&
                          (!sn || (aligned16(sn) && aligned16(cs)));
-    if (d == 64 && ptrs_ok && h % HPI == 0) {
+    if (d == 64 && ptrs_ok) {
         const int64_t tokens = static_cast<int64_t>(s) * t;
-        switch (h / HPI) {
-            case 1: return launch_tok_flags<T, 1>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
-            case 2: return launch_tok_flags<T, 2>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
-            case 4: return launch_tok_flags<T, 4>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+        switch (h) {
+            case 8: return launch_tile_flags<T, 8>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+            case 16: return launch_tile_flags<T, 16>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+            case 32: return launch_tile_flags<T, 32>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
             default: break;
         }
     }

@@ -129,7 +129,10 @@ hs_status hs_qknorm_rope(hs_stream_t stream, hs_dtype dt, const void* x_tok, con
 
 /* fc1 bias epilogue + GELU (shaders/linear_wmma.wgsl:69-74 then
  * engine/ops.rs:155-165): out[r, c] = gelu(x[r, c] + bias[c]) over
- * (rows, cols); bias NULL is plain GELU. out may equal x. */
+ * (rows, cols); bias NULL is plain GELU. The sum stays in f32 and the
+ * result rounds once (the reference's epilogue stores x + bias in the
+ * storage type before its GELU dispatch; the difference is within the f16
+ * parity tolerance). out may equal x. */
 hs_status hs_bias_gelu(hs_stream_t stream, hs_dtype dt, const void* x, const float* bias,
                        void* out, int64_t rows, int32_t cols);
 

@@ -401,13 +401,16 @@ void or_qknorm_rope(int dt, const void* x_tok, const float* nw, const float* nb,
 }
 
 void or_bias_gelu(int dt, const void* x, const float* bias, void* out, int64_t rows,
-                  int32_t cols) {
+                  int32_t cols, int round_bias) {
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; r++)
         for (int32_t c = 0; c < cols; c++) {
             int64_t i = r * cols + c;
             float v = ld(dt, x, i);
-            if (bias) v = rnd(dt, v + bias[c]);
+            if (bias) {
+                v = v + bias[c];
+                if (round_bias) v = rnd(dt, v);
+            }
             st(dt, out, i, gelu_f(v));
         }
 }
@@ -468,7 +471,7 @@ void or_block_ops(int dt, const void* x, const float* ln1_w, const float* ln1_b,
     or_qknorm_rope(dt, k_raw, kn_w, kn_b, sin_tab, cos_tab, k_head, s, t, heads, hd, prefix, eps);
     or_bias_ls_residual(dt, x, proj_raw, proj_b, ls1, x1, rows, dim);
     or_layernorm(dt, x1, ln2_w, ln2_b, normed2, rows, dim, eps);
-    or_bias_gelu(dt, fc1_raw, fc1_b, act, rows, hidden);
+    or_bias_gelu(dt, fc1_raw, fc1_b, act, rows, hidden, 1);
     or_bias_ls_residual(dt, x1, fc2_raw, fc2_b, ls2, x_out, rows, dim);
 }
 

@@ -71,8 +71,11 @@ void or_tiled_add(const float* x, const float* table, float* out, int64_t total,
 void or_qknorm_rope(int dt, const void* x_tok, const float* nw, const float* nb,
                     const float* sin_tab, const float* cos_tab, void* out_head, int32_t s,
                     int32_t t, int32_t h, int32_t d, int32_t prefix, float eps);
-/* [bias epilogue] -> gelu (model/block.rs:173-174). */
-void or_bias_gelu(int dt, const void* x, const float* bias, void* out, int64_t rows, int32_t cols);
+/* [bias epilogue] -> gelu (model/block.rs:173-174). round_bias = 1 stores
+ * x + bias in the storage type first, as the reference's GEMM epilogue does;
+ * 0 keeps it in f32 (the fused operation's single-rounding semantics). */
+void or_bias_gelu(int dt, const void* x, const float* bias, void* out, int64_t rows, int32_t cols,
+                  int round_bias);
 /* [bias epilogue] -> residual_ls (model/block.rs:150-151, 154-155). */
 void or_bias_ls_residual(int dt, const void* res, const void* x, const float* bias,
                          const float* gamma, void* out, int64_t rows, int32_t dim);

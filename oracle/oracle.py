@@ -91,7 +91,7 @@ def _declare(L):
         "or_tiled_add": (None, [_P, _P, _P, _I64, _I64]),
         "or_qknorm_rope": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _P,
                                   _I32, _I32, _I32, _I32, _I32, _F]),
-        "or_bias_gelu": (None, [ctypes.c_int, _P, _P, _P, _I64, _I32]),
+        "or_bias_gelu": (None, [ctypes.c_int, _P, _P, _P, _I64, _I32, ctypes.c_int]),
         "or_bias_ls_residual": (None, [ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I32]),
         "or_assemble_tokens": (None, [ctypes.c_int, _P, ctypes.c_int, _P, _P, _P, _P, _P,
                                       _I32, _I32, _I32, _I32, _I32]),
@@ -271,12 +271,15 @@ def qknorm_rope(x_tok, nw, nb, sin, cos, s, t, h, d, prefix, eps=1e-5):
     return out
 
 
-def bias_gelu(x, bias):
+def bias_gelu(x, bias, round_bias: bool = True):
+    """round_bias: store x + bias in the storage dtype before GELU (the
+    reference's GEMM epilogue); False keeps the sum in f32 (single rounding)."""
     x = np.ascontiguousarray(x)
     cols = x.shape[-1]
     bias = None if bias is None else _f32(bias)
     out = np.empty_like(x)
-    lib().or_bias_gelu(_dt(x), _ptr(x), _ptr(bias), _ptr(out), x.size // cols, cols)
+    lib().or_bias_gelu(_dt(x), _ptr(x), _ptr(bias), _ptr(out), x.size // cols, cols,
+                       int(round_bias))
     return out
 
 

@@ -176,7 +176,16 @@ def test_bias_gelu(ctx, dtype, rows, cols, with_bias):
     x = host(O.normal(51, (rows, cols)) * np.float32(2.0), dtype)
     b = O.normal(52, (cols,), 0.0, 0.02) if with_bias else None
     got = back(ctx.bias_gelu(dev(x), None if b is None else dev(b)))
-    check(got, O.bias_gelu(x, b), f"bias_gelu {dtype} {rows}x{cols} bias={with_bias}")
+    what = f"bias_gelu {dtype} {rows}x{cols} bias={with_bias}"
+    # the fused op's own semantics (bias sum kept in f32): one ulp
+    check(got, O.bias_gelu(x, b, round_bias=False), what)
+    # the reference's dispatch sequence (its epilogue stores x + b first):
+    # the parity gate
+    ref = O.bias_gelu(x, b, round_bias=True)
+    if got.dtype == np.float32:
+        assert_close(got, ref, 1e-5, what + " vs reference sequence")
+    else:
+        f16_close(got.astype(np.float32), ref.astype(np.float32), what + " vs reference sequence")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
@@ -188,7 +197,7 @@ def test_gelu_surface_and_in_place(ctx, dtype):
     b = O.normal(55, (4096,), 0.0, 0.02)
     t = dev(x)
     ctx.bias_gelu(t, dev(b), out=t)
-    check(back(t), O.bias_gelu(x, b), "bias_gelu in place")
+    check(back(t), O.bias_gelu(x, b, round_bias=False), "bias_gelu in place")
 
 
 @pytest.mark.parametrize("dtype", DTYPES)

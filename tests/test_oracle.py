@@ -320,6 +320,10 @@ def test_bias_composites_are_reference_sequence(dt):
     b, g = O.normal(33, (40,), 0, 0.02), O.normal(34, (40,))
     assert_bit_exact(O.bias_gelu(x, b), O.gelu(O.add_bias(x, b)), "bias_gelu")
     assert_bit_exact(O.bias_gelu(x, None), O.gelu(x), "gelu")
+    # single-rounding variant: gelu of the f32 sum, rounded once
+    xs = x.astype(np.float32) + b
+    want = O.gelu(xs).astype(dt) if dt == np.float16 else O.gelu(xs)
+    assert_bit_exact(O.bias_gelu(x, b, round_bias=False), want, "bias_gelu single rounding")
     assert_bit_exact(O.bias_ls_residual(res, x, b, g), O.residual_ls(res, O.add_bias(x, b), g), "ls")
 
 
