@@ -75,106 +75,26 @@ def parse():
 
 
 class Pass:
-    """Buffers and the launch sequence of one aggregator fused-op pass."""
+    """One aggregator fused-op pass (headshot_amd.aggregator.FusedOpPass)
+    plus its algorithmic byte counts."""
 
     def __init__(self, ctx, frames: int, dtype):
         import torch
-        from headshot_amd import rope
 
+        from headshot_amd.aggregator import FusedOpPass
+
+        self.fp = fp = FusedOpPass(ctx, frames, grid=GRID, n_reg=N_REG, n_frame=N_FRAME_BLOCKS,
+                                   n_global=N_GLOBAL_BLOCKS, dtype=dtype, eps=EPS)
         self.ctx, self.frames, self.dtype = ctx, frames, dtype
-        dev = ctx.device
-        p = GRID[0] * GRID[1]
-        self.p, self.t = p, p + 1 + N_REG
-        self.rows = rows = frames * self.t
-        g = torch.Generator(device=dev)
-        g.manual_seed(42)
-
-        def normal(shape, mean=0.0, std=1.0, dt=torch.float32):
-            return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std
-                    + mean).to(dt)
-
-        # stage inputs (DINO patch tokens are f32)
-        self.patches = normal((frames * p, DIM))
-        self.pos = normal((p, DIM), 0.0, 0.02)
-        self.patch_bias = normal((DIM,), 0.0, 0.02)
-        self.cam = normal((2, DIM), dt=dtype)
-        self.reg = normal((2 * N_REG, DIM), dt=dtype)
-        # synthetic GEMM outputs (raw: their biases are applied by the fused ops)
-        self.q_raw = normal((rows, DIM), dt=dtype)
-        self.k_raw = normal((rows, DIM), dt=dtype)
-        self.proj_raw = normal((rows, DIM), dt=dtype)
-        self.fc1_raw = normal((rows, HIDDEN), dt=dtype)
-        self.fc2_raw = normal((rows, DIM), dt=dtype)
-        # outputs / residual stream
-        e = lambda *s: torch.empty(s, device=dev, dtype=dtype)  # noqa: E731
-        self.x = [e(rows, DIM), e(rows, DIM)]
-        self.x1 = e(rows, DIM)
-        self.normed = e(rows, DIM)
-        self.normed2 = e(rows, DIM)
-        self.q_head = e(rows * DIM)
-        self.k_head = e(rows * DIM)
-        self.act = e(rows, HIDDEN)
-        sin, cos = rope.tables(rope.periods(), *GRID)
-        self.sin = torch.from_numpy(sin).to(dev)
-        self.cos = torch.from_numpy(cos).to(dev)
-        # per-block parameters (f32), random init as in the reference configs
-        self.blocks = []
-        for _ in range(N_FRAME_BLOCKS + N_GLOBAL_BLOCKS):
-            self.blocks.append(dict(
-                ln1=(normal((DIM,), 1.0, 0.02), normal((DIM,), 0.0, 0.02)),
-                ln2=(normal((DIM,), 1.0, 0.02), normal((DIM,), 0.0, 0.02)),
-                qn=(normal((HEAD_DIM,), 1.0, 0.02), normal((HEAD_DIM,), 0.0, 0.02)),
-                kn=(normal((HEAD_DIM,), 1.0, 0.02), normal((HEAD_DIM,), 0.0, 0.02)),
-                proj_b=normal((DIM,), 0.0, 0.02), ls1=torch.full((DIM,), 1e-5, device=dev),
-                fc1_b=normal((HIDDEN,), 0.0, 0.02), fc2_b=normal((DIM,), 0.0, 0.02),
-                ls2=torch.full((DIM,), 1e-5, device=dev)))
+        self.p, self.t, self.rows = fp.p, fp.t, fp.rows
+        self.seq = fp.seq
         esz = 2 if dtype == torch.float16 else 4
-        self.bytes = op_bytes(rows, esz, frames * p, p)
-        self.launches = {"assemble": 1}
-        for k in OPS[1:]:
-            self.launches[k] = len(self.blocks) * (1 if k == "bias_gelu" else 2)
+        self.bytes = op_bytes(self.rows, esz, frames * fp.p, fp.p)
+        self.launches = fp.launches()
         self.pass_bytes = sum(self.bytes[k] * self.launches[k] for k in OPS)
-        self.seq = self._launch_sequence()
-
-    def _launch_sequence(self):
-        """[(op, thunk)]: each thunk re-issues one validated C-ABI call on the
-        current stream (the HipContext checks ran once, here)."""
-        c = self.ctx
-        seq = []
-
-        def rec(op, fn, *args, **kw):
-            # run once through HipContext (validation + first launch), then
-            # keep the raw call for the timed loops
-            fn(*args, **kw)
-            seq.append((op, c.last_launch))
-
-        x = self.x[0]
-        rec("assemble", c.assemble_tokens, self.patches, self.frames, self.p, self.cam, self.reg,
-            patch_bias=self.patch_bias, pos=self.pos, out_dtype=self.dtype, out=x)
-        for i, b in enumerate(self.blocks):
-            frame_block = i % 2 == 0  # frame / global alternate (model/trunk.rs:92-143)
-            if frame_block:
-                s, t, rp = self.frames, self.t, (self.sin, self.cos, PREFIX)
-            else:
-                s, t, rp = 1, self.rows, None
-            x_out = self.x[1] if x is self.x[0] else self.x[0]
-            rec("layernorm", c.layernorm, x, *b["ln1"], eps=EPS, out=self.normed)
-            rec("qknorm_rope", c.qknorm_rope, self.q_raw, s, t, HEADS, HEAD_DIM, norm=b["qn"],
-                rope=rp, eps=EPS, out=self.q_head)
-            rec("qknorm_rope", c.qknorm_rope, self.k_raw, s, t, HEADS, HEAD_DIM, norm=b["kn"],
-                rope=rp, eps=EPS, out=self.k_head)
-            rec("bias_ls_residual", c.bias_ls_residual, x, self.proj_raw, b["ls1"], b["proj_b"],
-                out=self.x1)
-            rec("layernorm", c.layernorm, self.x1, *b["ln2"], eps=EPS, out=self.normed2)
-            rec("bias_gelu", c.bias_gelu, self.fc1_raw, b["fc1_b"], out=self.act)
-            rec("bias_ls_residual", c.bias_ls_residual, self.x1, self.fc2_raw, b["ls2"],
-                b["fc2_b"], out=x_out)
-            x = x_out
-        return seq
 
     def run(self):
-        for _, thunk in self.seq:
-            thunk()
+        self.fp.run()
 
 
 def per_op_times(bench: Pass, passes: int) -> dict:
@@ -215,15 +135,16 @@ def cpu_baseline(bench: Pass, target_s: float):
     dt = O.F16 if bench.dtype == torch.float16 else O.F32
     h = lambda t: t.cpu().numpy()  # noqa: E731
     rows, frames = bench.rows, bench.frames
-    x = h(bench.x[0])
-    q, k = h(bench.q_raw), h(bench.k_raw)
-    proj, fc1, fc2 = h(bench.proj_raw), h(bench.fc1_raw), h(bench.fc2_raw)
-    sin, cos = h(bench.sin), h(bench.cos)
+    fp = bench.fp
+    x = h(fp.x[0])
+    q, k = h(fp.io.q_raw), h(fp.io.k_raw)
+    proj, fc1, fc2 = h(fp.io.proj_raw), h(fp.io.fc1_raw), h(fp.io.fc2_raw)
+    sin, cos = h(fp.sin), h(fp.cos)
     out = dict(normed=np.empty_like(x), q_head=np.empty_like(q), k_head=np.empty_like(k),
                x1=np.empty_like(x), normed2=np.empty_like(x), act=np.empty_like(fc1),
                x_out=np.empty_like(x))
-    patches, pos, pb = h(bench.patches), h(bench.pos), h(bench.patch_bias)
-    cam, reg = h(bench.cam), h(bench.reg)
+    patches, pos, pb = h(fp.patches), h(fp.pos), h(fp.patch_bias)
+    cam, reg = h(fp.cam), h(fp.reg)
 
     done_bytes = 0
     blocks_done = 0
@@ -232,9 +153,10 @@ def cpu_baseline(bench: Pass, target_s: float):
     done_bytes += bench.bytes["assemble"]
     block_bytes = (2 * bench.bytes["layernorm"] + 2 * bench.bytes["qknorm_rope"]
                    + 2 * bench.bytes["bias_ls_residual"] + bench.bytes["bias_gelu"])
-    for i, b in enumerate(bench.blocks):
-        p = {kk: tuple(h(t) for t in v) if isinstance(v, tuple) else h(v) for kk, v in b.items()}
-        frame_block = i % 2 == 0
+    for kind, b in zip(fp.kinds, fp.blocks):
+        p = {kk: tuple(h(t) for t in v) if isinstance(v, tuple) else h(v)
+             for kk, v in vars(b).items()}
+        frame_block = kind == "frame"
         s, t = (frames, bench.t) if frame_block else (1, rows)
         O.block_ops(dt, x, *p["ln1"], q, k, *p["qn"], *p["kn"],
                     sin if frame_block else None, cos if frame_block else None, PREFIX,

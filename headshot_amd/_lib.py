@@ -78,6 +78,15 @@ def load(path: str = LIB_PATH) -> ctypes.CDLL:
         raise ImportError(
             f"libheadshot_hip.so not found at {path}; build it with "
             "`python -m headshot_amd.build` (there is no fallback path)")
+    # PyTorch ships its own HIP runtime under the same soname
+    # (libamdhip64.so.7). Whichever copy is loaded first serves the whole
+    # process, and stream handles from one runtime instance are meaningless
+    # to another, so torch's copy must be in place before this library
+    # resolves its dependency.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
     lib = ctypes.CDLL(path)
     for name, (res, args) in SIGNATURES.items():
         fn = getattr(lib, name)

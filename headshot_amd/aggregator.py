@@ -1,0 +1,196 @@
+"""The aggregator's per-layer op sequence on HipContext.
+
+``BlockParams`` holds one pre-norm block's f32 parameters and
+``run_block_ops`` issues that block's fused per-layer ops in the order of
+``Block::forward`` (crates/headshot-server/src/model/block.rs:118-159) with
+the GEMMs and attention left to the caller: their raw outputs come in as
+tensors, and the biases of proj/fc1/fc2 are applied by the fused ops.
+
+``FusedOpPass`` lays out every buffer of one aggregator pass (token
+assembly, model/trunk.rs:68-85, then alternating frame and global blocks,
+model/trunk.rs:92-143) and records the launch sequence as re-issuable C-ABI
+calls, so the whole pass can be replayed or captured in a HIP graph.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import rope as _rope
+from .context import HipContext
+
+DIM, HEADS, HEAD_DIM, HIDDEN = 1024, 16, 64, 4096
+
+
+@dataclass
+class BlockParams:
+    ln1: tuple            # (weight, bias) f32 (dim)
+    ln2: tuple
+    qn: tuple | None      # QK-norm (weight, bias) f32 (head_dim), None = no QK-norm
+    kn: tuple | None
+    proj_b: torch.Tensor  # f32 (dim)
+    ls1: torch.Tensor     # LayerScale gamma f32 (dim)
+    fc1_b: torch.Tensor   # f32 (hidden)
+    fc2_b: torch.Tensor   # f32 (dim)
+    ls2: torch.Tensor
+
+    @staticmethod
+    def random(dim: int, hidden: int, head_dim: int, device, generator, qk_norm: bool = True,
+               ls_init: float | None = 1e-5) -> "BlockParams":
+        """Random init of the reference configs: LN gamma ~N(1,.02), beta and
+        biases ~N(0,.02), LayerScale = ls_init (or ~N(0,1) when None)."""
+        def n(shape, mean=0.0, std=1.0):
+            return torch.randn(shape, generator=generator, device=device) * std + mean
+
+        def ls():
+            return torch.full((dim,), ls_init, device=device) if ls_init is not None else n(dim)
+
+        qn = (n(head_dim, 1.0, 0.02), n(head_dim, 0.0, 0.02)) if qk_norm else None
+        kn = (n(head_dim, 1.0, 0.02), n(head_dim, 0.0, 0.02)) if qk_norm else None
+        return BlockParams(ln1=(n(dim, 1.0, 0.02), n(dim, 0.0, 0.02)),
+                           ln2=(n(dim, 1.0, 0.02), n(dim, 0.0, 0.02)), qn=qn, kn=kn,
+                           proj_b=n(dim, 0.0, 0.02), ls1=ls(), fc1_b=n(hidden, 0.0, 0.02),
+                           fc2_b=n(dim, 0.0, 0.02), ls2=ls())
+
+
+@dataclass
+class BlockIO:
+    """Per-block buffers: inputs x and the raw GEMM outputs, plus outputs."""
+    x: torch.Tensor          # (S*T, dim) residual stream in
+    q_raw: torch.Tensor      # (S*T, H*hd) q projection (qkv bias already added)
+    k_raw: torch.Tensor
+    proj_raw: torch.Tensor   # (S*T, dim) attention projection without bias
+    fc1_raw: torch.Tensor    # (S*T, hidden) fc1 output without bias
+    fc2_raw: torch.Tensor    # (S*T, dim) fc2 output without bias
+    normed: torch.Tensor     # LN1 output
+    q_head: torch.Tensor     # (S, H, T, hd)
+    k_head: torch.Tensor
+    x1: torch.Tensor         # residual after attention
+    normed2: torch.Tensor    # LN2 output
+    act: torch.Tensor        # GELU output
+    x_out: torch.Tensor      # block output
+
+    @staticmethod
+    def empty_like_inputs(x, q_raw, k_raw, proj_raw, fc1_raw, fc2_raw) -> "BlockIO":
+        e = torch.empty_like
+        return BlockIO(x, q_raw, k_raw, proj_raw, fc1_raw, fc2_raw, e(x), e(q_raw), e(k_raw),
+                       e(x), e(x), e(fc1_raw), e(x))
+
+
+def run_block_ops(ctx: HipContext, p: BlockParams, io: BlockIO, s: int, t: int, heads: int,
+                  head_dim: int, rope=None, eps: float = 1e-5, record=None) -> None:
+    """One block's per-layer ops (model/block.rs:128-155 minus GEMMs and
+    attention). ``rope`` = (sin, cos, prefix) for frame blocks, None for
+    global blocks (which the trunk runs as one sequence, s=1, t=S*T).
+    ``record(op_name)`` is called after each launch (for launch recording)."""
+    rec = record or (lambda op: None)
+    ctx.layernorm(io.x, *p.ln1, eps=eps, out=io.normed)
+    rec("layernorm")
+    if p.qn is not None or rope is not None:
+        ctx.qknorm_rope(io.q_raw, s, t, heads, head_dim, norm=p.qn, rope=rope, eps=eps,
+                        out=io.q_head)
+        rec("qknorm_rope")
+        ctx.qknorm_rope(io.k_raw, s, t, heads, head_dim, norm=p.kn, rope=rope, eps=eps,
+                        out=io.k_head)
+        rec("qknorm_rope")
+    ctx.bias_ls_residual(io.x, io.proj_raw, p.ls1, p.proj_b, out=io.x1)
+    rec("bias_ls_residual")
+    ctx.layernorm(io.x1, *p.ln2, eps=eps, out=io.normed2)
+    rec("layernorm")
+    ctx.bias_gelu(io.fc1_raw, p.fc1_b, out=io.act)
+    rec("bias_gelu")
+    ctx.bias_ls_residual(io.x1, io.fc2_raw, p.ls2, p.fc2_b, out=io.x_out)
+    rec("bias_ls_residual")
+
+
+class FusedOpPass:
+    """All buffers and the launch sequence of one aggregator fused-op pass:
+    assembly, then ``n_frame`` frame blocks (QK-norm + RoPE, ``prefix``
+    unrotated tokens) alternating with ``n_global`` global blocks (QK-norm,
+    no RoPE). Inputs are synthetic: seeded N(0,1) activations and GEMM
+    outputs, random-init parameters (``BlockParams.random``)."""
+
+    def __init__(self, ctx: HipContext, frames: int, grid=(37, 37), n_reg: int = 4,
+                 n_frame: int = 24, n_global: int = 24, dtype=torch.float16, eps: float = 1e-6,
+                 dim: int = DIM, heads: int = HEADS, hidden: int = HIDDEN, seed: int = 42):
+        self.ctx, self.frames, self.dtype, self.eps = ctx, frames, dtype, eps
+        self.dim, self.heads, self.hidden = dim, heads, hidden
+        self.head_dim = dim // heads
+        dev = ctx.device
+        self.p = grid[0] * grid[1]
+        self.n_reg = n_reg
+        self.prefix = 1 + n_reg
+        self.t = self.p + self.prefix
+        self.rows = rows = frames * self.t
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed)
+
+        def normal(shape, mean=0.0, std=1.0, dt=torch.float32):
+            return (torch.randn(shape, generator=g, device=dev, dtype=torch.float32) * std
+                    + mean).to(dt)
+
+        self.patches = normal((frames * self.p, dim))          # f32 stage input
+        self.pos = normal((self.p, dim), 0.0, 0.02)
+        self.patch_bias = normal((dim,), 0.0, 0.02)
+        self.cam = normal((2, dim), dt=dtype)
+        self.reg = normal((2 * n_reg, dim), dt=dtype)
+        q_raw, k_raw = normal((rows, dim), dt=dtype), normal((rows, dim), dt=dtype)
+        proj_raw, fc2_raw = normal((rows, dim), dt=dtype), normal((rows, dim), dt=dtype)
+        fc1_raw = normal((rows, hidden), dt=dtype)
+        x0 = torch.empty((rows, dim), device=dev, dtype=dtype)
+        x_b = torch.empty_like(x0)
+        io = BlockIO.empty_like_inputs(x0, q_raw, k_raw, proj_raw, fc1_raw, fc2_raw)
+        io.x_out = x_b
+        self.io = io
+        self.x = [x0, x_b]
+        sin, cos = _rope.tables(_rope.periods(), *grid)
+        self.sin = torch.from_numpy(sin).to(dev)
+        self.cos = torch.from_numpy(cos).to(dev)
+        kinds = []
+        for i in range(max(n_frame, n_global)):
+            if i < n_frame:
+                kinds.append("frame")
+            if i < n_global:
+                kinds.append("global")
+        self.kinds = kinds
+        self.blocks = [BlockParams.random(dim, hidden, self.head_dim, dev, g) for _ in kinds]
+        self.seq = self._record()
+
+    def _record(self):
+        """Run the pass once through HipContext (validating every call) and
+        keep each launch as a re-issuable raw call: [(op, thunk)]."""
+        c = self.ctx
+        seq = []
+
+        def rec(op):
+            seq.append((op, c.last_launch))
+
+        io = self.io
+        c.assemble_tokens(self.patches, self.frames, self.p, self.cam, self.reg,
+                          patch_bias=self.patch_bias, pos=self.pos, out_dtype=self.dtype,
+                          out=self.x[0])
+        rec("assemble")
+        x = self.x[0]
+        for kind, p in zip(self.kinds, self.blocks):
+            io.x = x
+            io.x_out = self.x[1] if x is self.x[0] else self.x[0]
+            if kind == "frame":
+                s, t, rp = self.frames, self.t, (self.sin, self.cos, self.prefix)
+            else:
+                s, t, rp = 1, self.rows, None
+            run_block_ops(c, p, io, s, t, self.heads, self.head_dim, rope=rp, eps=self.eps,
+                          record=rec)
+            x = io.x_out
+        self.out = x
+        return seq
+
+    def run(self) -> None:
+        for _, thunk in self.seq:
+            thunk()
+
+    def launches(self) -> dict:
+        counts = {}
+        for op, _ in self.seq:
+            counts[op] = counts.get(op, 0) + 1
+        return counts
