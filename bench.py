@@ -71,6 +71,12 @@ def parse():
     ap.add_argument("--calibrate-copy-mib", type=int, default=512,
                     help="size of one plain torch copy launched before timing (HBM counter "
                          "calibration for rocprofv3 --pmc runs)")
+    ap.add_argument("--summarize", metavar="KERNEL_TRACE_CSV",
+                    help="print a summary of rocprofv3 output for this benchmark instead of "
+                         "running it")
+    ap.add_argument("--pmc-fetch", metavar="CSV", help="counter_collection CSV of a FETCH_SIZE run")
+    ap.add_argument("--pmc-write", metavar="CSV", help="counter_collection CSV of a WRITE_SIZE run")
+    ap.add_argument("--traffic-json", metavar="PATH", help="write per-op HBM bytes here")
     return ap.parse_args()
 
 
@@ -181,8 +187,120 @@ def cpu_baseline(bench: Pass, target_s: float):
     }
 
 
+KERNEL_OPS = {"ln_vec_kernel": "layernorm", "ln_generic_kernel": "layernorm",
+              "qkn_tile_kernel": "qknorm_rope", "qkn_generic_kernel": "qknorm_rope",
+              "bias_ls_kernel": "bias_ls_residual", "bias_gelu_kernel": "bias_gelu",
+              "assemble_kernel": "assemble"}
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "aggregator_pass_s32_f16_traffic.json")
+
+
+def kernel_op(name: str):
+    for k, op in KERNEL_OPS.items():
+        if k in name:
+            return op
+    return None
+
+
+def load_traffic(op: str, frames: int, dtype: str):
+    """HBM bytes per launch of `op` measured by rocprofv3 --pmc FETCH_SIZE and
+    WRITE_SIZE runs of this benchmark (written by --summarize), if recorded
+    for this workload."""
+    try:
+        t = json.load(open(TRAFFIC_JSON))
+    except (OSError, ValueError):
+        return None
+    if t.get("frames") != frames or t.get("dtype") != dtype or op not in t.get("ops", {}):
+        return None
+    return {"bytes_per_launch": t["ops"][op]["hbm_bytes_per_launch"],
+            "source": f"profiles/{os.path.basename(TRAFFIC_JSON)}"}
+
+
+def summarize(args) -> None:
+    """Markdown summary of rocprofv3 CSV output for this benchmark's kernels:
+    kernel-trace durations against the algorithmic bytes, and (with
+    --pmc-fetch/--pmc-write counter_collection CSVs) HBM bytes per launch,
+    scaled by what the counters read for the calibration copy
+    (--calibrate-copy-mib MiB each way, the largest copy-kernel dispatch)."""
+    import csv
+    import statistics as st
+    from collections import defaultdict
+
+    esz = 2 if args.dtype == "f16" else 4
+    p = GRID[0] * GRID[1]
+    rows = args.frames * (p + PREFIX)
+    nbytes = op_bytes(rows, esz, args.frames * p, p)
+    launches = {"assemble": 1, "layernorm": 96, "qknorm_rope": 96, "bias_ls_residual": 96,
+                "bias_gelu": 48}
+    dur = defaultdict(list)
+    for r in csv.DictReader(open(args.summarize)):
+        op = kernel_op(r["Kernel_Name"])
+        if op:
+            dur[op].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    out = [f"## Kernel durations (rocprofv3 --kernel-trace), S={args.frames} {args.dtype}", "",
+           "| op | kernel calls | mean us | median us | algorithmic MB/launch | GB/s (mean) "
+           "| of 8 TB/s |", "|---|---|---|---|---|---|---|"]
+    pass_us = 0.0
+    for op in OPS:
+        if not dur[op]:
+            continue
+        m, med = st.mean(dur[op]), st.median(dur[op])
+        gbs = nbytes[op] / (m * 1e-6) / 1e9
+        pass_us += m * launches[op]
+        out.append(f"| {op} | {len(dur[op])} | {m:.2f} | {med:.2f} | {nbytes[op] / 1e6:.1f} | "
+                   f"{gbs:.0f} | {gbs / PEAK_GBS:.1%} |")
+    out += ["", f"Sum of mean kernel times x launches per pass: {pass_us / 1e3:.3f} ms "
+                f"({sum(nbytes[o] * launches[o] for o in OPS) / (pass_us * 1e-6) / 1e9:.0f} GB/s "
+                f"algorithmic)."]
+    if args.pmc_fetch and args.pmc_write:
+        def counters(path, name):
+            # The calibration copy (torch's device-to-device copy_) runs as
+            # the runtime's blit kernel __amd_rocclr_copyBuffer.
+            per_op, copy = defaultdict(list), []
+            for r in csv.DictReader(open(path)):
+                if r.get("Counter_Name") != name:
+                    continue
+                v = float(r["Counter_Value"])
+                op = kernel_op(r["Kernel_Name"])
+                if op:
+                    per_op[op].append(v)
+                elif "rocclr_copyBuffer" in r["Kernel_Name"]:
+                    copy.append(v)
+            return per_op, (max(copy) if copy else None)
+
+        fetch, f_cal = counters(args.pmc_fetch, "FETCH_SIZE")
+        write, w_cal = counters(args.pmc_write, "WRITE_SIZE")
+        known_kib = args.calibrate_copy_mib * 1024.0
+        f_scale = known_kib / f_cal if f_cal else 1.0
+        w_scale = known_kib / w_cal if w_cal else 1.0
+        out += ["", "## HBM traffic (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE; KiB per dispatch)",
+                "", f"Calibration: a {args.calibrate_copy_mib} MiB device copy read "
+                f"{f_cal} KiB (FETCH_SIZE) and wrote {w_cal} KiB (WRITE_SIZE); scale factors "
+                f"{f_scale:.4f} (fetch), {w_scale:.4f} (write).", "",
+                "| op | dispatches | FETCH KiB | WRITE KiB | HBM MB/launch (scaled) | "
+                "algorithmic MB | ratio |", "|---|---|---|---|---|---|---|"]
+        traffic = {"frames": args.frames, "dtype": args.dtype, "fetch_scale": f_scale,
+                   "write_scale": w_scale, "ops": {}}
+        for op in OPS:
+            if not fetch[op] or not write[op]:
+                continue
+            fk, wk = st.mean(fetch[op]), st.mean(write[op])
+            hbm = (fk * f_scale + wk * w_scale) * 1024.0
+            traffic["ops"][op] = {"fetch_kib": fk, "write_kib": wk,
+                                  "hbm_bytes_per_launch": int(hbm),
+                                  "algorithmic_bytes": nbytes[op]}
+            out.append(f"| {op} | {len(fetch[op])} | {fk:.0f} | {wk:.0f} | {hbm / 1e6:.1f} | "
+                       f"{nbytes[op] / 1e6:.1f} | {hbm / nbytes[op]:.3f} |")
+        if args.traffic_json:
+            with open(args.traffic_json, "w") as f:
+                json.dump(traffic, f, indent=1)
+    print("\n".join(out))
+
+
 def main():
     args = parse()
+    if args.summarize:
+        summarize(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU: the fused per-layer ops are "
                                    "row-local and shard by frames with no exchange, so the "
@@ -238,15 +356,24 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
 
-    mean = per_op_times(bench, args.op_passes)
-    per_op = {}
-    for op in OPS:
-        us = mean[op] * 1e3
-        gbs = bench.bytes[op] / (us * 1e-6) / 1e9
-        per_op[op] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
-                      "bytes": bench.bytes[op], "launches_per_pass": bench.launches[op]}
-    ops_ms = sum(per_op[op]["us"] * bench.launches[op] for op in OPS) / 1e3
-    dominant = max(OPS, key=lambda op: per_op[op]["us"] * bench.launches[op])
+    per_op, roofline, ops_ms = {}, None, None
+    if args.op_passes > 0:
+        mean = per_op_times(bench, args.op_passes)
+        for op in OPS:
+            us = mean[op] * 1e3
+            gbs = bench.bytes[op] / (us * 1e-6) / 1e9
+            per_op[op] = {"us": round(us, 2), "GB/s": round(gbs, 1),
+                          "frac": round(gbs / PEAK_GBS, 4), "bytes": bench.bytes[op],
+                          "launches_per_pass": bench.launches[op]}
+        ops_ms = round(sum(per_op[op]["us"] * bench.launches[op] for op in OPS) / 1e3, 3)
+        dominant = max(OPS, key=lambda op: per_op[op]["us"] * bench.launches[op])
+        roofline = {"bound": "hbm", "kernel": dominant, "achieved": per_op[dominant]["GB/s"],
+                    "peak": PEAK_GBS, "unit": "GB/s", "frac": per_op[dominant]["frac"],
+                    "traffic": None}
+        traffic = load_traffic(dominant, args.frames, args.dtype)
+        if traffic is not None:
+            roofline["traffic"] = traffic["bytes_per_launch"]
+            roofline["traffic_source"] = traffic["source"]
     value = bench.pass_bytes / (ms * 1e-3) / 1e9
 
     line = {
@@ -271,11 +398,9 @@ def main():
         "frac_of_peak": round(value / PEAK_GBS, 4),
         "pass_bytes": bench.pass_bytes,
         "tokens_per_s": round(bench.rows / (ms * 1e-3), 1),
-        "ops_ms_per_step": round(ops_ms, 3),
+        "ops_ms_per_step": ops_ms,
         "ops": per_op,
-        "roofline": {"bound": "hbm", "kernel": dominant,
-                     "achieved": per_op[dominant]["GB/s"], "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": per_op[dominant]["frac"], "traffic": None},
+        "roofline": roofline,
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
