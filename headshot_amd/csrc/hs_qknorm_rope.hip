@@ -23,6 +23,8 @@
 // Generic path (any head_dim, either input layout): one wave per head vector,
 // lanes strided over the vector; used for rope_apply on head-major tensors
 // and for shapes the fast path does not cover.
+#include <type_traits>
+
 #include "hs_common.hpp"
 
 namespace hs {
@@ -61,6 +63,7 @@ struct QknTile {
     static constexpr int HB = H < HS_QK_HB ? H : HS_QK_HB;
     static constexpr int NB = H / HB;    // head batches per tile
     static_assert(H % HB == 0, "head batches must tile H");
+    __host__ __device__ static int64_t units(int64_t tokens) { return ceil_div(tokens, TPI) * NB; }
 
     const T* __restrict__ x;
     const float* __restrict__ sin_tab;
@@ -147,6 +150,96 @@ struct QknTile {
     }
 };
 
+// Row mapping: a work unit is one token row (all H heads). A load
+// instruction covers HPI = 64/G heads, so the row is CH contiguous 1 KiB
+// loads; the token index, its frame and the RoPE decision are wave-uniform
+// (scalar divide, uniform branch), and each store writes HPI heads' vectors
+// of one token (HPI separate 128-byte pieces of the head-major output).
+template <typename T, int H, bool NORM, bool ROPE>
+struct QknRow {
+    static constexpr int D = 64;
+    static constexpr int V = Vec<T>::N;
+    static constexpr int G = D / V;
+    static constexpr int HPI = 64 / G;
+    static constexpr int CH = H / HPI;
+    static_assert(H % HPI == 0, "whole load instructions per row");
+    static constexpr int HB = CH;  // loads per unit (buffer size)
+    __host__ __device__ static int64_t units(int64_t tokens) { return tokens; }
+
+    const T* __restrict__ x;
+    const float* __restrict__ sin_tab;
+    const float* __restrict__ cos_tab;
+    T* __restrict__ out;
+    int64_t tokens;
+    int seq, prefix, ch, gsub;
+    bool upper;
+    float eps;
+    float wr[V], br[V];
+
+    __device__ __forceinline__ void load(u32x4 (&raw)[HB], int64_t tok) const {
+        const T* xr = x + tok * (H * D) + gsub * D + ch;
+#pragma unroll
+        for (int c = 0; c < CH; c++) raw[c] = ld_stream(xr + c * HPI * D);
+    }
+
+    __device__ __forceinline__ void process(const u32x4 (&raw)[HB], int64_t tok) const {
+        // tokens < 2^31 (checked on the host): wave-uniform 32-bit divide
+        const uint32_t s = static_cast<uint32_t>(tok) / static_cast<uint32_t>(seq);
+        const int t = static_cast<int>(static_cast<uint32_t>(tok) - s * static_cast<uint32_t>(seq));
+        const bool rot = ROPE && t >= prefix;
+        float cs[V], sn[V];
+        if (rot) {
+            const int64_t row = static_cast<int64_t>(t - prefix) * D + ch;
+            const float sg = upper ? 1.0f : -1.0f;
+#pragma unroll
+            for (int k = 0; k < V; k += 4) {
+                const float4 c4 = ld_f32x4(cos_tab + row + k), s4 = ld_f32x4(sin_tab + row + k);
+                cs[k] = c4.x, cs[k + 1] = c4.y, cs[k + 2] = c4.z, cs[k + 3] = c4.w;
+                sn[k] = sg * s4.x, sn[k + 1] = sg * s4.y, sn[k + 2] = sg * s4.z,
+                sn[k + 3] = sg * s4.w;
+            }
+        }
+        T* obase = out + (static_cast<int64_t>(s) * H + gsub) * seq * D +
+                   static_cast<int64_t>(t) * D + ch;
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            float f[V];
+            unpack(raw[c], f, T{});
+            if constexpr (NORM) {
+                float sum = 0.0f;
+#pragma unroll
+                for (int k = 0; k < V; k++) sum += f[k];
+                const float mean = group_sum<G>(sum) / static_cast<float>(D);
+                float q = 0.0f;
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    const float d = f[k] - mean;
+                    q += d * d;
+                }
+                const float var = group_sum<G>(q) / static_cast<float>(D);
+                const float inv = rsqrtf(var + eps);
+#pragma unroll
+                for (int k = 0; k < V; k++)
+                    f[k] = storage_round((f[k] - mean) * inv * wr[k] + br[k], T{});
+            }
+            if (rot) {
+#pragma unroll
+                for (int k = 0; k < V; k++)
+                    f[k] = fmaf(f[k], cs[k], group_mirror<G>(f[k]) * sn[k]);
+            }
+            st_stream(obase + static_cast<int64_t>(c) * HPI * seq * D, pack(f, T{}));
+        }
+    }
+};
+
+#ifndef HS_QK_ROWS
+#define HS_QK_ROWS 1  // 1: token-row work units, 0: token-tile work units
+#endif
+
+template <typename T, int H, bool NORM, bool ROPE>
+using QknUnit = typename std::conditional<HS_QK_ROWS != 0, QknRow<T, H, NORM, ROPE>,
+                                          QknTile<T, H, NORM, ROPE>>::type;
+
 // Each wave runs K consecutive units with a two-buffer software pipeline:
 // the loads of unit i+1 are in flight while unit i is normalised, rotated
 // and stored, so waves overlap memory with arithmetic instead of alternating
@@ -156,7 +249,7 @@ __global__ __launch_bounds__(kBlock) void qkn_tile_kernel(
     const T* __restrict__ x, const float* __restrict__ nw, const float* __restrict__ nb,
     const float* __restrict__ sin_tab, const float* __restrict__ cos_tab, T* __restrict__ out,
     int64_t tokens, int seq, int prefix, float eps) {
-    using Tile = QknTile<T, H, NORM, ROPE>;
+    using Tile = QknUnit<T, H, NORM, ROPE>;
     constexpr int G = Tile::G, V = Tile::V, HB = Tile::HB;
     const int lane = lane_id();
     const int piece = lane % G;
@@ -176,7 +269,7 @@ __global__ __launch_bounds__(kBlock) void qkn_tile_kernel(
             tl.br[k] = b4.x, tl.br[k + 1] = b4.y, tl.br[k + 2] = b4.z, tl.br[k + 3] = b4.w;
         }
     }
-    const int64_t units = ceil_div(tokens, Tile::TPI) * Tile::NB;
+    const int64_t units = Tile::units(tokens);
     const int64_t u0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * K;
     if (u0 >= units) return;  // wave-uniform: the kernel has no barriers
     const int64_t u_end = u0 + K < units ? u0 + K : units;
@@ -261,9 +354,9 @@ template <typename T, int H, bool NORM, bool ROPE>
 hs_status launch_tile(hipStream_t st, const void* x, const float* nw, const float* nb,
                       const float* sn, const float* cs, void* out, int64_t tokens, int seq,
                       int prefix, float eps) {
-    using Tile = QknTile<T, H, NORM, ROPE>;
+    using Tile = QknUnit<T, H, NORM, ROPE>;
     constexpr int K = HS_QK_K;
-    const int64_t units = ceil_div(tokens, Tile::TPI) * Tile::NB;
+    const int64_t units = Tile::units(tokens);
     const int64_t blocks = ceil_div(ceil_div(units, K), kWavesPerBlock);
     qkn_tile_kernel<T, H, NORM, ROPE, K>
         <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(

@@ -1,0 +1,416 @@
+// headshot_hip.hpp — C++ host surface over the C ABI in headshot_hip.h.
+//
+// Mirrors headshot-server's `GpuContext` / `GpuTensor` for the per-layer op
+// path (crates/headshot-server/src/engine/ops.rs, engine/tensor.rs,
+// engine/rope.rs): the same method names and argument meaning, tensors that
+// own device memory (allocated on creation, freed on destruction), and the
+// reference's contract checks. Where the reference panics on a violated
+// contract (`assert!`), these methods throw hs::ContractViolation; a failed
+// HIP call throws hs::HipError. Header-only; compile with hipcc and link
+// libheadshot_hip.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <array>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "headshot_hip.h"
+
+namespace hs {
+
+// engine/tensor.rs:12-25
+enum class Dtype : int { F32 = HS_F32, F16 = HS_F16 };
+
+inline size_t dtype_size(Dtype dt) { return dt == Dtype::F16 ? 2 : 4; }
+
+struct ContractViolation : std::logic_error {
+    using std::logic_error::logic_error;
+};
+struct HipError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+#define HS_REQUIRE(cond, msg)                                                  \
+    do {                                                                       \
+        if (!(cond)) throw ::hs::ContractViolation(std::string(msg));          \
+    } while (0)
+
+inline void hip_check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw HipError(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+inline void check(hs_status st, const char* op) {
+    if (st == HS_OK) return;
+    std::string msg = std::string(op) + ": " + hs_last_error();
+    if (st == HS_EINVAL) throw ContractViolation(msg);
+    throw HipError(msg + " (" + hs_status_string(st) + ")");
+}
+
+// binary16 <-> binary32 with round-to-nearest-even (what the reference's
+// upload path does with half::f16::from_f32, engine/tensor.rs:71-91).
+inline uint16_t f32_to_f16(float f) {
+    uint32_t x;
+    std::memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u)
+        return static_cast<uint16_t>(sign | (ax == 0x7f800000u ? 0x7c00u : 0x7e00u | ((ax >> 13) & 0x3ffu)));
+    if (ax >= 0x477ff000u) return static_cast<uint16_t>(sign | 0x7c00u);
+    if (ax < 0x38800000u)
+        return static_cast<uint16_t>(sign | static_cast<uint32_t>(std::nearbyint(std::fabs(f) * 16777216.0f)));
+    uint32_t h = (((ax >> 23) - 112u) << 10) | ((ax & 0x7fffffu) >> 13);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+    return static_cast<uint16_t>(sign | h);
+}
+
+inline float f16_to_f32(uint16_t h) {
+    const uint32_t sign = static_cast<uint32_t>(h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
+    uint32_t bits;
+    if (exp == 0) {
+        float v = static_cast<float>(mant) * (1.0f / 16777216.0f);
+        std::memcpy(&bits, &v, 4);
+        bits |= sign;
+    } else if (exp == 31) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((exp + 112u) << 23) | (mant << 13);
+    }
+    float out;
+    std::memcpy(&out, &bits, 4);
+    return out;
+}
+
+// engine/tensor.rs:27-57: device buffer + shape + storage type.
+class HipTensor {
+   public:
+    HipTensor() = default;
+    HipTensor(std::vector<size_t> shape, Dtype dt) : shape_(std::move(shape)), dtype_(dt) {
+        const size_t n = bytes();
+        if (n) hip_check(hipMalloc(&ptr_, n), "hipMalloc");
+    }
+    ~HipTensor() {
+        if (ptr_) (void)hipFree(ptr_);
+    }
+    HipTensor(HipTensor&& o) noexcept { *this = std::move(o); }
+    HipTensor& operator=(HipTensor&& o) noexcept {
+        if (this != &o) {
+            if (ptr_) (void)hipFree(ptr_);
+            ptr_ = o.ptr_, shape_ = std::move(o.shape_), dtype_ = o.dtype_;
+            o.ptr_ = nullptr;
+        }
+        return *this;
+    }
+    HipTensor(const HipTensor&) = delete;
+    HipTensor& operator=(const HipTensor&) = delete;
+
+    size_t len() const {
+        size_t n = 1;
+        for (size_t s : shape_) n *= s;
+        return n;
+    }
+    size_t bytes() const { return len() * dtype_size(dtype_); }
+    size_t last() const { return shape_.empty() ? 0 : shape_.back(); }
+    const std::vector<size_t>& shape() const { return shape_; }
+    Dtype dtype() const { return dtype_; }
+    void* data() { return ptr_; }
+    const void* data() const { return ptr_; }
+    const float* f32() const { return static_cast<const float*>(ptr_); }
+
+    // engine/tensor.rs:52-56
+    HipTensor reshaped(std::vector<size_t> shape) && {
+        size_t n = 1;
+        for (size_t s : shape) n *= s;
+        HS_REQUIRE(n == len(), "reshape element count");
+        shape_ = std::move(shape);
+        return std::move(*this);
+    }
+
+   private:
+    void* ptr_ = nullptr;
+    std::vector<size_t> shape_;
+    Dtype dtype_ = Dtype::F32;
+};
+
+// RoPE tables + unrotated prefix for one attention call (model/block.rs:42-47).
+struct Rope {
+    const HipTensor* sin;
+    const HipTensor* cos;
+    size_t prefix;
+};
+
+// QK-norm weight and bias (model/block.rs:35-40, one side).
+struct Norm {
+    const HipTensor* weight;
+    const HipTensor* bias;
+};
+
+class HipContext {
+   public:
+    HipContext() {
+        HS_REQUIRE(hs_abi_version() == HS_ABI_VERSION, "libheadshot_hip ABI mismatch");
+        hip_check(hipStreamCreate(&stream_), "hipStreamCreate");
+    }
+    ~HipContext() {
+        if (stream_) {
+            (void)hipStreamSynchronize(stream_);
+            (void)hipStreamDestroy(stream_);
+        }
+    }
+    HipContext(const HipContext&) = delete;
+    HipContext& operator=(const HipContext&) = delete;
+
+    hipStream_t stream() const { return stream_; }
+    void sync() const { hip_check(hipStreamSynchronize(stream_), "hipStreamSynchronize"); }
+
+    // ------------------------------------------------------------- tensors
+
+    HipTensor empty_typed(std::vector<size_t> shape, Dtype dt) const {
+        return HipTensor(std::move(shape), dt);
+    }
+
+    // engine/tensor.rs:70-91: upload f32 data as dt storage
+    HipTensor tensor_from_f32(std::vector<size_t> shape, const std::vector<float>& data,
+                              Dtype dt) const {
+        HipTensor t(std::move(shape), dt);
+        HS_REQUIRE(data.size() == t.len(), "shape/data mismatch");
+        if (dt == Dtype::F32) {
+            hip_check(hipMemcpy(t.data(), data.data(), t.bytes(), hipMemcpyHostToDevice), "upload");
+        } else {
+            std::vector<uint16_t> h(data.size());
+            for (size_t i = 0; i < data.size(); i++) h[i] = f32_to_f16(data[i]);
+            hip_check(hipMemcpy(t.data(), h.data(), t.bytes(), hipMemcpyHostToDevice), "upload");
+        }
+        return t;
+    }
+    HipTensor tensor_from_slice(std::vector<size_t> shape, const std::vector<float>& data) const {
+        return tensor_from_f32(std::move(shape), data, Dtype::F32);
+    }
+
+    // engine/tensor.rs:162-198: flush and read back as f32
+    std::vector<float> download(const HipTensor& t) const {
+        sync();
+        std::vector<float> out(t.len());
+        if (t.dtype() == Dtype::F32) {
+            hip_check(hipMemcpy(out.data(), t.data(), t.bytes(), hipMemcpyDeviceToHost), "download");
+        } else {
+            std::vector<uint16_t> h(t.len());
+            hip_check(hipMemcpy(h.data(), t.data(), t.bytes(), hipMemcpyDeviceToHost), "download");
+            for (size_t i = 0; i < h.size(); i++) out[i] = f16_to_f32(h[i]);
+        }
+        return out;
+    }
+
+    // ------------------------------------------------------- reference ops
+
+    // engine/ops.rs:130-153 (eps 1e-5 there)
+    HipTensor layernorm(const HipTensor& x, const HipTensor& weight, const HipTensor& bias,
+                        float eps = 1e-5f) const {
+        const size_t dim = x.last();
+        HS_REQUIRE(weight.len() == dim, "norm weight length");
+        HS_REQUIRE(bias.len() == dim, "norm bias length");
+        HS_REQUIRE(weight.dtype() == Dtype::F32, "norm weight must be f32");
+        HS_REQUIRE(bias.dtype() == Dtype::F32, "norm bias must be f32");
+        HipTensor out = empty_typed(x.shape(), x.dtype());
+        check(hs_layernorm(stream_, hs_dtype(x.dtype()), x.data(), weight.f32(), bias.f32(),
+                           out.data(), dim ? static_cast<int64_t>(x.len() / dim) : 0,
+                           static_cast<int32_t>(dim), eps),
+              "layernorm");
+        return out;
+    }
+
+    // engine/ops.rs:155-165
+    HipTensor gelu(const HipTensor& x) const {
+        HipTensor out = empty_typed(x.shape(), x.dtype());
+        check(hs_gelu(stream_, hs_dtype(x.dtype()), x.data(), out.data(),
+                      static_cast<int64_t>(x.len())),
+              "gelu");
+        return out;
+    }
+
+    // engine/ops.rs:167-183
+    HipTensor residual_ls(const HipTensor& res, const HipTensor& x, const HipTensor& gamma) const {
+        HS_REQUIRE(res.len() == x.len(), "res/x length");
+        HS_REQUIRE(res.dtype() == x.dtype(), "res/x dtype");
+        HS_REQUIRE(gamma.dtype() == Dtype::F32, "gamma must be f32");
+        const size_t dim = gamma.len();
+        HS_REQUIRE(dim > 0 && x.len() % dim == 0, "gamma must tile x");
+        HipTensor out = empty_typed(res.shape(), x.dtype());
+        check(hs_residual_ls(stream_, hs_dtype(x.dtype()), res.data(), x.data(), gamma.f32(),
+                             out.data(), static_cast<int64_t>(x.len()), static_cast<int32_t>(dim)),
+              "residual_ls");
+        return out;
+    }
+
+    // engine/ops.rs:185-200
+    HipTensor split_heads(const HipTensor& x, size_t s, size_t t, size_t h, size_t d) const {
+        HS_REQUIRE(x.len() == s * t * h * d, "split_heads size");
+        HipTensor out = empty_typed({s, h, t, d}, x.dtype());
+        check(hs_split_heads(stream_, hs_dtype(x.dtype()), x.data(), out.data(), i32(s), i32(t),
+                             i32(h), i32(d)),
+              "split_heads");
+        return out;
+    }
+
+    // engine/ops.rs:202-223: in place on (S, H, T, D); tables (T - prefix, D)
+    void rope_apply(HipTensor& x, const HipTensor& sin, const HipTensor& cos, size_t prefix) const {
+        HS_REQUIRE(x.shape().size() == 4, "rope_apply wants (S,H,T,D)");
+        const size_t s = x.shape()[0], h = x.shape()[1], t = x.shape()[2], d = x.shape()[3];
+        HS_REQUIRE(prefix <= t, "prefix");
+        HS_REQUIRE(sin.len() == (t - prefix) * d, "table size");
+        HS_REQUIRE(cos.len() == sin.len(), "table size");
+        HS_REQUIRE(sin.dtype() == Dtype::F32 && cos.dtype() == Dtype::F32, "rope tables must be f32");
+        check(hs_rope_apply(stream_, hs_dtype(x.dtype()), x.data(), sin.f32(), cos.f32(), i32(s),
+                            i32(h), i32(t), i32(d), i32(prefix)),
+              "rope_apply");
+    }
+
+    // engine/ops.rs:336-348
+    HipTensor cast_to_f16(const HipTensor& x) const {
+        HS_REQUIRE(x.dtype() == Dtype::F32, "cast_to_f16 wants f32");
+        HipTensor out = empty_typed(x.shape(), Dtype::F16);
+        check(hs_cast_f32_to_f16(stream_, x.f32(), out.data(), static_cast<int64_t>(x.len())),
+              "cast_to_f16");
+        return out;
+    }
+
+    // engine/tensor.rs:146-160
+    void copy_rows(const HipTensor& src, size_t src_row, HipTensor& dst, size_t dst_row,
+                   size_t n_rows) const {
+        HS_REQUIRE(src.dtype() == dst.dtype(), "copy_rows dtype");
+        const size_t row = src.last() * dtype_size(src.dtype());
+        HS_REQUIRE(row == dst.last() * dtype_size(dst.dtype()), "copy_rows row width");
+        HS_REQUIRE((src_row + n_rows) * row <= src.bytes(), "copy_rows source rows");
+        HS_REQUIRE((dst_row + n_rows) * row <= dst.bytes(), "copy_rows destination rows");
+        check(hs_copy_rows(stream_, src.data(), static_cast<int64_t>(src_row), dst.data(),
+                           static_cast<int64_t>(dst_row), static_cast<int64_t>(n_rows),
+                           static_cast<int64_t>(row)),
+              "copy_rows");
+    }
+
+    // engine/ops.rs:374-389 (f32 only)
+    HipTensor tiled_add(const HipTensor& x, const HipTensor& table) const {
+        HS_REQUIRE(x.dtype() == Dtype::F32 && table.dtype() == Dtype::F32, "tiled_add is f32");
+        HS_REQUIRE(table.len() > 0 && x.len() % table.len() == 0, "table must tile x");
+        HipTensor out = empty_typed(x.shape(), Dtype::F32);
+        check(hs_tiled_add(stream_, x.f32(), table.f32(), static_cast<float*>(out.data()),
+                           static_cast<int64_t>(x.len()), static_cast<int64_t>(table.len())),
+              "tiled_add");
+        return out;
+    }
+
+    // ----------------------------------------------------------- fused ops
+
+    // split_heads + QK-norm + RoPE (model/block.rs:130-146) in one pass:
+    // (S*T, H*D) token-major -> (S, H, T, D) head-major.
+    HipTensor qknorm_rope(const HipTensor& x_tok, size_t s, size_t t, size_t h, size_t d,
+                          const Norm* norm, const Rope* rope, float eps = 1e-5f) const {
+        HS_REQUIRE(x_tok.len() == s * t * h * d, "qknorm_rope size");
+        const float *nw = nullptr, *nb = nullptr, *sn = nullptr, *cs = nullptr;
+        size_t prefix = 0;
+        if (norm) {
+            HS_REQUIRE(norm->weight->len() == d && norm->bias->len() == d, "qk-norm length");
+            HS_REQUIRE(norm->weight->dtype() == Dtype::F32 && norm->bias->dtype() == Dtype::F32,
+                       "qk-norm parameters must be f32");
+            nw = norm->weight->f32(), nb = norm->bias->f32();
+        }
+        if (rope) {
+            prefix = rope->prefix;
+            HS_REQUIRE(prefix <= t, "prefix");
+            HS_REQUIRE(rope->sin->len() == (t - prefix) * d && rope->cos->len() == rope->sin->len(),
+                       "table size");
+            HS_REQUIRE(rope->sin->dtype() == Dtype::F32 && rope->cos->dtype() == Dtype::F32,
+                       "rope tables must be f32");
+            sn = rope->sin->f32(), cs = rope->cos->f32();
+        }
+        HipTensor out = empty_typed({s, h, t, d}, x_tok.dtype());
+        check(hs_qknorm_rope(stream_, hs_dtype(x_tok.dtype()), x_tok.data(), nw, nb, sn, cs,
+                             out.data(), i32(s), i32(t), i32(h), i32(d), i32(prefix), eps),
+              "qknorm_rope");
+        return out;
+    }
+
+    // fc1 bias epilogue + GELU (model/block.rs:173-174)
+    HipTensor bias_gelu(const HipTensor& x, const HipTensor* bias) const {
+        const size_t cols = x.last();
+        if (bias) HS_REQUIRE(bias->len() == cols && bias->dtype() == Dtype::F32, "bias");
+        HipTensor out = empty_typed(x.shape(), x.dtype());
+        check(hs_bias_gelu(stream_, hs_dtype(x.dtype()), x.data(), bias ? bias->f32() : nullptr,
+                           out.data(), cols ? static_cast<int64_t>(x.len() / cols) : 0, i32(cols)),
+              "bias_gelu");
+        return out;
+    }
+
+    // proj/fc2 bias epilogue + LayerScale + residual (model/block.rs:150-155)
+    HipTensor bias_ls_residual(const HipTensor& res, const HipTensor& x, const HipTensor& gamma,
+                               const HipTensor* bias) const {
+        HS_REQUIRE(res.len() == x.len() && res.dtype() == x.dtype(), "res/x");
+        const size_t dim = x.last();
+        HS_REQUIRE(gamma.len() == dim && gamma.dtype() == Dtype::F32, "gamma");
+        if (bias) HS_REQUIRE(bias->len() == dim && bias->dtype() == Dtype::F32, "bias");
+        HipTensor out = empty_typed(res.shape(), x.dtype());
+        check(hs_bias_ls_residual(stream_, hs_dtype(x.dtype()), res.data(), x.data(),
+                                  bias ? bias->f32() : nullptr, gamma.f32(), out.data(),
+                                  dim ? static_cast<int64_t>(x.len() / dim) : 0, i32(dim)),
+              "bias_ls_residual");
+        return out;
+    }
+
+    // model/trunk.rs:68-85: per frame [cam[v], reg[v*R..], patches + bias + pos]
+    HipTensor assemble_tokens(const HipTensor& patches, size_t s, size_t p, const HipTensor& cam,
+                              const HipTensor* reg, const HipTensor* patch_bias,
+                              const HipTensor* pos, Dtype out_dt, int n_var = 2) const {
+        const size_t d = patches.last();
+        HS_REQUIRE(patches.len() == s * p * d, "patches shape");
+        HS_REQUIRE(cam.dtype() == out_dt && cam.len() == static_cast<size_t>(n_var) * d,
+                   "camera token shape/dtype");
+        const size_t r = reg ? reg->len() / (static_cast<size_t>(n_var) * d) : 0;
+        if (reg) HS_REQUIRE(reg->dtype() == out_dt, "register token dtype");
+        if (patch_bias) HS_REQUIRE(patch_bias->len() == d && patch_bias->dtype() == Dtype::F32, "bias");
+        if (pos) HS_REQUIRE(pos->len() == p * d && pos->dtype() == Dtype::F32, "pos embed");
+        HipTensor out = empty_typed({s * (1 + r + p), d}, out_dt);
+        check(hs_assemble_tokens(stream_, hs_dtype(out_dt), patches.data(),
+                                 hs_dtype(patches.dtype()), patch_bias ? patch_bias->f32() : nullptr,
+                                 pos ? pos->f32() : nullptr, cam.data(), reg ? reg->data() : nullptr,
+                                 out.data(), i32(s), i32(p), i32(r), i32(d), n_var),
+              "assemble_tokens");
+        return out;
+    }
+
+   private:
+    static ::hs_dtype hs_dtype(Dtype dt) { return static_cast<::hs_dtype>(static_cast<int>(dt)); }
+    static int32_t i32(size_t v) {
+        HS_REQUIRE(v <= 0x7fffffffu, "dimension exceeds int32");
+        return static_cast<int32_t>(v);
+    }
+    hipStream_t stream_ = nullptr;
+};
+
+namespace rope {
+
+// engine/rope.rs:8-10
+inline std::array<float, 16> periods() {
+    std::array<float, 16> p{};
+    hs_rope_periods(p.data());
+    return p;
+}
+
+// engine/rope.rs:18-43: (sin, cos), each (h_p*w_p, 64)
+inline std::pair<std::vector<float>, std::vector<float>> tables(const std::array<float, 16>& per,
+                                                                size_t h_p, size_t w_p) {
+    std::vector<float> sin(h_p * w_p * 64), cos(h_p * w_p * 64);
+    check(hs_rope_tables(per.data(), static_cast<int32_t>(h_p), static_cast<int32_t>(w_p),
+                         sin.data(), cos.data()),
+          "rope_tables");
+    return {std::move(sin), std::move(cos)};
+}
+
+}  // namespace rope
+}  // namespace hs

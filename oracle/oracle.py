@@ -50,7 +50,7 @@ _lib = None
 
 def build() -> str:
     """Compile liboracle.so with oracle/Makefile (gcc, -ffp-contract=off)."""
-    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    subprocess.run(["make", "-B", "-s", "-C", _HERE], check=True)
     return _LIB_PATH
 
 
