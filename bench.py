@@ -188,7 +188,7 @@ def cpu_baseline(bench: Pass, target_s: float):
 
 
 KERNEL_OPS = {"ln_vec_kernel": "layernorm", "ln_generic_kernel": "layernorm",
-              "qkn_tile_kernel": "qknorm_rope", "qkn_generic_kernel": "qknorm_rope",
+              "qkn_row_kernel": "qknorm_rope", "qkn_generic_kernel": "qknorm_rope",
               "bias_ls_kernel": "bias_ls_residual", "bias_gelu_kernel": "bias_gelu",
               "assemble_kernel": "assemble"}
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "aggregator_pass_s32_f16_traffic.json")

@@ -7,9 +7,9 @@
 // tiled_add.wesl semantics, out[i] = x[i] + table[i % block]) into the cast,
 // so each patch element is read once in its input dtype and written once.
 //
-// One wave64 per output row (persistent); each lane moves 4 consecutive
-// channels per step, CHUNKS steps per row. Rows are independent; the
-// camera/register gather is row-granular, so no LDS staging is needed.
+// One wave64 per output row; each lane moves 4 consecutive channels per
+// step, CHUNKS steps per row. Rows are independent; the camera/register
+// gather is row-granular, so no LDS staging is needed.
 #include "hs_common.hpp"
 
 namespace hs {
@@ -68,55 +68,83 @@ __device__ __forceinline__ float patch_value(float x, float b, float p, bool has
     return x;
 }
 
+// Workgroup -> rows, XCD-aware. Workgroups are dispatched round-robin over
+// the XCDs (workgroup b runs on XCD b % kXcds), each XCD with its own L2.
+// Patch rows come first: workgroup b handles patch position
+// p = (b / kXcds / C) * kXcds + b % kXcds for frames [4c, 4c + 4), c =
+// (b / kXcds) % C, C = ceil(S / 4). Every workgroup of one patch position
+// therefore runs on the same XCD and in C consecutive dispatch rounds, so
+// the positional-table row p is fetched from HBM once and then served by
+// that XCD's L2 to all S frames. Camera/register rows follow, 4 per
+// workgroup.
+constexpr int kXcds = 8;
+
+struct AssembleGrid {
+    int64_t patch_blocks;  // covers ceil(P / kXcds) * kXcds positions
+    int64_t special_blocks;
+    int chunks;            // C
+    __host__ __device__ static AssembleGrid make(int s, int np, int nr) {
+        AssembleGrid g;
+        g.chunks = static_cast<int>(ceil_div(s, kWavesPerBlock));
+        g.patch_blocks = static_cast<int64_t>(g.chunks) * ceil_div(np, kXcds) * kXcds;
+        g.special_blocks = ceil_div(static_cast<int64_t>(s) * (1 + nr), kWavesPerBlock);
+        return g;
+    }
+};
+
 template <typename TO, typename TP, int CHUNKS>
 __global__ __launch_bounds__(kBlock) void assemble_kernel(
     const TP* __restrict__ patches, const float* __restrict__ pbias, const float* __restrict__ pos,
-    const TO* __restrict__ cam, const TO* __restrict__ reg, TO* __restrict__ out, int64_t out_rows,
+    const TO* __restrict__ cam, const TO* __restrict__ reg, TO* __restrict__ out, int nframes,
     int seq, int np, int nr, int n_var) {
     constexpr int D = 256 * CHUNKS;
     const int lane = lane_id();
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
-    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
-    const bool has_b = pbias != nullptr, has_p = pos != nullptr;
-    float bv[CHUNKS][4];
-    if (has_b) {
+    const int w = threadIdx.x >> 6;
+    const AssembleGrid grid = AssembleGrid::make(nframes, np, nr);
+    const int64_t b = blockIdx.x;
+    if (b < grid.patch_blocks) {
+        const int64_t round = b / kXcds;
+        const int64_t p = (round / grid.chunks) * kXcds + b % kXcds;
+        const int f = static_cast<int>(round % grid.chunks) * kWavesPerBlock + w;
+        if (p >= np || f >= nframes) return;  // wave-uniform; the kernel has no barriers
+        const bool has_b = pbias != nullptr, has_p = pos != nullptr;
+        const TP* src = patches + (static_cast<int64_t>(f) * np + p) * D + lane * 4;
+        float x[CHUNKS][4], pe[CHUNKS][4], bv[CHUNKS][4];
 #pragma unroll
-        for (int c = 0; c < CHUNKS; c++) load4(pbias + c * 256 + lane * 4, bv[c]);
-    }
-    for (int64_t row = wave; row < out_rows; row += nwaves) {
-        const uint32_t f = static_cast<uint32_t>(row) / static_cast<uint32_t>(seq);
-        const int t = static_cast<int>(static_cast<uint32_t>(row) - f * static_cast<uint32_t>(seq));
-        const int v = (n_var == 2 && f != 0) ? 1 : 0;
-        TO* orow = out + row * D + lane * 4;
-        if (t <= nr) {
-            const TO* src = t == 0 ? cam + static_cast<int64_t>(v) * D
-                                   : reg + (static_cast<int64_t>(v) * nr + (t - 1)) * D;
-            float vals[CHUNKS][4];
+        for (int c = 0; c < CHUNKS; c++) load4_stream(src + c * 256, x[c]);
+        if (has_p) {
 #pragma unroll
-            for (int c = 0; c < CHUNKS; c++) load4(src + c * 256 + lane * 4, vals[c]);
-#pragma unroll
-            for (int c = 0; c < CHUNKS; c++) store4(orow + c * 256, vals[c]);
-        } else {
-            const int p = t - 1 - nr;
-            const TP* src = patches + (static_cast<int64_t>(f) * np + p) * D + lane * 4;
-            const float* prow = has_p ? pos + static_cast<int64_t>(p) * D + lane * 4 : nullptr;
-            float x[CHUNKS][4], pe[CHUNKS][4];
-#pragma unroll
-            for (int c = 0; c < CHUNKS; c++) load4_stream(src + c * 256, x[c]);
-            if (has_p) {
-#pragma unroll
-                for (int c = 0; c < CHUNKS; c++) load4(prow + c * 256, pe[c]);
-            }
-#pragma unroll
-            for (int c = 0; c < CHUNKS; c++) {
-#pragma unroll
-                for (int k = 0; k < 4; k++)
-                    x[c][k] = patch_value<TP>(x[c][k], has_b ? bv[c][k] : 0.0f,
-                                              has_p ? pe[c][k] : 0.0f, has_b, has_p);
-                store4(orow + c * 256, x[c]);
-            }
+            for (int c = 0; c < CHUNKS; c++) load4(pos + p * D + c * 256 + lane * 4, pe[c]);
         }
+        if (has_b) {
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) load4(pbias + c * 256 + lane * 4, bv[c]);
+        }
+        TO* orow = out + (static_cast<int64_t>(f) * seq + 1 + nr + p) * D + lane * 4;
+#pragma unroll
+        for (int c = 0; c < CHUNKS; c++) {
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                x[c][k] = patch_value<TP>(x[c][k], has_b ? bv[c][k] : 0.0f,
+                                          has_p ? pe[c][k] : 0.0f, has_b, has_p);
+            store4(orow + c * 256, x[c]);
+        }
+        return;
     }
+    // camera / register rows
+    const int64_t j = (b - grid.patch_blocks) * kWavesPerBlock + w;
+    if (j >= static_cast<int64_t>(nframes) * (1 + nr)) return;
+    const int f = static_cast<int>(j / (1 + nr));
+    const int t = static_cast<int>(j - static_cast<int64_t>(f) * (1 + nr));
+    const int v = (n_var == 2 && f != 0) ? 1 : 0;
+    const TO* src = t == 0 ? cam + static_cast<int64_t>(v) * D
+                           : reg + (static_cast<int64_t>(v) * nr + (t - 1)) * D;
+    TO* orow = out + (static_cast<int64_t>(f) * seq + t) * D + lane * 4;
+    float vals[CHUNKS][4];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) load4(src + c * 256 + lane * 4, vals[c]);
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) store4(orow + c * 256, vals[c]);
 }
 
 // Any D, any alignment: lanes strided over the row.
@@ -162,26 +190,32 @@ hs_status launch(hipStream_t st, const void* patches, const float* pbias, const 
     const int seq = 1 + nr + np;
     const int64_t out_rows = static_cast<int64_t>(s) * seq;
     const dim3 grid(static_cast<uint32_t>(persistent_blocks(out_rows)));
+    const AssembleGrid ag = AssembleGrid::make(s, np, nr);
     const auto* P = static_cast<const TP*>(patches);
     const auto* C = static_cast<const TO*>(cam);
     const auto* R = static_cast<const TO*>(reg);
     auto* O = static_cast<TO*>(out);
-    const bool vec_ok = d % 256 == 0 && aligned16(patches) && aligned16(out) && aligned16(cam) &&
+    // The dispatch packet counts work-items in 32 bits: one wave per row
+    // caps the non-persistent grid, beyond which the persistent kernel runs.
+    const int64_t vblocks = ag.patch_blocks + ag.special_blocks;
+    const bool vec_ok = d % 256 == 0 && vblocks * kBlock < (int64_t{1} << 32) &&
+                        aligned16(patches) && aligned16(out) && aligned16(cam) &&
                         (nr == 0 || aligned16(reg)) && (!pbias || aligned16(pbias)) &&
                         (!pos || aligned16(pos));
+    const dim3 vgrid(static_cast<uint32_t>(vblocks));
     if (vec_ok) {
         switch (d / 256) {
             case 1:
-                assemble_kernel<TO, TP, 1><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows, seq, np, nr, n_var);
+                assemble_kernel<TO, TP, 1><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, np, nr, n_var);
                 return check_launch("assemble_tokens");
             case 2:
-                assemble_kernel<TO, TP, 2><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows, seq, np, nr, n_var);
+                assemble_kernel<TO, TP, 2><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, np, nr, n_var);
                 return check_launch("assemble_tokens");
             case 4:
-                assemble_kernel<TO, TP, 4><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows, seq, np, nr, n_var);
+                assemble_kernel<TO, TP, 4><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, np, nr, n_var);
                 return check_launch("assemble_tokens");
             case 8:
-                assemble_kernel<TO, TP, 8><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows, seq, np, nr, n_var);
+                assemble_kernel<TO, TP, 8><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, np, nr, n_var);
                 return check_launch("assemble_tokens");
             default: break;
         }

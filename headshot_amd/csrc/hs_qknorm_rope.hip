@@ -3,37 +3,32 @@
 // in sequence by model/block.rs:130-146), plus the stand-alone split_heads
 // and in-place rope_apply surface ops.
 //
-// Fast path (head_dim 64): a wave owns a tile of TPI consecutive tokens of
-// the token-major projection (S*T, H*64) across all H heads. A 64-wide head
-// vector is spread over a group of G lanes (8 for f16, 16 for f32; TPI =
-// 64/G tokens per tile), each lane holding one 16-byte vector, so LN(64) is a
-// G-lane DPP reduction with no LDS. Rotate-half RoPE pairs channel i with
-// i+32; the lane holding channels [i, i+V) sits opposite the lane holding
-// [32+i, 32+i+V) under the DPP row mirror (lane j <-> G-1-j), so each lane
-// gets its partner's values with one permute per element. Norm, rotation and
-// the reference's intermediate storage rounding stay in registers; each
-// element crosses HBM once each way.
+// Fast path (head_dim 64): a wave owns one token row of the token-major
+// projection (S*T, H*64) at a time, all H heads. A 64-wide head vector is
+// spread over a group of G lanes (8 for f16, 16 for f32), each lane holding
+// one 16-byte vector, so one load instruction covers 64/G heads and LN(64)
+// is a G-lane DPP reduction with no LDS. Rotate-half RoPE pairs channel i
+// with i+32; the lane holding channels [i, i+V) sits opposite the lane
+// holding [32+i, 32+i+V) under the DPP row mirror (lane j <-> G-1-j), so
+// each lane gets its partner's values with one permute per element. Norm,
+// rotation and the reference's intermediate storage rounding stay in
+// registers; each element crosses HBM once each way.
 //
-// Memory pattern: the wave issues the loads of HB heads before computing
-// (HB KiB in flight for f16). Each store instruction writes one head's TPI
-// consecutive token vectors, a contiguous 1 KiB of the head-major (S, H, T,
-// 64) output that attention consumes; over the tile the wave reads its TPI
-// token rows (TPI * 2 KiB for f16) completely.
+// Memory pattern: the row's loads are contiguous 1 KiB pieces (f16) issued
+// together, and a wave pipelines K consecutive rows so the next row's loads
+// are in flight while the current one is computed and stored. Each store
+// writes 64/G heads' 128-byte vectors of one token into the head-major
+// (S, H, T, 64) output that attention consumes.
 //
 // Generic path (any head_dim, either input layout): one wave per head vector,
 // lanes strided over the vector; used for rope_apply on head-major tensors
 // and for shapes the fast path does not cover.
-#include <type_traits>
-
 #include "hs_common.hpp"
 
 namespace hs {
 namespace {
 
 // Launch shape (overridable at build time for tuning sweeps).
-#ifndef HS_QK_HB
-#define HS_QK_HB 8  // heads per work unit (loads issued together)
-#endif
 #ifndef HS_QK_K
 #define HS_QK_K 2  // work units per wave (software-pipelined)
 #endif
@@ -50,105 +45,6 @@ int64_t persistent_blocks(int64_t work_waves) {
     const int64_t blocks = ceil_div(work_waves, kWavesPerBlock);
     return blocks < cap ? blocks : cap;
 }
-
-// Work unit of the tile kernel: TPI consecutive tokens x HB consecutive
-// heads. Units are numbered tile-major (unit = tile * (H/HB) + batch), and a
-// wave runs K consecutive units, so it sweeps whole token rows.
-template <typename T, int H, bool NORM, bool ROPE>
-struct QknTile {
-    static constexpr int D = 64;
-    static constexpr int V = Vec<T>::N;  // elements per lane
-    static constexpr int G = D / V;      // lanes per head vector
-    static constexpr int TPI = 64 / G;   // tokens per tile
-    static constexpr int HB = H < HS_QK_HB ? H : HS_QK_HB;
-    static constexpr int NB = H / HB;    // head batches per tile
-    static_assert(H % HB == 0, "head batches must tile H");
-    __host__ __device__ static int64_t units(int64_t tokens) { return ceil_div(tokens, TPI) * NB; }
-
-    const T* __restrict__ x;
-    const float* __restrict__ sin_tab;
-    const float* __restrict__ cos_tab;
-    T* __restrict__ out;
-    int64_t tokens;
-    int seq, prefix, ch, gsub;
-    bool upper;
-    float eps;
-    float wr[V], br[V];
-
-    __device__ __forceinline__ void load(u32x4 (&raw)[HB], int64_t unit) const {
-        const int64_t tok = (unit / NB) * TPI + gsub;
-        const int h0 = static_cast<int>(unit % NB) * HB;
-        const bool valid = tok < tokens;
-        const T* xr = x + tok * (H * D) + h0 * D + ch;
-#pragma unroll
-        for (int j = 0; j < HB; j++) {
-            raw[j] = u32x4{0u, 0u, 0u, 0u};
-            if (valid) raw[j] = ld_stream(xr + j * D);
-        }
-    }
-
-    __device__ __forceinline__ void process(const u32x4 (&raw)[HB], int64_t unit) const {
-        const int64_t tok = (unit / NB) * TPI + gsub;
-        const int h0 = static_cast<int>(unit % NB) * HB;
-        const bool valid = tok < tokens;
-        // tokens < 2^31 (checked on the host): 32-bit divide
-        const uint32_t s = valid ? static_cast<uint32_t>(tok) / static_cast<uint32_t>(seq) : 0u;
-        const int t = valid ? static_cast<int>(static_cast<uint32_t>(tok) -
-                                               s * static_cast<uint32_t>(seq))
-                            : 0;
-        const bool rot = ROPE && valid && t >= prefix;
-        float cs[V], sn[V];
-        if constexpr (ROPE) {
-            // lower lanes rotate by -sin, upper lanes by +sin:
-            // x' = x*cos + rot(x)*sin, rot(x) = concat(-x[32:], x[:32])
-            const int64_t row = rot ? static_cast<int64_t>(t - prefix) * D + ch : ch;
-            const float sg = upper ? 1.0f : -1.0f;
-#pragma unroll
-            for (int k = 0; k < V; k += 4) {
-                float4 c4 = make_float4(0.f, 0.f, 0.f, 0.f), s4 = c4;
-                if (rot) c4 = ld_f32x4(cos_tab + row + k), s4 = ld_f32x4(sin_tab + row + k);
-                cs[k] = c4.x, cs[k + 1] = c4.y, cs[k + 2] = c4.z, cs[k + 3] = c4.w;
-                sn[k] = sg * s4.x, sn[k + 1] = sg * s4.y, sn[k + 2] = sg * s4.z,
-                sn[k + 3] = sg * s4.w;
-            }
-        }
-        T* orow = out + (static_cast<int64_t>(s) * H + h0) * seq * D +
-                  static_cast<int64_t>(t) * D + ch;
-        const int64_t head_stride = static_cast<int64_t>(seq) * D;
-#pragma unroll
-        for (int j = 0; j < HB; j++) {
-            float f[V];
-            unpack(raw[j], f, T{});
-            if constexpr (NORM) {
-                float sum = 0.0f;
-#pragma unroll
-                for (int k = 0; k < V; k++) sum += f[k];
-                const float mean = group_sum<G>(sum) / static_cast<float>(D);
-                float q = 0.0f;
-#pragma unroll
-                for (int k = 0; k < V; k++) {
-                    const float d = f[k] - mean;
-                    q += d * d;
-                }
-                const float var = group_sum<G>(q) / static_cast<float>(D);
-                const float inv = rsqrtf(var + eps);
-#pragma unroll
-                for (int k = 0; k < V; k++)
-                    f[k] = storage_round((f[k] - mean) * inv * wr[k] + br[k], T{});
-            }
-            if constexpr (ROPE) {
-                // Every lane takes part in the permute; prefix tokens and
-                // padding lanes then keep their own value unchanged.
-#pragma unroll
-                for (int k = 0; k < V; k++) {
-                    const float partner = group_mirror<G>(f[k]);
-                    f[k] = rot ? fmaf(f[k], cs[k], partner * sn[k]) : f[k];
-                }
-            }
-            if (valid) st_stream(orow + j * head_stride, pack(f, T{}));
-        }
-    }
-};
 
 // Row mapping: a work unit is one token row (all H heads). A load
 // instruction covers HPI = 64/G heads, so the row is CH contiguous 1 KiB
@@ -232,28 +128,20 @@ struct QknRow {
     }
 };
 
-#ifndef HS_QK_ROWS
-#define HS_QK_ROWS 1  // 1: token-row work units, 0: token-tile work units
-#endif
-
-template <typename T, int H, bool NORM, bool ROPE>
-using QknUnit = typename std::conditional<HS_QK_ROWS != 0, QknRow<T, H, NORM, ROPE>,
-                                          QknTile<T, H, NORM, ROPE>>::type;
-
 // Each wave runs K consecutive units with a two-buffer software pipeline:
 // the loads of unit i+1 are in flight while unit i is normalised, rotated
 // and stored, so waves overlap memory with arithmetic instead of alternating
 // between them in lockstep.
 template <typename T, int H, bool NORM, bool ROPE, int K>
-__global__ __launch_bounds__(kBlock) void qkn_tile_kernel(
+__global__ __launch_bounds__(kBlock) void qkn_row_kernel(
     const T* __restrict__ x, const float* __restrict__ nw, const float* __restrict__ nb,
     const float* __restrict__ sin_tab, const float* __restrict__ cos_tab, T* __restrict__ out,
     int64_t tokens, int seq, int prefix, float eps) {
-    using Tile = QknUnit<T, H, NORM, ROPE>;
-    constexpr int G = Tile::G, V = Tile::V, HB = Tile::HB;
+    using Row = QknRow<T, H, NORM, ROPE>;
+    constexpr int G = Row::G, V = Row::V, HB = Row::HB;
     const int lane = lane_id();
     const int piece = lane % G;
-    Tile tl;
+    Row tl;
     tl.x = x, tl.sin_tab = sin_tab, tl.cos_tab = cos_tab, tl.out = out;
     tl.tokens = tokens, tl.seq = seq, tl.prefix = prefix, tl.eps = eps;
     tl.gsub = lane / G;
@@ -269,7 +157,7 @@ __global__ __launch_bounds__(kBlock) void qkn_tile_kernel(
             tl.br[k] = b4.x, tl.br[k + 1] = b4.y, tl.br[k + 2] = b4.z, tl.br[k + 3] = b4.w;
         }
     }
-    const int64_t units = Tile::units(tokens);
+    const int64_t units = Row::units(tokens);
     const int64_t u0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * K;
     if (u0 >= units) return;  // wave-uniform: the kernel has no barriers
     const int64_t u_end = u0 + K < units ? u0 + K : units;
@@ -351,14 +239,14 @@ __global__ __launch_bounds__(kBlock) void qkn_generic_kernel(
 }
 
 template <typename T, int H, bool NORM, bool ROPE>
-hs_status launch_tile(hipStream_t st, const void* x, const float* nw, const float* nb,
+hs_status launch_rows(hipStream_t st, const void* x, const float* nw, const float* nb,
                       const float* sn, const float* cs, void* out, int64_t tokens, int seq,
                       int prefix, float eps) {
-    using Tile = QknUnit<T, H, NORM, ROPE>;
+    using Row = QknRow<T, H, NORM, ROPE>;
     constexpr int K = HS_QK_K;
-    const int64_t units = Tile::units(tokens);
+    const int64_t units = Row::units(tokens);
     const int64_t blocks = ceil_div(ceil_div(units, K), kWavesPerBlock);
-    qkn_tile_kernel<T, H, NORM, ROPE, K>
+    qkn_row_kernel<T, H, NORM, ROPE, K>
         <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
             static_cast<const T*>(x), nw, nb, sn, cs, static_cast<T*>(out), tokens, seq, prefix,
             eps);
@@ -366,17 +254,17 @@ hs_status launch_tile(hipStream_t st, const void* x, const float* nw, const floa
 }
 
 template <typename T, int H>
-hs_status launch_tile_flags(hipStream_t st, const void* x, const float* nw, const float* nb,
+hs_status launch_rows_flags(hipStream_t st, const void* x, const float* nw, const float* nb,
                             const float* sn, const float* cs, void* out, int64_t tokens, int seq,
                             int prefix, float eps) {
     const bool norm = nw != nullptr, rope = sn != nullptr && prefix < seq;
     if (norm && rope)
-        return launch_tile<T, H, true, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
+        return launch_rows<T, H, true, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
     if (norm)
-        return launch_tile<T, H, true, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
+        return launch_rows<T, H, true, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
     if (rope)
-        return launch_tile<T, H, false, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
-    return launch_tile<T, H, false, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
+        return launch_rows<T, H, false, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
+    return launch_rows<T, H, false, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
 }
 
 template <typename T>
@@ -391,7 +279,7 @@ hs_status launch_generic(hipStream_t st, const void* x, bool in_head_major, cons
     return check_launch("qknorm_rope");
 }
 
-// Token-major input: the tile path when head_dim is 64, H is one of the
+// Token-major input: the row path when head_dim is 64, H is one of the
 // instantiated head counts and every pointer is 16-byte aligned.
 template <typename T>
 hs_status dispatch_tok(hipStream_t st, const void* x, const float* nw, const float* nb,
@@ -400,12 +288,16 @@ hs_status dispatch_tok(hipStream_t st, const void* x, const float* nw, const flo
     const bool ptrs_ok = aligned16(x) && aligned16(out) &&
                          (!nw || (aligned16(nw) && aligned16(nb))) &&
                          (!sn || (aligned16(sn) && aligned16(cs)));
-    if (d == 64 && ptrs_ok) {
-        const int64_t tokens = static_cast<int64_t>(s) * t;
+    const int64_t tokens = static_cast<int64_t>(s) * t;
+    // The dispatch packet counts work-items in 32 bits: the row grid has one
+    // wave per K tokens; beyond that the persistent generic kernel runs.
+    const int64_t row_blocks = ceil_div(ceil_div(tokens, int64_t{HS_QK_K}), int64_t{kWavesPerBlock});
+    const bool grid_ok = row_blocks * kBlock < (int64_t{1} << 32);
+    if (d == 64 && ptrs_ok && grid_ok) {
         switch (h) {
-            case 8: return launch_tile_flags<T, 8>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
-            case 16: return launch_tile_flags<T, 16>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
-            case 32: return launch_tile_flags<T, 32>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+            case 8: return launch_rows_flags<T, 8>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+            case 16: return launch_rows_flags<T, 16>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
+            case 32: return launch_rows_flags<T, 32>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
             default: break;
         }
     }
