@@ -43,6 +43,9 @@ SIGNATURES = {
     "hs_bias_ls_residual": (_S, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32]),
     "hs_assemble_tokens": (_S, [_P, _I32, _P, _I32, _P, _P, _P, _P, _P,
                                 _I32, _I32, _I32, _I32, _I32]),
+    "hs_attention": (_S, [_P, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _I32]),
+    "hs_attn_merge": (_S, [_P, _I32, _P, _P, _I32, _I32, _I32, _I32]),
+    "hs_attention_merged": (_S, [_P, _I32, _P, _P, _P, _P, _I32, _I32, _I32, _I32]),
     "hs_rope_periods": (None, [_P]),
     "hs_rope_tables": (_S, [_P, _I32, _I32, _P, _P]),
 }

@@ -29,6 +29,7 @@ HIP_SOURCES = [
     "hs_qknorm_rope.hip",
     "hs_elementwise.hip",
     "hs_assemble.hip",
+    "hs_attention.hip",
 ]
 # Host-only C++ (bit-exact RoPE tables): no FMA contraction.
 CXX_SOURCES = ["hs_rope_tables.cpp"]

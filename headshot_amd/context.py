@@ -179,6 +179,28 @@ class HipContext:
                      _dev(out, "out"), x.numel(), table.numel())
         return out
 
+    def attention(self, q, k, v) -> torch.Tensor:
+        """engine/ops.rs:225-253: non-causal attention over head-major
+        (S, H, T, D) q, k, v; D 64 (f32/f16) or 128 (f32)."""
+        assert q.dim() == 4, "attention wants (S,H,T,D)"
+        s, h, t, d = q.shape
+        assert tuple(k.shape) == tuple(q.shape), "attention: k shape"
+        assert tuple(v.shape) == tuple(q.shape), "attention: v shape"
+        assert q.dtype == k.dtype == v.dtype, "attention: dtype"
+        out = self.empty_typed((s, h, t, d), q.dtype)
+        self._launch("attention", self.lib.hs_attention, _dt(q), _dev(q, "q"), _dev(k, "k"),
+                     _dev(v, "v"), _dev(out, "out"), s, h, t, d)
+        return out
+
+    def attn_merge(self, x) -> torch.Tensor:
+        """engine/ops.rs:255-267: (S, H, T, D) → (S·T, H·D)."""
+        assert x.dim() == 4, "attn_merge wants (S,H,T,D)"
+        s, h, t, d = x.shape
+        out = self.empty_typed((s * t, h * d), x.dtype)
+        self._launch("attn_merge", self.lib.hs_attn_merge, _dt(x), _dev(x, "x"),
+                     _dev(out, "out"), s, h, t, d)
+        return out
+
     # --------------------------------------------------------------- fused ops
 
     def qknorm_rope(self, x_tok, s: int, t: int, h: int, d: int, norm=None, rope=None,
@@ -203,6 +225,21 @@ class HipContext:
         assert out.dtype == x_tok.dtype and out.numel() == x_tok.numel(), "out shape/dtype"
         self._launch("qknorm_rope", self.lib.hs_qknorm_rope, _dt(x_tok), _dev(x_tok, "x"), nw, nb,
                      sn, cs, _dev(out, "out"), s, t, h, d, prefix, eps)
+        return out
+
+    def attention_merged(self, q, k, v, out=None) -> torch.Tensor:
+        """attention + attn_merge (model/block.rs:148-149) in one pass:
+        head-major (S, H, T, D) q, k, v → token-major (S·T, H·D)."""
+        assert q.dim() == 4, "attention wants (S,H,T,D)"
+        s, h, t, d = q.shape
+        assert tuple(k.shape) == tuple(q.shape), "attention: k shape"
+        assert tuple(v.shape) == tuple(q.shape), "attention: v shape"
+        assert q.dtype == k.dtype == v.dtype, "attention: dtype"
+        if out is None:
+            out = self.empty_typed((s * t, h * d), q.dtype)
+        assert out.dtype == q.dtype and out.numel() == q.numel(), "out shape/dtype"
+        self._launch("attention_merged", self.lib.hs_attention_merged, _dt(q), _dev(q, "q"),
+                     _dev(k, "k"), _dev(v, "v"), _dev(out, "out"), s, h, t, d)
         return out
 
     def bias_gelu(self, x, bias=None, out=None) -> torch.Tensor:

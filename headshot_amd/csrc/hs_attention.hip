@@ -1,0 +1,464 @@
+// Non-causal attention for gfx950 (replaces the reference's attention.wesl
+// and attn_merge.wesl, dispatched by engine/ops.rs:228-267 and called by
+// model/block.rs:148-149): softmax(q k^T / sqrt(d)) v per (frame, head) over
+// head-major (S, H, T, D) tensors, with the softmax statistics and the
+// accumulation in f32, plus the (S, H, T, D) -> (S*T, H*D) head merge.
+//
+// Fast path (f16, D = 64): flash attention on the matrix cores. A wave owns
+// 32 queries; a workgroup of kWaves waves shares 64-key K/V tiles staged in
+// LDS (double-buffered, next tile prefetched into registers while the
+// current one computes). The wave computes the transposed score block
+// S^T = K Q^T with v_mfma_f32_32x32x16_f16, so each lane holds one query's
+// column (16 keys per 32-key block, lanes l and l+32 splitting the keys):
+// the online-softmax max needs one cross-half exchange per tile and the row
+// sums none until the end. P^T is rounded to f16 in registers and fed
+// straight back as the B operand of O^T += V^T P^T; V is transposed while it
+// is written to LDS, with the key order inside each 16-key group permuted
+// (key bits 2 and 3 swapped) to match the order in which the score
+// accumulator holds P^T, so every operand is one 16-byte LDS read. The
+// output rescale is skipped when no query's running max changed (the factor
+// would be exactly 1). Workgroups are ordered XCD-aware: all query tiles of
+// one (frame, head) run on one XCD, so its K/V stream through that XCD's L2.
+//
+// Generic path (f32, or D = 128): one thread per query over LDS-staged f32
+// K/V tiles, the reference's per-key online softmax in its operand order.
+#include <math.h>
+
+#include "hs_common.hpp"
+
+namespace hs {
+namespace {
+
+typedef f16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kXcds = 8;
+
+// ---------------------------------------------------------------------------
+// flash attention, f16, D = 64
+
+#ifndef HS_ATT_WAVES
+#define HS_ATT_WAVES 4  // waves (32 queries each) per workgroup
+#endif
+constexpr int kD = 64;
+constexpr int kWaves = HS_ATT_WAVES;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kBM = 32 * kWaves;  // queries per workgroup
+constexpr int kBN = 64;           // keys per tile
+constexpr int kKPitch = kD + 8;   // LDS row pitch (halves) of K: 144 B, conflict-free b128 reads
+constexpr int kVPitch = kBN + 8;  // LDS row pitch (halves) of V^T
+constexpr int kKChunks = kBN * kD / 8;        // 16-byte chunks per K tile
+constexpr int kVPairs = (kBN / 2) * (kD / 8);  // (key pair, 8-channel) items per V tile
+constexpr int kKPer = kKChunks / kThreads;
+constexpr int kVPer = kVPairs / kThreads;
+static_assert(kKChunks % kThreads == 0 && kVPairs % kThreads == 0, "tile loads must be uniform");
+
+struct FlashSmem {
+    f16 k[2][kBN * kKPitch];
+    f16 vt[2][kD * kVPitch];
+};
+
+// Position of key j (0..63 within a tile) in a V^T row: bits 2 and 3
+// swapped, the order of P^T in the B operand (see the file comment).
+__device__ __forceinline__ int vt_pos(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
+
+// (a.lo16, b.lo16) and (a.hi16, b.hi16) as one word each.
+__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
+__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
+
+__device__ __forceinline__ h8 as_h8(u32x4 v) { return __builtin_bit_cast(h8, v); }
+
+__device__ __forceinline__ uint32_t pk_f16(float a, float b) {
+    f16x2 h;
+    h.x = static_cast<f16>(a), h.y = static_cast<f16>(b);
+    return h22u(h);
+}
+
+struct TileRegs {
+    u32x4 k[kKPer];
+    u32x4 v[kVPer][2];
+};
+
+// Loads the K/V rows [key0, key0 + 64) of one (frame, head); rows past the
+// sequence end are clamped to the last row (their scores are masked).
+__device__ __forceinline__ void load_tile(TileRegs& r, const f16* kb, const f16* vb, int key0,
+                                          int t, int tid) {
+#pragma unroll
+    for (int i = 0; i < kKPer; i++) {
+        const int c = tid + i * kThreads;
+        const int row = min(key0 + c / 8, t - 1);
+        r.k[i] = ld16(kb + static_cast<int64_t>(row) * kD + (c % 8) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < kVPer; i++) {
+        const int c = tid + i * kThreads;
+        const int key = key0 + (c / 8) * 2;
+        const int r0 = min(key, t - 1), r1 = min(key + 1, t - 1);
+        r.v[i][0] = ld16(vb + static_cast<int64_t>(r0) * kD + (c % 8) * 8);
+        r.v[i][1] = ld16(vb + static_cast<int64_t>(r1) * kD + (c % 8) * 8);
+    }
+}
+
+__device__ __forceinline__ void store_tile(const TileRegs& r, FlashSmem& sm, int buf, int tid) {
+#pragma unroll
+    for (int i = 0; i < kKPer; i++) {
+        const int c = tid + i * kThreads;
+        st16(&sm.k[buf][(c / 8) * kKPitch + (c % 8) * 8], r.k[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kVPer; i++) {
+        const int c = tid + i * kThreads;
+        const int pos = vt_pos((c / 8) * 2);  // even; key + 1 lands at pos + 1
+        const int d0 = (c % 8) * 8;
+        uint32_t* col = reinterpret_cast<uint32_t*>(&sm.vt[buf][pos]);
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            col[((d0 + 2 * w) * kVPitch) / 2] = pack_lo(r.v[i][0][w], r.v[i][1][w]);
+            col[((d0 + 2 * w + 1) * kVPitch) / 2] = pack_hi(r.v[i][0][w], r.v[i][1][w]);
+        }
+    }
+}
+
+// grid.x = kXcds * ceil(SH / kXcds) * QT workgroups; workgroup b runs on XCD
+// b % kXcds and takes (frame*head) index sh = (b / kXcds / QT) * kXcds +
+// b % kXcds, query tile (b / kXcds) % QT.
+__global__ __launch_bounds__(kThreads) void flash_f16_kernel(
+    const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
+    f16* __restrict__ out, int sh_count, int heads, int t, int qtiles, float c,
+    int token_major) {
+    __shared__ FlashSmem sm;
+    const int b = blockIdx.x;
+    const int slot = b / kXcds;
+    const int sh = (slot / qtiles) * kXcds + b % kXcds;
+    if (sh >= sh_count) return;  // workgroup-uniform, before any barrier
+    const int qt = slot % qtiles;
+    const int tid = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = tid >> 6;
+    const int n = lane & 31, hh = lane >> 5;
+    const int64_t base = static_cast<int64_t>(sh) * t * kD;
+    const f16* qb = q + base;
+    const f16* kb = k + base;
+    const f16* vb = v + base;
+
+    // Q^T as the B operand: lane (n, hh) holds q[n][16 ks + 8 hh .. + 8).
+    const int qi = qt * kBM + wave * 32 + n;
+    const int qc = min(qi, t - 1);
+    h8 qa[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) qa[ks] = as_h8(ld16(qb + static_cast<int64_t>(qc) * kD + 16 * ks + 8 * hh));
+
+    f32x16 o0 = {}, o1 = {};
+    float m = -INFINITY, l = 0.0f;
+    const int ntiles = static_cast<int>(ceil_div(t, kBN));
+
+    TileRegs pre;
+    load_tile(pre, kb, vb, 0, t, tid);
+    store_tile(pre, sm, 0, tid);
+    __syncthreads();
+
+    for (int j = 0; j < ntiles; j++) {
+        const int cur = j & 1;
+        if (j + 1 < ntiles) load_tile(pre, kb, vb, (j + 1) * kBN, t, tid);
+
+        // S^T (keys x queries): s0 keys [0, 32), s1 keys [32, 64) of the tile;
+        // register r of lane (n, hh) is key 8 (r / 4) + 4 hh + r % 4.
+        f32x16 s0 = {}, s1 = {};
+        const f16* ks0 = &sm.k[cur][n * kKPitch + 8 * hh];
+        const f16* ks1 = &sm.k[cur][(32 + n) * kKPitch + 8 * hh];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(ks0 + 16 * ks)), qa[ks], s0, 0, 0, 0);
+            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(ks1 + 16 * ks)), qa[ks], s1, 0, 0, 0);
+        }
+        const int key0 = j * kBN;
+        if (key0 + kBN > t) {  // partial last tile: keys past the end score -inf
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int kr = key0 + 8 * (r / 4) + 4 * hh + (r % 4);
+                if (kr >= t) s0[r] = -INFINITY;
+                if (kr + 32 >= t) s1[r] = -INFINITY;
+            }
+        }
+        float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+        for (int r = 1; r < 16; r++) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m, mx * c);
+        const float corr = __builtin_amdgcn_exp2f(m - m_new);
+        float ps = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            s0[r] = __builtin_amdgcn_exp2f(fmaf(s0[r], c, -m_new));
+            s1[r] = __builtin_amdgcn_exp2f(fmaf(s1[r], c, -m_new));
+            ps += s0[r] + s1[r];
+        }
+        l = fmaf(l, corr, ps);
+        m = m_new;
+        if (__any(corr != 1.0f)) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) o0[r] *= corr, o1[r] *= corr;
+        }
+        // P^T as f16 B operands: registers 8 kk .. 8 kk + 7 of s_kb.
+        u32x4 p[2][2];
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                p[0][kk][w] = pk_f16(s0[8 * kk + 2 * w], s0[8 * kk + 2 * w + 1]);
+                p[1][kk][w] = pk_f16(s1[8 * kk + 2 * w], s1[8 * kk + 2 * w + 1]);
+            }
+        // O^T (channels x queries) += V^T P^T; o0 channels [0, 32), o1 [32, 64).
+        const f16* vt0 = &sm.vt[cur][n * kVPitch + 8 * hh];
+        const f16* vt1 = &sm.vt[cur][(32 + n) * kVPitch + 8 * hh];
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+            for (int kk = 0; kk < 2; kk++) {
+                const int off = 32 * kb2 + 16 * kk;
+                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(vt0 + off)), as_h8(p[kb2][kk]), o0, 0, 0, 0);
+                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(vt1 + off)), as_h8(p[kb2][kk]), o1, 0, 0, 0);
+            }
+        if (j + 1 < ntiles) store_tile(pre, sm, cur ^ 1, tid);
+        __syncthreads();
+    }
+
+    const float lt = l + __shfl_xor(l, 32);
+    const float inv = 1.0f / lt;
+    if (qi >= t) return;
+    f16* orow;
+    if (token_major) {
+        const int s = sh / heads, h = sh - s * heads;
+        orow = out + ((static_cast<int64_t>(s) * t + qi) * heads + h) * kD;
+    } else {
+        orow = out + base + static_cast<int64_t>(qi) * kD;
+    }
+    // register r of o_mb is channel 32 mb + 8 (r / 4) + 4 hh + r % 4
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++) {
+        const int d0 = 8 * r4 + 4 * hh;
+        u32x2 w0, w1;
+        w0[0] = pk_f16(o0[4 * r4] * inv, o0[4 * r4 + 1] * inv);
+        w0[1] = pk_f16(o0[4 * r4 + 2] * inv, o0[4 * r4 + 3] * inv);
+        w1[0] = pk_f16(o1[4 * r4] * inv, o1[4 * r4 + 1] * inv);
+        w1[1] = pk_f16(o1[4 * r4 + 2] * inv, o1[4 * r4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d0) = w0;
+        *reinterpret_cast<u32x2*>(orow + 32 + d0) = w1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// generic attention: one thread per query, f32 math in the reference's order
+
+constexpr int kGThreads = 256;
+constexpr int kGKeys = 32;  // keys per LDS tile
+
+template <typename T, int D>
+__global__ __launch_bounds__(kGThreads) void attention_generic_kernel(
+    const T* __restrict__ q, const T* __restrict__ k, const T* __restrict__ v, T* __restrict__ out,
+    int heads, int t, float scale, int token_major) {
+    __shared__ float ks[kGKeys][D];
+    __shared__ float vs[kGKeys][D];
+    const int sh = blockIdx.y;
+    const int64_t base = static_cast<int64_t>(sh) * t * D;
+    const int qi = blockIdx.x * kGThreads + threadIdx.x;
+    const int qc = min(qi, t - 1);
+    float qv[D], acc[D];
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+        qv[d] = static_cast<float>(q[base + static_cast<int64_t>(qc) * D + d]);
+        acc[d] = 0.0f;
+    }
+    float m = -3.4e38f, l = 0.0f;
+    for (int k0 = 0; k0 < t; k0 += kGKeys) {
+        const int nk = min(kGKeys, t - k0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < kGKeys * D; i += kGThreads) {
+            const int r = i / D, d = i % D;
+            const int row = min(k0 + r, t - 1);
+            ks[r][d] = static_cast<float>(k[base + static_cast<int64_t>(row) * D + d]);
+            vs[r][d] = static_cast<float>(v[base + static_cast<int64_t>(row) * D + d]);
+        }
+        __syncthreads();
+        for (int kk = 0; kk < nk; kk++) {
+            // vec4 partial sums, then their horizontal sum (attention.wesl:65-70)
+            float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int d = 0; d < D; d += 4)
+#pragma unroll
+                for (int e = 0; e < 4; e++) s4[e] += qv[d + e] * ks[kk][d + e];
+            const float score = (s4[0] + s4[1] + s4[2] + s4[3]) * scale;
+            const float m_new = fmaxf(m, score);
+            const float corr = expf(m - m_new);
+            const float e = expf(score - m_new);
+            l = l * corr + e;
+#pragma unroll
+            for (int d = 0; d < D; d++) acc[d] = acc[d] * corr + e * vs[kk][d];
+            m = m_new;
+        }
+    }
+    if (qi >= t) return;
+    const float inv = 1.0f / l;
+    T* orow;
+    if (token_major) {
+        const int s = sh / heads, h = sh - s * heads;
+        orow = out + ((static_cast<int64_t>(s) * t + qi) * heads + h) * D;
+    } else {
+        orow = out + base + static_cast<int64_t>(qi) * D;
+    }
+#pragma unroll
+    for (int d = 0; d < D; d++) orow[d] = static_cast<T>(acc[d] * inv);
+}
+
+// ---------------------------------------------------------------------------
+// head merge: (S, H, T, D) -> (S*T, H*D), 16-byte vectors when D allows
+
+template <typename T>
+__global__ __launch_bounds__(256) void merge_vec_kernel(const T* __restrict__ x, T* __restrict__ out,
+                                                        int64_t nvec, int heads, int t, int d) {
+    constexpr int V = Vec<T>::N;
+    const int dv = d / V;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < nvec; i += stride) {
+        // i enumerates output vectors: token row r = s*T + ti, head h, chunk c
+        const int c = static_cast<int>(i % dv);
+        const int64_t rh = i / dv;
+        const int h = static_cast<int>(rh % heads);
+        const int64_t r = rh / heads;
+        const int64_t s = r / t;
+        const int ti = static_cast<int>(r - s * t);
+        const int64_t src = ((s * heads + h) * t + ti) * d + static_cast<int64_t>(c) * V;
+        st_stream(out + i * V, ld_stream(x + src));
+    }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void merge_scalar_kernel(const T* __restrict__ x, T* __restrict__ out,
+                                                           int64_t total, int heads, int t, int d) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += stride) {
+        const int dd = static_cast<int>(i % d);
+        const int64_t rh = i / d;
+        const int h = static_cast<int>(rh % heads);
+        const int64_t r = rh / heads;
+        const int64_t s = r / t;
+        const int ti = static_cast<int>(r - s * t);
+        out[i] = x[((s * heads + h) * t + ti) * d + dd];
+    }
+}
+
+int64_t grid_blocks(int64_t items) {
+    const int64_t cap = static_cast<int64_t>(num_cus()) * 8;
+    const int64_t blocks = ceil_div(items, 256);
+    return blocks < 1 ? 1 : (blocks < cap ? blocks : cap);
+}
+
+hs_status check_attention(const char* op, hs_dtype dt, const void* q, const void* k,
+                          const void* v, const void* out, int32_t s, int32_t h, int32_t t,
+                          int32_t d) {
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "%s: unknown dtype", op);
+    if (s < 0 || h < 0 || t < 0 || d <= 0)
+        return fail(HS_EINVAL, "%s: shape (%d, %d, %d, %d)", op, s, h, t, d);
+    const int64_t n = static_cast<int64_t>(s) * h * t * d;
+    if (static_cast<int64_t>(s) * h * t >= (int64_t{1} << 31) || n >= (int64_t{1} << 40))
+        return fail(HS_EINVAL, "%s: S*H*T must be below 2^31", op);
+    if (n == 0) return HS_OK;
+    if (!q || !k || !v || !out) return fail(HS_EINVAL, "%s: null buffer", op);
+    const int64_t bytes = n * dtype_size(dt);
+    if (overlaps(out, bytes, q, bytes) || overlaps(out, bytes, k, bytes) ||
+        overlaps(out, bytes, v, bytes))
+        return fail(HS_EINVAL, "%s: out overlaps an input", op);
+    return HS_OK;
+}
+
+hs_status launch_attention(hipStream_t st, hs_dtype dt, const void* q, const void* k,
+                           const void* v, void* out, int s, int h, int t, int d, int token_major) {
+    const int sh = s * h;
+    const float scale = 1.0f / sqrtf(static_cast<float>(d));
+    const bool flash_ok = dt == HS_F16 && d == kD && aligned16(q) && aligned16(k) && aligned16(v) &&
+                          (reinterpret_cast<uintptr_t>(out) & 7u) == 0;
+    if (flash_ok) {
+        const int qtiles = static_cast<int>(ceil_div(t, kBM));
+        const int64_t blocks = static_cast<int64_t>(kXcds) * ceil_div(sh, kXcds) * qtiles;
+        if (blocks < (int64_t{1} << 31) / kThreads) {
+            const float c = scale * 1.4426950408889634f;  // scores enter exp2
+            flash_f16_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st>>>(
+                static_cast<const f16*>(q), static_cast<const f16*>(k), static_cast<const f16*>(v),
+                static_cast<f16*>(out), sh, h, t, qtiles, c, token_major);
+            return check_launch("attention");
+        }
+    }
+    if (sh > 65535) return fail(HS_EUNSUPPORTED, "attention: S*H above 65535 on the generic path");
+    const dim3 grid(static_cast<uint32_t>(ceil_div(t, kGThreads)), static_cast<uint32_t>(sh));
+    if (d == 64 && dt == HS_F16)
+        attention_generic_kernel<f16, 64><<<grid, dim3(kGThreads), 0, st>>>(
+            static_cast<const f16*>(q), static_cast<const f16*>(k), static_cast<const f16*>(v),
+            static_cast<f16*>(out), h, t, scale, token_major);
+    else if (d == 64)
+        attention_generic_kernel<float, 64><<<grid, dim3(kGThreads), 0, st>>>(
+            static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+            static_cast<float*>(out), h, t, scale, token_major);
+    else
+        attention_generic_kernel<float, 128><<<grid, dim3(kGThreads), 0, st>>>(
+            static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+            static_cast<float*>(out), h, t, scale, token_major);
+    return check_launch("attention");
+}
+
+hs_status attention_entry(const char* op, hs_stream_t stream, hs_dtype dt, const void* q,
+                          const void* k, const void* v, void* out, int32_t s, int32_t h,
+                          int32_t t, int32_t d, int token_major) {
+    const hs_status rc = check_attention(op, dt, q, k, v, out, s, h, t, d);
+    if (rc != HS_OK || static_cast<int64_t>(s) * h * t == 0) return rc;
+    // head_dim 64 (f32 and f16) or 128 (f32 only), as engine/ops.rs:233-238
+    if (!(d == 64 || (d == 128 && dt == HS_F32)))
+        return fail(HS_EUNSUPPORTED, "%s: unsupported head_dim %d for this dtype", op, d);
+    return launch_attention(static_cast<hipStream_t>(stream), dt, q, k, v, out, s, h, t, d,
+                            token_major);
+}
+
+}  // namespace
+}  // namespace hs
+
+extern "C" hs_status hs_attention(hs_stream_t stream, hs_dtype dt, const void* q, const void* k,
+                                  const void* v, void* out, int32_t s, int32_t h, int32_t t,
+                                  int32_t d) {
+    return hs::attention_entry("attention", stream, dt, q, k, v, out, s, h, t, d, 0);
+}
+
+extern "C" hs_status hs_attention_merged(hs_stream_t stream, hs_dtype dt, const void* q,
+                                         const void* k, const void* v, void* out, int32_t s,
+                                         int32_t h, int32_t t, int32_t d) {
+    return hs::attention_entry("attention_merged", stream, dt, q, k, v, out, s, h, t, d, 1);
+}
+
+extern "C" hs_status hs_attn_merge(hs_stream_t stream, hs_dtype dt, const void* x, void* out,
+                                   int32_t s, int32_t h, int32_t t, int32_t d) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "attn_merge: unknown dtype");
+    if (s < 0 || h < 0 || t < 0 || d < 0)
+        return fail(HS_EINVAL, "attn_merge: shape (%d, %d, %d, %d)", s, h, t, d);
+    const int64_t total = static_cast<int64_t>(s) * h * t * d;
+    if (total >= (int64_t{1} << 40)) return fail(HS_EINVAL, "attn_merge: tensor too large");
+    if (total == 0) return HS_OK;
+    if (!x || !out) return fail(HS_EINVAL, "attn_merge: null buffer");
+    const int64_t bytes = total * dtype_size(dt);
+    if (overlaps(out, bytes, x, bytes)) return fail(HS_EINVAL, "attn_merge: out overlaps x");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int per = dt == HS_F16 ? 8 : 4;
+    if (d % per == 0 && aligned16(x) && aligned16(out)) {
+        const int64_t nvec = total / per;
+        const dim3 grid(static_cast<uint32_t>(grid_blocks(nvec)));
+        if (dt == HS_F16)
+            merge_vec_kernel<f16><<<grid, dim3(256), 0, st>>>(static_cast<const f16*>(x), static_cast<f16*>(out), nvec, h, t, d);
+        else
+            merge_vec_kernel<float><<<grid, dim3(256), 0, st>>>(static_cast<const float*>(x), static_cast<float*>(out), nvec, h, t, d);
+        return check_launch("attn_merge");
+    }
+    const dim3 grid(static_cast<uint32_t>(grid_blocks(total)));
+    if (dt == HS_F16)
+        merge_scalar_kernel<f16><<<grid, dim3(256), 0, st>>>(static_cast<const f16*>(x), static_cast<f16*>(out), total, h, t, d);
+    else
+        merge_scalar_kernel<float><<<grid, dim3(256), 0, st>>>(static_cast<const float*>(x), static_cast<float*>(out), total, h, t, d);
+    return check_launch("attn_merge");
+}

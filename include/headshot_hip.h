@@ -159,6 +159,31 @@ hs_status hs_assemble_tokens(hs_stream_t stream, hs_dtype out_dt, const void* pa
                              int32_t r, int32_t d, int32_t n_var);
 
 /* ---------------------------------------------------------------------- */
+/* Attention                                                                */
+
+/* GpuContext::attention (engine/ops.rs:225-253; shaders/attention.wesl):
+ * non-causal softmax(q k^T / sqrt(D)) v for each of the S*H sequences of
+ * head-major q, k, v (S, H, T, D); out is (S, H, T, D) in the same dtype.
+ * Softmax statistics and accumulation are f32. D is 64 (f32 or f16) or 128
+ * (f32 only), as the reference's kernel variants; other combinations return
+ * HS_EUNSUPPORTED. out must not overlap q, k or v. */
+hs_status hs_attention(hs_stream_t stream, hs_dtype dt, const void* q, const void* k,
+                       const void* v, void* out, int32_t s, int32_t h, int32_t t, int32_t d);
+
+/* GpuContext::attn_merge (engine/ops.rs:255-267; shaders/attn_merge.wesl):
+ * (S, H, T, D) head-major -> (S*T, H*D) token-major, an exact copy. out must
+ * not overlap x. */
+hs_status hs_attn_merge(hs_stream_t stream, hs_dtype dt, const void* x, void* out, int32_t s,
+                        int32_t h, int32_t t, int32_t d);
+
+/* attention followed by attn_merge (model/block.rs:148-149) in one pass: the
+ * same values as hs_attention, written token-major (S*T, H*D) into out, so
+ * the head-major attention output never reaches memory. */
+hs_status hs_attention_merged(hs_stream_t stream, hs_dtype dt, const void* q, const void* k,
+                              const void* v, void* out, int32_t s, int32_t h, int32_t t,
+                              int32_t d);
+
+/* ---------------------------------------------------------------------- */
 /* Host-side RoPE tables (computed once per session, as the reference does) */
 
 /* rope::periods (engine/rope.rs:5-10): out16[i] = 100^(2i/32) in f32. */

@@ -251,6 +251,52 @@ void or_attn_merge(int dt, const void* x, void* out, int32_t s, int32_t t, int32
 }
 
 /* ------------------------------------------------------------------------ */
+/* Attention (shaders/attention.wesl:36-88, dispatched by engine/ops.rs:228-253) */
+
+/* One query of one (frame, head) sequence at a time, exactly as the shader's
+ * thread does: q in f32, per key a vec4-lane dot product summed x+y+z+w and
+ * scaled, then the online softmax update (running max m, denominator l,
+ * f32 accumulator), and finally acc / l stored as Elem. Queries listed in
+ * q_idx (nq of them; q_idx NULL = all t in order) are computed for every
+ * sequence; out is (S*H, nq, D). */
+void or_attention(int dt, const void* q, const void* k, const void* v, void* out, int32_t s,
+                  int32_t h, int32_t t, int32_t d, const int32_t* q_idx, int32_t nq) {
+    const float scale = 1.0f / sqrtf((float)d); /* engine/ops.rs:242 */
+    const int64_t nseq = (int64_t)s * h;
+    if (!q_idx) nq = t;
+    if (d > 128 || d % 4) return;
+#pragma omp parallel for collapse(2) schedule(dynamic, 4)
+    for (int64_t sh = 0; sh < nseq; sh++)
+        for (int32_t j = 0; j < nq; j++) {
+            const int64_t base = sh * t * d;
+            const int32_t qi = q_idx ? q_idx[j] : j;
+            float qv[128], acc[128];
+            for (int32_t dd = 0; dd < d; dd++) {
+                qv[dd] = ld(dt, q, base + (int64_t)qi * d + dd);
+                acc[dd] = 0.0f;
+            }
+            float m = -3.4e38f, l = 0.0f;
+            for (int32_t kk = 0; kk < t; kk++) {
+                const int64_t kb = base + (int64_t)kk * d;
+                float s4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                for (int32_t dd = 0; dd < d; dd += 4)
+                    for (int e = 0; e < 4; e++) s4[e] += qv[dd + e] * ld(dt, k, kb + dd + e);
+                const float score = (s4[0] + s4[1] + s4[2] + s4[3]) * scale;
+                const float m_new = fmaxf(m, score);
+                const float corr = expf(m - m_new);
+                const float e = expf(score - m_new);
+                l = l * corr + e;
+                for (int32_t dd = 0; dd < d; dd++)
+                    acc[dd] = acc[dd] * corr + e * ld(dt, v, kb + dd);
+                m = m_new;
+            }
+            const float inv_l = 1.0f / l;
+            const int64_t o = (sh * nq + j) * d;
+            for (int32_t dd = 0; dd < d; dd++) st(dt, out, o + dd, acc[dd] * inv_l);
+        }
+}
+
+/* ------------------------------------------------------------------------ */
 /* RoPE apply (shaders/rope_apply.wesl:30-57)                                */
 
 /* One head vector in f32: pairs (dp, dp+half); table row (t - prefix). */

@@ -45,6 +45,12 @@ void or_layernorm(int dt, const void* x, const float* w, const float* b, void* o
 void or_split_heads(int dt, const void* x, void* out, int32_t s, int32_t t, int32_t h, int32_t d);
 /* shaders/attn_merge.wesl: (S, H, T, D) -> (S*T, H*D). */
 void or_attn_merge(int dt, const void* x, void* out, int32_t s, int32_t t, int32_t h, int32_t d);
+/* shaders/attention.wesl:36-88 (engine/ops.rs:228-253): head-major q, k, v
+ * (S, H, T, D), D a multiple of 4 up to 128, scale 1/sqrt(D). Computes the
+ * queries q_idx[0..nq) (q_idx NULL: all T) of every sequence into out
+ * (S*H, nq, D). */
+void or_attention(int dt, const void* q, const void* k, const void* v, void* out, int32_t s,
+                  int32_t h, int32_t t, int32_t d, const int32_t* q_idx, int32_t nq);
 /* shaders/rope_apply.wesl:30-57, in place on (S, H, T, D). */
 void or_rope_apply(int dt, void* x, const float* sin_tab, const float* cos_tab, int32_t s,
                    int32_t h, int32_t t, int32_t d, int32_t prefix);

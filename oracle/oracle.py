@@ -26,6 +26,9 @@ rope_apply_cpu/apply   complex rotation (lo + i hi) * exp(i theta) in f64;
 layernorm              float64 torch.nn.functional.layer_norm; the reference
                        test layernorm_matches_cpu (tests/kernels.rs:100-126)
 split_heads/merge      numpy reshape/transpose (exact); tests/kernels.rs:241-274
+attention              float64 full-matrix softmax as tests/kernels.rs:194-238
+                       (1e-4); invariants: constant V rows, q = 0 gives the
+                       mean of V, key permutation, T = 1 returns v
 gelu                   f64 math.erf at 1e-5 (tests/kernels.rs:128-147)
 residual_ls, bias,     numpy closed forms in float64 vs tolerance; f16
 cast, tiled_add        rounding points checked against numpy float16
@@ -82,6 +85,7 @@ def _declare(L):
         "or_layernorm": (None, [ctypes.c_int, _P, _P, _P, _P, _I64, _I32, _F]),
         "or_split_heads": (None, [ctypes.c_int, _P, _P, _I32, _I32, _I32, _I32]),
         "or_attn_merge": (None, [ctypes.c_int, _P, _P, _I32, _I32, _I32, _I32]),
+        "or_attention": (None, [ctypes.c_int, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _I32]),
         "or_rope_apply": (None, [ctypes.c_int, _P, _P, _P, _I32, _I32, _I32, _I32, _I32]),
         "or_erf_as": (_F, [_F]),
         "or_gelu": (None, [ctypes.c_int, _P, _P, _I64]),
@@ -199,6 +203,23 @@ def attn_merge(x: np.ndarray) -> np.ndarray:
     s, h, t, d = x.shape
     out = np.empty((s * t, h * d), x.dtype)
     lib().or_attn_merge(_dt(x), _ptr(x), _ptr(out), s, t, h, d)
+    return out
+
+
+def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, q_idx=None) -> np.ndarray:
+    """attention.wesl over head-major (S, H, T, D). With ``q_idx`` (query
+    indices) only those queries are computed: the result is (S, H, len, D)."""
+    q, k, v = (np.ascontiguousarray(a) for a in (q, k, v))
+    assert q.shape == k.shape == v.shape and q.dtype == k.dtype == v.dtype
+    s, h, t, d = q.shape
+    assert d % 4 == 0 and d <= 128
+    idx = None if q_idx is None else np.ascontiguousarray(q_idx, dtype=np.int32)
+    nq = t if idx is None else idx.size
+    if idx is not None:
+        assert idx.size == 0 or (idx.min() >= 0 and idx.max() < t)
+    out = np.empty((s, h, nq, d), q.dtype)
+    lib().or_attention(_dt(q), _ptr(q), _ptr(k), _ptr(v), _ptr(out), s, h, t, d,
+                       None if idx is None else _ptr(idx), nq)
     return out
 
 

@@ -1,0 +1,199 @@
+"""Attention (hs_attention, hs_attention_merged) and the head merge
+(hs_attn_merge) against the oracle on the reference's own test shapes, at
+tile edges, and at full size against a float32 torch reference on the device.
+
+Bars:
+- f32: within 1e-5 (abs + rel) of the oracle, and 1e-4 absolute of the
+  float64 naive softmax as tests/kernels.rs:232-235.
+- f16: within 2e-3*max(1,|e|) of the oracle's f16 result (f32 math on the
+  same f16 inputs, output rounded). The matrix-core path rounds the softmax
+  weights to f16 for the P.V product; this bound covers that.
+- f16 vs f32 on the same values: 5e-3 relative (tests/kernels.rs:377-401).
+- attn_merge bit-exact; attention_merged bit-exact against
+  attn_merge(attention(...)).
+"""
+import numpy as np
+import pytest
+import torch
+
+from headshot_amd import _lib
+from headshot_amd.parity import assert_bit_exact, assert_close, f16_close
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NP = {torch.float32: np.float32, torch.float16: np.float16}
+DTYPES = [torch.float32, torch.float16]
+
+
+def host(a: np.ndarray, dtype) -> np.ndarray:
+    return O.to_f16(a) if dtype == torch.float16 else np.ascontiguousarray(a, np.float32)
+
+
+def dev(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda:0")
+
+
+def back(t: torch.Tensor) -> np.ndarray:
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def check(got: np.ndarray, want: np.ndarray, what: str):
+    assert got.dtype == want.dtype, f"{what}: dtype {got.dtype} vs {want.dtype}"
+    if got.dtype == np.float32:
+        assert_close(got, want, 1e-5, what)
+    else:
+        f16_close(got.astype(np.float32), want.astype(np.float32), what)
+
+
+def naive64(q, k, v):
+    """tests/kernels.rs:207-231 in float64."""
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) / np.sqrt(q.shape[-1])
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return np.matmul(p / p.sum(-1, keepdims=True), v)
+
+
+def torch_attention32(q, k, v, q_rows=None):
+    """float32 reference on the device; q_rows selects queries (dim 2)."""
+    q32, k32, v32 = (x.float() for x in (q, k, v))
+    if q_rows is not None:
+        q32 = q32[:, :, q_rows].contiguous()
+    scale = 1.0 / float(np.sqrt(q.shape[-1]))
+    s = torch.matmul(q32, k32.transpose(-1, -2).contiguous()) * scale
+    return torch.matmul(torch.softmax(s, dim=-1), v32)
+
+
+def rand_qkv(seed, shape, dtype):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return [torch.randn(shape, generator=g).to(dtype).to("cuda:0") for _ in range(3)]
+
+
+# ------------------------------------------------------ the reference's cases
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("t", [17, 64, 150])
+def test_attention_reference_cases(ctx, dtype, t):
+    """tests/kernels.rs:185-238: (s, h, d) = (2, 3, 64), q, k, v from Rng(5 + t)."""
+    s, h, d = 2, 3, 64
+    stream = O.rng_vec(5 + t, 3 * s * h * t * d).reshape(3, s, h, t, d)
+    q, k, v = (host(stream[i], dtype) for i in range(3))
+    got = back(ctx.attention(dev(q), dev(k), dev(v)))
+    check(got, O.attention(q, k, v), f"attention t={t} {dtype}")
+    if dtype == torch.float32:
+        assert np.abs(got - naive64(q, k, v)).max() < 1e-4
+
+
+def test_attention_f16_matches_f32(ctx):
+    """tests/kernels.rs:377-401: (1, 2, 33, 64), Rng(9), 5e-3."""
+    s, h, t, d = 1, 2, 33, 64
+    stream = O.rng_vec(9, 3 * s * h * t * d).reshape(3, s, h, t, d)
+    f32 = back(ctx.attention(*(dev(stream[i]) for i in range(3))))
+    f16 = back(ctx.attention(*(dev(O.to_f16(stream[i])) for i in range(3))))
+    assert_close(f16.astype(np.float32), f32, 5e-3, "attention f16 vs f32")
+
+
+# ------------------------------------------------------------- tile edges
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("t", [1, 2, 31, 63, 65, 127, 128, 129, 257])
+@pytest.mark.parametrize("s,h", [(1, 1), (3, 5), (2, 13)])
+def test_attention_edges(ctx, dtype, t, s, h):
+    rng = np.random.default_rng(1000 * t + 10 * s + h)
+    q, k, v = (host(rng.standard_normal((s, h, t, 64)), dtype) for _ in range(3))
+    got = back(ctx.attention(dev(q), dev(k), dev(v)))
+    check(got, O.attention(q, k, v), f"attention t={t} s={s} h={h} {dtype}")
+
+
+@pytest.mark.parametrize("scale", [0.25, 4.0])
+def test_attention_f16_score_range(ctx, scale):
+    """Flat (scale 0.25) and peaked (scale 4: scores of std 16) softmax."""
+    rng = np.random.default_rng(77)
+    s, h, t = 2, 4, 300
+    q = O.to_f16(scale * rng.standard_normal((s, h, t, 64)))
+    k = O.to_f16(rng.standard_normal((s, h, t, 64)))
+    v = O.to_f16(rng.standard_normal((s, h, t, 64)))
+    got = back(ctx.attention(dev(q), dev(k), dev(v)))
+    check(got, O.attention(q, k, v), f"attention score scale {scale}")
+
+
+def test_attention_d128_f32(ctx):
+    """The camera head's head_dim 128 (f32 only, engine/ops.rs:233-238)."""
+    rng = np.random.default_rng(128)
+    q, k, v = (rng.standard_normal((1, 2, 40, 128)).astype(np.float32) for _ in range(3))
+    got = back(ctx.attention(dev(q), dev(k), dev(v)))
+    check(got, O.attention(q, k, v), "attention d128")
+    assert np.abs(got - naive64(q, k, v)).max() < 1e-4
+
+
+def test_attention_unsupported_shapes(ctx):
+    x16 = torch.zeros((1, 1, 8, 128), dtype=torch.float16, device="cuda:0")
+    with pytest.raises(_lib.HsError) as e:
+        ctx.attention(x16, x16, x16)
+    assert e.value.status == _lib.HS_EUNSUPPORTED
+    x32 = torch.zeros((1, 1, 8, 32), dtype=torch.float32, device="cuda:0")
+    with pytest.raises(_lib.HsError):
+        ctx.attention(x32, x32, x32)
+    with pytest.raises(AssertionError):
+        ctx.attention(x32, x32, torch.zeros((1, 1, 9, 32), device="cuda:0"))
+
+
+# ------------------------------------------------------------------ merge
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("s,h,t,d", [(2, 4, 5, 8), (2, 16, 37, 64), (1, 3, 11, 6), (3, 2, 7, 128)])
+def test_attn_merge_exact(ctx, dtype, s, h, t, d):
+    rng = np.random.default_rng(s * 1000 + t)
+    x = host(rng.standard_normal((s, h, t, d)), dtype)
+    got = back(ctx.attn_merge(dev(x)))
+    want = np.ascontiguousarray(x.transpose(0, 2, 1, 3).reshape(s * t, h * d))
+    assert_bit_exact(got, want, f"attn_merge {dtype} {(s, h, t, d)}")
+    assert_bit_exact(got, O.attn_merge(x), "attn_merge vs oracle")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("s,h,t", [(2, 3, 150), (3, 5, 65)])
+def test_attention_merged_is_merge_of_attention(ctx, dtype, s, h, t):
+    q, k, v = rand_qkv(s + h + t, (s, h, t, 64), dtype)
+    a = ctx.attn_merge(ctx.attention(q, k, v))
+    m = ctx.attention_merged(q, k, v)
+    assert_bit_exact(back(m), back(a), f"attention_merged {dtype}")
+
+
+# -------------------------------------------------------------- full size
+
+def test_attention_frame_blocks_full_size(ctx):
+    """Frame attention of the S=32 aggregator: (32, 16, 1374, 64) f16, every
+    output against float32 torch on the same f16 inputs; two sequences
+    against the oracle; the merged variant bit-exact."""
+    s, h, t = 32, 16, 1374
+    q, k, v = rand_qkv(32, (s, h, t, 64), torch.float16)
+    got = ctx.attention(q, k, v)
+    ref = torch_attention32(q, k, v)
+    f16_close(back(got).astype(np.float32), back(ref), "frame attention vs torch f32")
+    qs, ks, vs = (back(x)[[0, 31]][:, [0, 15]] for x in (q, k, v))
+    sub = np.ascontiguousarray(back(got)[[0, 31]][:, [0, 15]])
+    check(sub, O.attention(np.ascontiguousarray(qs), np.ascontiguousarray(ks),
+                           np.ascontiguousarray(vs)), "frame attention vs oracle")
+    merged = ctx.attention_merged(q, k, v)
+    assert_bit_exact(back(merged), back(ctx.attn_merge(got)), "frame attention merged")
+
+
+def test_attention_global_blocks_sampled(ctx):
+    """Global attention of the S=32 aggregator: one sequence of 32*1374 =
+    43968 tokens, 16 heads. Sampled queries against float32 torch and the
+    oracle; constant V rows reproduce that row everywhere."""
+    s, h, t = 1, 16, 32 * 1374
+    q, k, v = rand_qkv(43968, (s, h, t, 64), torch.float16)
+    got = back(ctx.attention(q, k, v))
+    rows = torch.from_numpy(np.random.default_rng(5).choice(t, 256, replace=False)).to("cuda:0")
+    ref = back(torch_attention32(q, k, v, rows))
+    r = rows.cpu().numpy()
+    f16_close(got[:, :, r].astype(np.float32), ref, "global attention vs torch f32")
+    idx = np.sort(r[:6]).astype(np.int32)
+    want = O.attention(back(q), back(k), back(v), q_idx=idx)
+    check(np.ascontiguousarray(got[:, :, idx]), want, "global attention vs oracle")
+    vc = v[:, :, :1].expand(s, h, t, 64).contiguous()
+    out = back(ctx.attention(q, k, vc)).astype(np.float32)
+    f16_close(out, np.broadcast_to(back(vc).astype(np.float32), out.shape), "constant V")

@@ -343,3 +343,63 @@ def test_assemble_tokens_vs_numpy(out_dt, n_var):
         rows.append(reg[v * r:(v + 1) * r])
         rows.append(((patches[f * p:(f + 1) * p] + pb[None]) + pos).astype(out_dt))
     assert_bit_exact(got, np.concatenate(rows), "assemble")
+
+
+# --------------------------------------------------------------- attention
+
+def _naive_attention64(q, k, v):
+    """The reference test's form (tests/kernels.rs:207-231) in float64: full
+    score matrix, max-subtracted exp, normalised weighted sum."""
+    q, k, v = (a.astype(np.float64) for a in (q, k, v))
+    s = np.matmul(q, np.swapaxes(k, -1, -2)) / np.sqrt(q.shape[-1])
+    p = np.exp(s - s.max(-1, keepdims=True))
+    return np.matmul(p / p.sum(-1, keepdims=True), v)
+
+
+@pytest.mark.parametrize("t", [17, 64, 150])
+def test_attention_matches_cpu_reference_test(t):
+    """tests/kernels.rs:185-238: (s, h, d) = (2, 3, 64), Rng(5 + t), 1e-4."""
+    s, h, d = 2, 3, 64
+    # the reference draws q, k, v from one Rng stream in sequence
+    stream = O.rng_vec(5 + t, 3 * s * h * t * d).reshape(3, s, h, t, d)
+    q, k, v = stream[0], stream[1], stream[2]
+    got = O.attention(q, k, v)
+    want = _naive_attention64(q, k, v)
+    assert np.abs(got - want).max() < 1e-4
+    assert_close(got, want.astype(np.float32), 1e-5, f"attention t={t}")
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_attention_invariants(d):
+    rng = np.random.default_rng(d)
+    s, h, t = 2, 2, 37
+    q, k, v = (rng.standard_normal((s, h, t, d)).astype(np.float32) for _ in range(3))
+    # constant value rows: every output row is that constant
+    vc = np.broadcast_to(rng.standard_normal((s, h, 1, d)).astype(np.float32), v.shape).copy()
+    assert_close(O.attention(q, k, vc), vc, 1e-6, "constant V")
+    # q = 0: uniform weights, the mean of V over keys
+    zq = np.zeros_like(q)
+    mean = np.broadcast_to(v.astype(np.float64).mean(2, keepdims=True), v.shape)
+    assert_close(O.attention(zq, k, v), mean.astype(np.float32), 1e-5, "q = 0")
+    # permuting the keys (k and v rows together) leaves the output unchanged
+    perm = rng.permutation(t)
+    assert_close(O.attention(q, k[:, :, perm], v[:, :, perm]), O.attention(q, k, v), 1e-5,
+                 "key permutation")
+    # one key: the output is that key's value row
+    assert_bit_exact(O.attention(q[:, :, :1], k[:, :, :1], v[:, :, :1]), v[:, :, :1], "T = 1")
+    # the scale is 1/sqrt(D): doubling q is the same as scaling scores by 2
+    got = O.attention(2 * q, k, v)
+    assert_close(got, _naive_attention64(2 * q, k, v).astype(np.float32), 1e-5, "scale")
+
+
+def test_attention_f16_storage_and_subset():
+    rng = np.random.default_rng(9)
+    q, k, v = (O.to_f16(rng.standard_normal((1, 2, 33, 64))) for _ in range(3))
+    got = O.attention(q, k, v)
+    want = _naive_attention64(q, k, v)
+    assert got.dtype == np.float16
+    assert_bit_exact(got, O.attention(q.astype(np.float32), k.astype(np.float32),
+                                      v.astype(np.float32)).astype(np.float16), "f16 = f32 math, RNE")
+    assert np.abs(got.astype(np.float64) - want).max() < 2e-3
+    idx = np.array([0, 5, 32], np.int32)
+    assert_bit_exact(O.attention(q, k, v, q_idx=idx), got[:, :, idx], "query subset")
