@@ -45,6 +45,13 @@ HIP_FLAGS = [
     f"-I{INCLUDE}",
     f"-I{CSRC}",
 ]
+# Per-source additions. Attention: MFMA accumulators in ordinary VGPRs (the
+# default AGPR form costs a copy of every score and output accumulator per
+# key tile), and no NaN-quieting canonicalisation around fmaxf in the
+# softmax max (NaN inputs give NaN-polluted output either way).
+SOURCE_FLAGS = {
+    "hs_attention.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
+}
 CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-Wall",
              f"-I{INCLUDE}"]
 
@@ -67,7 +74,8 @@ def build(verbose: bool = False, defines=(), lib_path: str = LIB, build_dir: str
     jobs = []
     for src in HIP_SOURCES:
         obj = os.path.join(build_dir, src.replace(".hip", ".o"))
-        jobs.append([HIPCC, *HIP_FLAGS, *dflags, "-c", os.path.join(CSRC, src), "-o", obj])
+        jobs.append([HIPCC, *HIP_FLAGS, *SOURCE_FLAGS.get(src, []), *dflags, "-c",
+                     os.path.join(CSRC, src), "-o", obj])
     for src in CXX_SOURCES:
         obj = os.path.join(build_dir, src.replace(".cpp", ".o"))
         jobs.append(["g++", *CXX_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])

@@ -6,19 +6,19 @@
 //
 // Fast path (f16, D = 64): flash attention on the matrix cores. A wave owns
 // 32 queries; a workgroup of kWaves waves shares 64-key K/V tiles staged in
-// LDS (double-buffered, next tile prefetched into registers while the
+// LDS (double-buffered, the next tile prefetched into registers while the
 // current one computes). The wave computes the transposed score block
 // S^T = K Q^T with v_mfma_f32_32x32x16_f16, so each lane holds one query's
 // column (16 keys per 32-key block, lanes l and l+32 splitting the keys):
 // the online-softmax max needs one cross-half exchange per tile and the row
 // sums none until the end. P^T is rounded to f16 in registers and fed
-// straight back as the B operand of O^T += V^T P^T; V is transposed while it
-// is written to LDS, with the key order inside each 16-key group permuted
-// (key bits 2 and 3 swapped) to match the order in which the score
-// accumulator holds P^T, so every operand is one 16-byte LDS read. The
-// output rescale is skipped when no query's running max changed (the factor
-// would be exactly 1). Workgroups are ordered XCD-aware: all query tiles of
-// one (frame, head) run on one XCD, so its K/V stream through that XCD's L2.
+// straight back as the B operand of O^T += V^T P^T; the V^T operand comes
+// from row-major V in LDS through the gfx950 transposing read
+// ds_read_b64_tr_b16, with the key order matching the order in which the
+// score accumulator holds P^T. The output rescale is skipped when no
+// query's running max changed (the factor would be exactly 1). Workgroups
+// are ordered XCD-aware: all query tiles of one (frame, head) run on one
+// XCD, so its K/V stream through that XCD's L2.
 //
 // Generic path (f32, or D = 128): one thread per query over LDS-staged f32
 // K/V tiles, the reference's per-key online softmax in its operand order.
@@ -38,33 +38,25 @@ constexpr int kXcds = 8;
 // flash attention, f16, D = 64
 
 #ifndef HS_ATT_WAVES
-#define HS_ATT_WAVES 4  // waves (32 queries each) per workgroup
+#define HS_ATT_WAVES 8  // waves (32 queries each) per workgroup
 #endif
 constexpr int kD = 64;
 constexpr int kWaves = HS_ATT_WAVES;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 32 * kWaves;  // queries per workgroup
 constexpr int kBN = 64;           // keys per tile
-constexpr int kKPitch = kD + 8;   // LDS row pitch (halves) of K: 144 B, conflict-free b128 reads
-constexpr int kVPitch = kBN + 8;  // LDS row pitch (halves) of V^T
-constexpr int kKChunks = kBN * kD / 8;        // 16-byte chunks per K tile
-constexpr int kVPairs = (kBN / 2) * (kD / 8);  // (key pair, 8-channel) items per V tile
-constexpr int kKPer = kKChunks / kThreads;
-constexpr int kVPer = kVPairs / kThreads;
-static_assert(kKChunks % kThreads == 0 && kVPairs % kThreads == 0, "tile loads must be uniform");
+// LDS row pitch (halves) of the K and V tiles: 160 B, so both the 16-byte
+// operand reads of 32 rows and the 8-byte transposing reads of 8 rows
+// spread evenly over the 64 banks.
+constexpr int kPitch = kD + 16;
+constexpr int kChunks = kBN * kD / 8;  // 16-byte chunks per K (or V) tile
+constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
+static_assert(kChunks % kThreads == 0 || kThreads % kChunks == 0, "tile split");
 
 struct FlashSmem {
-    f16 k[2][kBN * kKPitch];
-    f16 vt[2][kD * kVPitch];
+    f16 k[2][kBN * kPitch];
+    f16 v[2][kBN * kPitch];
 };
-
-// Position of key j (0..63 within a tile) in a V^T row: bits 2 and 3
-// swapped, the order of P^T in the B operand (see the file comment).
-__device__ __forceinline__ int vt_pos(int j) { return (j & ~12) | ((j & 4) << 1) | ((j & 8) >> 1); }
-
-// (a.lo16, b.lo16) and (a.hi16, b.hi16) as one word each.
-__device__ __forceinline__ uint32_t pack_lo(uint32_t a, uint32_t b) { return (a & 0xffffu) | (b << 16); }
-__device__ __forceinline__ uint32_t pack_hi(uint32_t a, uint32_t b) { return (a >> 16) | (b & 0xffff0000u); }
 
 __device__ __forceinline__ h8 as_h8(u32x4 v) { return __builtin_bit_cast(h8, v); }
 
@@ -74,48 +66,150 @@ __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
     return h22u(h);
 }
 
-struct TileRegs {
-    u32x4 k[kKPer];
-    u32x4 v[kVPer][2];
+// One thread's share of a 64-row K or V tile: 16-byte chunk c = tid + i *
+// kThreads is row c / 8, channels (c % 8) * 8 .. + 8.
+struct TileChunks {
+    u32x4 c[kPer];
 };
 
-// Loads the K/V rows [key0, key0 + 64) of one (frame, head); rows past the
+// Loads rows [key0, key0 + 64) of one (frame, head); rows past the
 // sequence end are clamped to the last row (their scores are masked).
-__device__ __forceinline__ void load_tile(TileRegs& r, const f16* kb, const f16* vb, int key0,
-                                          int t, int tid) {
+__device__ __forceinline__ void load_rows(TileChunks& r, const f16* src, int key0, int t, int tid) {
 #pragma unroll
-    for (int i = 0; i < kKPer; i++) {
+    for (int i = 0; i < kPer; i++) {
         const int c = tid + i * kThreads;
+        if (kChunks % kThreads != 0 && c >= kChunks) break;
         const int row = min(key0 + c / 8, t - 1);
-        r.k[i] = ld16(kb + static_cast<int64_t>(row) * kD + (c % 8) * 8);
-    }
-#pragma unroll
-    for (int i = 0; i < kVPer; i++) {
-        const int c = tid + i * kThreads;
-        const int key = key0 + (c / 8) * 2;
-        const int r0 = min(key, t - 1), r1 = min(key + 1, t - 1);
-        r.v[i][0] = ld16(vb + static_cast<int64_t>(r0) * kD + (c % 8) * 8);
-        r.v[i][1] = ld16(vb + static_cast<int64_t>(r1) * kD + (c % 8) * 8);
+        r.c[i] = ld16(src + static_cast<int64_t>(row) * kD + (c % 8) * 8);
     }
 }
 
-__device__ __forceinline__ void store_tile(const TileRegs& r, FlashSmem& sm, int buf, int tid) {
+// Row-major into LDS with the padded pitch.
+__device__ __forceinline__ void store_rows(const TileChunks& r, f16* buf, int tid) {
 #pragma unroll
-    for (int i = 0; i < kKPer; i++) {
+    for (int i = 0; i < kPer; i++) {
         const int c = tid + i * kThreads;
-        st16(&sm.k[buf][(c / 8) * kKPitch + (c % 8) * 8], r.k[i]);
+        if (kChunks % kThreads != 0 && c >= kChunks) break;
+        st16(&buf[(c / 8) * kPitch + (c % 8) * 8], r.c[i]);
     }
+}
+
+// S^T (keys x queries) of one 64-key tile for the wave's 32 queries: s0
+// holds keys [0, 32), s1 keys [32, 64); register r of lane (n, hh) is key
+// 8 (r / 4) + 4 hh + r % 4 of its block, query n.
+__device__ __forceinline__ void qk_scores(f32x16& s0, f32x16& s1, const f16* kbuf, const h8 (&qa)[4],
+                                          int n, int hh) {
+    const f16* a0 = kbuf + n * kPitch + 8 * hh;
+    const f16* a1 = a0 + 32 * kPitch;
+    const f32x16 z = {};
+    s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(a0)), qa[0], z, 0, 0, 0);
+    s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(a1)), qa[0], z, 0, 0, 0);
 #pragma unroll
-    for (int i = 0; i < kVPer; i++) {
-        const int c = tid + i * kThreads;
-        const int pos = vt_pos((c / 8) * 2);  // even; key + 1 lands at pos + 1
-        const int d0 = (c % 8) * 8;
-        uint32_t* col = reinterpret_cast<uint32_t*>(&sm.vt[buf][pos]);
+    for (int ks = 1; ks < 4; ks++) {
+        s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(a0 + 16 * ks)), qa[ks], s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(a1 + 16 * ks)), qa[ks], s1, 0, 0, 0);
+    }
+}
+
+// Keys at or past t score -inf (the partial last tile).
+__device__ __forceinline__ void mask_tail(f32x16& s0, f32x16& s1, int key0, int t, int hh) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int kr = key0 + 8 * (r / 4) + 4 * hh + (r % 4);
+        if (kr >= t) s0[r] = -INFINITY;
+        if (kr + 32 >= t) s1[r] = -INFINITY;
+    }
+}
+
+// Online-softmax update for one tile's scores (already masked): returns
+// P^T as f16 B operands (registers 8 kk .. 8 kk + 7 of s_kb in p[kb][kk])
+// and the factor the running output must be scaled by.
+__device__ __forceinline__ float softmax_tile(const f32x16& s0, const f32x16& s1, float c,
+                                              float& m, float& l, u32x4 (&p)[2][2]) {
+    float mx = fmaxf(s0[0], s1[0]);
+#pragma unroll
+    for (int r = 1; r < 16; r++) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m, mx * c);
+    const float corr = __builtin_amdgcn_exp2f(m - m_new);
+    // The row sum adds the f16 weights the P.V product uses, two per v_dot2.
+    float ps = 0.0f;
+    const f16x2 one2 = {static_cast<f16>(1.0f), static_cast<f16>(1.0f)};
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++)
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-            col[((d0 + 2 * w) * kVPitch) / 2] = pack_lo(r.v[i][0][w], r.v[i][1][w]);
-            col[((d0 + 2 * w + 1) * kVPitch) / 2] = pack_hi(r.v[i][0][w], r.v[i][1][w]);
+            const int r = 8 * kk + 2 * w;
+            p[0][kk][w] = pk_f16(__builtin_amdgcn_exp2f(fmaf(s0[r], c, -m_new)),
+                                 __builtin_amdgcn_exp2f(fmaf(s0[r + 1], c, -m_new)));
+            p[1][kk][w] = pk_f16(__builtin_amdgcn_exp2f(fmaf(s1[r], c, -m_new)),
+                                 __builtin_amdgcn_exp2f(fmaf(s1[r + 1], c, -m_new)));
+            ps = __builtin_amdgcn_fdot2(u2h2(p[0][kk][w]), one2, ps, false);
+            ps = __builtin_amdgcn_fdot2(u2h2(p[1][kk][w]), one2, ps, false);
         }
+    l = fmaf(l, corr, ps);
+    m = m_new;
+    return corr;
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// O^T (channels x queries) += V^T P^T; o0 channels [0, 32), o1 [32, 64).
+// The A operand (V^T rows = channels) comes from row-major V through
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives element j
+// from the (i % 4)-th half of lane 4 j + i / 4's 8-byte read. Lane 4 j' + q
+// of the group therefore reads V[key j'][c0 + 4 q .. + 4), and lane i gets
+// channel c0 + i of 4 keys; two such reads give the 8 keys of one operand,
+// in the order the score accumulator holds P^T (keys 16 kk + 4 hh + j and
+// 16 kk + 8 + 4 hh + j of a 32-key block).
+__device__ __forceinline__ void pv_update(f32x16& o0, f32x16& o1, const f16* vbuf,
+                                          const u32x4 (&p)[2][2], int n, int hh) {
+    const int lane16 = n & 15;  // lane within its 16-lane group
+    const int c0 = n & 16;      // channel base of the group within a 32-channel block
+    const f16* base = vbuf + (4 * hh + lane16 / 4) * kPitch + c0 + 4 * (lane16 % 4);
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+            const f16* r0 = base + (32 * kb2 + 16 * kk) * kPitch;
+            h8 a[2];
+#pragma unroll
+            for (int mb = 0; mb < 2; mb++) {
+                const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(r0 + 32 * mb));
+                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(r0 + 8 * kPitch + 32 * mb));
+                const u32x2 wl = __builtin_bit_cast(u32x2, lo), wh = __builtin_bit_cast(u32x2, hi);
+                u32x4 w;
+                w[0] = wl[0], w[1] = wl[1], w[2] = wh[0], w[3] = wh[1];
+                a[mb] = as_h8(w);
+            }
+            o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], as_h8(p[kb2][kk]), o0, 0, 0, 0);
+            o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], as_h8(p[kb2][kk]), o1, 0, 0, 0);
+        }
+}
+
+__device__ __forceinline__ void rescale(f32x16& o0, f32x16& o1, float corr) {
+    if (__any(corr != 1.0f)) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) o0[r] *= corr, o1[r] *= corr;
+    }
+}
+
+// Normalises and stores the wave's 32 output rows; register r of o_mb is
+// channel 32 mb + 8 (r / 4) + 4 hh + r % 4 of query n.
+__device__ __forceinline__ void store_out(const f32x16& o0, const f32x16& o1, float l, f16* orow,
+                                          int hh) {
+    const float inv = 1.0f / (l + __shfl_xor(l, 32));
+#pragma unroll
+    for (int r4 = 0; r4 < 4; r4++) {
+        const int d0 = 8 * r4 + 4 * hh;
+        u32x2 w0, w1;
+        w0[0] = pk_f16(o0[4 * r4] * inv, o0[4 * r4 + 1] * inv);
+        w0[1] = pk_f16(o0[4 * r4 + 2] * inv, o0[4 * r4 + 3] * inv);
+        w1[0] = pk_f16(o1[4 * r4] * inv, o1[4 * r4 + 1] * inv);
+        w1[1] = pk_f16(o1[4 * r4 + 2] * inv, o1[4 * r4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d0) = w0;
+        *reinterpret_cast<u32x2*>(orow + 32 + d0) = w1;
     }
 }
 
@@ -147,84 +241,46 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
     h8 qa[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) qa[ks] = as_h8(ld16(qb + static_cast<int64_t>(qc) * kD + 16 * ks + 8 * hh));
+    // Q must have arrived before the tile loop: otherwise the compiler sinks
+    // these loads into the loop's preheader and, unable to tell them from
+    // the prefetch loads issued inside the loop, waits for the prefetch at
+    // every tile's first MFMA.
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) asm volatile("" ::"v"(qa[ks]));
 
     f32x16 o0 = {}, o1 = {};
     float m = -INFINITY, l = 0.0f;
     const int ntiles = static_cast<int>(ceil_div(t, kBN));
 
-    TileRegs pre;
-    load_tile(pre, kb, vb, 0, t, tid);
-    store_tile(pre, sm, 0, tid);
+    // Double-buffered tiles: tile j + 1 is loaded into registers while tile
+    // j computes from LDS, then written to the other buffer (last read in
+    // iteration j - 1, which the barrier at its end closed).
+    TileChunks pk, pv;
+    load_rows(pk, kb, 0, t, tid);
+    load_rows(pv, vb, 0, t, tid);
+    store_rows(pk, sm.k[0], tid);
+    store_rows(pv, sm.v[0], tid);
     __syncthreads();
-
     for (int j = 0; j < ntiles; j++) {
         const int cur = j & 1;
-        if (j + 1 < ntiles) load_tile(pre, kb, vb, (j + 1) * kBN, t, tid);
-
-        // S^T (keys x queries): s0 keys [0, 32), s1 keys [32, 64) of the tile;
-        // register r of lane (n, hh) is key 8 (r / 4) + 4 hh + r % 4.
-        f32x16 s0 = {}, s1 = {};
-        const f16* ks0 = &sm.k[cur][n * kKPitch + 8 * hh];
-        const f16* ks1 = &sm.k[cur][(32 + n) * kKPitch + 8 * hh];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(ks0 + 16 * ks)), qa[ks], s0, 0, 0, 0);
-            s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(ks1 + 16 * ks)), qa[ks], s1, 0, 0, 0);
+        if (j + 1 < ntiles) {
+            load_rows(pk, kb, (j + 1) * kBN, t, tid);
+            load_rows(pv, vb, (j + 1) * kBN, t, tid);
         }
-        const int key0 = j * kBN;
-        if (key0 + kBN > t) {  // partial last tile: keys past the end score -inf
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int kr = key0 + 8 * (r / 4) + 4 * hh + (r % 4);
-                if (kr >= t) s0[r] = -INFINITY;
-                if (kr + 32 >= t) s1[r] = -INFINITY;
-            }
-        }
-        float mx = fmaxf(s0[0], s1[0]);
-#pragma unroll
-        for (int r = 1; r < 16; r++) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m, mx * c);
-        const float corr = __builtin_amdgcn_exp2f(m - m_new);
-        float ps = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            s0[r] = __builtin_amdgcn_exp2f(fmaf(s0[r], c, -m_new));
-            s1[r] = __builtin_amdgcn_exp2f(fmaf(s1[r], c, -m_new));
-            ps += s0[r] + s1[r];
-        }
-        l = fmaf(l, corr, ps);
-        m = m_new;
-        if (__any(corr != 1.0f)) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) o0[r] *= corr, o1[r] *= corr;
-        }
-        // P^T as f16 B operands: registers 8 kk .. 8 kk + 7 of s_kb.
+        f32x16 s0, s1;
+        qk_scores(s0, s1, sm.k[cur], qa, n, hh);
+        if ((j + 1) * kBN > t) mask_tail(s0, s1, j * kBN, t, hh);
         u32x4 p[2][2];
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-            for (int w = 0; w < 4; w++) {
-                p[0][kk][w] = pk_f16(s0[8 * kk + 2 * w], s0[8 * kk + 2 * w + 1]);
-                p[1][kk][w] = pk_f16(s1[8 * kk + 2 * w], s1[8 * kk + 2 * w + 1]);
-            }
-        // O^T (channels x queries) += V^T P^T; o0 channels [0, 32), o1 [32, 64).
-        const f16* vt0 = &sm.vt[cur][n * kVPitch + 8 * hh];
-        const f16* vt1 = &sm.vt[cur][(32 + n) * kVPitch + 8 * hh];
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; kb2++)
-#pragma unroll
-            for (int kk = 0; kk < 2; kk++) {
-                const int off = 32 * kb2 + 16 * kk;
-                o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(vt0 + off)), as_h8(p[kb2][kk]), o0, 0, 0, 0);
-                o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(vt1 + off)), as_h8(p[kb2][kk]), o1, 0, 0, 0);
-            }
-        if (j + 1 < ntiles) store_tile(pre, sm, cur ^ 1, tid);
+        const float corr = softmax_tile(s0, s1, c, m, l, p);
+        rescale(o0, o1, corr);
+        pv_update(o0, o1, sm.v[cur], p, n, hh);
+        if (j + 1 < ntiles) {
+            store_rows(pk, sm.k[cur ^ 1], tid);
+            store_rows(pv, sm.v[cur ^ 1], tid);
+        }
         __syncthreads();
     }
 
-    const float lt = l + __shfl_xor(l, 32);
-    const float inv = 1.0f / lt;
     if (qi >= t) return;
     f16* orow;
     if (token_major) {
@@ -233,18 +289,7 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
     } else {
         orow = out + base + static_cast<int64_t>(qi) * kD;
     }
-    // register r of o_mb is channel 32 mb + 8 (r / 4) + 4 hh + r % 4
-#pragma unroll
-    for (int r4 = 0; r4 < 4; r4++) {
-        const int d0 = 8 * r4 + 4 * hh;
-        u32x2 w0, w1;
-        w0[0] = pk_f16(o0[4 * r4] * inv, o0[4 * r4 + 1] * inv);
-        w0[1] = pk_f16(o0[4 * r4 + 2] * inv, o0[4 * r4 + 3] * inv);
-        w1[0] = pk_f16(o1[4 * r4] * inv, o1[4 * r4 + 1] * inv);
-        w1[1] = pk_f16(o1[4 * r4 + 2] * inv, o1[4 * r4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + d0) = w0;
-        *reinterpret_cast<u32x2*>(orow + 32 + d0) = w1;
-    }
+    store_out(o0, o1, l, orow, hh);
 }
 
 // ---------------------------------------------------------------------------
