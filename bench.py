@@ -19,6 +19,10 @@ Per-op kernel durations: every op of one more pass launched eagerly behind a
 GPU busy-wait head start, with a HIP event pair around each launch on the
 launch stream, averaged over ``--op-passes`` passes.
 
+The line also carries an ``attention`` section: the same pass's attention
+calls (frame and global, fused with the head merge) timed on their own and
+priced against the f16 matrix-core peak.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames S]
 """
 from __future__ import annotations
@@ -71,6 +75,8 @@ def parse():
     ap.add_argument("--calibrate-copy-mib", type=int, default=512,
                     help="size of one plain torch copy launched before timing (HBM counter "
                          "calibration for rocprofv3 --pmc runs)")
+    ap.add_argument("--attention-iters", type=int, default=10,
+                    help="timed launches of each attention shape (0 skips the attention leg)")
     ap.add_argument("--summarize", metavar="KERNEL_TRACE_CSV",
                     help="print a summary of rocprofv3 output for this benchmark instead of "
                          "running it")
@@ -125,6 +131,49 @@ def per_op_times(bench: Pass, passes: int) -> dict:
             sums[op] += a.elapsed_time(b)
             counts[op] += 1
     return {op: sums[op] / counts[op] for op in OPS}
+
+
+MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix peak
+
+
+def attention_times(ctx, frames: int, iters: int) -> dict:
+    """The aggregator's attention calls at this S, fused with the head merge
+    (hs_attention_merged, as model/block.rs:148-149 consumes it): frame
+    blocks run S sequences of 1374 tokens, global blocks one sequence of
+    S*1374, 16 heads of 64, f16. Kernel time from HIP events on the launch
+    stream; flops = 4*T^2*D per (sequence, head)."""
+    import torch
+
+    out = {}
+    t = GRID[0] * GRID[1] + PREFIX
+    shapes = {"frame": (frames, HEADS, t), "global": (1, HEADS, frames * t)}
+    g = torch.Generator(device="cpu").manual_seed(7)
+    for name, (s, h, tt) in shapes.items():
+        q, k, v = (torch.randn((s, h, tt, HEAD_DIM), generator=g).to(torch.float16).to(ctx.device)
+                   for _ in range(3))
+        o = torch.empty((s * tt, h * HEAD_DIM), dtype=torch.float16, device=ctx.device)
+        ctx.attention_merged(q, k, v, out=o)
+        call = ctx.last_launch
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            call()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / iters
+        flops = 4.0 * tt * tt * HEAD_DIM * s * h
+        tf = flops / (ms * 1e-3) / 1e12
+        out[name] = {"shape_SHTD": [s, h, tt, HEAD_DIM], "ms": round(ms, 3),
+                     "TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                     "calls_per_pass": N_FRAME_BLOCKS if name == "frame" else N_GLOBAL_BLOCKS}
+        del q, k, v, o
+    out["roofline"] = {"bound": "mfma", "kernel": "flash_f16_kernel (global)",
+                       "achieved": out["global"]["TFLOP/s"], "peak": MFMA_PEAK_TFLOPS,
+                       "unit": "TFLOP/s", "frac": out["global"]["frac"]}
+    out["ms_per_pass"] = round(sum(out[n]["ms"] * out[n]["calls_per_pass"]
+                                   for n in ("frame", "global")), 2)
+    return out
 
 
 def cpu_baseline(bench: Pass, target_s: float):
@@ -251,6 +300,26 @@ def summarize(args) -> None:
     out += ["", f"Sum of mean kernel times x launches per pass: {pass_us / 1e3:.3f} ms "
                 f"({sum(nbytes[o] * launches[o] for o in OPS) / (pass_us * 1e-6) / 1e9:.0f} GB/s "
                 f"algorithmic)."]
+    # Attention (the benchmark's attention leg): the flash kernel, told apart by
+    # grid size (work-items = 64 * waves * workgroups).
+    att = defaultdict(list)
+    t_tok = GRID[0] * GRID[1] + PREFIX
+    for r in csv.DictReader(open(args.summarize)):
+        if "flash_f16_kernel" in r["Kernel_Name"]:
+            att[int(r["Grid_Size_X"])].append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    if att:
+        out += ["", "## Attention (flash_f16_kernel, f16, 16 heads of 64)", "",
+                "| call | grid work-items | kernel calls | mean us | TFLOP/s | of 2.5 PFLOP/s |",
+                "|---|---|---|---|---|---|"]
+        shapes = {"frame": (args.frames, t_tok), "global": (1, args.frames * t_tok)}
+        by_size = sorted(att.items(), key=lambda kv: st.mean(kv[1]))
+        for (grid, durs), name in zip(by_size, ["frame", "global"]):
+            s_, tt = shapes[name]
+            m = st.mean(durs)
+            tf = 4.0 * tt * tt * HEAD_DIM * s_ * HEADS / (m * 1e-6) / 1e12
+            out.append(f"| {name} (S={s_}, T={tt}) | {grid} | {len(durs)} | {m:.1f} | {tf:.0f} | "
+                       f"{tf / MFMA_PEAK_TFLOPS:.1%} |")
     if args.pmc_fetch and args.pmc_write:
         def counters(path, name):
             # The calibration copy (torch's device-to-device copy_) runs as
@@ -402,6 +471,8 @@ def main():
         "ops": per_op,
         "roofline": roofline,
     }
+    if args.attention_iters > 0:
+        line["attention"] = attention_times(ctx, args.frames, args.attention_iters)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -43,7 +43,11 @@ constexpr int kXcds = 8;
 constexpr int kD = 64;
 constexpr int kWaves = HS_ATT_WAVES;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBM = 32 * kWaves;  // queries per workgroup
+#ifndef HS_ATT_QB
+#define HS_ATT_QB 1  // 32-query blocks per wave
+#endif
+constexpr int kQB = HS_ATT_QB;
+constexpr int kBM = 32 * kQB * kWaves;  // queries per workgroup
 constexpr int kBN = 64;           // keys per tile
 // LDS row pitch (halves) of the K and V tiles: 160 B, so both the 16-byte
 // operand reads of 32 rows and the 8-byte transposing reads of 8 rows
@@ -94,20 +98,23 @@ __device__ __forceinline__ void store_rows(const TileChunks& r, f16* buf, int ti
     }
 }
 
-// S^T (keys x queries) of one 64-key tile for the wave's 32 queries: s0
-// holds keys [0, 32), s1 keys [32, 64); register r of lane (n, hh) is key
-// 8 (r / 4) + 4 hh + r % 4 of its block, query n.
-__device__ __forceinline__ void qk_scores(f32x16& s0, f32x16& s1, const f16* kbuf, const h8 (&qa)[4],
-                                          int n, int hh) {
+// S^T (keys x queries) of one 64-key tile for the wave's query blocks:
+// s[b][0] holds keys [0, 32), s[b][1] keys [32, 64); register r of lane
+// (n, hh) is key 8 (r / 4) + 4 hh + r % 4 of its block, query n of block b.
+// Each K operand read from LDS feeds the MFMAs of every query block.
+__device__ __forceinline__ void qk_scores(f32x16 (&s)[kQB][2], const f16* kbuf,
+                                          const h8 (&qa)[kQB][4], int n, int hh) {
     const f16* a0 = kbuf + n * kPitch + 8 * hh;
     const f16* a1 = a0 + 32 * kPitch;
     const f32x16 z = {};
-    s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(a0)), qa[0], z, 0, 0, 0);
-    s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(a1)), qa[0], z, 0, 0, 0);
 #pragma unroll
-    for (int ks = 1; ks < 4; ks++) {
-        s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(a0 + 16 * ks)), qa[ks], s0, 0, 0, 0);
-        s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(as_h8(ld16(a1 + 16 * ks)), qa[ks], s1, 0, 0, 0);
+    for (int ks = 0; ks < 4; ks++) {
+        const h8 k0 = as_h8(ld16(a0 + 16 * ks)), k1 = as_h8(ld16(a1 + 16 * ks));
+#pragma unroll
+        for (int b = 0; b < kQB; b++) {
+            s[b][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qa[b][ks], ks ? s[b][0] : z, 0, 0, 0);
+            s[b][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qa[b][ks], ks ? s[b][1] : z, 0, 0, 0);
+        }
     }
 }
 
@@ -126,9 +133,10 @@ __device__ __forceinline__ void mask_tail(f32x16& s0, f32x16& s1, int key0, int 
 // and the factor the running output must be scaled by.
 __device__ __forceinline__ float softmax_tile(const f32x16& s0, const f32x16& s1, float c,
                                               float& m, float& l, u32x4 (&p)[2][2]) {
+    // a sequential chain, which the compiler turns into v_max3_f32
     float mx = fmaxf(s0[0], s1[0]);
 #pragma unroll
-    for (int r = 1; r < 16; r++) mx = fmaxf(mx, fmaxf(s0[r], s1[r]));
+    for (int r = 1; r < 16; r++) mx = fmaxf(fmaxf(mx, s0[r]), s1[r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m, mx * c);
     const float corr = __builtin_amdgcn_exp2f(m - m_new);
@@ -163,8 +171,8 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // channel c0 + i of 4 keys; two such reads give the 8 keys of one operand,
 // in the order the score accumulator holds P^T (keys 16 kk + 4 hh + j and
 // 16 kk + 8 + 4 hh + j of a 32-key block).
-__device__ __forceinline__ void pv_update(f32x16& o0, f32x16& o1, const f16* vbuf,
-                                          const u32x4 (&p)[2][2], int n, int hh) {
+__device__ __forceinline__ void pv_update(f32x16 (&o)[kQB][2], const f16* vbuf,
+                                          const u32x4 (&p)[kQB][2][2], int n, int hh) {
     const int lane16 = n & 15;  // lane within its 16-lane group
     const int c0 = n & 16;      // channel base of the group within a 32-channel block
     const f16* base = vbuf + (4 * hh + lane16 / 4) * kPitch + c0 + 4 * (lane16 % 4);
@@ -183,8 +191,11 @@ __device__ __forceinline__ void pv_update(f32x16& o0, f32x16& o1, const f16* vbu
                 w[0] = wl[0], w[1] = wl[1], w[2] = wh[0], w[3] = wh[1];
                 a[mb] = as_h8(w);
             }
-            o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], as_h8(p[kb2][kk]), o0, 0, 0, 0);
-            o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], as_h8(p[kb2][kk]), o1, 0, 0, 0);
+#pragma unroll
+            for (int b = 0; b < kQB; b++) {
+                o[b][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[0], as_h8(p[b][kb2][kk]), o[b][0], 0, 0, 0);
+                o[b][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[1], as_h8(p[b][kb2][kk]), o[b][1], 0, 0, 0);
+            }
         }
 }
 
@@ -235,21 +246,34 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
     const f16* kb = k + base;
     const f16* vb = v + base;
 
-    // Q^T as the B operand: lane (n, hh) holds q[n][16 ks + 8 hh .. + 8).
-    const int qi = qt * kBM + wave * 32 + n;
-    const int qc = min(qi, t - 1);
-    h8 qa[4];
+    // Q^T as the B operand: lane (n, hh) of block b holds
+    // q[qi_b][16 ks + 8 hh .. + 8), qi_b = query n of the wave's block b.
+    int qi[kQB];
+    h8 qa[kQB][4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) qa[ks] = as_h8(ld16(qb + static_cast<int64_t>(qc) * kD + 16 * ks + 8 * hh));
+    for (int b = 0; b < kQB; b++) {
+        qi[b] = qt * kBM + (wave * kQB + b) * 32 + n;
+        const int qc = min(qi[b], t - 1);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++)
+            qa[b][ks] = as_h8(ld16(qb + static_cast<int64_t>(qc) * kD + 16 * ks + 8 * hh));
+    }
     // Q must have arrived before the tile loop: otherwise the compiler sinks
     // these loads into the loop's preheader and, unable to tell them from
     // the prefetch loads issued inside the loop, waits for the prefetch at
     // every tile's first MFMA.
 #pragma unroll
-    for (int ks = 0; ks < 4; ks++) asm volatile("" ::"v"(qa[ks]));
+    for (int b = 0; b < kQB; b++)
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) asm volatile("" ::"v"(qa[b][ks]));
 
-    f32x16 o0 = {}, o1 = {};
-    float m = -INFINITY, l = 0.0f;
+    f32x16 o[kQB][2];
+    float m[kQB], l[kQB];
+#pragma unroll
+    for (int b = 0; b < kQB; b++) {
+        o[b][0] = f32x16{}, o[b][1] = f32x16{};
+        m[b] = -INFINITY, l[b] = 0.0f;
+    }
     const int ntiles = static_cast<int>(ceil_div(t, kBN));
 
     // Double-buffered tiles: tile j + 1 is loaded into registers while tile
@@ -267,13 +291,16 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
             load_rows(pk, kb, (j + 1) * kBN, t, tid);
             load_rows(pv, vb, (j + 1) * kBN, t, tid);
         }
-        f32x16 s0, s1;
-        qk_scores(s0, s1, sm.k[cur], qa, n, hh);
-        if ((j + 1) * kBN > t) mask_tail(s0, s1, j * kBN, t, hh);
-        u32x4 p[2][2];
-        const float corr = softmax_tile(s0, s1, c, m, l, p);
-        rescale(o0, o1, corr);
-        pv_update(o0, o1, sm.v[cur], p, n, hh);
+        f32x16 sc[kQB][2];
+        qk_scores(sc, sm.k[cur], qa, n, hh);
+        u32x4 p[kQB][2][2];
+#pragma unroll
+        for (int b = 0; b < kQB; b++) {
+            if ((j + 1) * kBN > t) mask_tail(sc[b][0], sc[b][1], j * kBN, t, hh);
+            const float corr = softmax_tile(sc[b][0], sc[b][1], c, m[b], l[b], p[b]);
+            rescale(o[b][0], o[b][1], corr);
+        }
+        pv_update(o, sm.v[cur], p, n, hh);
         if (j + 1 < ntiles) {
             store_rows(pk, sm.k[cur ^ 1], tid);
             store_rows(pv, sm.v[cur ^ 1], tid);
@@ -281,15 +308,18 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
         __syncthreads();
     }
 
-    if (qi >= t) return;
-    f16* orow;
-    if (token_major) {
-        const int s = sh / heads, h = sh - s * heads;
-        orow = out + ((static_cast<int64_t>(s) * t + qi) * heads + h) * kD;
-    } else {
-        orow = out + base + static_cast<int64_t>(qi) * kD;
+#pragma unroll
+    for (int b = 0; b < kQB; b++) {
+        if (qi[b] >= t) continue;
+        f16* orow;
+        if (token_major) {
+            const int s = sh / heads, h = sh - s * heads;
+            orow = out + ((static_cast<int64_t>(s) * t + qi[b]) * heads + h) * kD;
+        } else {
+            orow = out + base + static_cast<int64_t>(qi[b]) * kD;
+        }
+        store_out(o[b][0], o[b][1], l[b], orow, hh);
     }
-    store_out(o0, o1, l, orow, hh);
 }
 
 // ---------------------------------------------------------------------------

@@ -26,9 +26,6 @@ namespace {
 #ifndef HS_GELU_BPC
 #define HS_GELU_BPC 16
 #endif
-#ifndef HS_GELU_PIPE
-#define HS_GELU_PIPE 0  // 1: software-pipelined loads (two register buffers)
-#endif
 #ifndef HS_GELU_NTL
 #define HS_GELU_NTL (HS_NT != 0)  // non-temporal loads of the fc1 output
 #endif
@@ -109,15 +106,10 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
             bv[k] = b4.x, bv[k + 1] = b4.y, bv[k + 2] = b4.z, bv[k + 3] = b4.w;
         }
     }
-    // Loads past the end re-read the thread's first vector instead of
-    // branching, so every load is issued unconditionally and the compiler's
-    // memory counters stay exact across the pipeline (no vmcnt(0) waits).
     auto load = [&](u32x4 (&raw)[U], int64_t base) {
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int64_t i = base + u * stride;
-            raw[u] = ld_stream<HS_GELU_NTL>(x + (i < total ? i : e0));
-        }
+        for (int u = 0; u < U; u++)
+            if (base + u * stride < total) raw[u] = ld_stream<HS_GELU_NTL>(x + base + u * stride);
     };
     auto compute = [&](const u32x4 (&raw)[U], int64_t base) {
 #pragma unroll
@@ -137,28 +129,11 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
             st_stream<HS_GELU_NTS>(out + base + u * stride, pack(f, T{}));
         }
     };
-    const int64_t step = stride * U;
-#if HS_GELU_PIPE
-    // Two register buffers: the loads of the next U vectors are in flight
-    // while the current ones are computed and stored.
-    if (e0 >= total) return;
-    u32x4 a[U], b[U];
-    load(a, e0);
-    for (int64_t base = e0; base < total; base += 2 * step) {
-        load(b, base + step);
-        compute(a, base);
-        if (base + step >= total) break;
-        load(a, base + 2 * step);
-        compute(b, base + step);
-    }
-#else
-    if (e0 >= total) return;
-    for (int64_t base = e0; base < total; base += step) {
+    for (int64_t base = e0; base < total; base += stride * U) {
         u32x4 raw[U];
         load(raw, base);
         compute(raw, base);
     }
-#endif
 }
 
 template <typename T, bool BIAS, int U>

@@ -272,6 +272,43 @@ class HipContext {
               "rope_apply");
     }
 
+    // engine/ops.rs:225-253: non-causal attention over head-major (S, H, T, D)
+    HipTensor attention(const HipTensor& q, const HipTensor& k, const HipTensor& v) const {
+        HS_REQUIRE(q.shape().size() == 4, "attention wants (S,H,T,D)");
+        HS_REQUIRE(k.shape() == q.shape() && v.shape() == q.shape(), "attention: q/k/v shapes");
+        HS_REQUIRE(k.dtype() == q.dtype() && v.dtype() == q.dtype(), "attention: dtype");
+        const auto& sh = q.shape();
+        HipTensor out = empty_typed(sh, q.dtype());
+        check(hs_attention(stream_, hs_dtype(q.dtype()), q.data(), k.data(), v.data(), out.data(),
+                           i32(sh[0]), i32(sh[1]), i32(sh[2]), i32(sh[3])),
+              "attention");
+        return out;
+    }
+
+    // engine/ops.rs:255-267: (S, H, T, D) -> (S*T, H*D)
+    HipTensor attn_merge(const HipTensor& x) const {
+        HS_REQUIRE(x.shape().size() == 4, "attn_merge wants (S,H,T,D)");
+        const auto& sh = x.shape();
+        HipTensor out = empty_typed({sh[0] * sh[2], sh[1] * sh[3]}, x.dtype());
+        check(hs_attn_merge(stream_, hs_dtype(x.dtype()), x.data(), out.data(), i32(sh[0]),
+                            i32(sh[1]), i32(sh[2]), i32(sh[3])),
+              "attn_merge");
+        return out;
+    }
+
+    // attention + attn_merge (model/block.rs:148-149) in one pass
+    HipTensor attention_merged(const HipTensor& q, const HipTensor& k, const HipTensor& v) const {
+        HS_REQUIRE(q.shape().size() == 4, "attention wants (S,H,T,D)");
+        HS_REQUIRE(k.shape() == q.shape() && v.shape() == q.shape(), "attention: q/k/v shapes");
+        HS_REQUIRE(k.dtype() == q.dtype() && v.dtype() == q.dtype(), "attention: dtype");
+        const auto& sh = q.shape();
+        HipTensor out = empty_typed({sh[0] * sh[2], sh[1] * sh[3]}, q.dtype());
+        check(hs_attention_merged(stream_, hs_dtype(q.dtype()), q.data(), k.data(), v.data(),
+                                  out.data(), i32(sh[0]), i32(sh[1]), i32(sh[2]), i32(sh[3])),
+              "attention_merged");
+        return out;
+    }
+
     // engine/ops.rs:336-348
     HipTensor cast_to_f16(const HipTensor& x) const {
         HS_REQUIRE(x.dtype() == Dtype::F32, "cast_to_f16 wants f32");

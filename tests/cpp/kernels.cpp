@@ -278,6 +278,61 @@ void assemble_equals_cast_and_copy_rows(HipContext& ctx) {
     exact(ctx.download(fused), ctx.download(x), "assembly");
 }
 
+// tests/kernels.rs:185-238: (s, h, d) = (2, 3, 64), t in {17, 64, 150},
+// q, k, v from Rng(5 + t), naive full-matrix softmax, |a - e| < 1e-4; then
+// the same through the f16 path (f16 inputs, output) at 5e-3 of the f32
+// result (tests/kernels.rs:377-401), the merge as an exact permutation and
+// the fused merge equal to attn_merge(attention).
+void attention_matches_cpu(HipContext& ctx) {
+    for (size_t t : {17, 64, 150}) {
+        Rng rng{5 + t};
+        const size_t s = 2, h = 3, d = 64;
+        auto q = rng.vec(s * h * t * d), k = rng.vec(s * h * t * d), v = rng.vec(s * h * t * d);
+        auto gq = ctx.tensor_from_slice({s, h, t, d}, q), gk = ctx.tensor_from_slice({s, h, t, d}, k),
+             gv = ctx.tensor_from_slice({s, h, t, d}, v);
+        auto got = ctx.download(ctx.attention(gq, gk, gv));
+        const float scale = 1.0f / std::sqrt(static_cast<float>(d));
+        std::vector<float> sc(t);
+        for (size_t sh = 0; sh < s * h; sh++)
+            for (size_t qi = 0; qi < t; qi++) {
+                const float* qv = &q[(sh * t + qi) * d];
+                float mx = -3.4e38f;
+                for (size_t ki = 0; ki < t; ki++) {
+                    float acc = 0.0f;
+                    for (size_t dd = 0; dd < d; dd++) acc += qv[dd] * k[(sh * t + ki) * d + dd];
+                    sc[ki] = acc * scale;
+                    mx = std::fmax(mx, sc[ki]);
+                }
+                float den = 0.0f;
+                for (auto& x : sc) den += (x = std::exp(x - mx));
+                for (size_t dd = 0; dd < d; dd++) {
+                    float e = 0.0f;
+                    for (size_t ki = 0; ki < t; ki++) e += sc[ki] * v[(sh * t + ki) * d + dd];
+                    e /= den;
+                    const float a = got[(sh * t + qi) * d + dd];
+                    if (!(std::fabs(a - e) < 1e-4f))
+                        throw Failure("attention t=" + std::to_string(t) + ": " + std::to_string(a) +
+                                      " vs " + std::to_string(e));
+                }
+            }
+        auto hq = ctx.tensor_from_f32({s, h, t, d}, q, Dtype::F16);
+        auto hk = ctx.tensor_from_f32({s, h, t, d}, k, Dtype::F16);
+        auto hv = ctx.tensor_from_f32({s, h, t, d}, v, Dtype::F16);
+        auto att16 = ctx.attention(hq, hk, hv);
+        assert_close(ctx.download(att16), got, 5e-3f, "attention f16 vs f32");
+        auto merged = ctx.download(ctx.attn_merge(att16));
+        auto head = ctx.download(att16);
+        std::vector<float> want(merged.size());
+        for (size_t si = 0; si < s; si++)
+            for (size_t hi = 0; hi < h; hi++)
+                for (size_t ti = 0; ti < t; ti++)
+                    for (size_t dd = 0; dd < d; dd++)
+                        want[((si * t + ti) * h + hi) * d + dd] = head[(((si * h) + hi) * t + ti) * d + dd];
+        exact(merged, want, "attn_merge");
+        exact(ctx.download(ctx.attention_merged(hq, hk, hv)), merged, "attention_merged");
+    }
+}
+
 void contract_violations_throw(HipContext& ctx) {
     auto x = ctx.tensor_from_slice({4, 8}, std::vector<float>(32, 1.0f));
     auto w = ctx.tensor_from_slice({7}, std::vector<float>(7, 1.0f));
@@ -311,6 +366,7 @@ int main(int argc, char** argv) {
         {"every_op_f16_matches_f32", every_op_f16_matches_f32},
         {"fused_ops_equal_reference_sequence", fused_ops_equal_reference_sequence},
         {"assemble_equals_cast_and_copy_rows", assemble_equals_cast_and_copy_rows},
+        {"attention_matches_cpu", attention_matches_cpu},
         {"contract_violations_throw", contract_violations_throw},
     };
     HipContext ctx;
