@@ -19,9 +19,10 @@ Per-op kernel durations: every op of one more pass launched eagerly behind a
 GPU busy-wait head start, with a HIP event pair around each launch on the
 launch stream, averaged over ``--op-passes`` passes.
 
-The line also carries an ``attention`` section: the same pass's attention
-calls (frame and global, fused with the head merge) timed on their own and
-priced against the f16 matrix-core peak.
+The line also carries an ``attention`` section (the same pass's attention
+calls, frame and global, fused with the head merge, timed on their own and
+priced against the f16 matrix-core peak) and a ``cache_build`` section (the
+trunk's f32 head-input cache build at the same S, against HBM).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames S]
 """
@@ -176,6 +177,50 @@ def attention_times(ctx, frames: int, iters: int) -> dict:
     return out
 
 
+CACHED_LAYERS = 4  # trunk layers whose outputs feed the heads (model/trunk.rs:125-135)
+
+
+def cache_times(ctx, frames: int, iters: int) -> dict:
+    """Cache::build at this S (model/cache.rs:21-52): the frame- and
+    inter-block outputs (S*1374, 1024) f16 each, concatenated and cast to f32
+    in one pass (hs_cache_build); the reference's two-dispatch sequence
+    (concat_channels, then cast_to_f32) through the same library beside it.
+    Algorithmic bytes: rows * 2048 * (2 read + 4 written)."""
+    import torch
+
+    rows = frames * (GRID[0] * GRID[1] + PREFIX)
+    g = torch.Generator(device="cpu").manual_seed(11)
+    fo = torch.randn((rows, DIM), generator=g).half().to(ctx.device)
+    io = torch.randn((rows, DIM), generator=g).half().to(ctx.device)
+    out = torch.empty((rows, 2 * DIM), dtype=torch.float32, device=ctx.device)
+    nbytes = rows * 2 * DIM * (2 + 4)
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters
+
+    ctx.cache_build(fo, io, out=out)
+    fused = ctx.last_launch
+    ms = timed(fused)
+    cat = ctx.concat_channels(fo, io)
+    c1 = ctx.last_launch
+    ctx.cast_to_f32(cat)
+    c2 = ctx.last_launch
+    ms_seq = timed(lambda: (c1(), c2()))
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"rows": rows, "channels": 2 * DIM, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac": round(gbs / PEAK_GBS, 4), "bytes": nbytes,
+            "reference_sequence_us": round(ms_seq * 1e3, 2),
+            "calls_per_pass": CACHED_LAYERS}
+
+
 def cpu_baseline(bench: Pass, target_s: float):
     """Time the oracle (C restatement of the reference's f32-math kernels, run
     with the reference's unfused dispatch sequence and f16 storage rounding)
@@ -320,6 +365,22 @@ def summarize(args) -> None:
             tf = 4.0 * tt * tt * HEAD_DIM * s_ * HEADS / (m * 1e-6) / 1e12
             out.append(f"| {name} (S={s_}, T={tt}) | {grid} | {len(durs)} | {m:.1f} | {tf:.0f} | "
                        f"{tf / MFMA_PEAK_TFLOPS:.1%} |")
+    cache = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+             for r in csv.DictReader(open(args.summarize))
+             if "concat_vec_kernel" in r["Kernel_Name"] and "IDF16_fE" in r["Kernel_Name"]
+             and int(r["Grid_Size_X"]) >= 256 * 256]
+    if cache:
+        rows_c = args.frames * t_tok
+        cb = rows_c * 2 * DIM * 6
+        m = st.mean(cache)
+        # hs_cache_build and the reference sequence's cast_to_f32 run this
+        # kernel on the same number of 8-element chunks and move the same
+        # bytes (2 B in, 4 B out per element), so one row covers both.
+        out += ["", "## Cache build (concat_vec_kernel, f16 in, f32 out)", "",
+                "| calls | mean us | algorithmic MB per call | GB/s | of 8 TB/s |",
+                "|---|---|---|---|---|",
+                f"| {len(cache)} | {m:.1f} | {cb / 1e6:.1f} | {cb / (m * 1e-6) / 1e9:.0f} | "
+                f"{cb / (m * 1e-6) / 1e9 / PEAK_GBS:.1%} |"]
     if args.pmc_fetch and args.pmc_write:
         def counters(path, name):
             # The calibration copy (torch's device-to-device copy_) runs as
@@ -473,6 +534,7 @@ def main():
     }
     if args.attention_iters > 0:
         line["attention"] = attention_times(ctx, args.frames, args.attention_iters)
+        line["cache_build"] = cache_times(ctx, args.frames, args.attention_iters)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -30,6 +30,7 @@ HIP_SOURCES = [
     "hs_elementwise.hip",
     "hs_assemble.hip",
     "hs_attention.hip",
+    "hs_cache.hip",
 ]
 # Host-only C++ (bit-exact RoPE tables): no FMA contraction.
 CXX_SOURCES = ["hs_rope_tables.cpp"]

@@ -17,6 +17,8 @@ stream (for launch loops and graph capture without per-call Python checks).
 """
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import torch
 
@@ -179,6 +181,42 @@ class HipContext:
                      _dev(out, "out"), x.numel(), table.numel())
         return out
 
+    def concat_channels(self, a, b) -> torch.Tensor:
+        """engine/ops.rs:302-318: a (rows, c1) ++ b (rows, c2) → (rows, c1+c2)."""
+        c1, c2 = a.shape[-1], b.shape[-1]
+        rows = math.prod(a.shape[:-1])
+        assert math.prod(b.shape[:-1]) == rows, "row mismatch"
+        assert a.dtype == b.dtype, "concat_channels dtype"
+        out = self.empty_typed((rows, c1 + c2), a.dtype)
+        self._launch("concat_channels", self.lib.hs_concat_channels, _dt(a), _dev(a, "a"),
+                     _dev(b, "b"), _dev(out, "out"), rows, c1, c2)
+        return out
+
+    def cast_to_f32(self, x) -> torch.Tensor:
+        """engine/ops.rs:321-334 (f16 → f32)."""
+        assert x.dtype == F16, "cast_to_f32 wants f16"
+        out = self.empty_typed(x.shape, F32)
+        self._launch("cast_f16_to_f32", self.lib.hs_cast_f16_to_f32, _dev(x, "x"),
+                     _dev(out, "out"), x.numel())
+        return out
+
+    def copy_row_blocks(self, src, src_row: int, src_stride: int, dst, dst_row: int,
+                        dst_stride: int, n_blocks: int, rows_per_block: int) -> None:
+        """``n_blocks`` copy_rows calls (engine/tensor.rs:146-160) in one launch:
+        block j copies rows [src_row + j*src_stride, + rows_per_block) of src
+        to [dst_row + j*dst_stride, ...) of dst (model/trunk.rs:103-116)."""
+        assert src.dtype == dst.dtype, "copy_row_blocks dtype"
+        row = src.shape[-1] * src.element_size()
+        assert row == dst.shape[-1] * dst.element_size(), "copy_row_blocks row width"
+        if n_blocks and rows_per_block:
+            last_s = src_row + (n_blocks - 1) * src_stride + rows_per_block
+            last_d = dst_row + (n_blocks - 1) * dst_stride + rows_per_block
+            assert last_s * row <= src.numel() * src.element_size(), "src rows"
+            assert last_d * row <= dst.numel() * dst.element_size(), "dst rows"
+        self._launch("copy_row_blocks", self.lib.hs_copy_row_blocks, _dev(src, "src"), src_row,
+                     src_stride, _dev(dst, "dst"), dst_row, dst_stride, n_blocks,
+                     rows_per_block, row)
+
     def attention(self, q, k, v) -> torch.Tensor:
         """engine/ops.rs:225-253: non-causal attention over head-major
         (S, H, T, D) q, k, v; D 64 (f32/f16) or 128 (f32)."""
@@ -225,6 +263,21 @@ class HipContext:
         assert out.dtype == x_tok.dtype and out.numel() == x_tok.numel(), "out shape/dtype"
         self._launch("qknorm_rope", self.lib.hs_qknorm_rope, _dt(x_tok), _dev(x_tok, "x"), nw, nb,
                      sn, cs, _dev(out, "out"), s, t, h, d, prefix, eps)
+        return out
+
+    def cache_build(self, frame_out, inter_out, out=None) -> torch.Tensor:
+        """Cache::build (model/cache.rs:21-52) in one pass: concat_channels of
+        the frame- and inter-block outputs, cast to f32 → (rows, c1+c2) f32."""
+        c1, c2 = frame_out.shape[-1], inter_out.shape[-1]
+        rows = math.prod(frame_out.shape[:-1])
+        assert math.prod(inter_out.shape[:-1]) == rows, "row mismatch"
+        assert frame_out.dtype == inter_out.dtype, "cache_build dtype"
+        if out is None:
+            out = self.empty_typed((rows, c1 + c2), F32)
+        assert out.dtype == F32 and out.numel() == rows * (c1 + c2), "out shape/dtype"
+        self._launch("cache_build", self.lib.hs_cache_build, _dt(frame_out),
+                     _dev(frame_out, "frame_out"), _dev(inter_out, "inter_out"),
+                     _dev(out, "out"), rows, c1, c2)
         return out
 
     def attention_merged(self, q, k, v, out=None) -> torch.Tensor:

@@ -159,6 +159,37 @@ hs_status hs_assemble_tokens(hs_stream_t stream, hs_dtype out_dt, const void* pa
                              int32_t r, int32_t d, int32_t n_var);
 
 /* ---------------------------------------------------------------------- */
+/* Trunk cache build and register-token gather/scatter                      */
+
+/* GpuContext::concat_channels (engine/ops.rs:302-318;
+ * shaders/concat_channels.wesl): a (rows, c1) ++ b (rows, c2) -> out
+ * (rows, c1 + c2), exact. out must not overlap a or b. */
+hs_status hs_concat_channels(hs_stream_t stream, hs_dtype dt, const void* a, const void* b,
+                             void* out, int64_t rows, int32_t c1, int32_t c2);
+
+/* GpuContext::cast_to_f32 (engine/ops.rs:321-334; shaders/cast_f16_to_f32.wesl):
+ * f16 x -> f32 out, exact. */
+hs_status hs_cast_f16_to_f32(hs_stream_t stream, const void* x, float* out, int64_t total);
+
+/* Cache::build's per-group body (model/cache.rs:21-52): concat_channels of
+ * the frame- and inter-block outputs, then cast to f32 (f16 inputs), in one
+ * pass: out (rows, c1 + c2) f32 = [frame_out row | inter_out row]. The
+ * reference streams frame groups to stay under wgpu's 2 GiB buffer cap; the
+ * operation is row-independent, so any row range may be passed. */
+hs_status hs_cache_build(hs_stream_t stream, hs_dtype in_dt, const void* frame_out,
+                         const void* inter_out, float* out, int64_t rows, int32_t c1, int32_t c2);
+
+/* n_blocks copy_rows calls in one launch (model/trunk.rs:103-116 gathers the
+ * PREFIX rows of every frame with src_stride T, dst_stride PREFIX, and
+ * scatters them back with the strides swapped): for j in [0, n_blocks), rows
+ * [src_row0 + j*src_stride, + rows_per_block) of src go to rows
+ * [dst_row0 + j*dst_stride, ...) of dst; rows are row_bytes wide. src and dst
+ * must not overlap; strides must be at least rows_per_block. */
+hs_status hs_copy_row_blocks(hs_stream_t stream, const void* src, int64_t src_row0,
+                             int64_t src_stride, void* dst, int64_t dst_row0, int64_t dst_stride,
+                             int64_t n_blocks, int64_t rows_per_block, int64_t row_bytes);
+
+/* ---------------------------------------------------------------------- */
 /* Attention                                                                */
 
 /* GpuContext::attention (engine/ops.rs:225-253; shaders/attention.wesl):

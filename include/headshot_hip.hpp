@@ -272,6 +272,66 @@ class HipContext {
               "rope_apply");
     }
 
+    // engine/ops.rs:302-318: a (rows, c1) ++ b (rows, c2) -> (rows, c1 + c2)
+    HipTensor concat_channels(const HipTensor& a, const HipTensor& b) const {
+        const size_t c1 = a.last(), c2 = b.last();
+        HS_REQUIRE(c1 && c2, "concat_channels: empty rows");
+        const size_t rows = a.len() / c1;
+        HS_REQUIRE(b.len() / c2 == rows, "row mismatch");
+        HS_REQUIRE(a.dtype() == b.dtype(), "concat_channels dtype");
+        HipTensor out = empty_typed({rows, c1 + c2}, a.dtype());
+        check(hs_concat_channels(stream_, hs_dtype(a.dtype()), a.data(), b.data(), out.data(),
+                                 static_cast<int64_t>(rows), i32(c1), i32(c2)),
+              "concat_channels");
+        return out;
+    }
+
+    // engine/ops.rs:321-334 (f16 -> f32)
+    HipTensor cast_to_f32(const HipTensor& x) const {
+        HS_REQUIRE(x.dtype() == Dtype::F16, "cast_to_f32 wants f16");
+        HipTensor out = empty_typed(x.shape(), Dtype::F32);
+        check(hs_cast_f16_to_f32(stream_, x.data(), static_cast<float*>(out.data()),
+                                 static_cast<int64_t>(x.len())),
+              "cast_to_f32");
+        return out;
+    }
+
+    // Cache::build (model/cache.rs:21-52) in one pass: concat + cast to f32
+    HipTensor cache_build(const HipTensor& frame_out, const HipTensor& inter_out) const {
+        const size_t c1 = frame_out.last(), c2 = inter_out.last();
+        HS_REQUIRE(c1 && c2, "cache_build: empty rows");
+        const size_t rows = frame_out.len() / c1;
+        HS_REQUIRE(inter_out.len() / c2 == rows, "row mismatch");
+        HS_REQUIRE(frame_out.dtype() == inter_out.dtype(), "cache_build dtype");
+        HipTensor out = empty_typed({rows, c1 + c2}, Dtype::F32);
+        check(hs_cache_build(stream_, hs_dtype(frame_out.dtype()), frame_out.data(), inter_out.data(),
+                             static_cast<float*>(out.data()), static_cast<int64_t>(rows), i32(c1),
+                             i32(c2)),
+              "cache_build");
+        return out;
+    }
+
+    // n_blocks copy_rows calls in one launch (model/trunk.rs:103-116)
+    void copy_row_blocks(const HipTensor& src, size_t src_row, size_t src_stride, HipTensor& dst,
+                         size_t dst_row, size_t dst_stride, size_t n_blocks,
+                         size_t rows_per_block) const {
+        HS_REQUIRE(src.dtype() == dst.dtype(), "copy_row_blocks dtype");
+        const size_t row = src.last() * dtype_size(src.dtype());
+        HS_REQUIRE(row == dst.last() * dtype_size(dst.dtype()), "copy_row_blocks row width");
+        if (n_blocks && rows_per_block) {
+            HS_REQUIRE((src_row + (n_blocks - 1) * src_stride + rows_per_block) * row <=
+                           src.len() * dtype_size(src.dtype()), "src rows");
+            HS_REQUIRE((dst_row + (n_blocks - 1) * dst_stride + rows_per_block) * row <=
+                           dst.len() * dtype_size(dst.dtype()), "dst rows");
+        }
+        check(hs_copy_row_blocks(stream_, src.data(), static_cast<int64_t>(src_row),
+                                 static_cast<int64_t>(src_stride), dst.data(),
+                                 static_cast<int64_t>(dst_row), static_cast<int64_t>(dst_stride),
+                                 static_cast<int64_t>(n_blocks), static_cast<int64_t>(rows_per_block),
+                                 static_cast<int64_t>(row)),
+              "copy_row_blocks");
+    }
+
     // engine/ops.rs:225-253: non-causal attention over head-major (S, H, T, D)
     HipTensor attention(const HipTensor& q, const HipTensor& k, const HipTensor& v) const {
         HS_REQUIRE(q.shape().size() == 4, "attention wants (S,H,T,D)");

@@ -251,6 +251,48 @@ void or_attn_merge(int dt, const void* x, void* out, int32_t s, int32_t t, int32
 }
 
 /* ------------------------------------------------------------------------ */
+/* Cache build (shaders/concat_channels.wesl, shaders/cast_f16_to_f32.wesl,
+ * composed as model/cache.rs:37-44)                                        */
+
+/* One output element per index, as the shader's thread: c = i % (c1 + c2),
+ * row = i / (c1 + c2), from a or b. */
+void or_concat_channels(int dt, const void* a, const void* b, void* out, int64_t rows,
+                        int32_t c1, int32_t c2) {
+    const int64_t c_out = (int64_t)c1 + c2;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < rows * c_out; i++) {
+        const int64_t c = i % c_out, row = i / c_out;
+        if (dt == OR_F16)
+            ((uint16_t*)out)[i] = c < c1 ? ((const uint16_t*)a)[row * c1 + c]
+                                         : ((const uint16_t*)b)[row * c2 + (c - c1)];
+        else
+            ((float*)out)[i] = c < c1 ? ((const float*)a)[row * c1 + c]
+                                      : ((const float*)b)[row * c2 + (c - c1)];
+    }
+}
+
+/* out[i] = f32(x[i]) */
+void or_cast_f16_to_f32(const uint16_t* x, float* out, int64_t total) {
+    or_f16_to_f32_array(x, out, total);
+}
+
+/* Cache::build for one row range: concat_channels, then cast_to_f32 when the
+ * inputs are f16 (an f32 concatenation is stored as is). */
+void or_cache_build(int dt, const void* frame_out, const void* inter_out, float* out,
+                    int64_t rows, int32_t c1, int32_t c2) {
+    const int64_t n = rows * ((int64_t)c1 + c2);
+    if (dt == OR_F32) {
+        or_concat_channels(OR_F32, frame_out, inter_out, out, rows, c1, c2);
+        return;
+    }
+    uint16_t* cat = (uint16_t*)malloc((size_t)n * sizeof(uint16_t));
+    if (!cat) return;
+    or_concat_channels(OR_F16, frame_out, inter_out, cat, rows, c1, c2);
+    or_cast_f16_to_f32(cat, out, n);
+    free(cat);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Attention (shaders/attention.wesl:36-88, dispatched by engine/ops.rs:228-253) */
 
 /* One query of one (frame, head) sequence at a time, exactly as the shader's

@@ -45,6 +45,14 @@ void or_layernorm(int dt, const void* x, const float* w, const float* b, void* o
 void or_split_heads(int dt, const void* x, void* out, int32_t s, int32_t t, int32_t h, int32_t d);
 /* shaders/attn_merge.wesl: (S, H, T, D) -> (S*T, H*D). */
 void or_attn_merge(int dt, const void* x, void* out, int32_t s, int32_t t, int32_t h, int32_t d);
+/* shaders/concat_channels.wesl: a (rows, c1) ++ b (rows, c2). */
+void or_concat_channels(int dt, const void* a, const void* b, void* out, int64_t rows,
+                        int32_t c1, int32_t c2);
+/* shaders/cast_f16_to_f32.wesl */
+void or_cast_f16_to_f32(const uint16_t* x, float* out, int64_t total);
+/* model/cache.rs:37-44: concat_channels, then cast_to_f32 for f16 inputs. */
+void or_cache_build(int dt, const void* frame_out, const void* inter_out, float* out,
+                    int64_t rows, int32_t c1, int32_t c2);
 /* shaders/attention.wesl:36-88 (engine/ops.rs:228-253): head-major q, k, v
  * (S, H, T, D), D a multiple of 4 up to 128, scale 1/sqrt(D). Computes the
  * queries q_idx[0..nq) (q_idx NULL: all T) of every sequence into out

@@ -26,6 +26,7 @@ rope_apply_cpu/apply   complex rotation (lo + i hi) * exp(i theta) in f64;
 layernorm              float64 torch.nn.functional.layer_norm; the reference
                        test layernorm_matches_cpu (tests/kernels.rs:100-126)
 split_heads/merge      numpy reshape/transpose (exact); tests/kernels.rs:241-274
+concat/cast/cache      numpy concatenate + astype(float32), exact
 attention              float64 full-matrix softmax as tests/kernels.rs:194-238
                        (1e-4); invariants: constant V rows, q = 0 gives the
                        mean of V, key permutation, T = 1 returns v
@@ -85,6 +86,9 @@ def _declare(L):
         "or_layernorm": (None, [ctypes.c_int, _P, _P, _P, _P, _I64, _I32, _F]),
         "or_split_heads": (None, [ctypes.c_int, _P, _P, _I32, _I32, _I32, _I32]),
         "or_attn_merge": (None, [ctypes.c_int, _P, _P, _I32, _I32, _I32, _I32]),
+        "or_concat_channels": (None, [ctypes.c_int, _P, _P, _P, _I64, _I32, _I32]),
+        "or_cast_f16_to_f32": (None, [_P, _P, _I64]),
+        "or_cache_build": (None, [ctypes.c_int, _P, _P, _P, _I64, _I32, _I32]),
         "or_attention": (None, [ctypes.c_int, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _P, _I32]),
         "or_rope_apply": (None, [ctypes.c_int, _P, _P, _P, _I32, _I32, _I32, _I32, _I32]),
         "or_erf_as": (_F, [_F]),
@@ -203,6 +207,38 @@ def attn_merge(x: np.ndarray) -> np.ndarray:
     s, h, t, d = x.shape
     out = np.empty((s * t, h * d), x.dtype)
     lib().or_attn_merge(_dt(x), _ptr(x), _ptr(out), s, t, h, d)
+    return out
+
+
+def concat_channels(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """concat_channels.wesl: (rows, c1) ++ (rows, c2) → (rows, c1 + c2)."""
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    assert a.dtype == b.dtype
+    c1, c2 = a.shape[-1], b.shape[-1]
+    rows = int(np.prod(a.shape[:-1]))
+    assert int(np.prod(b.shape[:-1])) == rows
+    out = np.empty((rows, c1 + c2), a.dtype)
+    lib().or_concat_channels(_dt(a), _ptr(a), _ptr(b), _ptr(out), rows, c1, c2)
+    return out
+
+
+def cast_to_f32(x: np.ndarray) -> np.ndarray:
+    """cast_f16_to_f32.wesl."""
+    x = np.ascontiguousarray(x, dtype=np.float16)
+    out = np.empty(x.shape, np.float32)
+    lib().or_cast_f16_to_f32(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def cache_build(frame_out: np.ndarray, inter_out: np.ndarray) -> np.ndarray:
+    """Cache::build (model/cache.rs:37-44) over all rows: f32 (rows, c1 + c2)."""
+    a, b = np.ascontiguousarray(frame_out), np.ascontiguousarray(inter_out)
+    assert a.dtype == b.dtype
+    c1, c2 = a.shape[-1], b.shape[-1]
+    rows = int(np.prod(a.shape[:-1]))
+    assert int(np.prod(b.shape[:-1])) == rows
+    out = np.empty((rows, c1 + c2), np.float32)
+    lib().or_cache_build(_dt(a), _ptr(a), _ptr(b), _ptr(out), rows, c1, c2)
     return out
 
 

@@ -403,3 +403,21 @@ def test_attention_f16_storage_and_subset():
     assert np.abs(got.astype(np.float64) - want).max() < 2e-3
     idx = np.array([0, 5, 32], np.int32)
     assert_bit_exact(O.attention(q, k, v, q_idx=idx), got[:, :, idx], "query subset")
+
+
+# ------------------------------------------------------------- cache build
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+def test_concat_cast_cache_build_vs_numpy(dt):
+    rng = np.random.default_rng(31)
+    a = rng.standard_normal((37, 24)).astype(dt)
+    b = rng.standard_normal((37, 40)).astype(dt)
+    cat = np.concatenate([a, b], axis=1)
+    assert_bit_exact(O.concat_channels(a, b), cat, "concat")
+    assert_bit_exact(O.cache_build(a, b), cat.astype(np.float32), "cache_build")
+    if dt == np.float16:
+        x = np.arange(65536, dtype=np.uint16).view(np.float16)
+        got = O.cast_to_f32(x)
+        want = x.astype(np.float32)
+        assert np.array_equal(got.view(np.uint32)[~np.isnan(want)], want.view(np.uint32)[~np.isnan(want)])
+        assert np.isnan(got[np.isnan(want)]).all()
