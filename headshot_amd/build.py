@@ -31,6 +31,7 @@ HIP_SOURCES = [
     "hs_assemble.hip",
     "hs_attention.hip",
     "hs_cache.hip",
+    "hs_gemm.hip",
 ]
 # Host-only C++ (bit-exact RoPE tables): no FMA contraction.
 CXX_SOURCES = ["hs_rope_tables.cpp"]

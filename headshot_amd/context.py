@@ -101,6 +101,21 @@ class HipContext:
 
     # ----------------------------------------------------------- reference ops
 
+    def linear(self, x, weight, bias=None, out=None) -> torch.Tensor:
+        """engine/ops.rs:81-128: ``out (m, n) = x (m, k) @ weight (n, k)^T [+ bias]``."""
+        k = x.shape[-1]
+        m = x.numel() // k if k else 0
+        assert weight.dim() == 2 and weight.shape[1] == k, "weight k mismatch"
+        assert weight.dtype == x.dtype, "weight/activation dtype"
+        n = weight.shape[0]
+        b = _opt(bias, n, "bias")
+        if out is None:
+            out = self.empty_typed((m, n), x.dtype)
+        assert out.dtype == x.dtype and out.numel() == m * n, "out shape/dtype"
+        self._launch("linear", self.lib.hs_linear, _dt(x), _dev(x, "x"), _dev(weight, "weight"),
+                     b, _dev(out, "out"), m, n, k)
+        return out
+
     def layernorm(self, x, weight, bias, eps: float = 1e-5, out=None) -> torch.Tensor:
         """engine/ops.rs:130-153 (eps is 1e-5 there; pass it explicitly here)."""
         dim = x.shape[-1]
@@ -263,6 +278,39 @@ class HipContext:
         assert out.dtype == x_tok.dtype and out.numel() == x_tok.numel(), "out shape/dtype"
         self._launch("qknorm_rope", self.lib.hs_qknorm_rope, _dt(x_tok), _dev(x_tok, "x"), nw, nb,
                      sn, cs, _dev(out, "out"), s, t, h, d, prefix, eps)
+        return out
+
+    def linear_gelu(self, x, weight, bias=None, out=None) -> torch.Tensor:
+        """linear(fc1, bias) + GELU (model/block.rs:172-176) in one kernel."""
+        k = x.shape[-1]
+        m = x.numel() // k if k else 0
+        assert weight.dim() == 2 and weight.shape[1] == k, "weight k mismatch"
+        assert weight.dtype == x.dtype, "weight/activation dtype"
+        n = weight.shape[0]
+        b = _opt(bias, n, "bias")
+        if out is None:
+            out = self.empty_typed((m, n), x.dtype)
+        assert out.dtype == x.dtype and out.numel() == m * n, "out shape/dtype"
+        self._launch("linear_gelu", self.lib.hs_linear_gelu, _dt(x), _dev(x, "x"),
+                     _dev(weight, "weight"), b, _dev(out, "out"), m, n, k)
+        return out
+
+    def linear_ls_residual(self, x, weight, gamma, res, bias=None, out=None) -> torch.Tensor:
+        """linear(proj | fc2, bias) + LayerScale + residual (model/block.rs:150-155):
+        ``res + gamma * (x @ weight^T + bias)``; ``out`` may be ``res``."""
+        k = x.shape[-1]
+        m = x.numel() // k if k else 0
+        assert weight.dim() == 2 and weight.shape[1] == k, "weight k mismatch"
+        assert weight.dtype == x.dtype and res.dtype == x.dtype, "weight/res/activation dtype"
+        n = weight.shape[0]
+        assert res.numel() == m * n, "res shape"
+        g = _param(gamma, n, "gamma")
+        b = _opt(bias, n, "bias")
+        if out is None:
+            out = self.empty_typed((m, n), x.dtype)
+        assert out.dtype == x.dtype and out.numel() == m * n, "out shape/dtype"
+        self._launch("linear_ls_residual", self.lib.hs_linear_ls_residual, _dt(x), _dev(x, "x"),
+                     _dev(weight, "weight"), b, g, _dev(res, "res"), _dev(out, "out"), m, n, k)
         return out
 
     def cache_build(self, frame_out, inter_out, out=None) -> torch.Tensor:

@@ -190,6 +190,29 @@ hs_status hs_copy_row_blocks(hs_stream_t stream, const void* src, int64_t src_ro
                              int64_t n_blocks, int64_t rows_per_block, int64_t row_bytes);
 
 /* ---------------------------------------------------------------------- */
+/* Linear layers (GEMM) with the trunk's epilogues fused                     */
+
+/* GpuContext::linear (engine/ops.rs:81-128; shaders/linear_wmma.wgsl,
+ * shaders/linear.wesl): out (m, n) = x (m, k) @ w (n, k)^T + bias (n),
+ * accumulated in f32, stored in dt. bias (f32) may be NULL. out must not
+ * overlap x or w. */
+hs_status hs_linear(hs_stream_t stream, hs_dtype dt, const void* x, const void* w,
+                    const float* bias, void* out, int64_t m, int32_t n, int32_t k);
+
+/* linear(fc1, bias) then gelu (model/block.rs:172-176) in one kernel:
+ * out = gelu(x @ w^T + bias), the sum kept in f32 and rounded once (as
+ * hs_bias_gelu does). */
+hs_status hs_linear_gelu(hs_stream_t stream, hs_dtype dt, const void* x, const void* w,
+                         const float* bias, void* out, int64_t m, int32_t n, int32_t k);
+
+/* linear(proj | fc2, bias) then residual_ls (model/block.rs:150-155) in one
+ * kernel: out = res + gamma * dt(x @ w^T + bias), keeping the linear's
+ * storage rounding. gamma (n) f32; res (m, n) in dt; out may equal res. */
+hs_status hs_linear_ls_residual(hs_stream_t stream, hs_dtype dt, const void* x, const void* w,
+                                const float* bias, const float* gamma, const void* res, void* out,
+                                int64_t m, int32_t n, int32_t k);
+
+/* ---------------------------------------------------------------------- */
 /* Attention                                                                */
 
 /* GpuContext::attention (engine/ops.rs:225-253; shaders/attention.wesl):

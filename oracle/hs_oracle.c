@@ -251,6 +251,29 @@ void or_attn_merge(int dt, const void* x, void* out, int32_t s, int32_t t, int32
 }
 
 /* ------------------------------------------------------------------------ */
+/* Linear (shaders/linear.wesl:29-68, the scalar path of engine/ops.rs:81-128) */
+
+/* out (rows, n) = x (m, k) @ w (n, k)^T [+ bias]: f32 accumulation in k
+ * order, bias added after the sum, stored as Elem. Only the rows listed in
+ * rows_idx (nrows of them; NULL = all m in order) are computed, into
+ * consecutive rows of out. */
+void or_linear(int dt, const void* x, const void* w, const float* bias, void* out, int64_t m,
+               int32_t n, int32_t k, const int64_t* rows_idx, int64_t nrows) {
+    if (!rows_idx) nrows = m;
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int64_t j = 0; j < nrows; j++) {
+        const int64_t row = rows_idx ? rows_idx[j] : j;
+        for (int32_t col = 0; col < n; col++) {
+            float acc = 0.0f;
+            for (int32_t kk = 0; kk < k; kk++)
+                acc += ld(dt, x, row * k + kk) * ld(dt, w, (int64_t)col * k + kk);
+            if (bias) acc += bias[col];
+            st(dt, out, j * n + col, acc);
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Cache build (shaders/concat_channels.wesl, shaders/cast_f16_to_f32.wesl,
  * composed as model/cache.rs:37-44)                                        */
 

@@ -45,6 +45,10 @@ void or_layernorm(int dt, const void* x, const float* w, const float* b, void* o
 void or_split_heads(int dt, const void* x, void* out, int32_t s, int32_t t, int32_t h, int32_t d);
 /* shaders/attn_merge.wesl: (S, H, T, D) -> (S*T, H*D). */
 void or_attn_merge(int dt, const void* x, void* out, int32_t s, int32_t t, int32_t h, int32_t d);
+/* shaders/linear.wesl:29-68: out = x @ w^T [+ bias], f32 accumulation in k
+ * order; rows_idx (nrows) selects rows of x (NULL: all m). */
+void or_linear(int dt, const void* x, const void* w, const float* bias, void* out, int64_t m,
+               int32_t n, int32_t k, const int64_t* rows_idx, int64_t nrows);
 /* shaders/concat_channels.wesl: a (rows, c1) ++ b (rows, c2). */
 void or_concat_channels(int dt, const void* a, const void* b, void* out, int64_t rows,
                         int32_t c1, int32_t c2);

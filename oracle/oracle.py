@@ -26,6 +26,8 @@ rope_apply_cpu/apply   complex rotation (lo + i hi) * exp(i theta) in f64;
 layernorm              float64 torch.nn.functional.layer_norm; the reference
                        test layernorm_matches_cpu (tests/kernels.rs:100-126)
 split_heads/merge      numpy reshape/transpose (exact); tests/kernels.rs:241-274
+linear                 float64 numpy x @ w.T + b at f32 tolerance; small-
+                       integer inputs (exact in every precision) bit-exact
 concat/cast/cache      numpy concatenate + astype(float32), exact
 attention              float64 full-matrix softmax as tests/kernels.rs:194-238
                        (1e-4); invariants: constant V rows, q = 0 gives the
@@ -86,6 +88,7 @@ def _declare(L):
         "or_layernorm": (None, [ctypes.c_int, _P, _P, _P, _P, _I64, _I32, _F]),
         "or_split_heads": (None, [ctypes.c_int, _P, _P, _I32, _I32, _I32, _I32]),
         "or_attn_merge": (None, [ctypes.c_int, _P, _P, _I32, _I32, _I32, _I32]),
+        "or_linear": (None, [ctypes.c_int, _P, _P, _P, _P, _I64, _I32, _I32, _P, _I64]),
         "or_concat_channels": (None, [ctypes.c_int, _P, _P, _P, _I64, _I32, _I32]),
         "or_cast_f16_to_f32": (None, [_P, _P, _I64]),
         "or_cache_build": (None, [ctypes.c_int, _P, _P, _P, _I64, _I32, _I32]),
@@ -208,6 +211,36 @@ def attn_merge(x: np.ndarray) -> np.ndarray:
     out = np.empty((s * t, h * d), x.dtype)
     lib().or_attn_merge(_dt(x), _ptr(x), _ptr(out), s, t, h, d)
     return out
+
+
+def linear(x: np.ndarray, w: np.ndarray, bias=None, rows=None) -> np.ndarray:
+    """linear.wesl: x (m, k) @ w (n, k)^T [+ bias], stored in x's dtype.
+    ``rows`` (indices into x's rows) computes only those rows."""
+    x, w = np.ascontiguousarray(x), np.ascontiguousarray(w)
+    assert x.dtype == w.dtype
+    k = x.shape[-1]
+    m = x.size // k
+    n = w.shape[0]
+    assert w.shape[1] == k
+    b = None if bias is None else _f32(bias)
+    idx = None if rows is None else np.ascontiguousarray(rows, dtype=np.int64)
+    nr = m if idx is None else idx.size
+    out = np.empty((nr, n), x.dtype)
+    lib().or_linear(_dt(x), _ptr(x), _ptr(w), _ptr(b), _ptr(out), m, n, k,
+                    None if idx is None else _ptr(idx), nr)
+    return out
+
+
+def linear_gelu(x, w, bias=None, rows=None):
+    """The reference sequence linear (stores Elem) -> gelu (block.rs:172-176)."""
+    return gelu(linear(x, w, bias, rows))
+
+
+def linear_ls_residual(x, w, gamma, res, bias=None, rows=None):
+    """The reference sequence linear -> residual_ls (block.rs:150-155)."""
+    y = linear(x, w, bias, rows)
+    r = res if rows is None else np.ascontiguousarray(res[rows])
+    return residual_ls(r, y, gamma)
 
 
 def concat_channels(a: np.ndarray, b: np.ndarray) -> np.ndarray:

@@ -421,3 +421,25 @@ def test_concat_cast_cache_build_vs_numpy(dt):
         want = x.astype(np.float32)
         assert np.array_equal(got.view(np.uint32)[~np.isnan(want)], want.view(np.uint32)[~np.isnan(want)])
         assert np.isnan(got[np.isnan(want)]).all()
+
+
+# ------------------------------------------------------------------ linear
+
+@pytest.mark.parametrize("dt", [np.float32, np.float16])
+def test_linear_vs_float64_and_exact_integers(dt):
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((37, 80)).astype(dt)
+    w = rng.standard_normal((48, 80)).astype(dt)
+    b = rng.standard_normal(48).astype(np.float32)
+    got = O.linear(x, w, b).astype(np.float64)
+    want = x.astype(np.float64) @ w.astype(np.float64).T + b
+    tol = 1e-5 if dt == np.float32 else 2e-3
+    assert np.all(np.abs(got - want) <= tol * np.maximum(1.0, np.abs(want)) * (4 if dt == np.float32 else 1))
+    # small integers: every product and partial sum is exact, so the result is
+    xi = rng.integers(-3, 4, (19, 64)).astype(dt)
+    wi = rng.integers(-3, 4, (16, 64)).astype(dt)
+    assert_bit_exact(O.linear(xi, wi).astype(np.float64), xi.astype(np.float64) @ wi.astype(np.float64).T,
+                     "integer linear")
+    # row subset
+    rows = np.array([0, 5, 36])
+    assert_bit_exact(O.linear(x, w, b, rows), O.linear(x, w, b)[rows], "row subset")
