@@ -21,8 +21,10 @@ launch stream, averaged over ``--op-passes`` passes.
 
 The line also carries an ``attention`` section (the same pass's attention
 calls, frame and global, fused with the head merge, timed on their own and
-priced against the f16 matrix-core peak) and a ``cache_build`` section (the
-trunk's f32 head-input cache build at the same S, against HBM).
+priced against the f16 matrix-core peak), a ``cache_build`` section (the
+trunk's f32 head-input cache build at the same S, against HBM) and a
+``linear`` section (the block's four linear layers with their epilogues
+fused, against the matrix-core peak).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames S]
 """
@@ -221,6 +223,59 @@ def cache_times(ctx, frames: int, iters: int) -> dict:
             "calls_per_pass": CACHED_LAYERS}
 
 
+def gemm_times(ctx, frames: int, iters: int) -> dict:
+    """The aggregator block's four linear layers at this S (S*1374 rows, f16),
+    each with the epilogue the block applies fused in: qkv (bias), proj (bias
+    + LayerScale + residual), fc1 (bias + exact GELU), fc2 (bias + LayerScale
+    + residual). flops = 2*m*n*k. For reference the same shapes' plain
+    product through torch (the ROCm BLAS library, no bias or epilogue) is
+    timed beside them; it is not part of this library."""
+    import torch
+
+    m = frames * (GRID[0] * GRID[1] + PREFIX)
+    g = torch.Generator(device="cpu").manual_seed(13)
+    shapes = {"qkv": (3 * DIM, DIM), "proj": (DIM, DIM), "fc1": (HIDDEN, DIM), "fc2": (DIM, HIDDEN)}
+    out = {}
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters
+
+    total_ms = 0.0
+    for name, (n, k) in shapes.items():
+        x = torch.randn((m, k), generator=g).half().to(ctx.device)
+        w = (torch.randn((n, k), generator=g) / k ** 0.5).half().to(ctx.device)
+        b = (torch.randn(n, generator=g) * 0.02).to(ctx.device)
+        o = torch.empty((m, n), dtype=torch.float16, device=ctx.device)
+        if name == "qkv":
+            ctx.linear(x, w, b, out=o)
+        elif name == "fc1":
+            ctx.linear_gelu(x, w, b, out=o)
+        else:
+            res = torch.randn((m, n), generator=g).half().to(ctx.device)
+            gam = torch.full((n,), 1e-5, device=ctx.device)
+            ctx.linear_ls_residual(x, w, gam, res, b, out=o)
+        call = ctx.last_launch
+        ms = timed(call)
+        ms_lib = timed(lambda: torch.nn.functional.linear(x, w))
+        fl = 2.0 * m * n * k
+        tf = fl / (ms * 1e-3) / 1e12
+        out[name] = {"m": m, "n": n, "k": k, "ms": round(ms, 3), "TFLOP/s": round(tf, 1),
+                     "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "library_gemm_ms": round(ms_lib, 3)}
+        total_ms += ms
+        del x, w, o
+    out["ms_per_block"] = round(total_ms, 3)
+    out["ms_per_pass"] = round(total_ms * (N_FRAME_BLOCKS + N_GLOBAL_BLOCKS), 2)
+    return out
+
+
 def cpu_baseline(bench: Pass, target_s: float):
     """Time the oracle (C restatement of the reference's f32-math kernels, run
     with the reference's unfused dispatch sequence and f16 storage rounding)
@@ -381,6 +436,37 @@ def summarize(args) -> None:
                 "|---|---|---|---|---|",
                 f"| {len(cache)} | {m:.1f} | {cb / 1e6:.1f} | {cb / (m * 1e-6) / 1e9:.0f} | "
                 f"{cb / (m * 1e-6) / 1e9 / PEAK_GBS:.1%} |"]
+    gem = defaultdict(list)
+    for r in csv.DictReader(open(args.summarize)):
+        if "gemm_f16_kernel" in r["Kernel_Name"]:
+            epi = r["Kernel_Name"].split("gemm_f16_kernelILi")[1][0]
+            gem[(epi, int(r["Grid_Size_X"]))].append(
+                (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    if gem:
+        m = args.frames * t_tok
+        names = {"0": [("qkv", 3 * DIM, DIM)], "1": [("fc1", HIDDEN, DIM)],
+                 "2": [("proj", DIM, DIM), ("fc2", DIM, HIDDEN)]}
+        out += ["", "## Linear layers (gemm_f16_kernel, f16, epilogue fused)", "",
+                "| layer | epilogue | kernel calls | mean us | TFLOP/s | of 2.5 PFLOP/s |",
+                "|---|---|---|---|---|---|"]
+        for epi, cands in names.items():
+            groups = sorted((kv for kv in gem.items() if kv[0][0] == epi),
+                            key=lambda kv: st.mean(kv[1]))
+            # proj and fc2 share the epilogue and grid; fc2 (k = 4096) runs longer
+            for (key, durs), (name, n, k) in zip(groups, cands) if len(groups) == len(cands) else []:
+                mu = st.mean(durs)
+                tf = 2.0 * m * n * k / (mu * 1e-6) / 1e12
+                out.append(f"| {name} | {['bias', 'bias + GELU', 'bias + LayerScale + residual'][int(epi)]} "
+                           f"| {len(durs)} | {mu:.1f} | {tf:.0f} | {tf / MFMA_PEAK_TFLOPS:.1%} |")
+            if len(groups) == 1 and len(cands) == 2:
+                # same grid: split by duration around the median
+                durs = sorted(groups[0][1])
+                half = len(durs) // 2
+                for part, (name, n, k) in zip((durs[:half], durs[half:]), cands):
+                    mu = st.mean(part)
+                    tf = 2.0 * m * n * k / (mu * 1e-6) / 1e12
+                    out.append(f"| {name} | bias + LayerScale + residual | {len(part)} | {mu:.1f} | "
+                               f"{tf:.0f} | {tf / MFMA_PEAK_TFLOPS:.1%} |")
     if args.pmc_fetch and args.pmc_write:
         def counters(path, name):
             # The calibration copy (torch's device-to-device copy_) runs as
@@ -535,6 +621,7 @@ def main():
     if args.attention_iters > 0:
         line["attention"] = attention_times(ctx, args.frames, args.attention_iters)
         line["cache_build"] = cache_times(ctx, args.frames, args.attention_iters)
+        line["linear"] = gemm_times(ctx, args.frames, args.attention_iters)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -8,17 +8,19 @@
 //                                                 LayerScale + residual)
 // so the activation between a GEMM and its elementwise op never crosses HBM.
 //
-// Fast path (f16, N % 128 == 0, K % 32 == 0): matrix-core GEMM. A workgroup
-// of 4 waves computes a 256 (rows) x 128 (columns) tile of out, K in steps of
-// 32 staged through LDS (double-buffered, the next step prefetched into
-// registers while the current one computes). Both operands are K-contiguous
+// Fast path (f16, N % kBN == 0, K % kBK == 0): matrix-core GEMM. A workgroup
+// of kWaves waves computes a 256 (rows) x kBN (columns) tile of out, K in
+// steps of kBK staged through LDS (double-buffered; the next step's tiles go straight
+// from global memory into LDS with global_load_lds_dwordx4 while the current
+// one computes, with no registers in between). Both operands are K-contiguous
 // rows (x rows, w rows), which is exactly the operand layout of
 // v_mfma_f32_32x32x16_f16, so both come from LDS with 16-byte reads. Each
 // wave owns 128 rows x 64 columns and computes the transposed tile
 // out^T = w x^T: its accumulators then hold, per lane, 4 consecutive output
-// columns of one output row, so the epilogue reads bias/gamma/residual and
-// writes out in 8-byte pieces. Rows past M are clamped on load and masked on
-// store.
+// columns of one output row. The epilogue adds the bias (and applies GELU)
+// there, stages the f16 results through LDS, and then streams whole rows:
+// 16-byte reads of the residual and 16-byte writes of out. Rows past M are
+// clamped on load and masked on store.
 //
 // Generic path (f32, or shapes the fast path does not cover): a tiled
 // scalar kernel, f32 accumulation in K order.
@@ -54,58 +56,77 @@ __device__ __forceinline__ float gelu_erf(float v) {
 // ---------------------------------------------------------------------------
 // matrix-core path
 
-constexpr int kWaves = 4;
+#ifndef HS_GEMM_WAVES
+#define HS_GEMM_WAVES 8  // waves per workgroup: 2 row groups x (waves / 2) column groups
+#endif
+#ifndef HS_GEMM_BK
+#define HS_GEMM_BK 64  // K per LDS stage
+#endif
+constexpr int kWaves = HS_GEMM_WAVES;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBM = 256;  // output rows per workgroup
-constexpr int kBN = 128;  // output columns per workgroup
-constexpr int kBK = 32;   // K per LDS stage
-constexpr int kPitch = kBK + 8;  // halves per LDS row: 80 B, conflict-free 16-byte reads
-constexpr int kXChunks = kBM * kBK / 8;  // 16-byte chunks per stage
-constexpr int kWChunks = kBN * kBK / 8;
-constexpr int kXPer = kXChunks / kThreads;
-constexpr int kWPer = kWChunks / kThreads;
-static_assert(kXChunks % kThreads == 0 && kWChunks % kThreads == 0, "stage split");
+constexpr int kBM = 256;               // output rows per workgroup (2 x 128)
+constexpr int kBN = 64 * (kWaves / 2);  // output columns per workgroup
+constexpr int kBK = HS_GEMM_BK;
+constexpr int kRowChunks = kBK / 8;      // 16-byte chunks per LDS row
+constexpr int kRowsPerInstr = 64 / kRowChunks;
+constexpr int kRowsPer256B = 128 / kBK;  // LDS rows per 64-bank period
+// Stages are filled with global_load_lds_dwordx4: one wave instruction puts
+// its 64 lanes' 16-byte chunks into 1 KiB of LDS in lane order, i.e.
+// kRowsPerInstr unpadded rows. Lane L of instruction j supplies row
+// kRowsPerInstr * j + L / kRowChunks at physical chunk L % kRowChunks, which
+// holds logical chunk (L % kRowChunks) ^ swz(row), swz(row) = (row /
+// kRowsPer256B) % kRowChunks: with that XOR swizzle the operand reads (16
+// consecutive rows, one logical chunk) hit 16 distinct 16-byte bank groups.
+constexpr int kXInstr = kBM * kBK / 8 / 64;  // wave instructions per x stage
+constexpr int kWInstr = kBN * kBK / 8 / 64;  // per w stage
+static_assert(kXInstr % kWaves == 0 && kWInstr % kWaves == 0, "stage split");
 
 struct GemmSmem {
-    f16 x[2][kBM * kPitch];
-    f16 w[2][kBN * kPitch];
+    f16 x[2][kBM * kBK];
+    f16 w[2][kBN * kBK];
 };
-
-struct StageRegs {
-    u32x4 x[kXPer];
-    u32x4 w[kWPer];
-};
+// Epilogue staging: each wave's 128 x 64 output block as f16 rows of
+// kEpiPitch halves (144 B: 16-byte aligned rows, spread over the banks).
+constexpr int kEpiPitch = 64 + 8;
+constexpr int kEpiWave = 128 * kEpiPitch;  // halves per wave
+constexpr size_t kSmemBytes = sizeof(GemmSmem) > size_t{2} * kWaves * kEpiWave
+                                  ? sizeof(GemmSmem)
+                                  : size_t{2} * kWaves * kEpiWave;
 
 __device__ __forceinline__ h8 as_h8(u32x4 v) { return __builtin_bit_cast(h8, v); }
 
-// 16-byte chunk c of a stage: row c / 4, halves (c % 4) * 8 .. + 8 of the
-// 32-wide K slice. x rows past M read row M - 1 (their outputs are masked).
-__device__ __forceinline__ void load_stage(StageRegs& r, const f16* x, const f16* w, int64_t m0,
-                                           int64_t n0, int M, int K, int k0, int tid) {
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ int swz(int row) { return (row / kRowsPer256B) % kRowChunks; }
+
+// Issues this wave's direct-to-LDS loads of one stage (x rows past M read
+// row M - 1; their outputs are masked).
+__device__ __forceinline__ void issue_stage(GemmSmem& sm, int buf, const f16* x, const f16* w,
+                                            int64_t m0, int64_t n0, int M, int K, int k0,
+                                            int wave, int lane) {
+    const int prow = lane / kRowChunks, pc = lane % kRowChunks;
 #pragma unroll
-    for (int i = 0; i < kXPer; i++) {
-        const int c = tid + i * kThreads;
-        const int64_t row = min(m0 + c / 4, static_cast<int64_t>(M) - 1);
-        r.x[i] = ld16(x + row * K + k0 + (c % 4) * 8);
+    for (int i = 0; i < kXInstr / kWaves; i++) {
+        const int j = wave + kWaves * i;
+        const int row = kRowsPerInstr * j + prow;
+        const int64_t grow = min(m0 + row, static_cast<int64_t>(M) - 1);
+        const int c = pc ^ swz(row);
+        __builtin_amdgcn_global_load_lds(x + grow * K + k0 + 8 * c,
+                                         (lds_void*)(&sm.x[buf][j * 512]), 16, 0, 0);
     }
 #pragma unroll
-    for (int i = 0; i < kWPer; i++) {
-        const int c = tid + i * kThreads;
-        r.w[i] = ld16(w + (n0 + c / 4) * K + k0 + (c % 4) * 8);
+    for (int i = 0; i < kWInstr / kWaves; i++) {
+        const int j = wave + kWaves * i;
+        const int row = kRowsPerInstr * j + prow;
+        const int c = pc ^ swz(row);
+        __builtin_amdgcn_global_load_lds(w + (n0 + row) * K + k0 + 8 * c,
+                                         (lds_void*)(&sm.w[buf][j * 512]), 16, 0, 0);
     }
 }
 
-__device__ __forceinline__ void store_stage(const StageRegs& r, GemmSmem& sm, int buf, int tid) {
-#pragma unroll
-    for (int i = 0; i < kXPer; i++) {
-        const int c = tid + i * kThreads;
-        st16(&sm.x[buf][(c / 4) * kPitch + (c % 4) * 8], r.x[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < kWPer; i++) {
-        const int c = tid + i * kThreads;
-        st16(&sm.w[buf][(c / 4) * kPitch + (c % 4) * 8], r.w[i]);
-    }
+// Operand read: logical chunk k of LDS row `row` (rows of kBK halves).
+__device__ __forceinline__ h8 ld_op(const f16* buf, int row, int k) {
+    return as_h8(ld16(buf + row * kBK + 8 * (k ^ swz(row))));
 }
 
 __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
@@ -117,19 +138,20 @@ __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
 // Grid: tiles_m * tiles_n workgroups, column tiles fastest, so workgroups
 // running together share their x rows.
 template <int EPI>
-__global__ __launch_bounds__(kThreads) void gemm_f16_kernel(
+__global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     const f16* __restrict__ x, const f16* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ gamma, const f16* res, f16* out, int M, int N, int K,
     int tiles_n) {
-    __shared__ GemmSmem sm;
+    __shared__ __align__(16) unsigned char smem_raw[kSmemBytes];
+    GemmSmem& sm = *reinterpret_cast<GemmSmem*>(smem_raw);
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = tid >> 6;
     const int l32 = lane & 31, hh = lane >> 5;
     const int64_t m0 = static_cast<int64_t>(blockIdx.x / tiles_n) * kBM;
     const int64_t n0 = static_cast<int64_t>(blockIdx.x % tiles_n) * kBN;
-    const int wm = (wave >> 1) * 128;  // wave's rows within the tile
-    const int wn = (wave & 1) * 64;    // wave's columns within the tile
+    const int wm = (wave / (kWaves / 2)) * 128;  // wave's rows within the tile
+    const int wn = (wave % (kWaves / 2)) * 64;   // wave's columns within the tile
 
     // acc[a][b]: out^T block of columns wn + 32 a .. + 32 (MFMA rows) and
     // rows wm + 32 b .. + 32 (MFMA columns); register r of lane (l32, hh)
@@ -141,64 +163,88 @@ __global__ __launch_bounds__(kThreads) void gemm_f16_kernel(
         for (int b = 0; b < 4; b++) acc[a][b] = f32x16{};
 
     const int nsteps = K / kBK;
-    StageRegs pre;
-    load_stage(pre, x, w, m0, n0, M, K, 0, tid);
-    store_stage(pre, sm, 0, tid);
+    issue_stage(sm, 0, x, w, m0, n0, M, K, 0, wave, lane);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     for (int s = 0; s < nsteps; s++) {
         const int cur = s & 1;
-        if (s + 1 < nsteps) load_stage(pre, x, w, m0, n0, M, K, (s + 1) * kBK, tid);
-        const f16* wa = &sm.w[cur][(wn + l32) * kPitch + 8 * hh];
-        const f16* xb = &sm.x[cur][(wm + l32) * kPitch + 8 * hh];
+        // the other buffer was last read in step s - 1, closed by its barrier
+        if (s + 1 < nsteps) issue_stage(sm, cur ^ 1, x, w, m0, n0, M, K, (s + 1) * kBK, wave, lane);
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ks++) {
+            const int kc = 2 * ks + hh;
             h8 A[2], B[4];
 #pragma unroll
-            for (int a = 0; a < 2; a++) A[a] = as_h8(ld16(wa + a * 32 * kPitch + 16 * ks));
+            for (int a = 0; a < 2; a++) A[a] = ld_op(sm.w[cur], wn + 32 * a + l32, kc);
 #pragma unroll
-            for (int b = 0; b < 4; b++) B[b] = as_h8(ld16(xb + b * 32 * kPitch + 16 * ks));
+            for (int b = 0; b < 4; b++) B[b] = ld_op(sm.x[cur], wm + 32 * b + l32, kc);
 #pragma unroll
             for (int a = 0; a < 2; a++)
 #pragma unroll
                 for (int b = 0; b < 4; b++)
                     acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[a], B[b], acc[a][b], 0, 0, 0);
         }
-        if (s + 1 < nsteps) store_stage(pre, sm, cur ^ 1, tid);
+        // the next stage's loads have landed in LDS (this wave's), then
+        // every wave's (barrier)
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
     }
 
-    // Epilogue: per (a, b) and r4, lane (l32, hh) owns row m, columns
-    // n .. n + 4 of out.
+    // Epilogue, in two phases so that global memory sees whole rows.
+    // 1. Each lane turns its accumulators (row l32 of block b, columns
+    //    32 a + 8 r4 + 4 hh .. + 4) into the linear's stored value,
+    //    f16(acc + bias) (for GELU: f16(gelu(acc + bias))), and writes it
+    //    to the wave's staging block in LDS (free once every wave has left
+    //    the main loop).
+    f16* stage = reinterpret_cast<f16*>(smem_raw) + wave * kEpiWave;
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-        const int64_t m = m0 + wm + 32 * b + l32;
-        if (m >= M) continue;
+    for (int a = 0; a < 2; a++)
 #pragma unroll
-        for (int a = 0; a < 2; a++)
+        for (int r4 = 0; r4 < 4; r4++) {
+            const int cl = 32 * a + 8 * r4 + 4 * hh;  // column within the wave's block
+            const float4 bv = bias ? ld_f32x4(bias + n0 + wn + cl) : float4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int r4 = 0; r4 < 4; r4++) {
-                const int64_t n = n0 + wn + 32 * a + 8 * r4 + 4 * hh;
+            for (int b = 0; b < 4; b++) {
                 float v[4];
-                const float4 bv = bias ? ld_f32x4(bias + n) : float4{0.0f, 0.0f, 0.0f, 0.0f};
                 v[0] = acc[a][b][4 * r4] + bv.x, v[1] = acc[a][b][4 * r4 + 1] + bv.y;
                 v[2] = acc[a][b][4 * r4 + 2] + bv.z, v[3] = acc[a][b][4 * r4 + 3] + bv.w;
                 if constexpr (EPI == EPI_GELU) {
 #pragma unroll
                     for (int e = 0; e < 4; e++) v[e] = gelu_erf(v[e]);
-                } else if constexpr (EPI == EPI_LS) {
-                    // the GEMM epilogue's f16 store, then res + gamma * x
-                    const float4 g = ld_f32x4(gamma + n);
-                    const u32x2 rw = *reinterpret_cast<const u32x2*>(res + m * N + n);
-                    const f16x2 r01 = u2h2(rw[0]), r23 = u2h2(rw[1]);
-                    v[0] = fmaf(g.x, static_cast<float>(static_cast<f16>(v[0])), static_cast<float>(r01.x));
-                    v[1] = fmaf(g.y, static_cast<float>(static_cast<f16>(v[1])), static_cast<float>(r01.y));
-                    v[2] = fmaf(g.z, static_cast<float>(static_cast<f16>(v[2])), static_cast<float>(r23.x));
-                    v[3] = fmaf(g.w, static_cast<float>(static_cast<f16>(v[3])), static_cast<float>(r23.y));
                 }
                 u32x2 o;
                 o[0] = pk_f16(v[0], v[1]), o[1] = pk_f16(v[2], v[3]);
-                *reinterpret_cast<u32x2*>(out + m * N + n) = o;
+                *reinterpret_cast<u32x2*>(stage + (32 * b + l32) * kEpiPitch + cl) = o;
             }
+        }
+    // only this wave reads its block back: a wave-level fence suffices
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // 2. 8 lanes per 128-byte row piece, 8 rows per instruction: 16-byte
+    //    loads of the staged values (and of res), 16-byte stores of out.
+    const int c8 = 8 * (lane & 7);
+    const int64_t n = n0 + wn + c8;
+    float4 g0 = {0.0f, 0.0f, 0.0f, 0.0f}, g1 = g0;
+    if constexpr (EPI == EPI_LS) g0 = ld_f32x4(gamma + n), g1 = ld_f32x4(gamma + n + 4);
+#pragma unroll 4
+    for (int rr = 0; rr < 128; rr += 8) {
+        const int rl = rr + (lane >> 3);
+        const int64_t m = m0 + wm + rl;
+        if (m >= M) break;  // rows grow with rr: the rest are past M too
+        u32x4 v = ld16(stage + rl * kEpiPitch + c8);
+        if constexpr (EPI == EPI_LS) {
+            // res + gamma * x, x the linear's stored (f16) value
+            const u32x4 r = ld16(res + m * N + n);
+            const float gg[8] = {g0.x, g0.y, g0.z, g0.w, g1.x, g1.y, g1.z, g1.w};
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const f16x2 xv = u2h2(v[q]), rv = u2h2(r[q]);
+                v[q] = pk_f16(fmaf(gg[2 * q], static_cast<float>(xv.x), static_cast<float>(rv.x)),
+                              fmaf(gg[2 * q + 1], static_cast<float>(xv.y), static_cast<float>(rv.y)));
+            }
+        }
+        st16(out + m * N + n, v);
     }
 }
 
@@ -262,8 +308,7 @@ hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, cons
                  const char* op) {
     const bool fast = dt == HS_F16 && N % kBN == 0 && K % kBK == 0 && aligned16(x) && aligned16(w) &&
                       (!bias || aligned16(bias)) && (!gamma || aligned16(gamma)) &&
-                      (reinterpret_cast<uintptr_t>(out) & 7u) == 0 &&
-                      (!res || (reinterpret_cast<uintptr_t>(res) & 7u) == 0);
+                      aligned16(out) && (!res || aligned16(res));
     if (fast) {
         const int tiles_n = N / kBN;
         const int64_t blocks = ceil_div(M, kBM) * tiles_n;
