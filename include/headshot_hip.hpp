@@ -272,6 +272,44 @@ class HipContext {
               "rope_apply");
     }
 
+    // engine/ops.rs:81-128: out (m, n) = x (m, k) @ w (n, k)^T [+ bias]
+    HipTensor linear(const HipTensor& x, const HipTensor& w, const HipTensor* bias = nullptr) const {
+        size_t m, n, k;
+        linear_shape(x, w, bias, m, n, k);
+        HipTensor out = empty_typed({m, n}, x.dtype());
+        check(hs_linear(stream_, hs_dtype(x.dtype()), x.data(), w.data(), bias ? bias->f32() : nullptr,
+                        out.data(), static_cast<int64_t>(m), i32(n), i32(k)),
+              "linear");
+        return out;
+    }
+
+    // linear(fc1, bias) + GELU (model/block.rs:172-176) in one kernel
+    HipTensor linear_gelu(const HipTensor& x, const HipTensor& w, const HipTensor* bias = nullptr) const {
+        size_t m, n, k;
+        linear_shape(x, w, bias, m, n, k);
+        HipTensor out = empty_typed({m, n}, x.dtype());
+        check(hs_linear_gelu(stream_, hs_dtype(x.dtype()), x.data(), w.data(),
+                             bias ? bias->f32() : nullptr, out.data(), static_cast<int64_t>(m), i32(n),
+                             i32(k)),
+              "linear_gelu");
+        return out;
+    }
+
+    // linear(proj | fc2, bias) + LayerScale + residual (model/block.rs:150-155)
+    HipTensor linear_ls_residual(const HipTensor& x, const HipTensor& w, const HipTensor& gamma,
+                                 const HipTensor& res, const HipTensor* bias = nullptr) const {
+        size_t m, n, k;
+        linear_shape(x, w, bias, m, n, k);
+        HS_REQUIRE(gamma.dtype() == Dtype::F32 && gamma.len() == n, "gamma must be f32 (n)");
+        HS_REQUIRE(res.dtype() == x.dtype() && res.len() == m * n, "res shape/dtype");
+        HipTensor out = empty_typed({m, n}, x.dtype());
+        check(hs_linear_ls_residual(stream_, hs_dtype(x.dtype()), x.data(), w.data(),
+                                    bias ? bias->f32() : nullptr, gamma.f32(), res.data(), out.data(),
+                                    static_cast<int64_t>(m), i32(n), i32(k)),
+              "linear_ls_residual");
+        return out;
+    }
+
     // engine/ops.rs:302-318: a (rows, c1) ++ b (rows, c2) -> (rows, c1 + c2)
     HipTensor concat_channels(const HipTensor& a, const HipTensor& b) const {
         const size_t c1 = a.last(), c2 = b.last();
@@ -483,6 +521,15 @@ class HipContext {
 
    private:
     static ::hs_dtype hs_dtype(Dtype dt) { return static_cast<::hs_dtype>(static_cast<int>(dt)); }
+    static void linear_shape(const HipTensor& x, const HipTensor& w, const HipTensor* bias, size_t& m,
+                             size_t& n, size_t& k) {
+        k = x.last();
+        HS_REQUIRE(k > 0 && w.shape().size() == 2 && w.shape()[1] == k, "weight k mismatch");
+        HS_REQUIRE(w.dtype() == x.dtype(), "weight/activation dtype");
+        m = x.len() / k, n = w.shape()[0];
+        if (bias) HS_REQUIRE(bias->dtype() == Dtype::F32 && bias->len() == n, "bias must be f32 (n)");
+    }
+
     static int32_t i32(size_t v) {
         HS_REQUIRE(v <= 0x7fffffffu, "dimension exceeds int32");
         return static_cast<int32_t>(v);

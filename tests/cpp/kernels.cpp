@@ -4,6 +4,7 @@
 // same seeds, naive CPU expectations and tolerances, plus checks that each
 // fused op equals the reference's sequence of single ops run through the
 // same context. Exit status 0 when every test passes.
+#include <array>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -333,6 +334,55 @@ void attention_matches_cpu(HipContext& ctx) {
     }
 }
 
+// tests/kernels.rs:63-99 and 313-365: linear against float64 sums on the
+// (f16-rounded) inputs; the f16 cases also at a matrix-core shape
+// (N % 256 == 0, K % 64 == 0), and the fused epilogues against the
+// reference's two-dispatch sequences.
+void linear_matches_cpu(HipContext& ctx) {
+    auto reference = [](const std::vector<float>& x, const std::vector<float>& w,
+                        const std::vector<float>* b, size_t m, size_t n, size_t k, bool f16_out) {
+        std::vector<float> e(m * n);
+        for (size_t r = 0; r < m; r++)
+            for (size_t c = 0; c < n; c++) {
+                double acc = 0.0;
+                for (size_t kk = 0; kk < k; kk++) acc += double(x[r * k + kk]) * double(w[c * k + kk]);
+                float v = static_cast<float>(acc) + (b ? (*b)[c] : 0.0f);
+                e[r * n + c] = f16_out ? hs::f16_to_f32(hs::f32_to_f16(v)) : v;
+            }
+        return e;
+    };
+    {
+        Rng rng{2};
+        const size_t m = 37, k = 53, n = 29;
+        auto x = rng.vec(m * k), w = rng.vec(n * k), b = rng.vec(n);
+        auto gx = ctx.tensor_from_slice({m, k}, x), gw = ctx.tensor_from_slice({n, k}, w);
+        auto gb = ctx.tensor_from_slice({n}, b);
+        assert_close(ctx.download(ctx.linear(gx, gw, &gb)), reference(x, w, &b, m, n, k, false), 1e-4f,
+                     "linear");
+        assert_close(ctx.download(ctx.linear(gx, gw)), reference(x, w, nullptr, m, n, k, false), 1e-4f,
+                     "linear-nobias");
+    }
+    for (auto [m, k, n] : {std::array<size_t, 3>{37, 96, 128}, std::array<size_t, 3>{37, 128, 256}}) {
+        Rng rng{8};
+        auto x = rng.vec(m * k), w = rng.vec(n * k), b = rng.vec(n);
+        auto round = [](std::vector<float> v) {
+            for (auto& e : v) e = hs::f16_to_f32(hs::f32_to_f16(e));
+            return v;
+        };
+        auto xr = round(x), wr = round(w);
+        auto gx = ctx.tensor_from_f32({m, k}, x, Dtype::F16), gw = ctx.tensor_from_f32({n, k}, w, Dtype::F16);
+        auto gb = ctx.tensor_from_slice({n}, b);
+        auto lin = ctx.linear(gx, gw, &gb);
+        assert_close(ctx.download(lin), reference(xr, wr, &b, m, n, k, true), 1e-2f, "linear f16");
+        // fused epilogues == the reference's sequences through the same context
+        f16_gate(ctx.download(ctx.linear_gelu(gx, gw, &gb)), ctx.download(ctx.gelu(lin)), "linear_gelu");
+        auto res = ctx.tensor_from_f32({m, n}, rng.vec(m * n), Dtype::F16);
+        auto gam = ctx.tensor_from_slice({n}, rng.vec(n));
+        f16_gate(ctx.download(ctx.linear_ls_residual(gx, gw, gam, res, &gb)),
+                 ctx.download(ctx.residual_ls(res, lin, gam)), "linear_ls_residual");
+    }
+}
+
 void contract_violations_throw(HipContext& ctx) {
     auto x = ctx.tensor_from_slice({4, 8}, std::vector<float>(32, 1.0f));
     auto w = ctx.tensor_from_slice({7}, std::vector<float>(7, 1.0f));
@@ -367,6 +417,7 @@ int main(int argc, char** argv) {
         {"fused_ops_equal_reference_sequence", fused_ops_equal_reference_sequence},
         {"assemble_equals_cast_and_copy_rows", assemble_equals_cast_and_copy_rows},
         {"attention_matches_cpu", attention_matches_cpu},
+        {"linear_matches_cpu", linear_matches_cpu},
         {"contract_violations_throw", contract_violations_throw},
     };
     HipContext ctx;
