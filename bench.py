@@ -24,7 +24,9 @@ calls, frame and global, fused with the head merge, timed on their own and
 priced against the f16 matrix-core peak), a ``cache_build`` section (the
 trunk's f32 head-input cache build at the same S, against HBM) and a
 ``linear`` section (the block's four linear layers with their epilogues
-fused, against the matrix-core peak).
+fused, against the matrix-core peak) and a ``block`` section (a whole frame
+block and global block on HIP, fused, beside the reference's unfused
+dispatch sequence through the same library).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames S]
 """
@@ -273,6 +275,45 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
         del x, w, o
     out["ms_per_block"] = round(total_ms, 3)
     out["ms_per_pass"] = round(total_ms * (N_FRAME_BLOCKS + N_GLOBAL_BLOCKS), 2)
+    return out
+
+
+def block_times(ctx, frames: int, iters: int) -> dict:
+    """One whole frame block and one global block at this S with every op on
+    HIP (headshot_amd.aggregator.block_forward: linears with fused
+    epilogues, fused QK-norm/RoPE, attention written token-major), and the
+    reference's unfused dispatch sequence through the same library's single
+    ops beside it (block_forward_reference). Random-init f16 weights."""
+    import torch
+
+    from headshot_amd import rope as _rope
+    from headshot_amd.aggregator import BlockWeights, block_forward, block_forward_reference
+
+    t = GRID[0] * GRID[1] + PREFIX
+    gen = torch.Generator(device=ctx.device).manual_seed(17)
+    wts = BlockWeights.random(DIM, HIDDEN, HEAD_DIM, torch.float16, ctx.device, gen)
+    x = torch.randn((frames * t, DIM), generator=gen, device=ctx.device).half()
+    sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(_rope.periods(), *GRID))
+    out = {}
+    for kind, (s, tt, rope) in {"frame": (frames, t, (sin, cos, PREFIX)),
+                                "global": (1, frames * t, None)}.items():
+        res = {}
+        for name, fn in (("fused", block_forward), ("reference_sequence", block_forward_reference)):
+            fn(ctx, wts, x, s, tt, rope=rope, eps=EPS)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(iters):
+                fn(ctx, wts, x, s, tt, rope=rope, eps=EPS)
+            b.record()
+            torch.cuda.synchronize()
+            res[name + "_ms"] = round(a.elapsed_time(b) / iters, 3)
+        out[kind] = res
+    out["aggregator_ms"] = round(N_FRAME_BLOCKS * out["frame"]["fused_ms"]
+                                 + N_GLOBAL_BLOCKS * out["global"]["fused_ms"], 1)
+    out["aggregator_reference_sequence_ms"] = round(
+        N_FRAME_BLOCKS * out["frame"]["reference_sequence_ms"]
+        + N_GLOBAL_BLOCKS * out["global"]["reference_sequence_ms"], 1)
     return out
 
 
@@ -622,6 +663,7 @@ def main():
         line["attention"] = attention_times(ctx, args.frames, args.attention_iters)
         line["cache_build"] = cache_times(ctx, args.frames, args.attention_iters)
         line["linear"] = gemm_times(ctx, args.frames, args.attention_iters)
+        line["block"] = block_times(ctx, args.frames, max(1, args.attention_iters // 2))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -194,3 +194,86 @@ class FusedOpPass:
         for op, _ in self.seq:
             counts[op] = counts.get(op, 0) + 1
         return counts
+
+
+# ---------------------------------------------------------------------------
+# a whole block on HipContext: GEMMs and attention included
+
+
+@dataclass
+class BlockWeights:
+    """One block's weights (model/block.rs:60-110): the linear weights in
+    the storage dtype, everything else f32 (``p``)."""
+    p: BlockParams
+    q_w: torch.Tensor     # (dim, dim) storage dtype; rows = output features
+    k_w: torch.Tensor
+    v_w: torch.Tensor
+    q_b: torch.Tensor     # f32 (dim)
+    k_b: torch.Tensor
+    v_b: torch.Tensor
+    proj_w: torch.Tensor  # (dim, dim)
+    fc1_w: torch.Tensor   # (hidden, dim)
+    fc2_w: torch.Tensor   # (dim, hidden)
+
+    @staticmethod
+    def random(dim: int, hidden: int, head_dim: int, dtype, device, generator,
+               qk_norm: bool = True, ls_init: float | None = 1e-5) -> "BlockWeights":
+        """Random init: linear weights ~N(0, 1/fan_in), biases ~N(0, .02),
+        the rest as BlockParams.random."""
+        def w(n, k):
+            return (torch.randn((n, k), generator=generator, device=device) / k ** 0.5).to(dtype)
+
+        def b(n):
+            return torch.randn(n, generator=generator, device=device) * 0.02
+
+        p = BlockParams.random(dim, hidden, head_dim, device, generator, qk_norm, ls_init)
+        return BlockWeights(p, w(dim, dim), w(dim, dim), w(dim, dim), b(dim), b(dim), b(dim),
+                            w(dim, dim), w(hidden, dim), w(dim, hidden))
+
+
+def block_forward(ctx: HipContext, wts: BlockWeights, x, s: int, t: int, heads: int = HEADS,
+                  rope=None, eps: float = 1e-6):
+    """Block::forward (model/block.rs:118-193) with every op on HIP and the
+    epilogues fused: LN1 -> q/k/v linear -> split_heads + QK-norm + RoPE ->
+    attention written token-major -> proj + LayerScale + residual -> LN2 ->
+    fc1 + GELU -> fc2 + LayerScale + residual. ``rope`` = (sin, cos, prefix)
+    or None (global blocks). Returns the block output (S*T, dim)."""
+    p = wts.p
+    dim = x.shape[-1]
+    hd = dim // heads
+    normed = ctx.layernorm(x, *p.ln1, eps=eps)
+    q = ctx.qknorm_rope(ctx.linear(normed, wts.q_w, wts.q_b), s, t, heads, hd, norm=p.qn,
+                        rope=rope, eps=eps)
+    k = ctx.qknorm_rope(ctx.linear(normed, wts.k_w, wts.k_b), s, t, heads, hd, norm=p.kn,
+                        rope=rope, eps=eps)
+    v = ctx.qknorm_rope(ctx.linear(normed, wts.v_w, wts.v_b), s, t, heads, hd)
+    attn = ctx.attention_merged(q, k, v)
+    x1 = ctx.linear_ls_residual(attn, wts.proj_w, p.ls1, x, p.proj_b)
+    normed2 = ctx.layernorm(x1, *p.ln2, eps=eps)
+    act = ctx.linear_gelu(normed2, wts.fc1_w, p.fc1_b)
+    return ctx.linear_ls_residual(act, wts.fc2_w, p.ls2, x1, p.fc2_b)
+
+
+def block_forward_reference(ctx: HipContext, wts: BlockWeights, x, s: int, t: int,
+                            heads: int = HEADS, rope=None, eps: float = 1e-6):
+    """The reference's unfused dispatch sequence (model/block.rs:118-193)
+    through the same library's single ops: linear (with bias) -> split_heads
+    -> layernorm(q|k) -> rope_apply -> attention -> attn_merge -> linear ->
+    residual_ls -> layernorm -> linear -> gelu -> linear -> residual_ls."""
+    p = wts.p
+    dim = x.shape[-1]
+    hd = dim // heads
+    normed = ctx.layernorm(x, *p.ln1, eps=eps)
+    q, k, v = (ctx.split_heads(ctx.linear(normed, w_, b_), s, t, heads, hd)
+               for w_, b_ in ((wts.q_w, wts.q_b), (wts.k_w, wts.k_b), (wts.v_w, wts.v_b)))
+    if p.qn is not None:
+        q = ctx.layernorm(q, *p.qn, eps=eps)
+        k = ctx.layernorm(k, *p.kn, eps=eps)
+    if rope is not None:
+        ctx.rope_apply(q, *rope)
+        ctx.rope_apply(k, *rope)
+    merged = ctx.attn_merge(ctx.attention(q, k, v))
+    x1 = ctx.residual_ls(x, ctx.linear(merged, wts.proj_w, p.proj_b), p.ls1)
+    normed2 = ctx.layernorm(x1, *p.ln2, eps=eps)
+    mlp = ctx.linear(ctx.gelu(ctx.linear(normed2, wts.fc1_w, p.fc1_b)), wts.fc2_w, p.fc2_b)
+    return ctx.residual_ls(x1, mlp, p.ls2)
