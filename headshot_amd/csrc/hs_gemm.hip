@@ -62,6 +62,9 @@ __device__ __forceinline__ float gelu_erf(float v) {
 #ifndef HS_GEMM_BK
 #define HS_GEMM_BK 64  // K per LDS stage
 #endif
+#ifndef HS_GEMM_XCD
+#define HS_GEMM_XCD 1  // XCD-aware tile order
+#endif
 constexpr int kWaves = HS_GEMM_WAVES;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kBM = 256;               // output rows per workgroup (2 x 128)
@@ -141,15 +144,26 @@ template <int EPI>
 __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     const f16* __restrict__ x, const f16* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ gamma, const f16* res, f16* out, int M, int N, int K,
-    int tiles_n) {
+    int tiles_n, int ntiles) {
     __shared__ __align__(16) unsigned char smem_raw[kSmemBytes];
     GemmSmem& sm = *reinterpret_cast<GemmSmem*>(smem_raw);
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = tid >> 6;
     const int l32 = lane & 31, hh = lane >> 5;
-    const int64_t m0 = static_cast<int64_t>(blockIdx.x / tiles_n) * kBM;
-    const int64_t n0 = static_cast<int64_t>(blockIdx.x % tiles_n) * kBN;
+#if HS_GEMM_XCD
+    // Workgroup b runs on XCD b % 8; XCD x takes the contiguous tile range
+    // [x * per, (x + 1) * per), so the column tiles of one row tile (which
+    // share its x rows) run on one XCD and its L2. The grid is padded to a
+    // multiple of 8 workgroups.
+    const int per = static_cast<int>(gridDim.x / 8);
+    const int tile = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+    if (tile >= ntiles) return;  // padding, before any barrier
+#else
+    const int tile = static_cast<int>(blockIdx.x);
+#endif
+    const int64_t m0 = static_cast<int64_t>(tile / tiles_n) * kBM;
+    const int64_t n0 = static_cast<int64_t>(tile % tiles_n) * kBN;
     const int wm = (wave / (kWaves / 2)) * 128;  // wave's rows within the tile
     const int wn = (wave % (kWaves / 2)) * 64;   // wave's columns within the tile
 
@@ -311,10 +325,12 @@ hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, cons
                       aligned16(out) && (!res || aligned16(res));
     if (fast) {
         const int tiles_n = N / kBN;
-        const int64_t blocks = ceil_div(M, kBM) * tiles_n;
+        const int64_t ntiles = ceil_div(M, kBM) * tiles_n;
+        const int64_t blocks = HS_GEMM_XCD ? ceil_div(ntiles, 8) * 8 : ntiles;
         gemm_f16_kernel<EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st>>>(
             static_cast<const f16*>(x), static_cast<const f16*>(w), bias, gamma,
-            static_cast<const f16*>(res), static_cast<f16*>(out), M, N, K, tiles_n);
+            static_cast<const f16*>(res), static_cast<f16*>(out), M, N, K, tiles_n,
+            static_cast<int>(ntiles));
         return check_launch(op);
     }
     const int tiles_n = static_cast<int>(ceil_div(N, kGT));
