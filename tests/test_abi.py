@@ -111,6 +111,58 @@ def test_assemble_contract():
     assert a(None, F16, None, F32, None, None, None, None, None, 0, 6, 4, 1024, 2) == _lib.HS_OK
 
 
+def test_attention_and_merge_contract():
+    a = L.hs_attention
+    _einval(a(None, 7, FAKE, FAKE, FAKE, FAKE2, 1, 2, 8, 64), "dtype")
+    _einval(a(None, F16, FAKE, FAKE, FAKE, FAKE2, 1, -2, 8, 64), "shape")
+    _einval(a(None, F16, None, FAKE, FAKE, FAKE2, 1, 2, 8, 64), "null")
+    _einval(a(None, F16, FAKE, FAKE, FAKE, ctypes.c_void_p(0x10000 + 64), 1, 2, 8, 64), "overlap")
+    _einval(a(None, F16, FAKE, FAKE, FAKE, FAKE2, 1 << 20, 1 << 10, 4, 64), "2^31")
+    # f16 with head_dim 128, or head_dim 32: the reference has no such variant
+    big = [ctypes.c_void_p(0x1000000 * i) for i in range(1, 5)]
+    assert a(None, F16, *big, 1, 2, 8, 128) == _lib.HS_EUNSUPPORTED
+    assert a(None, F32, *big, 1, 2, 8, 32) == _lib.HS_EUNSUPPORTED
+    assert L.hs_attention_merged(None, F32, *big, 1, 2, 8, 48) == _lib.HS_EUNSUPPORTED
+    assert a(None, F16, None, None, None, None, 0, 2, 8, 64) == _lib.HS_OK
+    m = L.hs_attn_merge
+    _einval(m(None, F16, None, FAKE2, 1, 2, 8, 64), "null")
+    _einval(m(None, F16, FAKE, ctypes.c_void_p(0x10000 + 16), 1, 2, 8, 64), "overlap")
+    assert m(None, F16, None, None, 0, 2, 8, 64) == _lib.HS_OK
+
+
+def test_cache_and_row_block_contract():
+    _einval(L.hs_concat_channels(None, 9, FAKE, FAKE, FAKE2, 4, 8, 8), "dtype")
+    _einval(L.hs_concat_channels(None, F16, None, FAKE, FAKE2, 4, 8, 8), "null")
+    _einval(L.hs_cache_build(None, F16, FAKE, FAKE, ctypes.c_void_p(0x10000 + 32), 4, 8, 8),
+            "overlap")
+    assert L.hs_cache_build(None, F16, None, None, None, 0, 8, 8) == _lib.HS_OK
+    _einval(L.hs_cast_f16_to_f32(None, FAKE, None, 8), "null")
+    _einval(L.hs_cast_f16_to_f32(None, FAKE, FAKE, -1), "negative")
+    r = L.hs_copy_row_blocks
+    _einval(r(None, FAKE, 0, 2, ctypes.c_void_p(0x1000000), 0, 4, 5, 3, 64), "stride")
+    _einval(r(None, FAKE, 0, 4, ctypes.c_void_p(0x10000 + 64), 0, 4, 5, 2, 64), "overlap")
+    _einval(r(None, FAKE, -1, 4, FAKE2, 0, 4, 5, 2, 64), "negative")
+    assert r(None, None, 0, 4, None, 0, 4, 0, 2, 64) == _lib.HS_OK
+
+
+def test_linear_contract():
+    big = [ctypes.c_void_p(0x1000000 * i) for i in range(1, 6)]
+    _einval(L.hs_linear(None, 4, big[0], big[1], None, big[2], 4, 128, 64), "dtype")
+    _einval(L.hs_linear(None, F16, big[0], big[1], None, big[2], -4, 128, 64), "shape")
+    _einval(L.hs_linear(None, F16, None, big[1], None, big[2], 4, 128, 64), "null")
+    _einval(L.hs_linear(None, F16, big[0], big[1], None, ctypes.c_void_p(0x1000000 + 64), 4, 128, 64),
+            "overlap")
+    _einval(L.hs_linear_gelu(None, F16, big[0], None, None, big[2], 4, 128, 64), "null")
+    _einval(L.hs_linear_ls_residual(None, F16, big[0], big[1], None, None, big[3], big[2], 4, 128, 64),
+            "gamma")
+    _einval(L.hs_linear_ls_residual(None, F16, big[0], big[1], None, big[4], None, big[2], 4, 128, 64),
+            "null")
+    # out partly over res (equal is allowed: in place)
+    _einval(L.hs_linear_ls_residual(None, F16, big[0], big[1], None, big[4], big[3],
+                                    ctypes.c_void_p(0x4000000 + 2), 4, 128, 64), "res")
+    assert L.hs_linear(None, F16, None, None, None, None, 0, 128, 64) == _lib.HS_OK
+
+
 def test_python_surface_raises_contract_errors():
     with pytest.raises(_lib.HsContractError) as e:
         _lib.check(L.hs_gelu(None, F16, FAKE, FAKE2, -5), "gelu")
