@@ -317,6 +317,53 @@ def block_times(ctx, frames: int, iters: int) -> dict:
     return out
 
 
+def cpu_baseline_legs(frames: int) -> dict:
+    """The oracle (the reference's kernels restated in C: attention.wesl's
+    one-query-at-a-time online softmax, linear.wesl's k-order sums, the
+    concat + cast of the cache build) on the host cores, over bounded
+    samples of the extra legs' workloads at this S, in their units."""
+    import numpy as np
+
+    from oracle import oracle as O
+
+    threads = min(16, os.cpu_count() or 1)
+    O.set_num_threads(threads)
+    rng = np.random.default_rng(3)
+    t = GRID[0] * GRID[1] + PREFIX
+    out = {}
+    # global attention: 16 heads x 8 queries against all S*1374 keys
+    tt = frames * t
+    q, k, v = (rng.standard_normal((1, HEADS, tt, HEAD_DIM)).astype(np.float16) for _ in range(3))
+    idx = np.arange(8, dtype=np.int32) * (tt // 8)
+    t0 = time.perf_counter()
+    O.attention(q, k, v, q_idx=idx)
+    dt = time.perf_counter() - t0
+    fl = 4.0 * idx.size * tt * HEAD_DIM * HEADS
+    out["attention_global"] = {"value": round(fl / dt / 1e12, 5), "unit": "TFLOP/s",
+                               "sample": f"{HEADS} heads x {idx.size} queries x {tt} keys, f16 "
+                                         f"storage, {dt:.2f} s"}
+    # fc1 linear rows: 64 rows of (S*1374, 1024) x (4096, 1024)^T
+    x = rng.standard_normal((64, DIM)).astype(np.float16)
+    w = (rng.standard_normal((HIDDEN, DIM)) / 32).astype(np.float16)
+    t0 = time.perf_counter()
+    O.linear(x, w)
+    dt = time.perf_counter() - t0
+    out["linear_fc1"] = {"value": round(2.0 * 64 * HIDDEN * DIM / dt / 1e12, 5), "unit": "TFLOP/s",
+                         "sample": f"64 rows x {HIDDEN} x {DIM}, f16 storage, {dt:.2f} s"}
+    # cache build: 4096 rows of 1024 + 1024 f16 -> f32
+    a = rng.standard_normal((4096, DIM)).astype(np.float16)
+    b = rng.standard_normal((4096, DIM)).astype(np.float16)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        O.cache_build(a, b)
+    dt = (time.perf_counter() - t0) / 5
+    out["cache_build"] = {"value": round(4096 * 2 * DIM * 6 / dt / 1e9, 3), "unit": "GB/s",
+                          "sample": f"4096 rows x 2048 channels, {dt * 1e3:.1f} ms"}
+    out["cores"] = threads
+    out["kind"] = "port"
+    return out
+
+
 def cpu_baseline(bench: Pass, target_s: float):
     """Time the oracle (C restatement of the reference's f32-math kernels, run
     with the reference's unfused dispatch sequence and f16 storage rounding)
@@ -666,6 +713,8 @@ def main():
         line["block"] = block_times(ctx, args.frames, max(1, args.attention_iters // 2))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
+        if args.attention_iters > 0:
+            line["cpu_baseline_legs"] = cpu_baseline_legs(args.frames)
     print(json.dumps(line), flush=True)
 
 
