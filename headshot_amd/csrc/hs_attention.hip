@@ -48,7 +48,11 @@ constexpr int kThreads = 64 * kWaves;
 #endif
 constexpr int kQB = HS_ATT_QB;
 constexpr int kBM = 32 * kQB * kWaves;  // queries per workgroup
-constexpr int kBN = 64;           // keys per tile
+#ifndef HS_ATT_BN
+#define HS_ATT_BN 64  // keys per tile (a multiple of 32)
+#endif
+constexpr int kBN = HS_ATT_BN;    // keys per tile
+constexpr int kKB = kBN / 32;     // 32-key blocks per tile
 // LDS row pitch (halves) of the K and V tiles: 160 B, so both the 16-byte
 // operand reads of 32 rows and the 8-byte transposing reads of 8 rows
 // spread evenly over the 64 banks.
@@ -98,45 +102,49 @@ __device__ __forceinline__ void store_rows(const TileChunks& r, f16* buf, int ti
     }
 }
 
-// S^T (keys x queries) of one 64-key tile for the wave's query blocks:
-// s[b][0] holds keys [0, 32), s[b][1] keys [32, 64); register r of lane
-// (n, hh) is key 8 (r / 4) + 4 hh + r % 4 of its block, query n of block b.
+// S^T (keys x queries) of one tile for the wave's query blocks: s[b][kb]
+// holds keys [32 kb, 32 kb + 32) of the tile; register r of lane (n, hh) is
+// key 8 (r / 4) + 4 hh + r % 4 of its block, query n of query block b.
 // Each K operand read from LDS feeds the MFMAs of every query block.
-__device__ __forceinline__ void qk_scores(f32x16 (&s)[kQB][2], const f16* kbuf,
+__device__ __forceinline__ void qk_scores(f32x16 (&s)[kQB][kKB], const f16* kbuf,
                                           const h8 (&qa)[kQB][4], int n, int hh) {
     const f16* a0 = kbuf + n * kPitch + 8 * hh;
-    const f16* a1 = a0 + 32 * kPitch;
     const f32x16 z = {};
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
-        const h8 k0 = as_h8(ld16(a0 + 16 * ks)), k1 = as_h8(ld16(a1 + 16 * ks));
 #pragma unroll
-        for (int b = 0; b < kQB; b++) {
-            s[b][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k0, qa[b][ks], ks ? s[b][0] : z, 0, 0, 0);
-            s[b][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(k1, qa[b][ks], ks ? s[b][1] : z, 0, 0, 0);
+        for (int kb = 0; kb < kKB; kb++) {
+            const h8 kv = as_h8(ld16(a0 + 32 * kb * kPitch + 16 * ks));
+#pragma unroll
+            for (int b = 0; b < kQB; b++)
+                s[b][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kv, qa[b][ks], ks ? s[b][kb] : z, 0, 0, 0);
         }
     }
 }
 
 // Keys at or past t score -inf (the partial last tile).
-__device__ __forceinline__ void mask_tail(f32x16& s0, f32x16& s1, int key0, int t, int hh) {
+__device__ __forceinline__ void mask_tail(f32x16 (&s)[kKB], int key0, int t, int hh) {
 #pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const int kr = key0 + 8 * (r / 4) + 4 * hh + (r % 4);
-        if (kr >= t) s0[r] = -INFINITY;
-        if (kr + 32 >= t) s1[r] = -INFINITY;
-    }
+    for (int kb = 0; kb < kKB; kb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int kr = key0 + 32 * kb + 8 * (r / 4) + 4 * hh + (r % 4);
+            if (kr >= t) s[kb][r] = -INFINITY;
+        }
 }
 
 // Online-softmax update for one tile's scores (already masked): returns
-// P^T as f16 B operands (registers 8 kk .. 8 kk + 7 of s_kb in p[kb][kk])
+// P^T as f16 B operands (registers 8 kk .. 8 kk + 7 of s[kb] in p[kb][kk])
 // and the factor the running output must be scaled by.
-__device__ __forceinline__ float softmax_tile(const f32x16& s0, const f32x16& s1, float c,
-                                              float& m, float& l, u32x4 (&p)[2][2]) {
+__device__ __forceinline__ float softmax_tile(const f32x16 (&s)[kKB], float c, float& m, float& l,
+                                              u32x4 (&p)[kKB][2]) {
     // a sequential chain, which the compiler turns into v_max3_f32
-    float mx = fmaxf(s0[0], s1[0]);
+    float mx = s[0][0];
 #pragma unroll
-    for (int r = 1; r < 16; r++) mx = fmaxf(fmaxf(mx, s0[r]), s1[r]);
+    for (int kb = 0; kb < kKB; kb++)
+#pragma unroll
+        for (int r = (kb == 0 ? 1 : 0); r < 16; r += 2)
+            mx = r + 1 < 16 ? fmaxf(fmaxf(mx, s[kb][r]), s[kb][r + 1]) : fmaxf(mx, s[kb][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float m_new = fmaxf(m, mx * c);
     const float corr = __builtin_amdgcn_exp2f(m - m_new);
@@ -146,15 +154,14 @@ __device__ __forceinline__ float softmax_tile(const f32x16& s0, const f32x16& s1
 #pragma unroll
     for (int kk = 0; kk < 2; kk++)
 #pragma unroll
-        for (int w = 0; w < 4; w++) {
-            const int r = 8 * kk + 2 * w;
-            p[0][kk][w] = pk_f16(__builtin_amdgcn_exp2f(fmaf(s0[r], c, -m_new)),
-                                 __builtin_amdgcn_exp2f(fmaf(s0[r + 1], c, -m_new)));
-            p[1][kk][w] = pk_f16(__builtin_amdgcn_exp2f(fmaf(s1[r], c, -m_new)),
-                                 __builtin_amdgcn_exp2f(fmaf(s1[r + 1], c, -m_new)));
-            ps = __builtin_amdgcn_fdot2(u2h2(p[0][kk][w]), one2, ps, false);
-            ps = __builtin_amdgcn_fdot2(u2h2(p[1][kk][w]), one2, ps, false);
-        }
+        for (int w = 0; w < 4; w++)
+#pragma unroll
+            for (int kb = 0; kb < kKB; kb++) {
+                const int r = 8 * kk + 2 * w;
+                p[kb][kk][w] = pk_f16(__builtin_amdgcn_exp2f(fmaf(s[kb][r], c, -m_new)),
+                                      __builtin_amdgcn_exp2f(fmaf(s[kb][r + 1], c, -m_new)));
+                ps = __builtin_amdgcn_fdot2(u2h2(p[kb][kk][w]), one2, ps, false);
+            }
     l = fmaf(l, corr, ps);
     m = m_new;
     return corr;
@@ -172,12 +179,12 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // in the order the score accumulator holds P^T (keys 16 kk + 4 hh + j and
 // 16 kk + 8 + 4 hh + j of a 32-key block).
 __device__ __forceinline__ void pv_update(f32x16 (&o)[kQB][2], const f16* vbuf,
-                                          const u32x4 (&p)[kQB][2][2], int n, int hh) {
+                                          const u32x4 (&p)[kQB][kKB][2], int n, int hh) {
     const int lane16 = n & 15;  // lane within its 16-lane group
     const int c0 = n & 16;      // channel base of the group within a 32-channel block
     const f16* base = vbuf + (4 * hh + lane16 / 4) * kPitch + c0 + 4 * (lane16 % 4);
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; kb2++)
+    for (int kb2 = 0; kb2 < kKB; kb2++)
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
             const f16* r0 = base + (32 * kb2 + 16 * kk) * kPitch;
@@ -291,13 +298,13 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
             load_rows(pk, kb, (j + 1) * kBN, t, tid);
             load_rows(pv, vb, (j + 1) * kBN, t, tid);
         }
-        f32x16 sc[kQB][2];
+        f32x16 sc[kQB][kKB];
         qk_scores(sc, sm.k[cur], qa, n, hh);
-        u32x4 p[kQB][2][2];
+        u32x4 p[kQB][kKB][2];
 #pragma unroll
         for (int b = 0; b < kQB; b++) {
-            if ((j + 1) * kBN > t) mask_tail(sc[b][0], sc[b][1], j * kBN, t, hh);
-            const float corr = softmax_tile(sc[b][0], sc[b][1], c, m[b], l[b], p[b]);
+            if ((j + 1) * kBN > t) mask_tail(sc[b], j * kBN, t, hh);
+            const float corr = softmax_tile(sc[b], c, m[b], l[b], p[b]);
             rescale(o[b][0], o[b][1], corr);
         }
         pv_update(o, sm.v[cur], p, n, hh);
