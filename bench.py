@@ -532,29 +532,33 @@ def summarize(args) -> None:
                 (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     if gem:
         m = args.frames * t_tok
-        names = {"0": [("qkv", 3 * DIM, DIM)], "1": [("fc1", HIDDEN, DIM)],
-                 "2": [("proj", DIM, DIM), ("fc2", DIM, HIDDEN)]}
+
+        def grid_items(n):
+            # the fast path's launch: 256 x 256 output tiles, rounded up to a
+            # multiple of 8 workgroups (one per XCD), 512 work-items each
+            tiles = -(-m // 256) * (n // 256)
+            return -(-tiles // 8) * 8 * 512
+
+        # (epilogue, n) -> the layers of that launch shape; proj and fc2
+        # share both, and fc2 (k = 4096) runs the longer half of the calls
+        layers = {("0", 3 * DIM): [("qkv", DIM)], ("0", DIM): [("q / k / v (whole-block leg)", DIM)],
+                  ("0", HIDDEN): [("fc1, no epilogue (comparison)", DIM)],
+                  ("1", HIDDEN): [("fc1", DIM)], ("2", DIM): [("proj", DIM), ("fc2", HIDDEN)]}
+        epis = ["bias", "bias + GELU", "bias + LayerScale + residual"]
         out += ["", "## Linear layers (gemm_f16_kernel, f16, epilogue fused)", "",
                 "| layer | epilogue | kernel calls | mean us | TFLOP/s | of 2.5 PFLOP/s |",
                 "|---|---|---|---|---|---|"]
-        for epi, cands in names.items():
-            groups = sorted((kv for kv in gem.items() if kv[0][0] == epi),
-                            key=lambda kv: st.mean(kv[1]))
-            # proj and fc2 share the epilogue and grid; fc2 (k = 4096) runs longer
-            for (key, durs), (name, n, k) in zip(groups, cands) if len(groups) == len(cands) else []:
-                mu = st.mean(durs)
+        for (epi, n), cands in layers.items():
+            durs = sorted(gem.get((epi, grid_items(n)), []))
+            if not durs:
+                continue
+            size = len(durs) // len(cands)
+            for i, (name, k) in enumerate(cands):
+                part = durs[i * size:(i + 1) * size]
+                mu = st.mean(part)
                 tf = 2.0 * m * n * k / (mu * 1e-6) / 1e12
-                out.append(f"| {name} | {['bias', 'bias + GELU', 'bias + LayerScale + residual'][int(epi)]} "
-                           f"| {len(durs)} | {mu:.1f} | {tf:.0f} | {tf / MFMA_PEAK_TFLOPS:.1%} |")
-            if len(groups) == 1 and len(cands) == 2:
-                # same grid: split by duration around the median
-                durs = sorted(groups[0][1])
-                half = len(durs) // 2
-                for part, (name, n, k) in zip((durs[:half], durs[half:]), cands):
-                    mu = st.mean(part)
-                    tf = 2.0 * m * n * k / (mu * 1e-6) / 1e12
-                    out.append(f"| {name} | bias + LayerScale + residual | {len(part)} | {mu:.1f} | "
-                               f"{tf:.0f} | {tf / MFMA_PEAK_TFLOPS:.1%} |")
+                out.append(f"| {name} | {epis[int(epi)]} | {len(part)} | {mu:.1f} | "
+                           f"{tf:.0f} | {tf / MFMA_PEAK_TFLOPS:.1%} |")
     if args.pmc_fetch and args.pmc_write:
         def counters(path, name):
             # The calibration copy (torch's device-to-device copy_) runs as

@@ -230,6 +230,32 @@ class BlockWeights:
         return BlockWeights(p, w(dim, dim), w(dim, dim), w(dim, dim), b(dim), b(dim), b(dim),
                             w(dim, dim), w(hidden, dim), w(dim, hidden))
 
+    @staticmethod
+    def load(weights, prefix: str, qk_norm: bool, precision, device) -> "BlockWeights":
+        """``{prefix}.{norm1, attn.qkv, ...}`` from a converted checkpoint
+        (model/block.rs:60-110): linear weights at ``precision``, norms,
+        biases and gammas f32. The fused qkv projection, stored as q | k | v
+        stacked on its output rows, is split into three (dim, dim) weights
+        and three biases, each a contiguous row slice."""
+        from .weights import upload_at, upload_f32
+
+        f32t = lambda s: upload_f32(weights, f"{prefix}.{s}", device)  # noqa: E731
+        gemm = lambda s: upload_at(weights, f"{prefix}.{s}", precision, device)  # noqa: E731
+        dim = weights.tensor(f"{prefix}.norm1.weight").shape[0]
+        qkv_w, qkv_b = gemm("attn.qkv.weight"), f32t("attn.qkv.bias")
+        assert tuple(qkv_w.shape) == (3 * dim, dim), f"{prefix}: qkv weight shape"
+        q_w, k_w, v_w = (qkv_w[i * dim:(i + 1) * dim].contiguous() for i in range(3))
+        q_b, k_b, v_b = (qkv_b[i * dim:(i + 1) * dim].contiguous() for i in range(3))
+        qn = (f32t("attn.q_norm.weight"), f32t("attn.q_norm.bias")) if qk_norm else None
+        kn = (f32t("attn.k_norm.weight"), f32t("attn.k_norm.bias")) if qk_norm else None
+        p = BlockParams(ln1=(f32t("norm1.weight"), f32t("norm1.bias")),
+                        ln2=(f32t("norm2.weight"), f32t("norm2.bias")), qn=qn, kn=kn,
+                        proj_b=f32t("attn.proj.bias"), ls1=f32t("ls1.gamma"),
+                        fc1_b=f32t("mlp.fc1.bias"), fc2_b=f32t("mlp.fc2.bias"),
+                        ls2=f32t("ls2.gamma"))
+        return BlockWeights(p, q_w, k_w, v_w, q_b, k_b, v_b, gemm("attn.proj.weight"),
+                            gemm("mlp.fc1.weight"), gemm("mlp.fc2.weight"))
+
 
 def block_forward(ctx: HipContext, wts: BlockWeights, x, s: int, t: int, heads: int = HEADS,
                   rope=None, eps: float = 1e-6):

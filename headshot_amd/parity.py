@@ -110,3 +110,74 @@ def ulp_diff_f16(actual, expected) -> np.ndarray:
     a = np.where(a < 0, -32768 - a, a)
     e = np.where(e < 0, -32768 - e, e)
     return np.abs(a - e)
+
+
+# ---------------------------------------------------------------------------
+# locally generated fixtures (parity.rs:106-176)
+
+def fixtures_dir():
+    """Where the locally generated fixtures live (converted weights in the
+    directory itself, reference activation dumps under ``dumps/``):
+    ``$HEADSHOT_FIXTURES_DIR``, else ``fixtures/`` at the repository root
+    (parity.rs:106-112). Fixtures are derived from the gated checkpoint and
+    are never committed."""
+    import os
+    from pathlib import Path
+
+    env = os.environ.get("HEADSHOT_FIXTURES_DIR")
+    return Path(env) if env else Path(__file__).resolve().parent.parent / "fixtures"
+
+
+@dataclass(frozen=True)
+class DumpMeta:
+    """The ``headshot`` metadata a reference dump carries (parity.rs:114-125)."""
+    scene: str
+    variant: str
+    device: str
+    n_frames: int
+    width: int
+    height: int
+    seed: int
+    shapes: dict  # name -> shape list
+
+
+class Dump:
+    """A reference activation dump, one scene x one precision variant
+    (``dump_{scene}_{variant}.safetensors``; parity.rs:127-176). Tensors are
+    all f32."""
+
+    def __init__(self, meta: DumpMeta, st):
+        self.meta, self._st = meta, st
+
+    @staticmethod
+    def open(scene: str, variant: str) -> "Dump":
+        return Dump.open_path(fixtures_dir() / "dumps" / f"dump_{scene}_{variant}.safetensors")
+
+    @staticmethod
+    def open_path(path) -> "Dump":
+        import json
+
+        from .weights import SafeTensorsFile, WeightsIoError
+
+        try:
+            st = SafeTensorsFile(path)
+        except WeightsIoError as e:
+            raise FileNotFoundError(f"{path}: {e} (generate with tools/dump_reference.py)") from None
+        raw = (st.metadata or {}).get("headshot")
+        if raw is None:
+            raise ValueError(f"{path}: missing `headshot` metadata")
+        m = json.loads(raw)
+        meta = DumpMeta(str(m["scene"]), str(m["variant"]), str(m["device"]), int(m["n_frames"]),
+                        int(m["width"]), int(m["height"]), int(m["seed"]),
+                        {k: [int(d) for d in v] for k, v in m["shapes"].items()})
+        return Dump(meta, st)
+
+    def tensor(self, name: str):
+        """(shape, f32 values) of one tensor; anything but f32 is an error."""
+        if self._st.dtype(name) != "F32":
+            raise ValueError(f"{name}: dump tensors must be f32, got {self._st.dtype(name)}")
+        a = self._st.tensor(name)
+        return list(a.shape), np.array(a, dtype=np.float32).ravel()
+
+    def names(self) -> list:
+        return self._st.names()

@@ -1,0 +1,185 @@
+"""The aggregator trunk on HIP from a converted checkpoint
+(headshot_amd.trunk.Trunk; model/trunk.rs), on a synthetic trunk-only
+checkpoint of 5 block pairs (layers 0-4: layer 2 is a register-attention
+layer, layer 4 a cached one), 2 frames of a 4 x 6 patch grid (T = 41).
+
+Three comparisons, each over every tap (trunk.frame.NN, trunk.inter.NN,
+cache.NN) with parity.rs's metrics:
+- f16 fused trunk vs the reference's dispatch sequence through this
+  library's single ops: they differ only where fused ops skip or reorder
+  an f16 storage rounding (a few ulp: rel_max 2e-3, 1 - cosine 2e-7);
+- f16 fused trunk vs a float32 torch trunk written here from the
+  checkpoint's values as the safetensors library reads them (independent
+  of the package's loader): the f16 engine's storage roundings, gated as
+  the reference gates its f16 trunk (cosine >= 0.999) and tighter
+  (rel_max 5e-3, 1 - cosine 2e-6);
+- f32 trunk vs the same float32 torch trunk: sum-order differences only,
+  gated with the reference's shallow f32 gate (rel_max 1e-4, cosine
+  1 - 1e-6) and tighter (rel_max 5e-6, 1 - cosine 1e-10).
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from headshot_amd import rope as rp
+from headshot_amd import weights as W
+from headshot_amd.parity import Gate, compare
+from headshot_amd.trunk import CACHED_LAYERS, PREFIX, REGISTER_ATTENTION_LAYERS, Trunk
+from tests.ckpt_synth import synth_values, write_checkpoint
+
+pytestmark = pytest.mark.gpu
+
+DEPTH, N, GRID = 5, 2, (4, 6)
+F32_STORED = "aggregator.frame_blocks.1.mlp.fc2.weight"   # an "outlier" weight kept f32
+
+
+@pytest.fixture(scope="module")
+def ckpt(tmp_path_factory):
+    tree = W.trunk_tree(DEPTH)
+    vals = synth_values(tree, 11, f32_names={F32_STORED})
+    d = write_checkpoint(tmp_path_factory.mktemp("trunk_ckpt"), vals)
+    from safetensors.numpy import load_file
+    return d, tree, load_file(str(d / "model.safetensors"))
+
+
+@pytest.fixture(scope="module")
+def dino():
+    g = torch.Generator(device="cpu").manual_seed(21)
+    return torch.randn((N * GRID[0] * GRID[1], 1024), generator=g)
+
+
+def run(ctx, trunk, tokens, fused=True):
+    taps = {}
+
+    def tap(name, t):
+        torch.cuda.synchronize()
+        taps[name] = t.float().cpu().numpy().copy()
+
+    caches = trunk.forward(ctx, tokens.to("cuda:0"), N, *GRID, tap=tap, fused=fused)
+    assert len(caches) == len([k for k in CACHED_LAYERS if k < DEPTH])
+    return taps
+
+
+def torch_trunk(st, tokens, precision_round: bool):
+    """float32 restatement of Trunk::forward (trunk.rs:49-146) on the
+    checkpoint's values; ``precision_round`` rounds the assembled tokens to
+    f16 first, as the f16 engine's input is."""
+    dev = "cuda:0"
+    f = lambda name: torch.from_numpy(st[name].astype(np.float32)).to(dev)  # noqa: E731
+    h_p, w_p = GRID
+    p = h_p * w_p
+    t = p + PREFIX
+    cam = f("aggregator.camera_token").reshape(2, 1024)
+    reg = f("aggregator.register_token").reshape(32, 1024)
+    frames = []
+    for i in range(N):
+        v = int(i != 0)
+        frames += [cam[v:v + 1], reg[v * 16:(v + 1) * 16], tokens[i * p:(i + 1) * p].to(dev)]
+    x = torch.cat(frames)
+    if precision_round:
+        x = x.half().float()
+    sin, cos = (torch.from_numpy(a).to(dev) for a in rp.tables(st["aggregator.rope_embed.periods"],
+                                                                h_p, w_p))
+
+    def ln(a, pre):
+        return F.layer_norm(a, (a.shape[-1],), f(pre + ".weight"), f(pre + ".bias"), 1e-5)
+
+    def block(x, pre, s, tt, rope):
+        normed = ln(x, pre + ".norm1")
+        qkv = normed @ f(pre + ".attn.qkv.weight").t().contiguous() + f(pre + ".attn.qkv.bias")
+        q, k, v = (a.reshape(s, tt, 16, 64).permute(0, 2, 1, 3).contiguous()
+                   for a in qkv.split(1024, dim=-1))
+        q, k = ln(q, pre + ".attn.q_norm"), ln(k, pre + ".attn.k_norm")
+        if rope:
+            def rot(a):
+                lo, hi = a[..., PREFIX:, :32], a[..., PREFIX:, 32:]
+                out = a.clone()
+                out[..., PREFIX:, :32] = lo * cos[:, :32] - hi * sin[:, :32]
+                out[..., PREFIX:, 32:] = hi * cos[:, 32:] + lo * sin[:, 32:]
+                return out
+            q, k = rot(q), rot(k)
+        sc = torch.matmul(q, k.transpose(-1, -2).contiguous()) / 8.0
+        o = torch.matmul(torch.softmax(sc, dim=-1), v).permute(0, 2, 1, 3).reshape(s * tt, 1024)
+        x1 = x + f(pre + ".ls1.gamma") * (o @ f(pre + ".attn.proj.weight").t().contiguous()
+                                          + f(pre + ".attn.proj.bias"))
+        h = F.gelu(ln(x1, pre + ".norm2") @ f(pre + ".mlp.fc1.weight").t().contiguous()
+                   + f(pre + ".mlp.fc1.bias"))
+        return x1 + f(pre + ".ls2.gamma") * (h @ f(pre + ".mlp.fc2.weight").t().contiguous()
+                                             + f(pre + ".mlp.fc2.bias"))
+
+    taps = {}
+    for k in range(DEPTH):
+        fo = block(x, f"aggregator.frame_blocks.{k}", N, t, True)
+        taps[f"trunk.frame.{k:02}"] = fo.cpu().numpy()
+        ib = f"aggregator.inter_frame_blocks.{k}"
+        if k in REGISTER_ATTENTION_LAYERS:
+            idx = torch.cat([torch.arange(i * t, i * t + PREFIX) for i in range(N)]).to(dev)
+            ro = block(fo[idx], ib, 1, N * PREFIX, False)
+            taps[f"trunk.inter.{k:02}"] = ro.cpu().numpy()
+            fo = fo.clone()
+            fo[idx] = ro
+            x = fo
+        else:
+            io = block(fo, ib, 1, N * t, False)
+            taps[f"trunk.inter.{k:02}"] = io.cpu().numpy()
+            if k in CACHED_LAYERS:
+                taps[f"cache.{k:02}"] = torch.cat([fo, io], dim=-1).cpu().numpy()
+            x = io
+    return taps
+
+
+def gate_all(ours, ref, gate, what):
+    assert sorted(ours) == sorted(ref), f"{what}: tap names"
+    worst = {}
+    for name in sorted(ref):
+        assert ours[name].shape == ref[name].shape, f"{what} {name}: shape"
+        m = gate.check(f"{what} {name}", compare(ours[name], ref[name]))
+        worst[name] = (m.rel_max_err(), 1.0 - m.cosine_sim)
+    print(what, {k: f"rel_max {a:.2e} 1-cos {b:.1e}" for k, (a, b) in worst.items()})
+
+
+def test_trunk_load_matches_checkpoint(ckpt):
+    d, tree, st = ckpt
+    w = W.Weights.open(d, tree=tree)
+    tr = Trunk.load(w, torch.float16, "cuda:0", depth=DEPTH)
+    assert tr.depth == DEPTH
+    qkv = st["aggregator.inter_frame_blocks.3.attn.qkv.weight"]
+    assert tr.inter_blocks[3].v_w.cpu().numpy().tobytes() == qkv[2048:3072].tobytes()
+    np.testing.assert_array_equal(tr.frame_blocks[1].fc2_w.cpu().numpy(),
+                                  torch.from_numpy(st[F32_STORED]).half().numpy())
+    np.testing.assert_array_equal(tr.register_token.cpu().float().numpy(),
+                                  st["aggregator.register_token"].reshape(32, 1024).astype(np.float16)
+                                  .astype(np.float32))
+    np.testing.assert_array_equal(tr.periods, st["aggregator.rope_embed.periods"])
+
+
+def test_trunk_f16_fused_vs_reference_sequence(ctx, ckpt, dino):
+    d, tree, _ = ckpt
+    tr = Trunk.load(W.Weights.open(d, tree=tree), torch.float16, "cuda:0", depth=DEPTH)
+    fused = run(ctx, tr, dino, fused=True)
+    seq = run(ctx, tr, dino, fused=False)
+    # every tap stays within f16 storage noise of the reference sequence,
+    # and the cache is the exact f32 widening of the two outputs it joins
+    gate_all(fused, seq, Gate(2e-3, 1.0 - 2e-7), "f16 fused vs reference sequence")
+    cat = fused["cache.04"]
+    np.testing.assert_array_equal(cat[:, :1024], fused["trunk.frame.04"])
+    np.testing.assert_array_equal(cat[:, 1024:], fused["trunk.inter.04"])
+
+
+def test_trunk_f16_vs_float32(ctx, ckpt, dino):
+    d, tree, st = ckpt
+    tr = Trunk.load(W.Weights.open(d, tree=tree), torch.float16, "cuda:0", depth=DEPTH)
+    ours = run(ctx, tr, dino)
+    ref = torch_trunk(st, dino, precision_round=True)
+    gate_all(ours, ref, Gate.F16_TRUNK, "f16 trunk vs float32 (reference f16 gate)")
+    gate_all(ours, ref, Gate(5e-3, 1.0 - 2e-6), "f16 trunk vs float32")
+
+
+def test_trunk_f32_vs_float32(ctx, ckpt, dino):
+    d, tree, st = ckpt
+    tr = Trunk.load(W.Weights.open(d, tree=tree), torch.float32, "cuda:0", depth=DEPTH)
+    ours = run(ctx, tr, dino)
+    ref = torch_trunk(st, dino, precision_round=False)
+    gate_all(ours, ref, Gate.F32_TIGHT, "f32 trunk vs float32 (reference f32 gate)")
+    gate_all(ours, ref, Gate(5e-6, 1.0 - 1e-10), "f32 trunk vs float32")
