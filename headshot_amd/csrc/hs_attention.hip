@@ -53,17 +53,30 @@ constexpr int kBM = 32 * kQB * kWaves;  // queries per workgroup
 #endif
 constexpr int kBN = HS_ATT_BN;    // keys per tile
 constexpr int kKB = kBN / 32;     // 32-key blocks per tile
-// LDS row pitch (halves) of the K and V tiles: 160 B, so both the 16-byte
-// operand reads of 32 rows and the 8-byte transposing reads of 8 rows
-// spread evenly over the 64 banks.
-constexpr int kPitch = kD + 16;
+// LDS row pitches (halves) of the K and V tiles, multiples of 8 so rows
+// stay 16-byte aligned. The LDS has 64 4-byte banks and serves a 16-byte
+// read 16 lanes at a time, an 8-byte read 32 lanes at a time. K (144 B
+// rows): the 16 rows of one 16-byte read start 36 banks apart, covering
+// all 64 banks once. V (192 B rows): the transposing read's 32 lanes cover
+// 4 rows x 64 bytes, and rows 48 banks apart put the four 16-bank spans on
+// disjoint banks. Both are conflict-free (a common 160 B pitch makes every
+// K read and V read two-way conflicted).
+#ifndef HS_ATT_KPAD
+#define HS_ATT_KPAD 8
+#endif
+#ifndef HS_ATT_VPAD
+#define HS_ATT_VPAD 32
+#endif
+constexpr int kKPitch = kD + HS_ATT_KPAD;
+constexpr int kVPitch = kD + HS_ATT_VPAD;
+static_assert(HS_ATT_KPAD % 8 == 0 && HS_ATT_VPAD % 8 == 0, "rows must stay 16-byte aligned");
 constexpr int kChunks = kBN * kD / 8;  // 16-byte chunks per K (or V) tile
 constexpr int kPer = (kChunks + kThreads - 1) / kThreads;
 static_assert(kChunks % kThreads == 0 || kThreads % kChunks == 0, "tile split");
 
 struct FlashSmem {
-    f16 k[2][kBN * kPitch];
-    f16 v[2][kBN * kPitch];
+    f16 k[2][kBN * kKPitch];
+    f16 v[2][kBN * kVPitch];
 };
 
 __device__ __forceinline__ h8 as_h8(u32x4 v) { return __builtin_bit_cast(h8, v); }
@@ -92,7 +105,8 @@ __device__ __forceinline__ void load_rows(TileChunks& r, const f16* src, int key
     }
 }
 
-// Row-major into LDS with the padded pitch.
+// Row-major into LDS with a padded pitch.
+template <int kPitch>
 __device__ __forceinline__ void store_rows(const TileChunks& r, f16* buf, int tid) {
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
@@ -108,13 +122,13 @@ __device__ __forceinline__ void store_rows(const TileChunks& r, f16* buf, int ti
 // Each K operand read from LDS feeds the MFMAs of every query block.
 __device__ __forceinline__ void qk_scores(f32x16 (&s)[kQB][kKB], const f16* kbuf,
                                           const h8 (&qa)[kQB][4], int n, int hh) {
-    const f16* a0 = kbuf + n * kPitch + 8 * hh;
+    const f16* a0 = kbuf + n * kKPitch + 8 * hh;
     const f32x16 z = {};
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
 #pragma unroll
         for (int kb = 0; kb < kKB; kb++) {
-            const h8 kv = as_h8(ld16(a0 + 32 * kb * kPitch + 16 * ks));
+            const h8 kv = as_h8(ld16(a0 + 32 * kb * kKPitch + 16 * ks));
 #pragma unroll
             for (int b = 0; b < kQB; b++)
                 s[b][kb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kv, qa[b][ks], ks ? s[b][kb] : z, 0, 0, 0);
@@ -182,17 +196,17 @@ __device__ __forceinline__ void pv_update(f32x16 (&o)[kQB][2], const f16* vbuf,
                                           const u32x4 (&p)[kQB][kKB][2], int n, int hh) {
     const int lane16 = n & 15;  // lane within its 16-lane group
     const int c0 = n & 16;      // channel base of the group within a 32-channel block
-    const f16* base = vbuf + (4 * hh + lane16 / 4) * kPitch + c0 + 4 * (lane16 % 4);
+    const f16* base = vbuf + (4 * hh + lane16 / 4) * kVPitch + c0 + 4 * (lane16 % 4);
 #pragma unroll
     for (int kb2 = 0; kb2 < kKB; kb2++)
 #pragma unroll
         for (int kk = 0; kk < 2; kk++) {
-            const f16* r0 = base + (32 * kb2 + 16 * kk) * kPitch;
+            const f16* r0 = base + (32 * kb2 + 16 * kk) * kVPitch;
             h8 a[2];
 #pragma unroll
             for (int mb = 0; mb < 2; mb++) {
                 const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(r0 + 32 * mb));
-                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(r0 + 8 * kPitch + 32 * mb));
+                const s16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(r0 + 8 * kVPitch + 32 * mb));
                 const u32x2 wl = __builtin_bit_cast(u32x2, lo), wh = __builtin_bit_cast(u32x2, hi);
                 u32x4 w;
                 w[0] = wl[0], w[1] = wl[1], w[2] = wh[0], w[3] = wh[1];
@@ -289,8 +303,8 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
     TileChunks pk, pv;
     load_rows(pk, kb, 0, t, tid);
     load_rows(pv, vb, 0, t, tid);
-    store_rows(pk, sm.k[0], tid);
-    store_rows(pv, sm.v[0], tid);
+    store_rows<kKPitch>(pk, sm.k[0], tid);
+    store_rows<kVPitch>(pv, sm.v[0], tid);
     __syncthreads();
     for (int j = 0; j < ntiles; j++) {
         const int cur = j & 1;
@@ -309,8 +323,8 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
         }
         pv_update(o, sm.v[cur], p, n, hh);
         if (j + 1 < ntiles) {
-            store_rows(pk, sm.k[cur ^ 1], tid);
-            store_rows(pv, sm.v[cur ^ 1], tid);
+            store_rows<kKPitch>(pk, sm.k[cur ^ 1], tid);
+            store_rows<kVPitch>(pv, sm.v[cur ^ 1], tid);
         }
         __syncthreads();
     }
