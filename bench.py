@@ -88,6 +88,9 @@ def parse():
     ap.add_argument("--pmc-fetch", metavar="CSV", help="counter_collection CSV of a FETCH_SIZE run")
     ap.add_argument("--pmc-write", metavar="CSV", help="counter_collection CSV of a WRITE_SIZE run")
     ap.add_argument("--traffic-json", metavar="PATH", help="write per-op HBM bytes here")
+    ap.add_argument("--summarize-counters", metavar="CSV", nargs="+",
+                    help="print derived shader-counter ratios (matrix-core and LDS use) per "
+                         "kernel from rocprofv3 --pmc counter_collection CSVs of this benchmark")
     return ap.parse_args()
 
 
@@ -452,6 +455,58 @@ def load_traffic(op: str, frames: int, dtype: str):
             "source": f"profiles/{os.path.basename(TRAFFIC_JSON)}"}
 
 
+def summarize_counters(paths) -> None:
+    """Per matrix-core kernel and launch shape, the mean of each shader
+    counter over its dispatches, and ratios derived from them (MI355X: 8
+    XCDs, 256 CUs, 1024 SIMDs; rocprofv3 reports GRBM_GUI_ACTIVE summed over
+    the XCDs, so one XCD's busy cycles are an eighth of it)."""
+    import csv
+    import statistics as st
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(list))
+    dur = defaultdict(list)
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            name = r["Kernel_Name"]
+            op = kernel_op(name)
+            if op is None:
+                if "flash_f16_kernel" in name:
+                    op = "flash_f16_kernel"
+                elif "gemm_f16_kernel" in name:
+                    op = "gemm_f16_kernel<" + name.split("gemm_f16_kernelILi")[1][0] + ">"
+                else:
+                    continue
+            key = (op, int(r["Grid_Size"]))
+            vals[key][r["Counter_Name"]].append(float(r["Counter_Value"]))
+            dur[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9)
+    out = ["| kernel | grid work-items | dispatches | matrix core busy | VALU co-issue with MFMA "
+           "| cycles / MFMA | VALU / MFMA | transcendental / MFMA | LDS busy "
+           "| bank-conflict cycles / LDS instr |", "|---|---|---|---|---|---|---|---|---|---|"]
+    for key in sorted(vals):
+        c = {k: st.mean(v) for k, v in vals[key].items()}
+        cyc = c.get("GRBM_GUI_ACTIVE", 0.0) / 8.0
+        if not cyc or not c.get("SQ_INSTS_MFMA"):
+            continue  # matrix-core kernels only
+
+        def f(expr, fmt):
+            try:
+                return format(expr(), fmt)
+            except (KeyError, ZeroDivisionError):
+                return "-"
+        mf = c.get("SQ_INSTS_MFMA", 0.0)
+        out.append("| " + " | ".join([
+            key[0], str(key[1]), str(len(dur[key]) // max(1, len(vals[key]))),
+            f(lambda: c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * 1024), ".1%"),
+            f(lambda: c["SQ_VALU_MFMA_COEXEC_CYCLES"] / (cyc * 1024), ".1%"),
+            f(lambda: c["SQ_VALU_MFMA_BUSY_CYCLES"] / mf, ".1f"),
+            f(lambda: (c["SQ_INSTS_VALU"] - mf) / mf, ".2f"),
+            f(lambda: c["SQ_INSTS_VALU_TRANS_F32"] / mf, ".2f"),
+            f(lambda: c["SQ_LDS_IDX_ACTIVE"] / (cyc * 256), ".1%"),
+            f(lambda: c["SQ_LDS_BANK_CONFLICT"] / c["SQ_INSTS_LDS"], ".2f")]) + " |")
+    print("\n".join(out))
+
+
 def summarize(args) -> None:
     """Markdown summary of rocprofv3 CSV output for this benchmark's kernels:
     kernel-trace durations against the algorithmic bytes, and (with
@@ -608,6 +663,9 @@ def main():
     args = parse()
     if args.summarize:
         summarize(args)
+        return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU: the fused per-layer ops are "
