@@ -46,6 +46,8 @@ SIGNATURES = {
     "hs_linear": (_S, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32]),
     "hs_linear_gelu": (_S, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32]),
     "hs_linear_ls_residual": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32]),
+    "hs_linear_qkv_heads": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                 _I32, _I32, _I32, _I32, _I32, _I32, _F]),
     "hs_concat_channels": (_S, [_P, _I32, _P, _P, _P, _I64, _I32, _I32]),
     "hs_cast_f16_to_f32": (_S, [_P, _P, _P, _I64]),
     "hs_cache_build": (_S, [_P, _I32, _P, _P, _P, _I64, _I32, _I32]),

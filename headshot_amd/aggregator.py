@@ -203,17 +203,26 @@ class FusedOpPass:
 @dataclass
 class BlockWeights:
     """One block's weights (model/block.rs:60-110): the linear weights in
-    the storage dtype, everything else f32 (``p``)."""
+    the storage dtype, everything else f32 (``p``). The attention input
+    projection stays fused as the checkpoint stores it, q | k | v on the
+    output rows of ``qkv_w``; ``q_w`` .. ``v_b`` are its row slices (views)."""
     p: BlockParams
-    q_w: torch.Tensor     # (dim, dim) storage dtype; rows = output features
-    k_w: torch.Tensor
-    v_w: torch.Tensor
-    q_b: torch.Tensor     # f32 (dim)
-    k_b: torch.Tensor
-    v_b: torch.Tensor
+    qkv_w: torch.Tensor   # (3 dim, dim) storage dtype; rows = output features
+    qkv_b: torch.Tensor   # f32 (3 dim)
     proj_w: torch.Tensor  # (dim, dim)
     fc1_w: torch.Tensor   # (hidden, dim)
     fc2_w: torch.Tensor   # (dim, hidden)
+
+    def _third(self, t, i):
+        dim = self.qkv_w.shape[1]
+        return t[i * dim:(i + 1) * dim]
+
+    q_w = property(lambda self: self._third(self.qkv_w, 0))
+    k_w = property(lambda self: self._third(self.qkv_w, 1))
+    v_w = property(lambda self: self._third(self.qkv_w, 2))
+    q_b = property(lambda self: self._third(self.qkv_b, 0))
+    k_b = property(lambda self: self._third(self.qkv_b, 1))
+    v_b = property(lambda self: self._third(self.qkv_b, 2))
 
     @staticmethod
     def random(dim: int, hidden: int, head_dim: int, dtype, device, generator,
@@ -227,16 +236,18 @@ class BlockWeights:
             return torch.randn(n, generator=generator, device=device) * 0.02
 
         p = BlockParams.random(dim, hidden, head_dim, device, generator, qk_norm, ls_init)
-        return BlockWeights(p, w(dim, dim), w(dim, dim), w(dim, dim), b(dim), b(dim), b(dim),
-                            w(dim, dim), w(hidden, dim), w(dim, hidden))
+        qkv_w = torch.cat([w(dim, dim) for _ in range(3)])
+        qkv_b = torch.cat([b(dim) for _ in range(3)])
+        return BlockWeights(p, qkv_w, qkv_b, w(dim, dim), w(hidden, dim), w(dim, hidden))
 
     @staticmethod
     def load(weights, prefix: str, qk_norm: bool, precision, device) -> "BlockWeights":
         """``{prefix}.{norm1, attn.qkv, ...}`` from a converted checkpoint
         (model/block.rs:60-110): linear weights at ``precision``, norms,
-        biases and gammas f32. The fused qkv projection, stored as q | k | v
-        stacked on its output rows, is split into three (dim, dim) weights
-        and three biases, each a contiguous row slice."""
+        biases and gammas f32. The qkv projection, stored as q | k | v
+        stacked on its output rows, stays one (3 dim, dim) weight (the
+        reference splits it into three GEMMs to stay under wgpu's buffer
+        size cap; here one fused launch computes all three)."""
         from .weights import upload_at, upload_f32
 
         f32t = lambda s: upload_f32(weights, f"{prefix}.{s}", device)  # noqa: E731
@@ -244,8 +255,6 @@ class BlockWeights:
         dim = weights.tensor(f"{prefix}.norm1.weight").shape[0]
         qkv_w, qkv_b = gemm("attn.qkv.weight"), f32t("attn.qkv.bias")
         assert tuple(qkv_w.shape) == (3 * dim, dim), f"{prefix}: qkv weight shape"
-        q_w, k_w, v_w = (qkv_w[i * dim:(i + 1) * dim].contiguous() for i in range(3))
-        q_b, k_b, v_b = (qkv_b[i * dim:(i + 1) * dim].contiguous() for i in range(3))
         qn = (f32t("attn.q_norm.weight"), f32t("attn.q_norm.bias")) if qk_norm else None
         kn = (f32t("attn.k_norm.weight"), f32t("attn.k_norm.bias")) if qk_norm else None
         p = BlockParams(ln1=(f32t("norm1.weight"), f32t("norm1.bias")),
@@ -253,26 +262,22 @@ class BlockWeights:
                         proj_b=f32t("attn.proj.bias"), ls1=f32t("ls1.gamma"),
                         fc1_b=f32t("mlp.fc1.bias"), fc2_b=f32t("mlp.fc2.bias"),
                         ls2=f32t("ls2.gamma"))
-        return BlockWeights(p, q_w, k_w, v_w, q_b, k_b, v_b, gemm("attn.proj.weight"),
-                            gemm("mlp.fc1.weight"), gemm("mlp.fc2.weight"))
+        return BlockWeights(p, qkv_w, qkv_b, gemm("attn.proj.weight"), gemm("mlp.fc1.weight"),
+                            gemm("mlp.fc2.weight"))
 
 
 def block_forward(ctx: HipContext, wts: BlockWeights, x, s: int, t: int, heads: int = HEADS,
                   rope=None, eps: float = 1e-6):
     """Block::forward (model/block.rs:118-193) with every op on HIP and the
-    epilogues fused: LN1 -> q/k/v linear -> split_heads + QK-norm + RoPE ->
-    attention written token-major -> proj + LayerScale + residual -> LN2 ->
-    fc1 + GELU -> fc2 + LayerScale + residual. ``rope`` = (sin, cos, prefix)
-    or None (global blocks). Returns the block output (S*T, dim)."""
+    epilogues fused: LN1 -> the q|k|v linear with split_heads, QK-norm and
+    RoPE in its epilogue -> attention written token-major -> proj +
+    LayerScale + residual -> LN2 -> fc1 + GELU -> fc2 + LayerScale +
+    residual (9 launches). ``rope`` = (sin, cos, prefix) or None (global
+    blocks). Returns the block output (S*T, dim)."""
     p = wts.p
-    dim = x.shape[-1]
-    hd = dim // heads
     normed = ctx.layernorm(x, *p.ln1, eps=eps)
-    q = ctx.qknorm_rope(ctx.linear(normed, wts.q_w, wts.q_b), s, t, heads, hd, norm=p.qn,
-                        rope=rope, eps=eps)
-    k = ctx.qknorm_rope(ctx.linear(normed, wts.k_w, wts.k_b), s, t, heads, hd, norm=p.kn,
-                        rope=rope, eps=eps)
-    v = ctx.qknorm_rope(ctx.linear(normed, wts.v_w, wts.v_b), s, t, heads, hd)
+    q, k, v = ctx.linear_qkv_heads(normed, wts.qkv_w, wts.qkv_b, s, t, heads, qn=p.qn, kn=p.kn,
+                                   rope=rope, eps=eps)
     attn = ctx.attention_merged(q, k, v)
     x1 = ctx.linear_ls_residual(attn, wts.proj_w, p.ls1, x, p.proj_b)
     normed2 = ctx.layernorm(x1, *p.ln2, eps=eps)

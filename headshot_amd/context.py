@@ -280,6 +280,51 @@ class HipContext:
                      sn, cs, _dev(out, "out"), s, t, h, d, prefix, eps)
         return out
 
+    def linear_qkv_heads(self, x, w_qkv, b_qkv, s: int, t: int, h: int, qn=None, kn=None,
+                         rope=None, eps: float = 1e-5, out=None):
+        """The attention input projection (model/block.rs:128-146) in one
+        kernel: x (S*T, k) @ w_qkv^T + b_qkv with w_qkv (3*H*d, k) holding q |
+        k | v on its output rows, split into head-major (S, H, T, d) q, k, v,
+        QK-norm (``qn``, ``kn`` = (weight, bias) or None) and RoPE (``rope``
+        = (sin, cos, prefix) or None) on q and k. Bit-identical to linear then
+        qknorm_rope per third for 8, 16 or 32 heads (within one f16 ulp for
+        other head counts); that sequence is what runs for shapes the fused
+        kernel does not cover (f32, head dim other than 64). Returns (q, k, v)."""
+        n3, k = w_qkv.shape
+        assert n3 % (3 * h) == 0, "w_qkv rows must be 3 * H * d"
+        d = n3 // (3 * h)
+        assert x.numel() == s * t * k and x.dtype == w_qkv.dtype, "x shape/dtype"
+        hd = h * d
+        if not (x.dtype == F16 and d == 64 and n3 % 256 == 0 and k % 64 == 0):
+            outs = []
+            for i, norm in enumerate((qn, kn, None)):
+                b = None if b_qkv is None else b_qkv[i * hd:(i + 1) * hd]
+                proj = self.linear(x, w_qkv[i * hd:(i + 1) * hd], b)
+                outs.append(self.qknorm_rope(proj, s, t, h, d, norm=norm,
+                                             rope=rope if i < 2 else None, eps=eps,
+                                             out=None if out is None else out[i]))
+            return tuple(outs)
+        b = _opt(b_qkv, n3, "qkv bias")
+        qw = qb = kw = kb = sn = cs = None
+        prefix = 0
+        if qn is not None:
+            qw, qb = _param(qn[0], d, "q-norm weight"), _param(qn[1], d, "q-norm bias")
+        if kn is not None:
+            kw, kb = _param(kn[0], d, "k-norm weight"), _param(kn[1], d, "k-norm bias")
+        if rope is not None:
+            sin, cos, prefix = rope
+            assert 0 <= prefix <= t, "prefix"
+            sn = _param(sin, (t - prefix) * d, "rope sin table")
+            cs = _param(cos, (t - prefix) * d, "rope cos table")
+        if out is None:
+            out = tuple(self.empty_typed((s, h, t, d), x.dtype) for _ in range(3))
+        for o in out:
+            assert o.dtype == x.dtype and o.numel() == s * t * hd, "out shape/dtype"
+        self._launch("linear_qkv_heads", self.lib.hs_linear_qkv_heads, _dt(x), _dev(x, "x"),
+                     _dev(w_qkv, "w_qkv"), b, qw, qb, kw, kb, sn, cs, _dev(out[0], "q out"),
+                     _dev(out[1], "k out"), _dev(out[2], "v out"), s, t, h, d, k, prefix, eps)
+        return tuple(out)
+
     def linear_gelu(self, x, weight, bias=None, out=None) -> torch.Tensor:
         """linear(fc1, bias) + GELU (model/block.rs:172-176) in one kernel."""
         k = x.shape[-1]

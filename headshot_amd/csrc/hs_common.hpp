@@ -143,11 +143,21 @@ __device__ __forceinline__ u32x4 pack(const float (&f)[4], float) {
     return v;
 }
 
+// v as a materialised f32 value. The reference computes in f32 and then
+// stores its storage type: two roundings. Left alone, the compiler may fold
+// a multiply-add and the following f16 conversion into one v_fma_mix_f16
+// (one rounding, from the exact result), which differs exactly at f16 ties,
+// and it makes that choice differently in different kernels.
+__device__ __forceinline__ float as_f32(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 // The value a later dispatch would read back after storing v as T: the
 // reference rounds to its storage type after every dispatch, and the fused
 // kernels reproduce those rounding points in registers.
 __device__ __forceinline__ float storage_round(float v, f16) {
-    return static_cast<float>(static_cast<f16>(v));
+    return static_cast<float>(static_cast<f16>(as_f32(v)));
 }
 __device__ __forceinline__ float storage_round(float v, float) { return v; }
 
@@ -218,6 +228,47 @@ __device__ __forceinline__ float group_mirror(float v) {
     static_assert(G == 8 || G == 16, "mirror within 8 or 16 lanes");
     if constexpr (G == 8) return dpp<kRowHalfMirror>(v);
     if constexpr (G == 16) return dpp<kRowMirror>(v);
+}
+
+// QK-norm and rotate-half RoPE of one 64-wide head vector spread over a
+// group of G lanes, V = 64 / G values per lane. The lane of piece p < G / 2
+// holds channels [p V, p V + V), the lane of piece p >= G / 2 the matching
+// upper channels [32 + (G - 1 - p) V, + V), so a channel's RoPE partner sits
+// in the mirror lane. LayerNorm over the 64 channels with f32 statistics
+// (eps, weight wr, bias br of the lane's channels), the storage rounding the
+// reference applies between its layernorm and rope_apply dispatches, then,
+// when rot, the rotation with cs = cos and sn = -sin (lower lanes) or +sin
+// (upper lanes) of the lane's channels. Every lane of a group must take the
+// same branches (the reductions and the mirror read across the group). The
+// results are f32 values the caller rounds to T once more on store, as the
+// reference's rope_apply output is.
+template <typename T, int G, bool NORM, int V>
+__device__ __forceinline__ void qk_norm_rope_vec(float (&f)[V], const float (&wr)[V],
+                                                 const float (&br)[V], float eps, bool rot,
+                                                 const float (&cs)[V], const float (&sn)[V]) {
+    static_assert(G * V == 64, "one 64-wide head vector per group");
+    if constexpr (NORM) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < V; k++) sum += f[k];
+        const float mean = group_sum<G>(sum) / 64.0f;
+        // the multiply-adds are spelled out as fmaf so that every kernel
+        // sharing this code rounds them the same way
+        float q = 0.0f;
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            const float d = f[k] - mean;
+            q = fmaf(d, d, q);
+        }
+        const float var = group_sum<G>(q) / 64.0f;
+        const float inv = rsqrtf(var + eps);
+#pragma unroll
+        for (int k = 0; k < V; k++) f[k] = storage_round(fmaf((f[k] - mean) * inv, wr[k], br[k]), T{});
+    }
+    if (rot) {
+#pragma unroll
+        for (int k = 0; k < V; k++) f[k] = as_f32(fmaf(f[k], cs[k], group_mirror<G>(f[k]) * sn[k]));
+    }
 }
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

@@ -6,6 +6,9 @@
 //   EPI_GELU      out = f16(gelu(acc + bias))                 (fc1 + GELU)
 //   EPI_LS        out = f16(res + gamma * f16(acc + bias))    (proj/fc2 +
 //                                                 LayerScale + residual)
+//   EPI_QKV       the fused q|k|v projection: f16(acc + bias), split into
+//                 heads and written head-major, with QK-norm and RoPE
+//                 applied to q and k (model/block.rs:128-146)
 // so the activation between a GEMM and its elementwise op never crosses HBM.
 //
 // Fast path (f16, N % kBN == 0, K % kBK == 0): matrix-core GEMM. A workgroup
@@ -34,7 +37,20 @@ namespace {
 typedef f16 h8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_LS = 2 };
+enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_LS = 2, EPI_QKV = 3 };
+
+// The q|k|v epilogue's outputs and parameters: out[0..2] head-major (S, H,
+// T, 64) q, k, v; QK-norm weight / bias per q and k (null: none); RoPE
+// tables (T - prefix, 64) (null: none).
+struct QkvArgs {
+    f16* out[3];
+    const float* nw[2];
+    const float* nb[2];
+    const float* sin_tab;
+    const float* cos_tab;
+    int seq, heads, prefix;
+    float eps;
+};
 
 // Exact-erf GELU in the A&S 7.1.26 form used by the elementwise GELU kernel
 // (gelu.wesl:18-38 with the 1/sqrt(2) folded into the constants).
@@ -138,13 +154,73 @@ __device__ __forceinline__ uint32_t pk_f16(float a, float b) {
     return h22u(h);
 }
 
+// Phase 2 of the q|k|v epilogue: the wave's staged block is 128 token rows
+// of one head of q, k or v (its 64 columns). 8 lanes per row hold the head
+// vector in the lane layout of qk_norm_rope_vec (the QK-norm / RoPE fused
+// op's), so each head vector is normalised, rotated and rounded by the same
+// code as there; each row's 128 bytes go to (frame, head, token) of the
+// head-major output.
+__device__ __forceinline__ void qkv_heads_out(const f16* stage, const QkvArgs& qa, int64_t row0,
+                                              int M, int64_t col, int lane) {
+    const int hd = qa.heads * 64;
+    const int which = static_cast<int>(col / hd);            // 0 q, 1 k, 2 v: wave-uniform
+    const int head = static_cast<int>(col - int64_t{which} * hd) / 64;
+    const int piece = lane & 7;
+    const bool upper = piece >= 4;
+    const int ch = upper ? 32 + (7 - piece) * 8 : piece * 8;
+    const float* nw = which < 2 ? qa.nw[which] : nullptr;
+    const float* nb = which < 2 ? qa.nb[which] : nullptr;
+    const bool norm = nw != nullptr;
+    const bool rope = which < 2 && qa.sin_tab != nullptr;
+    float wr[8], br[8];
+    if (norm) {
+        const float4 w0 = ld_f32x4(nw + ch), w1 = ld_f32x4(nw + ch + 4);
+        const float4 b0 = ld_f32x4(nb + ch), b1 = ld_f32x4(nb + ch + 4);
+        wr[0] = w0.x, wr[1] = w0.y, wr[2] = w0.z, wr[3] = w0.w;
+        wr[4] = w1.x, wr[5] = w1.y, wr[6] = w1.z, wr[7] = w1.w;
+        br[0] = b0.x, br[1] = b0.y, br[2] = b0.z, br[3] = b0.w;
+        br[4] = b1.x, br[5] = b1.y, br[6] = b1.z, br[7] = b1.w;
+    }
+    f16* obase = qa.out[which] + static_cast<int64_t>(head) * qa.seq * 64 + ch;
+    const float sg = upper ? 1.0f : -1.0f;
+    // this lane's row: token m = s * seq + t (m < 2^31), advanced by 8 rows
+    // per step
+    int64_t m = row0 + (lane >> 3);
+    uint32_t s = static_cast<uint32_t>(m) / static_cast<uint32_t>(qa.seq);
+    int t = static_cast<int>(static_cast<uint32_t>(m) - s * static_cast<uint32_t>(qa.seq));
+    for (int rr = 0; rr < 128; rr += 8) {
+        if (m >= M) break;  // rows grow with rr: the rest are past M too
+        float f[8];
+        unpack(ld16(stage + (rr + (lane >> 3)) * kEpiPitch + ch), f, f16{});
+        const bool rot = rope && t >= qa.prefix;  // the same for the row's 8 lanes
+        float cs[8], sn[8];
+        if (rot) {
+            const int64_t trow = static_cast<int64_t>(t - qa.prefix) * 64 + ch;
+            const float4 c0 = ld_f32x4(qa.cos_tab + trow), c1 = ld_f32x4(qa.cos_tab + trow + 4);
+            const float4 s0 = ld_f32x4(qa.sin_tab + trow), s1 = ld_f32x4(qa.sin_tab + trow + 4);
+            cs[0] = c0.x, cs[1] = c0.y, cs[2] = c0.z, cs[3] = c0.w;
+            cs[4] = c1.x, cs[5] = c1.y, cs[6] = c1.z, cs[7] = c1.w;
+            sn[0] = sg * s0.x, sn[1] = sg * s0.y, sn[2] = sg * s0.z, sn[3] = sg * s0.w;
+            sn[4] = sg * s1.x, sn[5] = sg * s1.y, sn[6] = sg * s1.z, sn[7] = sg * s1.w;
+        }
+        if (norm)
+            qk_norm_rope_vec<f16, 8, true>(f, wr, br, qa.eps, rot, cs, sn);
+        else
+            qk_norm_rope_vec<f16, 8, false>(f, wr, br, qa.eps, rot, cs, sn);
+        st16(obase + (static_cast<int64_t>(s) * qa.heads * qa.seq + t) * 64, pack(f, f16{}));
+        m += 8;
+        t += 8;
+        while (t >= qa.seq) t -= qa.seq, s++;
+    }
+}
+
 // Grid: tiles_m * tiles_n workgroups, column tiles fastest, so workgroups
 // running together share their x rows.
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     const f16* __restrict__ x, const f16* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ gamma, const f16* res, f16* out, int M, int N, int K,
-    int tiles_n, int ntiles) {
+    int tiles_n, int ntiles, QkvArgs qa) {
     __shared__ __align__(16) unsigned char smem_raw[kSmemBytes];
     GemmSmem& sm = *reinterpret_cast<GemmSmem*>(smem_raw);
     const int tid = threadIdx.x;
@@ -235,6 +311,10 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if constexpr (EPI == EPI_QKV) {
+        qkv_heads_out(stage, qa, m0 + wm, M, n0 + wn, lane);
+        return;
+    }
     // 2. 8 lanes per 128-byte row piece, 8 rows per instruction: 16-byte
     //    loads of the staged values (and of res), 16-byte stores of out.
     const int c8 = 8 * (lane & 7);
@@ -316,34 +396,43 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(
     }
 }
 
+bool fast_shape(hs_dtype dt, int N, int K, const void* x, const void* w, const float* bias,
+                const float* gamma, const void* out, const void* res) {
+    return dt == HS_F16 && N % kBN == 0 && K % kBK == 0 && aligned16(x) && aligned16(w) &&
+           (!bias || aligned16(bias)) && (!gamma || aligned16(gamma)) && aligned16(out) &&
+           (!res || aligned16(res));
+}
+
 template <int EPI>
 hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, const float* bias,
                  const float* gamma, const void* res, void* out, int M, int N, int K,
-                 const char* op) {
-    const bool fast = dt == HS_F16 && N % kBN == 0 && K % kBK == 0 && aligned16(x) && aligned16(w) &&
-                      (!bias || aligned16(bias)) && (!gamma || aligned16(gamma)) &&
-                      aligned16(out) && (!res || aligned16(res));
-    if (fast) {
+                 const char* op, const QkvArgs& qa = QkvArgs{}) {
+    if (fast_shape(dt, N, K, x, w, bias, gamma, out, res)) {
         const int tiles_n = N / kBN;
         const int64_t ntiles = ceil_div(M, kBM) * tiles_n;
         const int64_t blocks = HS_GEMM_XCD ? ceil_div(ntiles, 8) * 8 : ntiles;
         gemm_f16_kernel<EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st>>>(
             static_cast<const f16*>(x), static_cast<const f16*>(w), bias, gamma,
             static_cast<const f16*>(res), static_cast<f16*>(out), M, N, K, tiles_n,
-            static_cast<int>(ntiles));
+            static_cast<int>(ntiles), qa);
         return check_launch(op);
     }
-    const int tiles_n = static_cast<int>(ceil_div(N, kGT));
-    const int64_t blocks = ceil_div(M, kGT) * tiles_n;
-    if (dt == HS_F16)
-        gemm_generic_kernel<f16, EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, st>>>(
-            static_cast<const f16*>(x), static_cast<const f16*>(w), bias, gamma,
-            static_cast<const f16*>(res), static_cast<f16*>(out), M, N, K, tiles_n);
-    else
-        gemm_generic_kernel<float, EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, st>>>(
-            static_cast<const float*>(x), static_cast<const float*>(w), bias, gamma,
-            static_cast<const float*>(res), static_cast<float*>(out), M, N, K, tiles_n);
-    return check_launch(op);
+    if constexpr (EPI == EPI_QKV) {
+        return fail(HS_EUNSUPPORTED, "%s: needs f16, K %% %d == 0 and 16-byte aligned buffers", op,
+                    kBK);
+    } else {
+        const int tiles_n = static_cast<int>(ceil_div(N, kGT));
+        const int64_t blocks = ceil_div(M, kGT) * tiles_n;
+        if (dt == HS_F16)
+            gemm_generic_kernel<f16, EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, st>>>(
+                static_cast<const f16*>(x), static_cast<const f16*>(w), bias, gamma,
+                static_cast<const f16*>(res), static_cast<f16*>(out), M, N, K, tiles_n);
+        else
+            gemm_generic_kernel<float, EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, st>>>(
+                static_cast<const float*>(x), static_cast<const float*>(w), bias, gamma,
+                static_cast<const float*>(res), static_cast<float*>(out), M, N, K, tiles_n);
+        return check_launch(op);
+    }
 }
 
 hs_status check(const char* op, hs_dtype dt, const void* x, const void* w, const void* res,
@@ -394,4 +483,56 @@ extern "C" hs_status hs_linear_ls_residual(hs_stream_t stream, hs_dtype dt, cons
     if (rc != HS_OK || m == 0 || n == 0) return rc;
     return launch<EPI_LS>(static_cast<hipStream_t>(stream), dt, x, w, bias, gamma, res, out,
                           static_cast<int>(m), n, k, "linear_ls_residual");
+}
+
+extern "C" hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x,
+                                         const void* w_qkv, const float* b_qkv, const float* qn_w,
+                                         const float* qn_b, const float* kn_w, const float* kn_b,
+                                         const float* sin_tab, const float* cos_tab, void* q_out,
+                                         void* k_out, void* v_out, int32_t S, int32_t T,
+                                         int32_t H, int32_t d, int32_t k, int32_t prefix,
+                                         float eps) {
+    using namespace hs;
+    const char* op = "linear_qkv_heads";
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "%s: unknown dtype", op);
+    if (S < 0 || T < 0 || H <= 0 || d <= 0 || k <= 0)
+        return fail(HS_EINVAL, "%s: shape S=%d T=%d H=%d d=%d k=%d", op, S, T, H, d, k);
+    if (prefix < 0 || prefix > T) return fail(HS_EINVAL, "%s: prefix %d outside [0, %d]", op, prefix, T);
+    if ((qn_w == nullptr) != (qn_b == nullptr) || (kn_w == nullptr) != (kn_b == nullptr))
+        return fail(HS_EINVAL, "%s: a norm needs both weight and bias", op);
+    if ((sin_tab == nullptr) != (cos_tab == nullptr))
+        return fail(HS_EINVAL, "%s: RoPE needs both tables", op);
+    if (!(eps > 0.0f)) return fail(HS_EINVAL, "%s: eps must be positive", op);
+    const int64_t M = int64_t{S} * T;
+    const int64_t N = int64_t{3} * H * d;
+    if (N >= (int64_t{1} << 31) || M >= (int64_t{1} << 31) || M * N >= (int64_t{1} << 40) ||
+        M * k >= (int64_t{1} << 40))
+        return fail(HS_EINVAL, "%s: too large", op);
+    if (M == 0) return HS_OK;
+    if (!x || !w_qkv || !q_out || !k_out || !v_out) return fail(HS_EINVAL, "%s: null buffer", op);
+    const int64_t esz = dtype_size(dt), ob = M * H * d * esz;  // each of q, k, v
+    const void* outs[3] = {q_out, k_out, v_out};
+    for (int i = 0; i < 3; i++) {
+        if (overlaps(outs[i], ob, x, M * k * esz) || overlaps(outs[i], ob, w_qkv, N * k * esz))
+            return fail(HS_EINVAL, "%s: an output overlaps x or w", op);
+        for (int j = 0; j < i; j++)
+            if (overlaps(outs[i], ob, outs[j], ob)) return fail(HS_EINVAL, "%s: outputs overlap", op);
+    }
+    // The fused epilogue needs one head per wave (64 columns) and whole
+    // 256-column tiles; other shapes run linear then qknorm_rope.
+    if (dt != HS_F16 || d != 64 || N % kBN != 0)
+        return fail(HS_EUNSUPPORTED, "%s: needs f16, head dim 64 and 3*H*64 %% %d == 0", op, kBN);
+    const float* params[6] = {qn_w, qn_b, kn_w, kn_b, sin_tab, cos_tab};
+    for (const float* p : params)
+        if (p && !aligned16(p)) return fail(HS_EUNSUPPORTED, "%s: parameters must be 16-byte aligned", op);
+    if (!aligned16(k_out) || !aligned16(v_out))
+        return fail(HS_EUNSUPPORTED, "%s: outputs must be 16-byte aligned", op);
+    QkvArgs qa{};
+    qa.out[0] = static_cast<f16*>(q_out), qa.out[1] = static_cast<f16*>(k_out);
+    qa.out[2] = static_cast<f16*>(v_out);
+    qa.nw[0] = qn_w, qa.nb[0] = qn_b, qa.nw[1] = kn_w, qa.nb[1] = kn_b;
+    qa.sin_tab = sin_tab, qa.cos_tab = cos_tab;
+    qa.seq = T, qa.heads = H, qa.prefix = prefix, qa.eps = eps;
+    return launch<EPI_QKV>(static_cast<hipStream_t>(stream), dt, x, w_qkv, b_qkv, nullptr, nullptr,
+                           q_out, static_cast<int>(M), static_cast<int>(N), k, op, qa);
 }

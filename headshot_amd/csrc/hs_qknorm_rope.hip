@@ -101,28 +101,7 @@ struct QknRow {
         for (int c = 0; c < CH; c++) {
             float f[V];
             unpack(raw[c], f, T{});
-            if constexpr (NORM) {
-                float sum = 0.0f;
-#pragma unroll
-                for (int k = 0; k < V; k++) sum += f[k];
-                const float mean = group_sum<G>(sum) / static_cast<float>(D);
-                float q = 0.0f;
-#pragma unroll
-                for (int k = 0; k < V; k++) {
-                    const float d = f[k] - mean;
-                    q += d * d;
-                }
-                const float var = group_sum<G>(q) / static_cast<float>(D);
-                const float inv = rsqrtf(var + eps);
-#pragma unroll
-                for (int k = 0; k < V; k++)
-                    f[k] = storage_round((f[k] - mean) * inv * wr[k] + br[k], T{});
-            }
-            if (rot) {
-#pragma unroll
-                for (int k = 0; k < V; k++)
-                    f[k] = fmaf(f[k], cs[k], group_mirror<G>(f[k]) * sn[k]);
-            }
+            qk_norm_rope_vec<T, G, NORM>(f, wr, br, eps, rot, cs, sn);
             st_stream(obase + static_cast<int64_t>(c) * HPI * seq * D, pack(f, T{}));
         }
     }

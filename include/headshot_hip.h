@@ -212,6 +212,27 @@ hs_status hs_linear_ls_residual(hs_stream_t stream, hs_dtype dt, const void* x, 
                                 const float* bias, const float* gamma, const void* res, void* out,
                                 int64_t m, int32_t n, int32_t k);
 
+/* The attention input projection of model/block.rs:128-146 in one kernel:
+ * linear(x, w_qkv, b_qkv) with w_qkv (3*H*d, k) holding q | k | v stacked on
+ * its output rows (the checkpoint's attn.qkv layout, which Block::load
+ * splits), then split_heads (engine/ops.rs:185-200) of q, k and v into
+ * head-major (S, H, T, d) outputs, QK-norm (layernorm over d, f32
+ * statistics) and rotate-half RoPE (engine/ops.rs:202-223) of q and k.
+ * Results are bit-identical to hs_linear followed by hs_qknorm_rope on each
+ * third when H is 8, 16 or 32 (the head counts hs_qknorm_rope's row kernel
+ * covers, whose head-vector code this shares), within one f16 ulp for
+ * other H. qn_w/qn_b, kn_w/kn_b (d, f32) NULL = no QK-norm; sin/cos (T -
+ * prefix, d) f32 NULL = no RoPE; b_qkv (3*H*d) f32 may be NULL. x is (S*T,
+ * k). Fast path only: f16, d == 64, H % 4 == 0, k % 64 == 0, 16-byte aligned
+ * buffers; other shapes return HS_EUNSUPPORTED (run hs_linear then
+ * hs_qknorm_rope). Outputs must not overlap x, w_qkv or each other. */
+hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x, const void* w_qkv,
+                              const float* b_qkv, const float* qn_w, const float* qn_b,
+                              const float* kn_w, const float* kn_b, const float* sin_tab,
+                              const float* cos_tab, void* q_out, void* k_out, void* v_out,
+                              int32_t S, int32_t T, int32_t H, int32_t d, int32_t k,
+                              int32_t prefix, float eps);
+
 /* ---------------------------------------------------------------------- */
 /* Attention                                                                */
 

@@ -163,6 +163,37 @@ def test_linear_contract():
     assert L.hs_linear(None, F16, None, None, None, None, 0, 128, 64) == _lib.HS_OK
 
 
+def test_linear_qkv_heads_contract():
+    """Validation before any launch: fake, non-overlapping device addresses
+    (x, w, q, k, v at 16 MiB steps, each region far larger than its use)."""
+    x, w, q, k, v = (ctypes.c_void_p(0x1000000 * i) for i in range(1, 6))
+    nw = nb = ctypes.c_void_p(0x9000000)
+    f = L.hs_linear_qkv_heads
+
+    def call(dt=F16, x=x, w=w, qw=nw, qb=nb, kw=nw, kb=nb, sn=None, cs=None, q=q, k=k, v=v,
+             S=2, T=8, H=4, d=64, kk=64, prefix=0, eps=1e-5):
+        return f(None, dt, x, w, None, qw, qb, kw, kb, sn, cs, q, k, v, S, T, H, d, kk, prefix, eps)
+
+    assert call() is not None  # signature binds
+    _einval(call(dt=4), "dtype")
+    _einval(call(H=0), "shape")
+    _einval(call(prefix=9), "prefix")
+    _einval(call(qb=None), "weight and bias")
+    _einval(call(sn=nw), "both tables")
+    _einval(call(eps=0.0), "eps")
+    _einval(call(k=None), "null")
+    _einval(call(x=None), "null")
+    _einval(call(k=ctypes.c_void_p(0x3000000 + 64)), "outputs overlap")
+    _einval(call(v=ctypes.c_void_p(0x1000000 + 64)), "overlaps x or w")
+    assert call(dt=_lib.HS_F32) == _lib.HS_EUNSUPPORTED
+    # each output is (S*T, H*d), not (S*T, 3*H*d): w may start right after q
+    # (f32 stops with HS_EUNSUPPORTED after the overlap checks, before any launch)
+    assert call(dt=_lib.HS_F32, w=ctypes.c_void_p(0x3000000 + 2 * 8 * 4 * 64 * 4)) == _lib.HS_EUNSUPPORTED
+    assert call(d=32) == _lib.HS_EUNSUPPORTED
+    assert call(H=2) == _lib.HS_EUNSUPPORTED            # 3 * 2 * 64 = 384 columns
+    assert call(S=0) == _lib.HS_OK                      # zero tokens: no-op
+
+
 def test_python_surface_raises_contract_errors():
     with pytest.raises(_lib.HsContractError) as e:
         _lib.check(L.hs_gelu(None, F16, FAKE, FAKE2, -5), "gelu")

@@ -11,7 +11,7 @@ import pytest
 import torch
 
 from headshot_amd import _lib
-from headshot_amd.parity import assert_bit_exact, assert_close, f16_close
+from headshot_amd.parity import assert_bit_exact, assert_close, f16_close, ulp_diff_f16
 from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -129,3 +129,98 @@ def test_linear_contract(ctx):
                                                  x.data_ptr(), w.data_ptr(), None, None,
                                                  x.data_ptr(), x.data_ptr(), 4, 128, 32),
                    "linear_ls_residual")
+
+
+# ---------------------------------------------------- fused q|k|v projection
+
+def qkv_sequence(ctx, x, w, b, s, t, h, qn, kn, rope, eps):
+    """The unfused sequence: linear per third, then qknorm_rope (q, k) or the
+    plain head split (v)."""
+    hd = h * 64
+    outs = []
+    for i, norm in enumerate((qn, kn, None)):
+        proj = ctx.linear(x, w[i * hd:(i + 1) * hd], None if b is None else b[i * hd:(i + 1) * hd])
+        outs.append(ctx.qknorm_rope(proj, s, t, h, 64, norm=norm, rope=rope if i < 2 else None,
+                                    eps=eps))
+    return outs
+
+
+def qkv_case(seed, s, t, h, k, norm, prefix):
+    from headshot_amd import rope as rp
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    x = torch.randn((s * t, k), generator=g).half().to("cuda:0")
+    w = (torch.randn((3 * h * 64, k), generator=g) / k ** 0.5).half().to("cuda:0")
+    b = (torch.randn(3 * h * 64, generator=g) * 0.02).to("cuda:0")
+    nrm = lambda: ((1 + 0.1 * torch.randn(64, generator=g)).to("cuda:0"),  # noqa: E731
+                   (0.1 * torch.randn(64, generator=g)).to("cuda:0"))
+    qn, kn = (nrm(), nrm()) if norm else (None, None)
+    rope = None
+    if prefix is not None:
+        sin, cos = (torch.from_numpy(a).to("cuda:0") for a in rp.tables(rp.periods(), 1, t - prefix))
+        rope = (sin, cos, prefix)
+    return x, w, b, qn, kn, rope
+
+
+# (s, t, h, k, QK-norm, RoPE prefix or None); t = 3 and 1 are shorter than
+# the epilogue's 8-row step (its token counter wraps within a step)
+QKV_CASES = [(2, 41, 16, 256, True, 5), (1, 300, 16, 1024, True, None), (3, 20, 8, 64, False, 17),
+             (50, 3, 8, 128, True, 1), (1, 1, 8, 64, True, None), (5, 77, 32, 192, False, None),
+             (7, 30, 4, 128, True, 3), (4, 9, 12, 64, True, None)]
+
+
+@pytest.mark.parametrize("s,t,h,k,norm,prefix", QKV_CASES)
+def test_linear_qkv_heads_is_the_sequence(ctx, s, t, h, k, norm, prefix):
+    """hs_linear_qkv_heads against hs_linear + hs_qknorm_rope per third:
+    bit-exact where hs_qknorm_rope runs its row kernel (8, 16 or 32 heads:
+    the same head-vector code), within one f16 ulp where it runs its generic
+    kernel (other head counts: another reduction order); q against the
+    oracle's reference sequence (linear.wesl, split_heads, layernorm,
+    rope_apply) within the f16 gate."""
+    x, w, b, qn, kn, rope = qkv_case(s * 1000 + t, s, t, h, k, norm, prefix)
+    got = ctx.linear_qkv_heads(x, w, b, s, t, h, qn=qn, kn=kn, rope=rope, eps=1e-5)
+    want = qkv_sequence(ctx, x, w, b, s, t, h, qn, kn, rope, 1e-5)
+    for name, a, e in zip("qkv", got, want):
+        assert tuple(a.shape) == (s, h, t, 64)
+        what = f"{name} {(s, t, h, k, norm, prefix)}"
+        if h in (8, 16, 32) or name == "v":
+            assert_bit_exact(back(a), back(e), what)
+        else:
+            assert ulp_diff_f16(back(a), back(e)).max() <= 1, what
+    qproj = O.linear(back(x), back(w[:h * 64]), back(b[:h * 64]))
+    tabs = (None, None, 0) if rope is None else (back(rope[0]), back(rope[1]), prefix)
+    qo = O.qknorm_rope(qproj, *(tuple(back(a) for a in qn) if qn else (None, None)),
+                       tabs[0], tabs[1], s, t, h, 64, tabs[2], 1e-5)
+    f16_close(back(got[0]).astype(np.float32), qo.astype(np.float32), "q vs oracle")
+
+
+def test_linear_qkv_heads_full_size_frame(ctx):
+    """The S=32 frame block's projection (43,968 tokens, 37x37 grid, prefix
+    5, 16 heads, dim 1024) bit-exact against the unfused sequence."""
+    from headshot_amd import rope as rp
+    s, t, h, k = 32, 1374, 16, 1024
+    g = torch.Generator(device="cpu").manual_seed(77)
+    x = torch.randn((s * t, k), generator=g).half().to("cuda:0")
+    w = (torch.randn((3 * h * 64, k), generator=g) / k ** 0.5).half().to("cuda:0")
+    b = (torch.randn(3 * h * 64, generator=g) * 0.02).to("cuda:0")
+    qn = (torch.ones(64, device="cuda:0") * 1.1, torch.full((64,), 0.05, device="cuda:0"))
+    kn = (torch.ones(64, device="cuda:0") * 0.9, torch.full((64,), -0.05, device="cuda:0"))
+    sin, cos = (torch.from_numpy(a).to("cuda:0") for a in rp.tables(rp.periods(), 37, 37))
+    got = ctx.linear_qkv_heads(x, w, b, s, t, h, qn=qn, kn=kn, rope=(sin, cos, 5), eps=1e-6)
+    want = qkv_sequence(ctx, x, w, b, s, t, h, qn, kn, (sin, cos, 5), 1e-6)
+    for name, a, e in zip("qkv", got, want):
+        assert torch.equal(a, e), f"full-size {name}"
+
+
+def test_linear_qkv_heads_fallback_f32(ctx):
+    """f32 (and head dims other than 64) run the unfused sequence."""
+    x, w, b, qn, kn, rope = qkv_case(3, 2, 41, 4, 64, True, 5)
+    x, w = x.float(), w.float()
+    got = ctx.linear_qkv_heads(x, w, b, 2, 41, 4, qn=qn, kn=kn, rope=rope)
+    want = qkv_sequence(ctx, x, w, b, 2, 41, 4, qn, kn, rope, 1e-5)
+    for a, e in zip(got, want):
+        assert torch.equal(a, e)
+    with pytest.raises(_lib.HsError):
+        _lib.check(ctx.lib.hs_linear_qkv_heads(
+            torch.cuda.current_stream().cuda_stream, _lib.HS_F32, x.data_ptr(), w.data_ptr(),
+            None, None, None, None, None, None, None, got[0].data_ptr(), got[1].data_ptr(),
+            got[2].data_ptr(), 2, 41, 4, 64, 64, 0, 1e-5), "linear_qkv_heads")
