@@ -230,11 +230,13 @@ def cache_times(ctx, frames: int, iters: int) -> dict:
 
 def gemm_times(ctx, frames: int, iters: int) -> dict:
     """The aggregator block's four linear layers at this S (S*1374 rows, f16),
-    each with the epilogue the block applies fused in: qkv (bias), proj (bias
-    + LayerScale + residual), fc1 (bias + exact GELU), fc2 (bias + LayerScale
-    + residual). flops = 2*m*n*k. For reference the same shapes' plain
-    product through torch (the ROCm BLAS library, no bias or epilogue) is
-    timed beside them; it is not part of this library."""
+    each with the epilogue the block applies fused in: qkv (bias, split into
+    heads, QK-norm and RoPE of a frame block), proj (bias + LayerScale +
+    residual), fc1 (bias + exact GELU), fc2 (bias + LayerScale + residual).
+    flops = 2*m*n*k. For reference the same shapes' plain product through
+    torch (the ROCm BLAS library, no bias or epilogue) is timed beside them;
+    it is not part of this library."""
+    from headshot_amd import rope as _rope
     import torch
 
     m = frames * (GRID[0] * GRID[1] + PREFIX)
@@ -260,7 +262,13 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
         b = (torch.randn(n, generator=g) * 0.02).to(ctx.device)
         o = torch.empty((m, n), dtype=torch.float16, device=ctx.device)
         if name == "qkv":
-            ctx.linear(x, w, b, out=o)
+            t = GRID[0] * GRID[1] + PREFIX
+            sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(_rope.periods(), *GRID))
+            nrm = (torch.ones(HEAD_DIM, device=ctx.device), torch.zeros(HEAD_DIM, device=ctx.device))
+            qkv = tuple(torch.empty((frames, HEADS, t, HEAD_DIM), dtype=torch.float16,
+                                    device=ctx.device) for _ in range(3))
+            ctx.linear_qkv_heads(x, w, b, frames, t, HEADS, qn=nrm, kn=nrm, rope=(sin, cos, PREFIX),
+                                 eps=EPS, out=qkv)
         elif name == "fc1":
             ctx.linear_gelu(x, w, b, out=o)
         else:
@@ -596,10 +604,12 @@ def summarize(args) -> None:
 
         # (epilogue, n) -> the layers of that launch shape; proj and fc2
         # share both, and fc2 (k = 4096) runs the longer half of the calls
-        layers = {("0", 3 * DIM): [("qkv", DIM)], ("0", DIM): [("q / k / v (whole-block leg)", DIM)],
-                  ("0", HIDDEN): [("fc1, no epilogue (comparison)", DIM)],
+        layers = {("3", 3 * DIM): [("qkv", DIM)],
+                  ("0", DIM): [("q / k / v (reference sequence, comparison)", DIM)],
+                  ("0", HIDDEN): [("fc1, no epilogue (reference sequence, comparison)", DIM)],
                   ("1", HIDDEN): [("fc1", DIM)], ("2", DIM): [("proj", DIM), ("fc2", HIDDEN)]}
-        epis = ["bias", "bias + GELU", "bias + LayerScale + residual"]
+        epis = ["bias", "bias + GELU", "bias + LayerScale + residual",
+                "bias, heads, QK-norm + RoPE"]
         out += ["", "## Linear layers (gemm_f16_kernel, f16, epilogue fused)", "",
                 "| layer | epilogue | kernel calls | mean us | TFLOP/s | of 2.5 PFLOP/s |",
                 "|---|---|---|---|---|---|"]

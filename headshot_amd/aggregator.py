@@ -272,7 +272,7 @@ def block_forward(ctx: HipContext, wts: BlockWeights, x, s: int, t: int, heads: 
     epilogues fused: LN1 -> the q|k|v linear with split_heads, QK-norm and
     RoPE in its epilogue -> attention written token-major -> proj +
     LayerScale + residual -> LN2 -> fc1 + GELU -> fc2 + LayerScale +
-    residual (9 launches). ``rope`` = (sin, cos, prefix) or None (global
+    residual (7 launches). ``rope`` = (sin, cos, prefix) or None (global
     blocks). Returns the block output (S*T, dim)."""
     p = wts.p
     normed = ctx.layernorm(x, *p.ln1, eps=eps)
