@@ -18,6 +18,7 @@
 #include <cstring>
 #include <stdexcept>
 #include <string>
+#include <tuple>
 #include <utility>
 #include <vector>
 
@@ -469,6 +470,66 @@ class HipContext {
         check(hs_qknorm_rope(stream_, hs_dtype(x_tok.dtype()), x_tok.data(), nw, nb, sn, cs,
                              out.data(), i32(s), i32(t), i32(h), i32(d), i32(prefix), eps),
               "qknorm_rope");
+        return out;
+    }
+
+    // The q|k|v projection with split_heads, QK-norm and RoPE
+    // (model/block.rs:128-146) in one launch on the fused (3*h*d, k) weight.
+    // Returns head-major q, k, v. Shapes the fused kernel does not cover
+    // (f32, d != 64, 3*h*64 not a multiple of 256) run linear then
+    // qknorm_rope per third.
+    struct Qkv {
+        HipTensor q, k, v;
+    };
+    Qkv linear_qkv_heads(const HipTensor& x, const HipTensor& w_qkv, const HipTensor* b_qkv,
+                         size_t s, size_t t, size_t h, const Norm* qn, const Norm* kn,
+                         const Rope* rope, float eps = 1e-5f) const {
+        HS_REQUIRE(w_qkv.shape().size() == 2 && w_qkv.shape()[0] % (3 * h) == 0, "w_qkv shape");
+        const size_t n3 = w_qkv.shape()[0], k = w_qkv.shape()[1], d = n3 / (3 * h), hd = h * d;
+        HS_REQUIRE(x.len() == s * t * k && x.dtype() == w_qkv.dtype(), "x shape/dtype");
+        HS_REQUIRE(!b_qkv || (b_qkv->dtype() == Dtype::F32 && b_qkv->len() == n3), "qkv bias");
+        const bool fused = x.dtype() == Dtype::F16 && d == 64 && n3 % 256 == 0 && k % 64 == 0;
+        if (!fused) {
+            Qkv out;
+            HipTensor* dst[3] = {&out.q, &out.k, &out.v};
+            const Norm* norms[3] = {qn, kn, nullptr};
+            const size_t esz = dtype_size(x.dtype());
+            for (int i = 0; i < 3; i++) {
+                // third i of the weight rows and of the bias
+                HipTensor proj = empty_typed({s * t, hd}, x.dtype());
+                check(hs_linear(stream_, hs_dtype(x.dtype()), x.data(),
+                                static_cast<const char*>(w_qkv.data()) + i * hd * k * esz,
+                                b_qkv ? b_qkv->f32() + i * hd : nullptr, proj.data(),
+                                static_cast<int64_t>(s * t), i32(hd), i32(k)),
+                      "linear");
+                *dst[i] = qknorm_rope(proj, s, t, h, d, norms[i], i < 2 ? rope : nullptr, eps);
+            }
+            return out;
+        }
+        const float *qw = nullptr, *qb = nullptr, *kw = nullptr, *kb = nullptr;
+        const float *sn = nullptr, *cs = nullptr;
+        size_t prefix = 0;
+        for (const auto& [n, w, b] : {std::tuple{qn, &qw, &qb}, std::tuple{kn, &kw, &kb}}) {
+            if (!n) continue;
+            HS_REQUIRE(n->weight->len() == d && n->bias->len() == d, "qk-norm length");
+            HS_REQUIRE(n->weight->dtype() == Dtype::F32 && n->bias->dtype() == Dtype::F32,
+                       "qk-norm parameters must be f32");
+            *w = n->weight->f32(), *b = n->bias->f32();
+        }
+        if (rope) {
+            prefix = rope->prefix;
+            HS_REQUIRE(prefix <= t, "prefix");
+            HS_REQUIRE(rope->sin->len() == (t - prefix) * d && rope->cos->len() == rope->sin->len(),
+                       "table size");
+            sn = rope->sin->f32(), cs = rope->cos->f32();
+        }
+        Qkv out{empty_typed({s, h, t, d}, x.dtype()), empty_typed({s, h, t, d}, x.dtype()),
+                empty_typed({s, h, t, d}, x.dtype())};
+        check(hs_linear_qkv_heads(stream_, hs_dtype(x.dtype()), x.data(), w_qkv.data(),
+                                  b_qkv ? b_qkv->f32() : nullptr, qw, qb, kw, kb, sn, cs,
+                                  out.q.data(), out.k.data(), out.v.data(), i32(s), i32(t), i32(h),
+                                  i32(d), i32(k), i32(prefix), eps),
+              "linear_qkv_heads");
         return out;
     }
 

@@ -383,6 +383,37 @@ void linear_matches_cpu(HipContext& ctx) {
     }
 }
 
+// The fused q|k|v projection == linear per third, then qknorm_rope
+// (bit-exact for 16 heads: the same head-vector code), and its f32
+// fallback == that sequence exactly.
+void qkv_heads_equal_sequence(HipContext& ctx) {
+    Rng rng{11};
+    const size_t s = 2, h = 16, d = 64, prefix = 5, t = 6 + prefix, k = 128, n3 = 3 * h * d;
+    auto x = rng.vec(s * t * k), w = rng.vec(n3 * k), b = rng.vec(n3), nw = rng.vec(d), nb = rng.vec(d);
+    for (auto& e : w) e *= 0.1f;
+    auto [sin, cos] = hs::rope::tables(hs::rope::periods(), 2, 3);
+    auto gw_n = ctx.tensor_from_slice({d}, nw), gb_n = ctx.tensor_from_slice({d}, nb);
+    auto st = ctx.tensor_from_slice({t - prefix, d}, sin), ct = ctx.tensor_from_slice({t - prefix, d}, cos);
+    hs::Norm norm{&gw_n, &gb_n};
+    hs::Rope rope{&st, &ct, prefix};
+    auto gb = ctx.tensor_from_slice({n3}, b);
+    for (Dtype dt : {Dtype::F16, Dtype::F32}) {
+        auto gx = ctx.tensor_from_f32({s * t, k}, x, dt), gw = ctx.tensor_from_f32({n3, k}, w, dt);
+        auto fused = ctx.linear_qkv_heads(gx, gw, &gb, s, t, h, &norm, &norm, &rope);
+        const HipTensor* outs[3] = {&fused.q, &fused.k, &fused.v};
+        for (size_t i = 0; i < 3; i++) {
+            std::vector<float> wi(w.begin() + i * h * d * k, w.begin() + (i + 1) * h * d * k);
+            std::vector<float> bi(b.begin() + i * h * d, b.begin() + (i + 1) * h * d);
+            auto gwi = ctx.tensor_from_f32({h * d, k}, wi, dt);
+            auto gbi = ctx.tensor_from_slice({h * d}, bi);
+            auto proj = ctx.linear(gx, gwi, &gbi);
+            auto seq = ctx.qknorm_rope(proj, s, t, h, d, i < 2 ? &norm : nullptr, i < 2 ? &rope : nullptr);
+            exact(ctx.download(*outs[i]), ctx.download(seq),
+                  dt == Dtype::F16 ? "linear_qkv_heads f16" : "linear_qkv_heads f32 fallback");
+        }
+    }
+}
+
 void contract_violations_throw(HipContext& ctx) {
     auto x = ctx.tensor_from_slice({4, 8}, std::vector<float>(32, 1.0f));
     auto w = ctx.tensor_from_slice({7}, std::vector<float>(7, 1.0f));
@@ -418,6 +449,7 @@ int main(int argc, char** argv) {
         {"assemble_equals_cast_and_copy_rows", assemble_equals_cast_and_copy_rows},
         {"attention_matches_cpu", attention_matches_cpu},
         {"linear_matches_cpu", linear_matches_cpu},
+        {"qkv_heads_equal_sequence", qkv_heads_equal_sequence},
         {"contract_violations_throw", contract_violations_throw},
     };
     HipContext ctx;
