@@ -24,9 +24,11 @@ calls, frame and global, fused with the head merge, timed on their own and
 priced against the f16 matrix-core peak), a ``cache_build`` section (the
 trunk's f32 head-input cache build at the same S, against HBM) and a
 ``linear`` section (the block's four linear layers with their epilogues
-fused, against the matrix-core peak) and a ``block`` section (a whole frame
+fused, against the matrix-core peak), a ``block`` section (a whole frame
 block and global block on HIP, fused, beside the reference's unfused
-dispatch sequence through the same library).
+dispatch sequence through the same library) and a ``trunk`` section (one
+whole aggregator trunk forward from DINO tokens to the head-input caches,
+the same two ways).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames S]
 """
@@ -325,6 +327,46 @@ def block_times(ctx, frames: int, iters: int) -> dict:
     out["aggregator_reference_sequence_ms"] = round(
         N_FRAME_BLOCKS * out["frame"]["reference_sequence_ms"]
         + N_GLOBAL_BLOCKS * out["global"]["reference_sequence_ms"], 1)
+    return out
+
+
+def trunk_times(ctx, frames: int, iters: int) -> dict:
+    """One whole aggregator trunk forward at this S (model/trunk.rs:49-146)
+    on HIP: token assembly from f32 DINO tokens (S x 37 x 37 patches, 17
+    prefix tokens), 24 frame blocks and 24 inter-frame blocks (5 of them
+    register-attention layers over S*17 tokens, 19 global over S*1386), the
+    register gather/scatter and the 4 head-input caches. Random-init f16
+    weights in the checkpoint's layout (fused q|k|v), generated on the
+    device. Beside it the reference's dispatch sequence through the same
+    library's single ops (Trunk.forward(fused=False))."""
+    import torch
+
+    from headshot_amd.aggregator import BlockWeights
+    from headshot_amd.trunk import DIM as TDIM
+    from headshot_amd.trunk import N_REG as TREG
+    from headshot_amd.trunk import Trunk
+
+    gen = torch.Generator(device=ctx.device).manual_seed(23)
+    blocks = lambda: [BlockWeights.random(TDIM, 4 * TDIM, HEAD_DIM, torch.float16, ctx.device,  # noqa: E731
+                                          gen, ls_init=0.05) for _ in range(N_FRAME_BLOCKS)]
+    cam = torch.randn((2, TDIM), generator=gen, device=ctx.device).half()
+    reg = torch.randn((2 * TREG, TDIM), generator=gen, device=ctx.device).half()
+    from headshot_amd import rope as _rope
+    trunk = Trunk(cam, reg, blocks(), blocks(), _rope.periods(), torch.float16)
+    p = GRID[0] * GRID[1]
+    tokens = torch.randn((frames * p, TDIM), generator=gen, device=ctx.device)
+    out = {"frames": frames, "tokens_per_frame": p + 17}
+    for name, fused in (("fused", True), ("reference_sequence", False)):
+        trunk.forward(ctx, tokens, frames, *GRID, fused=fused)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            trunk.forward(ctx, tokens, frames, *GRID, fused=fused)
+        b.record()
+        torch.cuda.synchronize()
+        out[name + "_ms"] = round(a.elapsed_time(b) / iters, 1)
+    out["frames_per_s"] = round(frames / (out["fused_ms"] * 1e-3), 1)
     return out
 
 
@@ -783,6 +825,7 @@ def main():
         line["cache_build"] = cache_times(ctx, args.frames, args.attention_iters)
         line["linear"] = gemm_times(ctx, args.frames, args.attention_iters)
         line["block"] = block_times(ctx, args.frames, max(1, args.attention_iters // 2))
+        line["trunk"] = trunk_times(ctx, args.frames, max(1, args.attention_iters // 5))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
         if args.attention_iters > 0:
