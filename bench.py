@@ -474,7 +474,19 @@ def cpu_baseline(bench: Pass, target_s: float):
                    f"{done_bytes / 1e9:.2f} GB algorithmic in {elapsed:.1f} s, "
                    f"{threads} OpenMP threads"),
         "ms_per_block": round(elapsed * 1e3 / max(blocks_done, 1), 1),
+        "cpu_model": cpu_model(),
     }
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), for the baseline record."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 KERNEL_OPS = {"ln_vec_kernel": "layernorm", "ln_generic_kernel": "layernorm",
