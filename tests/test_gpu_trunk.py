@@ -183,3 +183,45 @@ def test_trunk_f32_vs_float32(ctx, ckpt, dino):
     ref = torch_trunk(st, dino, precision_round=False)
     gate_all(ours, ref, Gate.F32_TIGHT, "f32 trunk vs float32 (reference f32 gate)")
     gate_all(ours, ref, Gate(5e-6, 1.0 - 1e-10), "f32 trunk vs float32")
+
+
+def test_trunk_full_depth_fused_vs_reference_sequence(ctx):
+    """All 24 block pairs (register-attention layers 2, 6, 9, 14, 20; cached
+    layers 4, 11, 17, 23), 3 frames of a 3 x 5 grid, random-init f16
+    weights generated on the device: every tap of the fused trunk against
+    the reference's dispatch sequence, within the reference's f16 trunk gate
+    and tighter, and the four caches exact f32 joins of their layers."""
+    from headshot_amd import rope as rp
+    from headshot_amd.aggregator import BlockWeights
+
+    gen = torch.Generator(device="cuda:0").manual_seed(29)
+    blocks = lambda: [BlockWeights.random(1024, 4096, 64, torch.float16, "cuda:0", gen,  # noqa: E731
+                                          ls_init=0.05) for _ in range(24)]
+    cam = torch.randn((2, 1024), generator=gen, device="cuda:0").half()
+    reg = torch.randn((32, 1024), generator=gen, device="cuda:0").half()
+    tr = Trunk(cam, reg, blocks(), blocks(), rp.periods(), torch.float16)
+    n, grid = 3, (3, 5)
+    tokens = torch.randn((n * grid[0] * grid[1], 1024), generator=gen, device="cuda:0")
+    taps = {}
+    for fused in (True, False):
+        got = {}
+
+        def tap(name, t):
+            torch.cuda.synchronize()
+            got[name] = t.float().cpu().numpy().copy()
+
+        caches = tr.forward(ctx, tokens, n, *grid, tap=tap, fused=fused)
+        assert len(caches) == 4
+        taps[fused] = got
+    assert len(taps[True]) == 24 + 24 + 4
+    gate_all(taps[True], taps[False], Gate.F16_TRUNK, "full-depth fused vs sequence (reference gate)")
+    # measured over the 52 taps: rel_max <= 2.3e-3, 1 - cosine <= 4.2e-7
+    gate_all(taps[True], taps[False], Gate(5e-3, 1.0 - 2e-6), "full-depth fused vs sequence")
+    t = grid[0] * grid[1] + PREFIX
+    for k in CACHED_LAYERS:
+        c = taps[True][f"cache.{k:02}"]
+        assert c.shape == (n * t, 2048)
+        np.testing.assert_array_equal(c[:, :1024], taps[True][f"trunk.frame.{k:02}"])
+        np.testing.assert_array_equal(c[:, 1024:], taps[True][f"trunk.inter.{k:02}"])
+    for k in REGISTER_ATTENTION_LAYERS:
+        assert taps[True][f"trunk.inter.{k:02}"].shape == (n * PREFIX, 1024)
