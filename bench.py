@@ -58,7 +58,7 @@ def op_bytes(rows: int, esz: int, n_patch_rows: int, n_pos_rows: int) -> dict:
     """Algorithmic (minimal) HBM bytes per launch of each fused op."""
     return {
         "layernorm": rows * DIM * esz * 2,                   # read x, write out
-        "qknorm_rope": rows * DIM * esz * 2,                 # one of q / k
+        "qknorm_rope": rows * DIM * esz * 2 * 2,             # q and k, one launch
         "bias_ls_residual": rows * DIM * esz * 3,            # read res, x; write out
         "bias_gelu": rows * HIDDEN * esz * 2,                # read h, write act
         "assemble": (n_patch_rows * DIM * 4                  # read f32 patches
@@ -447,7 +447,7 @@ def cpu_baseline(bench: Pass, target_s: float):
     t0 = time.perf_counter()
     O.assemble_tokens(patches, pb, pos, cam, reg, frames, bench.p, N_REG, x.dtype)
     done_bytes += bench.bytes["assemble"]
-    block_bytes = (2 * bench.bytes["layernorm"] + 2 * bench.bytes["qknorm_rope"]
+    block_bytes = (2 * bench.bytes["layernorm"] + bench.bytes["qknorm_rope"]
                    + 2 * bench.bytes["bias_ls_residual"] + bench.bytes["bias_gelu"])
     for kind, b in zip(fp.kinds, fp.blocks):
         p = {kk: tuple(h(t) for t in v) if isinstance(v, tuple) else h(v)
@@ -583,7 +583,7 @@ def summarize(args) -> None:
     p = GRID[0] * GRID[1]
     rows = args.frames * (p + PREFIX)
     nbytes = op_bytes(rows, esz, args.frames * p, p)
-    launches = {"assemble": 1, "layernorm": 96, "qknorm_rope": 96, "bias_ls_residual": 96,
+    launches = {"assemble": 1, "layernorm": 96, "qknorm_rope": 48, "bias_ls_residual": 96,
                 "bias_gelu": 48}
     dur = defaultdict(list)
     for r in csv.DictReader(open(args.summarize)):

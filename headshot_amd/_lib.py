@@ -39,6 +39,8 @@ SIGNATURES = {
     "hs_copy_rows": (_S, [_P, _P, _I64, _P, _I64, _I64, _I64]),
     "hs_tiled_add": (_S, [_P, _P, _P, _P, _I64, _I64]),
     "hs_qknorm_rope": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F]),
+    "hs_qknorm_rope_pair": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                 _I32, _I32, _I32, _I32, _I32, _F]),
     "hs_bias_gelu": (_S, [_P, _I32, _P, _P, _P, _I64, _I32]),
     "hs_bias_ls_residual": (_S, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32]),
     "hs_assemble_tokens": (_S, [_P, _I32, _P, _I32, _P, _P, _P, _P, _P,

@@ -280,6 +280,35 @@ class HipContext:
                      sn, cs, _dev(out, "out"), s, t, h, d, prefix, eps)
         return out
 
+    def qknorm_rope_pair(self, q_tok, k_tok, s: int, t: int, h: int, d: int, qn=None, kn=None,
+                         rope=None, eps: float = 1e-5, out_q=None, out_k=None):
+        """``qknorm_rope`` on q (norm ``qn``) and on k (norm ``kn``) in one
+        launch, bit-identical to two calls (model/block.rs:130-146). Both
+        norms are given or neither. Returns (q_head, k_head)."""
+        assert q_tok.numel() == s * t * h * d and k_tok.numel() == q_tok.numel(), "qk size"
+        assert q_tok.dtype == k_tok.dtype, "q/k dtype"
+        assert (qn is None) == (kn is None), "QK-norm for both q and k or for neither"
+        qw = qb = kw = kb = sn = cs = None
+        prefix = 0
+        if qn is not None:
+            qw, qb = _param(qn[0], d, "q-norm weight"), _param(qn[1], d, "q-norm bias")
+            kw, kb = _param(kn[0], d, "k-norm weight"), _param(kn[1], d, "k-norm bias")
+        if rope is not None:
+            sin, cos, prefix = rope
+            assert 0 <= prefix <= t, "prefix"
+            sn = _param(sin, (t - prefix) * d, "rope sin table")
+            cs = _param(cos, (t - prefix) * d, "rope cos table")
+        outs = []
+        for o in (out_q, out_k):
+            if o is None:
+                o = self.empty_typed((s, h, t, d), q_tok.dtype)
+            assert o.dtype == q_tok.dtype and o.numel() == q_tok.numel(), "out shape/dtype"
+            outs.append(o)
+        self._launch("qknorm_rope_pair", self.lib.hs_qknorm_rope_pair, _dt(q_tok),
+                     _dev(q_tok, "q"), _dev(k_tok, "k"), qw, qb, kw, kb, sn, cs,
+                     _dev(outs[0], "out_q"), _dev(outs[1], "out_k"), s, t, h, d, prefix, eps)
+        return outs[0], outs[1]
+
     def linear_qkv_heads(self, x, w_qkv, b_qkv, s: int, t: int, h: int, qn=None, kn=None,
                          rope=None, eps: float = 1e-5, out=None):
         """The attention input projection (model/block.rs:128-146) in one

@@ -99,7 +99,7 @@ __global__ __launch_bounds__(kBlock) void assemble_kernel(
     int seq, int np, int nr, int n_var) {
     constexpr int D = 256 * CHUNKS;
     const int lane = lane_id();
-    const int w = threadIdx.x >> 6;
+    const int w = wave_in_block();
     const AssembleGrid grid = AssembleGrid::make(nframes, np, nr);
     const int64_t b = blockIdx.x;
     if (b < grid.patch_blocks) {
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(kBlock) void assemble_generic_kernel(
     const TP* patches, const float* pbias, const float* pos, const TO* cam, const TO* reg, TO* out,
     int64_t out_rows, int seq, int np, int nr, int d, int n_var) {
     const int lane = lane_id();
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
     const bool has_b = pbias != nullptr, has_p = pos != nullptr;
     for (int64_t row = wave; row < out_rows; row += nwaves) {

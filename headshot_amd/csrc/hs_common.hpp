@@ -273,4 +273,12 @@ __device__ __forceinline__ void qk_norm_rope_vec(float (&f)[V], const float (&wr
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
+// Index of the calling wave within its workgroup, as a wave-uniform (scalar)
+// value: the compiler cannot prove threadIdx.x >> 6 uniform by itself, and
+// without this it keeps every index derived from it, and the integer
+// divisions on it, in vector registers and vector instructions.
+__device__ __forceinline__ int wave_in_block() {
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+}
+
 }  // namespace hs

@@ -18,13 +18,15 @@ namespace {
 // Launch shape (overridable at build time for tuning sweeps).
 // U: 16-byte vectors per input stream per thread per iteration; BPC:
 // workgroups launched per CU. Chosen by timing the whole aggregator pass,
-// not the op alone: with U = 1 GELU itself runs ~8% faster but the kernels
-// after it (LayerNorm most) lose more than that.
+// not the op alone. GELU runs fastest with one vector per thread and 32
+// workgroups per CU; it must keep non-temporal stores, because with plain
+// stores its output occupies the cache and the LayerNorm after it slows by
+// a third.
 #ifndef HS_GELU_U
-#define HS_GELU_U 2
+#define HS_GELU_U 1
 #endif
 #ifndef HS_GELU_BPC
-#define HS_GELU_BPC 16
+#define HS_GELU_BPC 32
 #endif
 #ifndef HS_GELU_NTL
 #define HS_GELU_NTL (HS_NT != 0)  // non-temporal loads of the fc1 output

@@ -5,16 +5,22 @@
 // lane loads CHUNKS 16-byte vectors (a 1024-wide f16 row is 2 loads per
 // lane, each load instruction a contiguous 1 KiB), mean and variance are
 // reduced across the wave with DPP lane permutes (no LDS, no barrier), and
-// the row is written back with 16-byte stores. Waves are persistent: each
-// keeps the weight and bias slices it needs in registers and walks rows in
-// groups of U, issuing all U*CHUNKS loads before it reduces, so every wave
-// has U*2 KiB of HBM reads in flight.
+// the row is written back with 16-byte stores. Each wave keeps the weight
+// and bias slices it needs in registers and takes U rows, issuing all
+// U*CHUNKS loads before it reduces, so every wave has U*2 KiB of HBM reads
+// in flight. The grid has one wave per U rows (a grid-stride loop covers
+// row counts beyond 2^22 workgroups): measured against persistent grids of
+// 2-8 workgroups per CU, which walk several row groups per wave, it is the
+// fastest at 44k rows, alone (69.5% of peak against 65.5%) and inside the
+// aggregator pass (72.1% against 69.7%).
 //
 // Generic path: any dim, one wave per row, strided over the row three
 // times (mean, variance, output) with the second and third reads served by
 // the cache.
-// LayerNorm rows measure faster with cached (temporal) accesses: the second
-// row of a wave's pair shares DRAM pages with the first.
+// LayerNorm keeps cached (temporal) accesses. Alone, non-temporal ones are
+// faster (72.7% of peak against 69.5%), but inside the aggregator pass they
+// slowed LayerNorm (66.8% against 72.1%) and the LayerScale + residual op
+// after it, which reads the same residual rows again (67.7% against 78.5%).
 #ifndef HS_NT
 #define HS_NT 0
 #endif
@@ -28,12 +34,12 @@ namespace {
 #define HS_LN_U 2  // rows per wave per iteration
 #endif
 #ifndef HS_LN_BPC
-#define HS_LN_BPC 4  // resident workgroups per CU
+#define HS_LN_BPC 0  // workgroups per CU of a persistent grid; 0: one wave per U rows
 #endif
 
 constexpr int kBlock = 256;  // 4 waves per workgroup
 constexpr int kWavesPerBlock = kBlock / 64;
-constexpr int kBlocksPerCu = HS_LN_BPC;
+constexpr int kBlocksPerCu = 4;  // generic path
 
 template <typename T, int CHUNKS, int U>
 __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float* __restrict__ w,
@@ -42,7 +48,7 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
     constexpr int V = Vec<T>::N;
     constexpr int DIM = 64 * V * CHUNKS;
     const int lane = lane_id();
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
 
     float wr[CHUNKS][V], br[CHUNKS][V];
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(kBlock) void ln_generic_kernel(const T* x, const fl
                                                             const float* __restrict__ b, T* out,
                                                             int64_t rows, int dim, float eps) {
     const int lane = lane_id();
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
     for (int64_t row = wave; row < rows; row += nwaves) {
         const T* xr = x + row * dim;
@@ -136,7 +142,10 @@ template <typename T, int CHUNKS>
 hs_status launch_vec(hipStream_t st, const void* x, const float* w, const float* b, void* out,
                      int64_t rows, float eps) {
     constexpr int U = HS_LN_U;
-    const int64_t blocks = persistent_blocks(ceil_div(rows, U));
+    const int64_t want = ceil_div(ceil_div(rows, U), kWavesPerBlock);
+    const int64_t cap = HS_LN_BPC > 0 ? static_cast<int64_t>(num_cus()) * HS_LN_BPC
+                                      : int64_t{1} << 22;
+    const int64_t blocks = want < cap ? want : cap;
     ln_vec_kernel<T, CHUNKS, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
         static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, eps);
     return check_launch("layernorm");

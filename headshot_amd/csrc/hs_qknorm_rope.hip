@@ -60,7 +60,6 @@ struct QknRow {
     static constexpr int CH = H / HPI;
     static_assert(H % HPI == 0, "whole load instructions per row");
     static constexpr int HB = CH;  // loads per unit (buffer size)
-    __host__ __device__ static int64_t units(int64_t tokens) { return tokens; }
 
     const T* __restrict__ x;
     const float* __restrict__ sin_tab;
@@ -82,9 +81,12 @@ struct QknRow {
         // tokens < 2^31 (checked on the host): wave-uniform 32-bit divide
         const uint32_t s = static_cast<uint32_t>(tok) / static_cast<uint32_t>(seq);
         const int t = static_cast<int>(static_cast<uint32_t>(tok) - s * static_cast<uint32_t>(seq));
-        const bool rot = ROPE && t >= prefix;
+        T* obase = out + (static_cast<int64_t>(s) * H + gsub) * seq * D +
+                   static_cast<int64_t>(t) * D + ch;
         float cs[V], sn[V];
-        if (rot) {
+        // Two copies of the row code, chosen by a wave-uniform branch, so
+        // the rotated and the unrotated results never meet in one register.
+        if (ROPE && t >= prefix) {
             const int64_t row = static_cast<int64_t>(t - prefix) * D + ch;
             const float sg = upper ? 1.0f : -1.0f;
 #pragma unroll
@@ -94,17 +96,37 @@ struct QknRow {
                 sn[k] = sg * s4.x, sn[k + 1] = sg * s4.y, sn[k + 2] = sg * s4.z,
                 sn[k + 3] = sg * s4.w;
             }
+            emit<true>(raw, obase, cs, sn);
+        } else {
+#pragma unroll
+            for (int k = 0; k < V; k++) cs[k] = sn[k] = 0.0f;
+            emit<false>(raw, obase, cs, sn);
         }
-        T* obase = out + (static_cast<int64_t>(s) * H + gsub) * seq * D +
-                   static_cast<int64_t>(t) * D + ch;
+    }
+
+    template <bool ROT>
+    __device__ __forceinline__ void emit(const u32x4 (&raw)[HB], T* obase, const float (&cs)[V],
+                                         const float (&sn)[V]) const {
 #pragma unroll
         for (int c = 0; c < CH; c++) {
             float f[V];
             unpack(raw[c], f, T{});
-            qk_norm_rope_vec<T, G, NORM>(f, wr, br, eps, rot, cs, sn);
+            qk_norm_rope_vec<T, G, NORM>(f, wr, br, eps, ROT, cs, sn);
             st_stream(obase + static_cast<int64_t>(c) * HPI * seq * D, pack(f, T{}));
         }
     }
+};
+
+// One or two tensors of the same shape that share the RoPE tables and one
+// launch (q and k of a block): waves [0, W) take the first, [W, 2W) the
+// second, W = ceil(tokens / K).
+template <typename T>
+struct QknTensors {
+    const T* x[2];
+    const float* nw[2];
+    const float* nb[2];
+    T* out[2];
+    int n;
 };
 
 // Each wave runs K consecutive units with a two-buffer software pipeline:
@@ -113,15 +135,22 @@ struct QknRow {
 // between them in lockstep.
 template <typename T, int H, bool NORM, bool ROPE, int K>
 __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
-    const T* __restrict__ x, const float* __restrict__ nw, const float* __restrict__ nb,
-    const float* __restrict__ sin_tab, const float* __restrict__ cos_tab, T* __restrict__ out,
+    QknTensors<T> ts, const float* __restrict__ sin_tab, const float* __restrict__ cos_tab,
     int64_t tokens, int seq, int prefix, float eps) {
     using Row = QknRow<T, H, NORM, ROPE>;
     constexpr int G = Row::G, V = Row::V, HB = Row::HB;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
+    const int64_t per_tensor = ceil_div(tokens, int64_t{K});
+    const int which = wave >= per_tensor ? 1 : 0;
+    if (which >= ts.n) return;  // wave-uniform: the kernel has no barriers
+    const int64_t u0 = (wave - which * per_tensor) * K;
+    if (u0 >= tokens) return;  // the grid's last workgroup may run past the second tensor
+    const int64_t u_end = u0 + K < tokens ? u0 + K : tokens;
     const int lane = lane_id();
     const int piece = lane % G;
     Row tl;
-    tl.x = x, tl.sin_tab = sin_tab, tl.cos_tab = cos_tab, tl.out = out;
+    tl.x = ts.x[which], tl.out = ts.out[which];
+    tl.sin_tab = sin_tab, tl.cos_tab = cos_tab;
     tl.tokens = tokens, tl.seq = seq, tl.prefix = prefix, tl.eps = eps;
     tl.gsub = lane / G;
     // Channels held by this lane: lower-half pieces hold [piece*V, +V), the
@@ -129,6 +158,8 @@ __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
     tl.upper = piece >= G / 2;
     tl.ch = tl.upper ? 32 + (G - 1 - piece) * V : piece * V;
     if constexpr (NORM) {
+        const float* nw = ts.nw[which];
+        const float* nb = ts.nb[which];
 #pragma unroll
         for (int k = 0; k < V; k += 4) {
             float4 w4 = ld_f32x4(nw + tl.ch + k), b4 = ld_f32x4(nb + tl.ch + k);
@@ -136,10 +167,6 @@ __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
             tl.br[k] = b4.x, tl.br[k + 1] = b4.y, tl.br[k + 2] = b4.z, tl.br[k + 3] = b4.w;
         }
     }
-    const int64_t units = Row::units(tokens);
-    const int64_t u0 = (static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6)) * K;
-    if (u0 >= units) return;  // wave-uniform: the kernel has no barriers
-    const int64_t u_end = u0 + K < units ? u0 + K : units;
 
     u32x4 a[HB], b[HB];
     tl.load(a, u0);
@@ -162,7 +189,7 @@ __global__ __launch_bounds__(kBlock) void qkn_generic_kernel(
     const float* __restrict__ sin_tab, const float* __restrict__ cos_tab, T* out, int nseq,
     int seq, int heads, int d, int prefix, float eps) {
     const int lane = lane_id();
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + (threadIdx.x >> 6);
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
     const int64_t nvec = static_cast<int64_t>(nseq) * seq * heads;
     const bool norm = nw != nullptr;
@@ -218,32 +245,24 @@ __global__ __launch_bounds__(kBlock) void qkn_generic_kernel(
 }
 
 template <typename T, int H, bool NORM, bool ROPE>
-hs_status launch_rows(hipStream_t st, const void* x, const float* nw, const float* nb,
-                      const float* sn, const float* cs, void* out, int64_t tokens, int seq,
-                      int prefix, float eps) {
-    using Row = QknRow<T, H, NORM, ROPE>;
+hs_status launch_rows(hipStream_t st, const QknTensors<T>& ts, const float* sn, const float* cs,
+                      int64_t tokens, int seq, int prefix, float eps) {
     constexpr int K = HS_QK_K;
-    const int64_t units = Row::units(tokens);
-    const int64_t blocks = ceil_div(ceil_div(units, K), kWavesPerBlock);
+    const int64_t blocks = ceil_div(ceil_div(tokens, int64_t{K}) * ts.n, int64_t{kWavesPerBlock});
     qkn_row_kernel<T, H, NORM, ROPE, K>
-        <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
-            static_cast<const T*>(x), nw, nb, sn, cs, static_cast<T*>(out), tokens, seq, prefix,
-            eps);
+        <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(ts, sn, cs, tokens, seq,
+                                                                      prefix, eps);
     return check_launch("qknorm_rope");
 }
 
 template <typename T, int H>
-hs_status launch_rows_flags(hipStream_t st, const void* x, const float* nw, const float* nb,
-                            const float* sn, const float* cs, void* out, int64_t tokens, int seq,
-                            int prefix, float eps) {
-    const bool norm = nw != nullptr, rope = sn != nullptr && prefix < seq;
-    if (norm && rope)
-        return launch_rows<T, H, true, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
-    if (norm)
-        return launch_rows<T, H, true, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
-    if (rope)
-        return launch_rows<T, H, false, true>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
-    return launch_rows<T, H, false, false>(st, x, nw, nb, sn, cs, out, tokens, seq, prefix, eps);
+hs_status launch_rows_flags(hipStream_t st, const QknTensors<T>& ts, const float* sn,
+                            const float* cs, int64_t tokens, int seq, int prefix, float eps) {
+    const bool norm = ts.nw[0] != nullptr, rope = sn != nullptr && prefix < seq;
+    if (norm && rope) return launch_rows<T, H, true, true>(st, ts, sn, cs, tokens, seq, prefix, eps);
+    if (norm) return launch_rows<T, H, true, false>(st, ts, sn, cs, tokens, seq, prefix, eps);
+    if (rope) return launch_rows<T, H, false, true>(st, ts, sn, cs, tokens, seq, prefix, eps);
+    return launch_rows<T, H, false, false>(st, ts, sn, cs, tokens, seq, prefix, eps);
 }
 
 template <typename T>
@@ -258,29 +277,46 @@ hs_status launch_generic(hipStream_t st, const void* x, bool in_head_major, cons
     return check_launch("qknorm_rope");
 }
 
-// Token-major input: the row path when head_dim is 64, H is one of the
-// instantiated head counts and every pointer is 16-byte aligned.
+// Token-major input, one or two tensors: the row path when head_dim is 64,
+// H is one of the instantiated head counts and every pointer is 16-byte
+// aligned; otherwise the generic kernel, one launch per tensor.
+template <typename T>
+hs_status dispatch_tok(hipStream_t st, const QknTensors<T>& ts, const float* sn, const float* cs,
+                       int s, int t, int h, int d, int prefix, float eps) {
+    bool ptrs_ok = !sn || (aligned16(sn) && aligned16(cs));
+    for (int i = 0; i < ts.n; i++)
+        ptrs_ok = ptrs_ok && aligned16(ts.x[i]) && aligned16(ts.out[i]) &&
+                  (!ts.nw[i] || (aligned16(ts.nw[i]) && aligned16(ts.nb[i])));
+    const int64_t tokens = static_cast<int64_t>(s) * t;
+    // The dispatch packet counts work-items in 32 bits: the row grid has one
+    // wave per K tokens per tensor; beyond that the persistent generic
+    // kernel runs.
+    const int64_t row_blocks =
+        ceil_div(ceil_div(tokens, int64_t{HS_QK_K}) * ts.n, int64_t{kWavesPerBlock});
+    const bool grid_ok = row_blocks * kBlock < (int64_t{1} << 32);
+    if (d == 64 && ptrs_ok && grid_ok) {
+        switch (h) {
+            case 8: return launch_rows_flags<T, 8>(st, ts, sn, cs, tokens, t, prefix, eps);
+            case 16: return launch_rows_flags<T, 16>(st, ts, sn, cs, tokens, t, prefix, eps);
+            case 32: return launch_rows_flags<T, 32>(st, ts, sn, cs, tokens, t, prefix, eps);
+            default: break;
+        }
+    }
+    for (int i = 0; i < ts.n; i++)
+        if (hs_status e = launch_generic<T>(st, ts.x[i], false, ts.nw[i], ts.nb[i], sn, cs,
+                                            ts.out[i], s, t, h, d, prefix, eps))
+            return e;
+    return HS_OK;
+}
+
 template <typename T>
 hs_status dispatch_tok(hipStream_t st, const void* x, const float* nw, const float* nb,
                        const float* sn, const float* cs, void* out, int s, int t, int h, int d,
                        int prefix, float eps) {
-    const bool ptrs_ok = aligned16(x) && aligned16(out) &&
-                         (!nw || (aligned16(nw) && aligned16(nb))) &&
-                         (!sn || (aligned16(sn) && aligned16(cs)));
-    const int64_t tokens = static_cast<int64_t>(s) * t;
-    // The dispatch packet counts work-items in 32 bits: the row grid has one
-    // wave per K tokens; beyond that the persistent generic kernel runs.
-    const int64_t row_blocks = ceil_div(ceil_div(tokens, int64_t{HS_QK_K}), int64_t{kWavesPerBlock});
-    const bool grid_ok = row_blocks * kBlock < (int64_t{1} << 32);
-    if (d == 64 && ptrs_ok && grid_ok) {
-        switch (h) {
-            case 8: return launch_rows_flags<T, 8>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
-            case 16: return launch_rows_flags<T, 16>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
-            case 32: return launch_rows_flags<T, 32>(st, x, nw, nb, sn, cs, out, tokens, t, prefix, eps);
-            default: break;
-        }
-    }
-    return launch_generic<T>(st, x, false, nw, nb, sn, cs, out, s, t, h, d, prefix, eps);
+    QknTensors<T> ts{};
+    ts.x[0] = static_cast<const T*>(x), ts.nw[0] = nw, ts.nb[0] = nb;
+    ts.out[0] = static_cast<T*>(out), ts.n = 1;
+    return dispatch_tok<T>(st, ts, sn, cs, s, t, h, d, prefix, eps);
 }
 
 hs_status check_shape(const char* op, int32_t s, int32_t t, int32_t h, int32_t d) {
@@ -322,6 +358,49 @@ hs_status hs_qknorm_rope(hs_stream_t stream, hs_dtype dt, const void* x_tok, con
     return dt == HS_F16
                ? dispatch_tok<f16>(st, x_tok, nw, nb, sin_tab, cos_tab, out_head, s, t, h, d, prefix, eps)
                : dispatch_tok<float>(st, x_tok, nw, nb, sin_tab, cos_tab, out_head, s, t, h, d, prefix, eps);
+}
+
+hs_status hs_qknorm_rope_pair(hs_stream_t stream, hs_dtype dt, const void* q_tok,
+                              const void* k_tok, const float* qn_w, const float* qn_b,
+                              const float* kn_w, const float* kn_b, const float* sin_tab,
+                              const float* cos_tab, void* q_head, void* k_head, int32_t s,
+                              int32_t t, int32_t h, int32_t d, int32_t prefix, float eps) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "qknorm_rope_pair: unknown dtype %d", (int)dt);
+    if (hs_status e = check_shape("qknorm_rope_pair", s, t, h, d)) return e;
+    if ((qn_w == nullptr) != (qn_b == nullptr) || (kn_w == nullptr) != (kn_b == nullptr))
+        return fail(HS_EINVAL,
+                    "qknorm_rope_pair: each norm's weight and bias must both be given or both NULL");
+    if ((qn_w == nullptr) != (kn_w == nullptr))
+        return fail(HS_EINVAL, "qknorm_rope_pair: QK-norm must be given for both q and k or for neither");
+    if ((sin_tab == nullptr) != (cos_tab == nullptr))
+        return fail(HS_EINVAL, "qknorm_rope_pair: sin and cos tables must both be given or both NULL");
+    if (sin_tab && (prefix < 0 || prefix > t))
+        return fail(HS_EINVAL, "qknorm_rope_pair: prefix %d outside [0, T=%d]", prefix, t);
+    if (sin_tab && d % 2 != 0)
+        return fail(HS_EINVAL, "qknorm_rope_pair: RoPE needs an even head_dim");
+    const int64_t n = static_cast<int64_t>(s) * t * h * d;
+    if (n == 0) return HS_OK;
+    if (!q_tok || !k_tok || !q_head || !k_head)
+        return fail(HS_EINVAL, "qknorm_rope_pair: null buffer");
+    const int64_t bytes = n * dtype_size(dt);
+    const void* outs[2] = {q_head, k_head};
+    for (const void* o : outs)
+        if (overlaps(q_tok, bytes, o, bytes) || overlaps(k_tok, bytes, o, bytes))
+            return fail(HS_EINVAL, "qknorm_rope_pair: an output overlaps an input");
+    if (overlaps(q_head, bytes, k_head, bytes))
+        return fail(HS_EINVAL, "qknorm_rope_pair: q_head overlaps k_head");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    auto run = [&](auto tag) {
+        using T = decltype(tag);
+        QknTensors<T> ts{};
+        ts.x[0] = static_cast<const T*>(q_tok), ts.x[1] = static_cast<const T*>(k_tok);
+        ts.nw[0] = qn_w, ts.nb[0] = qn_b, ts.nw[1] = kn_w, ts.nb[1] = kn_b;
+        ts.out[0] = static_cast<T*>(q_head), ts.out[1] = static_cast<T*>(k_head);
+        ts.n = 2;
+        return dispatch_tok<T>(st, ts, sin_tab, cos_tab, s, t, h, d, prefix, eps);
+    };
+    return dt == HS_F16 ? run(f16{}) : run(float{});
 }
 
 hs_status hs_split_heads(hs_stream_t stream, hs_dtype dt, const void* x, void* out, int32_t s,

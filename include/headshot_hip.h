@@ -127,6 +127,18 @@ hs_status hs_qknorm_rope(hs_stream_t stream, hs_dtype dt, const void* x_tok, con
                          void* out_head, int32_t s, int32_t t, int32_t h, int32_t d,
                          int32_t prefix, float eps);
 
+/* hs_qknorm_rope on q and on k in one launch (the six dispatches of
+ * model/block.rs:130-146): q_tok -> q_head with norm qn_w/qn_b, k_tok ->
+ * k_head with kn_w/kn_b, both with the same shape, RoPE tables and prefix.
+ * Either both norms are given or neither. Results are bit-identical to two
+ * hs_qknorm_rope calls. No output may overlap an input or the other
+ * output. */
+hs_status hs_qknorm_rope_pair(hs_stream_t stream, hs_dtype dt, const void* q_tok,
+                              const void* k_tok, const float* qn_w, const float* qn_b,
+                              const float* kn_w, const float* kn_b, const float* sin_tab,
+                              const float* cos_tab, void* q_head, void* k_head, int32_t s,
+                              int32_t t, int32_t h, int32_t d, int32_t prefix, float eps);
+
 /* fc1 bias epilogue + GELU (shaders/linear_wmma.wgsl:69-74 then
  * engine/ops.rs:155-165): out[r, c] = gelu(x[r, c] + bias[c]) over
  * (rows, cols); bias NULL is plain GELU. The sum stays in f32 and the

@@ -16,6 +16,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <initializer_list>
 #include <stdexcept>
 #include <string>
 #include <tuple>
@@ -470,6 +471,45 @@ class HipContext {
         check(hs_qknorm_rope(stream_, hs_dtype(x_tok.dtype()), x_tok.data(), nw, nb, sn, cs,
                              out.data(), i32(s), i32(t), i32(h), i32(d), i32(prefix), eps),
               "qknorm_rope");
+        return out;
+    }
+
+    // qknorm_rope on q (norm qn) and k (norm kn) in one launch; both norms
+    // or neither. Bit-identical to two qknorm_rope calls.
+    struct QkHeads {
+        HipTensor q, k;
+    };
+    QkHeads qknorm_rope_pair(const HipTensor& q_tok, const HipTensor& k_tok, size_t s, size_t t,
+                             size_t h, size_t d, const Norm* qn, const Norm* kn, const Rope* rope,
+                             float eps = 1e-5f) const {
+        HS_REQUIRE(q_tok.len() == s * t * h * d && k_tok.len() == q_tok.len(), "qk size");
+        HS_REQUIRE(q_tok.dtype() == k_tok.dtype(), "q/k dtype");
+        HS_REQUIRE((qn == nullptr) == (kn == nullptr), "QK-norm for both q and k or neither");
+        const float *qw = nullptr, *qb = nullptr, *kw = nullptr, *kb = nullptr;
+        const float *sn = nullptr, *cs = nullptr;
+        size_t prefix = 0;
+        for (const Norm* n : {qn, kn}) {
+            if (!n) continue;
+            HS_REQUIRE(n->weight->len() == d && n->bias->len() == d, "qk-norm length");
+            HS_REQUIRE(n->weight->dtype() == Dtype::F32 && n->bias->dtype() == Dtype::F32,
+                       "qk-norm parameters must be f32");
+        }
+        if (qn) qw = qn->weight->f32(), qb = qn->bias->f32(), kw = kn->weight->f32(),
+                kb = kn->bias->f32();
+        if (rope) {
+            prefix = rope->prefix;
+            HS_REQUIRE(prefix <= t, "prefix");
+            HS_REQUIRE(rope->sin->len() == (t - prefix) * d && rope->cos->len() == rope->sin->len(),
+                       "table size");
+            HS_REQUIRE(rope->sin->dtype() == Dtype::F32 && rope->cos->dtype() == Dtype::F32,
+                       "rope tables must be f32");
+            sn = rope->sin->f32(), cs = rope->cos->f32();
+        }
+        QkHeads out{empty_typed({s, h, t, d}, q_tok.dtype()), empty_typed({s, h, t, d}, q_tok.dtype())};
+        check(hs_qknorm_rope_pair(stream_, hs_dtype(q_tok.dtype()), q_tok.data(), k_tok.data(), qw,
+                                  qb, kw, kb, sn, cs, out.q.data(), out.k.data(), i32(s), i32(t),
+                                  i32(h), i32(d), i32(prefix), eps),
+              "qknorm_rope_pair");
         return out;
     }
 

@@ -414,6 +414,26 @@ void qkv_heads_equal_sequence(HipContext& ctx) {
     }
 }
 
+// q and k in one launch == two qknorm_rope calls, with and without RoPE.
+void qknorm_rope_pair_equals_two_calls(HipContext& ctx) {
+    Rng rng{13};
+    const size_t s = 3, h = 16, d = 64, prefix = 5, t = 6 + prefix;
+    auto [sin, cos] = hs::rope::tables(hs::rope::periods(), 2, 3);
+    auto st = ctx.tensor_from_slice({t - prefix, d}, sin), ct = ctx.tensor_from_slice({t - prefix, d}, cos);
+    auto qw = ctx.tensor_from_slice({d}, rng.vec(d)), qb = ctx.tensor_from_slice({d}, rng.vec(d));
+    auto kw = ctx.tensor_from_slice({d}, rng.vec(d)), kb = ctx.tensor_from_slice({d}, rng.vec(d));
+    hs::Norm qn{&qw, &qb}, kn{&kw, &kb};
+    hs::Rope rope{&st, &ct, prefix};
+    for (Dtype dt : {Dtype::F16, Dtype::F32})
+        for (const hs::Rope* rp : {static_cast<const hs::Rope*>(&rope), static_cast<const hs::Rope*>(nullptr)}) {
+            auto q = ctx.tensor_from_f32({s * t, h * d}, rng.vec(s * t * h * d), dt);
+            auto k = ctx.tensor_from_f32({s * t, h * d}, rng.vec(s * t * h * d), dt);
+            auto pair = ctx.qknorm_rope_pair(q, k, s, t, h, d, &qn, &kn, rp);
+            exact(ctx.download(pair.q), ctx.download(ctx.qknorm_rope(q, s, t, h, d, &qn, rp)), "pair q");
+            exact(ctx.download(pair.k), ctx.download(ctx.qknorm_rope(k, s, t, h, d, &kn, rp)), "pair k");
+        }
+}
+
 void contract_violations_throw(HipContext& ctx) {
     auto x = ctx.tensor_from_slice({4, 8}, std::vector<float>(32, 1.0f));
     auto w = ctx.tensor_from_slice({7}, std::vector<float>(7, 1.0f));
@@ -450,6 +470,7 @@ int main(int argc, char** argv) {
         {"attention_matches_cpu", attention_matches_cpu},
         {"linear_matches_cpu", linear_matches_cpu},
         {"qkv_heads_equal_sequence", qkv_heads_equal_sequence},
+        {"qknorm_rope_pair_equals_two_calls", qknorm_rope_pair_equals_two_calls},
         {"contract_violations_throw", contract_violations_throw},
     };
     HipContext ctx;

@@ -77,6 +77,29 @@ def test_qknorm_rope_contract():
     assert q(None, F16, None, None, None, None, None, None, 0, 11, 16, 64, 5, 1e-5) == _lib.HS_OK
 
 
+def test_qknorm_rope_pair_contract():
+    q = L.hs_qknorm_rope_pair
+    K, QH, KH = ctypes.c_void_p(0x30000), FAKE2, ctypes.c_void_p(0x40000)
+    shape = (2, 11, 16, 64, 5, 1e-5)
+    _einval(q(None, 7, FAKE, K, None, None, None, None, None, None, QH, KH, *shape), "dtype")
+    _einval(q(None, F16, FAKE, K, FAKE, None, None, None, None, None, QH, KH, *shape),
+            "weight and bias")
+    _einval(q(None, F16, FAKE, K, FAKE, FAKE, None, None, None, None, QH, KH, *shape),
+            "both q and k")
+    _einval(q(None, F16, FAKE, K, None, None, None, None, FAKE, None, QH, KH, *shape), "sin and cos")
+    _einval(q(None, F16, FAKE, K, None, None, None, None, FAKE, FAKE, QH, KH, 2, 11, 16, 64, 12,
+              1e-5), "prefix")
+    _einval(q(None, F16, FAKE, K, None, None, None, None, None, None, QH, None, *shape), "null")
+    # each output against each input, and the outputs against each other
+    _einval(q(None, F16, FAKE, K, None, None, None, None, None, None, QH, K, *shape), "overlaps an input")
+    _einval(q(None, F16, FAKE, K, None, None, None, None, None, None, FAKE, KH, *shape),
+            "overlaps an input")
+    _einval(q(None, F16, FAKE, K, None, None, None, None, None, None, QH, QH, *shape),
+            "q_head overlaps k_head")
+    assert q(None, F16, None, None, None, None, None, None, None, None, None, None, 0, 11, 16, 64,
+             5, 1e-5) == _lib.HS_OK
+
+
 def test_split_rope_apply_contract():
     _einval(L.hs_split_heads(None, F32, FAKE, FAKE, 2, 5, 4, 8), "overlap")
     _einval(L.hs_split_heads(None, F32, None, FAKE, 2, 5, 4, 8), "null")

@@ -85,6 +85,8 @@ QK_CASES = [
     (2, 11, 16, 64, 5, (2, 3)),
     (2, 21, 16, 64, 5, (4, 4)),
     (3, 37, 8, 64, 17, (4, 5)),
+    (3, 6, 32, 64, 2, (2, 2)),    # frames shorter than a token tile: tiles span frames
+    (5, 7, 8, 64, 1, (2, 3)),
     (1, 9, 4, 64, 3, (2, 3)),
     (2, 11, 3, 64, 5, (2, 3)),    # H not a multiple of a load's heads: generic path
     (2, 10, 2, 32, 4, (2, 3)),    # head_dim 32: generic path (tables cut to 32 channels)
@@ -123,6 +125,38 @@ def test_qknorm_rope(ctx, dtype, case, norm, use_rope):
         # prefix tokens pass through untouched
         xs = x.reshape(s, t, h, d).transpose(0, 2, 1, 3)
         assert_bit_exact(got[:, :, :prefix], np.ascontiguousarray(xs[:, :, :prefix]), what + " prefix")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", QK_CASES)
+@pytest.mark.parametrize("norm,use_rope", [(True, True), (True, False), (False, True),
+                                           (False, False)])
+def test_qknorm_rope_pair(ctx, dtype, case, norm, use_rope):
+    """q and k in one launch: bit-identical to two hs_qknorm_rope calls with
+    their own norms (row kernel and generic fallback alike), and the oracle
+    holds for k."""
+    s, t, h, d, prefix, grid = case
+    q = host(O.normal(31, (s * t, h * d)), dtype)
+    k = host(O.normal(32, (s * t, h * d)), dtype)
+    qn = (O.normal(33, (d,), 1.0, 0.02), O.normal(34, (d,), 0.0, 0.02))
+    kn = (O.normal(35, (d,), 1.0, 0.02), O.normal(36, (d,), 0.0, 0.02))
+    sin, cos = _tables(t, prefix, grid, d)
+    rp = (dev(sin), dev(cos), prefix) if use_rope else None
+    dq, dk = dev(q), dev(k)
+    gq, gk = ctx.qknorm_rope_pair(dq, dk, s, t, h, d,
+                                  qn=tuple(dev(a) for a in qn) if norm else None,
+                                  kn=tuple(dev(a) for a in kn) if norm else None,
+                                  rope=rp, eps=1e-6)
+    wq = ctx.qknorm_rope(dq, s, t, h, d, norm=tuple(dev(a) for a in qn) if norm else None,
+                         rope=rp, eps=1e-6)
+    wk = ctx.qknorm_rope(dk, s, t, h, d, norm=tuple(dev(a) for a in kn) if norm else None,
+                         rope=rp, eps=1e-6)
+    what = f"qknorm_rope_pair {dtype} {case} norm={norm} rope={use_rope}"
+    assert_bit_exact(back(gq), back(wq), what + " q")
+    assert_bit_exact(back(gk), back(wk), what + " k")
+    want = O.qknorm_rope(k, *(kn if norm else (None, None)), sin if use_rope else None,
+                         cos if use_rope else None, s, t, h, d, prefix, 1e-6)
+    check(back(gk), want, what + " k oracle", stages=2 if (norm and use_rope) else 1)
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
