@@ -7,9 +7,10 @@
 // tiled_add.wesl semantics, out[i] = x[i] + table[i % block]) into the cast,
 // so each patch element is read once in its input dtype and written once.
 //
-// One wave64 per output row; each lane moves 4 consecutive channels per
-// step, CHUNKS steps per row. Rows are independent; the camera/register
-// gather is row-granular, so no LDS staging is needed.
+// Each lane moves LV = 4 consecutive channels per step, CHUNKS steps per
+// row (8 channels per lane, one 16-byte f16 store each, measured slower:
+// 66% of peak against 72.7% at S=32). Rows are independent; the
+// camera/register gather is row-granular, so no LDS staging is needed.
 #include "hs_common.hpp"
 
 namespace hs {
@@ -19,44 +20,85 @@ constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / 64;
 // Launch shape (overridable at build time for tuning sweeps).
 #ifndef HS_AS_BPC
-#define HS_AS_BPC 8  // resident workgroups per CU
+#define HS_AS_BPC 8  // resident workgroups per CU (generic path)
+#endif
+#ifndef HS_AS_F
+#define HS_AS_F 8  // frames per wave of one patch position
 #endif
 constexpr int kBlocksPerCu = HS_AS_BPC;
+constexpr int kFramesPerWave = HS_AS_F;
 
-__device__ __forceinline__ void load4(const float* p, float (&f)[4]) {
-    float4 v = ld_f32x4(p);
-    f[0] = v.x, f[1] = v.y, f[2] = v.z, f[3] = v.w;
+// LV consecutive channels per lane (4 or 8), converted to f32.
+template <int LV>
+__device__ __forceinline__ void loadv(const float* p, float (&f)[LV]) {
+#pragma unroll
+    for (int i = 0; i < LV; i += 4) {
+        const float4 v = ld_f32x4(p + i);
+        f[i] = v.x, f[i + 1] = v.y, f[i + 2] = v.z, f[i + 3] = v.w;
+    }
 }
-__device__ __forceinline__ void load4(const f16* p, float (&f)[4]) {
-    u32x2 v = *reinterpret_cast<const u32x2*>(p);
-    const f16x2 a = u2h2(v[0]), b = u2h2(v[1]);
-    f[0] = static_cast<float>(a.x), f[1] = static_cast<float>(a.y);
-    f[2] = static_cast<float>(b.x), f[3] = static_cast<float>(b.y);
+__device__ __forceinline__ void unpack_h(uint32_t u, float& a, float& b) {
+    const f16x2 h = u2h2(u);
+    a = static_cast<float>(h.x), b = static_cast<float>(h.y);
+}
+template <int LV>
+__device__ __forceinline__ void loadv(const f16* p, float (&f)[LV]) {
+    if constexpr (LV == 8) {
+        const u32x4 v = ld16(p);
+#pragma unroll
+        for (int k = 0; k < 4; k++) unpack_h(v[k], f[2 * k], f[2 * k + 1]);
+    } else {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(p);
+        unpack_h(v[0], f[0], f[1]), unpack_h(v[1], f[2], f[3]);
+    }
 }
 // Patch loads and token stores stream (non-temporal); camera/register rows
 // and the positional table are reread across frames and stay cached.
-__device__ __forceinline__ void load4_stream(const float* p, float (&f)[4]) {
-    const u32x4 v = ld_stream(p);
-    f[0] = u2f(v[0]), f[1] = u2f(v[1]), f[2] = u2f(v[2]), f[3] = u2f(v[3]);
+template <int LV>
+__device__ __forceinline__ void loadv_stream(const float* p, float (&f)[LV]) {
+#pragma unroll
+    for (int i = 0; i < LV; i += 4) {
+        const u32x4 v = ld_stream(p + i);
+        f[i] = u2f(v[0]), f[i + 1] = u2f(v[1]), f[i + 2] = u2f(v[2]), f[i + 3] = u2f(v[3]);
+    }
 }
-__device__ __forceinline__ void load4_stream(const f16* p, float (&f)[4]) {
-    const u32x2 v = ld_stream_as(reinterpret_cast<const u32x2*>(p));
-    const f16x2 a = u2h2(v[0]), b = u2h2(v[1]);
-    f[0] = static_cast<float>(a.x), f[1] = static_cast<float>(a.y);
-    f[2] = static_cast<float>(b.x), f[3] = static_cast<float>(b.y);
+template <int LV>
+__device__ __forceinline__ void loadv_stream(const f16* p, float (&f)[LV]) {
+    if constexpr (LV == 8) {
+        const u32x4 v = ld_stream(p);
+#pragma unroll
+        for (int k = 0; k < 4; k++) unpack_h(v[k], f[2 * k], f[2 * k + 1]);
+    } else {
+        const u32x2 v = ld_stream_as(reinterpret_cast<const u32x2*>(p));
+        unpack_h(v[0], f[0], f[1]), unpack_h(v[1], f[2], f[3]);
+    }
 }
-__device__ __forceinline__ void store4(float* p, const float (&f)[4]) {
-    u32x4 v;
-    v[0] = f2u(f[0]), v[1] = f2u(f[1]), v[2] = f2u(f[2]), v[3] = f2u(f[3]);
-    st_stream(p, v);
+template <int LV>
+__device__ __forceinline__ void storev(float* p, const float (&f)[LV]) {
+#pragma unroll
+    for (int i = 0; i < LV; i += 4) {
+        u32x4 v;
+        v[0] = f2u(f[i]), v[1] = f2u(f[i + 1]), v[2] = f2u(f[i + 2]), v[3] = f2u(f[i + 3]);
+        st_stream(p + i, v);
+    }
 }
-__device__ __forceinline__ void store4(f16* p, const float (&f)[4]) {
-    f16x2 a, b;
-    a.x = static_cast<f16>(f[0]), a.y = static_cast<f16>(f[1]);
-    b.x = static_cast<f16>(f[2]), b.y = static_cast<f16>(f[3]);
-    u32x2 v;
-    v[0] = h22u(a), v[1] = h22u(b);
-    st_stream_as(reinterpret_cast<u32x2*>(p), v);
+__device__ __forceinline__ uint32_t pack_h(float a, float b) {
+    f16x2 h;
+    h.x = static_cast<f16>(a), h.y = static_cast<f16>(b);
+    return h22u(h);
+}
+template <int LV>
+__device__ __forceinline__ void storev(f16* p, const float (&f)[LV]) {
+    if constexpr (LV == 8) {
+        u32x4 v;
+#pragma unroll
+        for (int k = 0; k < 4; k++) v[k] = pack_h(f[2 * k], f[2 * k + 1]);
+        st_stream(p, v);
+    } else {
+        u32x2 v;
+        v[0] = pack_h(f[0], f[1]), v[1] = pack_h(f[2], f[3]);
+        st_stream_as(reinterpret_cast<u32x2*>(p), v);
+    }
 }
 
 // Patch-row value as the reference sequence stores it: the GEMM epilogue
@@ -70,13 +112,15 @@ __device__ __forceinline__ float patch_value(float x, float b, float p, bool has
 
 // Workgroup -> rows, XCD-aware. Workgroups are dispatched round-robin over
 // the XCDs (workgroup b runs on XCD b % kXcds), each XCD with its own L2.
-// Patch rows come first: workgroup b handles patch position
-// p = (b / kXcds / C) * kXcds + b % kXcds for frames [4c, 4c + 4), c =
-// (b / kXcds) % C, C = ceil(S / 4). Every workgroup of one patch position
-// therefore runs on the same XCD and in C consecutive dispatch rounds, so
-// the positional-table row p is fetched from HBM once and then served by
-// that XCD's L2 to all S frames. Camera/register rows follow, 4 per
-// workgroup.
+// Patch rows come first: a wave takes one patch position for F =
+// kFramesPerWave consecutive frames, keeping that position's table row and
+// the bias in registers, so each is read once per F frames instead of once
+// per row. Workgroup b handles position p = (b / kXcds / C) * kXcds + b %
+// kXcds for frames [4 F c, 4 F (c + 1)), c = (b / kXcds) % C, C =
+// ceil(S / (4 F)). Every workgroup of one patch position therefore runs on
+// the same XCD and in C consecutive dispatch rounds, so the table row is
+// fetched from HBM once and then served by that XCD's L2. Camera/register
+// rows follow, 4 per workgroup.
 constexpr int kXcds = 8;
 
 struct AssembleGrid {
@@ -85,49 +129,67 @@ struct AssembleGrid {
     int chunks;            // C
     __host__ __device__ static AssembleGrid make(int s, int np, int nr) {
         AssembleGrid g;
-        g.chunks = static_cast<int>(ceil_div(s, kWavesPerBlock));
+        g.chunks = static_cast<int>(ceil_div(ceil_div(s, kFramesPerWave), kWavesPerBlock));
         g.patch_blocks = static_cast<int64_t>(g.chunks) * ceil_div(np, kXcds) * kXcds;
         g.special_blocks = ceil_div(static_cast<int64_t>(s) * (1 + nr), kWavesPerBlock);
         return g;
     }
 };
 
-template <typename TO, typename TP, int CHUNKS>
+template <typename TO, typename TP, int CHUNKS, int LV>
 __global__ __launch_bounds__(kBlock) void assemble_kernel(
     const TP* __restrict__ patches, const float* __restrict__ pbias, const float* __restrict__ pos,
     const TO* __restrict__ cam, const TO* __restrict__ reg, TO* __restrict__ out, int nframes,
     int seq, int np, int nr, int n_var) {
-    constexpr int D = 256 * CHUNKS;
+    constexpr int CW = 64 * LV;  // channels per chunk: LV per lane
+    constexpr int D = CW * CHUNKS;
     const int lane = lane_id();
     const int w = wave_in_block();
     const AssembleGrid grid = AssembleGrid::make(nframes, np, nr);
     const int64_t b = blockIdx.x;
     if (b < grid.patch_blocks) {
+        constexpr int F = kFramesPerWave;
         const int64_t round = b / kXcds;
         const int64_t p = (round / grid.chunks) * kXcds + b % kXcds;
-        const int f = static_cast<int>(round % grid.chunks) * kWavesPerBlock + w;
-        if (p >= np || f >= nframes) return;  // wave-uniform; the kernel has no barriers
+        const int f0 = (static_cast<int>(round % grid.chunks) * kWavesPerBlock + w) * F;
+        if (p >= np || f0 >= nframes) return;  // wave-uniform; the kernel has no barriers
+        const int f1 = f0 + F < nframes ? f0 + F : nframes;
         const bool has_b = pbias != nullptr, has_p = pos != nullptr;
-        const TP* src = patches + (static_cast<int64_t>(f) * np + p) * D + lane * 4;
-        float x[CHUNKS][4], pe[CHUNKS][4], bv[CHUNKS][4];
-#pragma unroll
-        for (int c = 0; c < CHUNKS; c++) load4_stream(src + c * 256, x[c]);
-        if (has_p) {
-#pragma unroll
-            for (int c = 0; c < CHUNKS; c++) load4(pos + p * D + c * 256 + lane * 4, pe[c]);
-        }
-        if (has_b) {
-#pragma unroll
-            for (int c = 0; c < CHUNKS; c++) load4(pbias + c * 256 + lane * 4, bv[c]);
-        }
-        TO* orow = out + (static_cast<int64_t>(f) * seq + 1 + nr + p) * D + lane * 4;
+        float pe[CHUNKS][LV], bv[CHUNKS][LV];
 #pragma unroll
         for (int c = 0; c < CHUNKS; c++) {
 #pragma unroll
-            for (int k = 0; k < 4; k++)
-                x[c][k] = patch_value<TP>(x[c][k], has_b ? bv[c][k] : 0.0f,
-                                          has_p ? pe[c][k] : 0.0f, has_b, has_p);
-            store4(orow + c * 256, x[c]);
+            for (int k = 0; k < LV; k++) pe[c][k] = bv[c][k] = 0.0f;
+            if (has_p) loadv(pos + p * D + c * CW + lane * LV, pe[c]);
+            if (has_b) loadv(pbias + c * CW + lane * LV, bv[c]);
+        }
+        const TP* src = patches + (static_cast<int64_t>(f0) * np + p) * D + lane * LV;
+        TO* orow = out + (static_cast<int64_t>(f0) * seq + 1 + nr + p) * D + lane * LV;
+        const int64_t src_step = static_cast<int64_t>(np) * D, out_step = static_cast<int64_t>(seq) * D;
+        auto load = [&](float (&x)[CHUNKS][LV], int f) {
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) loadv_stream(src + (f - f0) * src_step + c * CW, x[c]);
+        };
+        auto emit = [&](float (&x)[CHUNKS][LV], int f) {
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) {
+#pragma unroll
+                for (int k = 0; k < LV; k++)
+                    x[c][k] = patch_value<TP>(x[c][k], bv[c][k], pe[c][k], has_b, has_p);
+                storev(orow + (f - f0) * out_step + c * CW, x[c]);
+            }
+        };
+        // two-buffer pipeline over the wave's frames: the next frame's row
+        // is in flight while the current one is summed and stored
+        float xa[CHUNKS][LV], xb[CHUNKS][LV];
+        load(xa, f0);
+#pragma unroll 1
+        for (int f = f0; f < f1; f += 2) {
+            if (f + 1 < f1) load(xb, f + 1);
+            emit(xa, f);
+            if (f + 1 >= f1) break;
+            if (f + 2 < f1) load(xa, f + 2);
+            emit(xb, f + 1);
         }
         return;
     }
@@ -139,12 +201,12 @@ __global__ __launch_bounds__(kBlock) void assemble_kernel(
     const int v = (n_var == 2 && f != 0) ? 1 : 0;
     const TO* src = t == 0 ? cam + static_cast<int64_t>(v) * D
                            : reg + (static_cast<int64_t>(v) * nr + (t - 1)) * D;
-    TO* orow = out + (static_cast<int64_t>(f) * seq + t) * D + lane * 4;
-    float vals[CHUNKS][4];
+    TO* orow = out + (static_cast<int64_t>(f) * seq + t) * D + lane * LV;
+    float vals[CHUNKS][LV];
 #pragma unroll
-    for (int c = 0; c < CHUNKS; c++) load4(src + c * 256 + lane * 4, vals[c]);
+    for (int c = 0; c < CHUNKS; c++) loadv(src + c * CW + lane * LV, vals[c]);
 #pragma unroll
-    for (int c = 0; c < CHUNKS; c++) store4(orow + c * 256, vals[c]);
+    for (int c = 0; c < CHUNKS; c++) storev(orow + c * CW, vals[c]);
 }
 
 // Any D, any alignment: lanes strided over the row.
@@ -204,21 +266,18 @@ hs_status launch(hipStream_t st, const void* patches, const float* pbias, const 
                         (!pos || aligned16(pos));
     const dim3 vgrid(static_cast<uint32_t>(vblocks));
     if (vec_ok) {
+#define HS_AS_LAUNCH(CH, LV)                                                                      \
+    assemble_kernel<TO, TP, CH, LV><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, \
+                                                                   np, nr, n_var);                \
+    return check_launch("assemble_tokens")
         switch (d / 256) {
-            case 1:
-                assemble_kernel<TO, TP, 1><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, np, nr, n_var);
-                return check_launch("assemble_tokens");
-            case 2:
-                assemble_kernel<TO, TP, 2><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, np, nr, n_var);
-                return check_launch("assemble_tokens");
-            case 4:
-                assemble_kernel<TO, TP, 4><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, np, nr, n_var);
-                return check_launch("assemble_tokens");
-            case 8:
-                assemble_kernel<TO, TP, 8><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, np, nr, n_var);
-                return check_launch("assemble_tokens");
+            case 1: HS_AS_LAUNCH(1, 4);
+            case 2: HS_AS_LAUNCH(2, 4);
+            case 4: HS_AS_LAUNCH(4, 4);
+            case 8: HS_AS_LAUNCH(8, 4);
             default: break;
         }
+#undef HS_AS_LAUNCH
     }
     assemble_generic_kernel<TO, TP><<<grid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, out_rows,
                                                                    seq, np, nr, d, n_var);

@@ -284,7 +284,10 @@ def test_tiled_add_and_copy_rows(ctx):
 @pytest.mark.parametrize("out_dtype", DTYPES)
 @pytest.mark.parametrize("patch_dtype", DTYPES)
 @pytest.mark.parametrize("s,grid,r,d,n_var", [(3, (2, 3), 4, 1024, 2), (2, (2, 3), 16, 256, 2),
-                                              (2, (3, 2), 4, 96, 1), (1, (1, 4), 0, 512, 2)])
+                                              (2, (3, 2), 4, 96, 1), (1, (1, 4), 0, 512, 2),
+                                              # several waves per patch position, the last
+                                              # partial; several workgroup rounds per position
+                                              (11, (2, 3), 4, 1024, 2), (37, (3, 3), 4, 256, 2)])
 @pytest.mark.parametrize("bias,pos", [(True, True), (False, False), (True, False)])
 def test_assemble_tokens(ctx, out_dtype, patch_dtype, s, grid, r, d, n_var, bias, pos):
     p = grid[0] * grid[1]
