@@ -83,10 +83,17 @@ def parse():
                     help="size of one plain torch copy launched before timing (HBM counter "
                          "calibration for rocprofv3 --pmc runs)")
     ap.add_argument("--attention-iters", type=int, default=10,
-                    help="timed launches of each attention shape (0 skips the attention leg)")
+                    help="timed launches of each attention shape (0 skips the attention, "
+                         "cache, linear, block and trunk legs)")
+    ap.add_argument("--trunk-iters", type=int, default=-1,
+                    help="timed trunk forwards (default attention-iters // 5, at least 1; "
+                         "0 skips the trunk leg)")
     ap.add_argument("--summarize", metavar="KERNEL_TRACE_CSV",
                     help="print a summary of rocprofv3 output for this benchmark instead of "
                          "running it")
+    ap.add_argument("--legs-trace", metavar="KERNEL_TRACE_CSV",
+                    help="kernel trace of a run with the attention/cache/linear legs (default: "
+                         "the --summarize trace)")
     ap.add_argument("--pmc-fetch", metavar="CSV", help="counter_collection CSV of a FETCH_SIZE run")
     ap.add_argument("--pmc-write", metavar="CSV", help="counter_collection CSV of a WRITE_SIZE run")
     ap.add_argument("--traffic-json", metavar="PATH", help="write per-op HBM bytes here")
@@ -591,6 +598,7 @@ def summarize(args) -> None:
     nbytes = op_bytes(rows, esz, args.frames * p, p)
     launches = {"assemble": 1, "layernorm": 96, "qknorm_rope": 48, "bias_ls_residual": 96,
                 "bias_gelu": 48}
+    legs = args.legs_trace or args.summarize
     dur = defaultdict(list)
     for r in csv.DictReader(open(args.summarize)):
         op = kernel_op(r["Kernel_Name"])
@@ -612,27 +620,32 @@ def summarize(args) -> None:
                 f"({sum(nbytes[o] * launches[o] for o in OPS) / (pass_us * 1e-6) / 1e9:.0f} GB/s "
                 f"algorithmic)."]
     # Attention (the benchmark's attention leg): the flash kernel, told apart by
-    # grid size (work-items = 64 * waves * workgroups).
+    # grid size: one workgroup of 8 waves (512 work-items) per 256 queries of
+    # one (sequence, head), the (sequence, head) count rounded up to the 8 XCDs.
     att = defaultdict(list)
     t_tok = GRID[0] * GRID[1] + PREFIX
-    for r in csv.DictReader(open(args.summarize)):
+    for r in csv.DictReader(open(legs)):
         if "flash_f16_kernel" in r["Kernel_Name"]:
             att[int(r["Grid_Size_X"])].append(
                 (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
-    if att:
+    shapes = {"frame": (args.frames, t_tok), "global": (1, args.frames * t_tok)}
+    att_grid = {name: 8 * -(-(s_ * HEADS) // 8) * -(-tt // 256) * 512
+                for name, (s_, tt) in shapes.items()}
+    if any(att_grid[n] in att for n in shapes):
         out += ["", "## Attention (flash_f16_kernel, f16, 16 heads of 64)", "",
                 "| call | grid work-items | kernel calls | mean us | TFLOP/s | of 2.5 PFLOP/s |",
                 "|---|---|---|---|---|---|"]
-        shapes = {"frame": (args.frames, t_tok), "global": (1, args.frames * t_tok)}
-        by_size = sorted(att.items(), key=lambda kv: st.mean(kv[1]))
-        for (grid, durs), name in zip(by_size, ["frame", "global"]):
-            s_, tt = shapes[name]
+        for name, (s_, tt) in shapes.items():
+            grid = att_grid[name]
+            durs = att.get(grid)
+            if not durs:
+                continue
             m = st.mean(durs)
             tf = 4.0 * tt * tt * HEAD_DIM * s_ * HEADS / (m * 1e-6) / 1e12
             out.append(f"| {name} (S={s_}, T={tt}) | {grid} | {len(durs)} | {m:.1f} | {tf:.0f} | "
                        f"{tf / MFMA_PEAK_TFLOPS:.1%} |")
     cache = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-             for r in csv.DictReader(open(args.summarize))
+             for r in csv.DictReader(open(legs))
              if "concat_vec_kernel" in r["Kernel_Name"] and "IDF16_fE" in r["Kernel_Name"]
              and int(r["Grid_Size_X"]) >= 256 * 256]
     if cache:
@@ -648,7 +661,7 @@ def summarize(args) -> None:
                 f"| {len(cache)} | {m:.1f} | {cb / 1e6:.1f} | {cb / (m * 1e-6) / 1e9:.0f} | "
                 f"{cb / (m * 1e-6) / 1e9 / PEAK_GBS:.1%} |"]
     gem = defaultdict(list)
-    for r in csv.DictReader(open(args.summarize)):
+    for r in csv.DictReader(open(legs)):
         if "gemm_f16_kernel" in r["Kernel_Name"]:
             epi = r["Kernel_Name"].split("gemm_f16_kernelILi")[1][0]
             gem[(epi, int(r["Grid_Size_X"]))].append(
@@ -843,7 +856,9 @@ def main():
         line["cache_build"] = cache_times(ctx, args.frames, args.attention_iters)
         line["linear"] = gemm_times(ctx, args.frames, args.attention_iters)
         line["block"] = block_times(ctx, args.frames, max(1, args.attention_iters // 2))
-        line["trunk"] = trunk_times(ctx, args.frames, max(1, args.attention_iters // 5))
+        trunk_iters = args.trunk_iters if args.trunk_iters >= 0 else max(1, args.attention_iters // 5)
+        if trunk_iters > 0:
+            line["trunk"] = trunk_times(ctx, args.frames, trunk_iters)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
         if args.attention_iters > 0:
