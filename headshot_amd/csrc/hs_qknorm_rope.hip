@@ -20,6 +20,10 @@
 // writes 64/G heads' 128-byte vectors of one token into the head-major
 // (S, H, T, 64) output that attention consumes.
 //
+// hs_qknorm_rope_pair runs q and k in one launch (the first half of the grid
+// takes q with its norm, the second half k): each launch pays ~4 us of
+// fill and drain at S=32, so one launch for both halves that cost.
+//
 // Generic path (any head_dim, either input layout): one wave per head vector,
 // lanes strided over the vector; used for rope_apply on head-major tensors
 // and for shapes the fast path does not cover.
