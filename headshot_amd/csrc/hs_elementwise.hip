@@ -18,15 +18,16 @@ namespace {
 // Launch shape (overridable at build time for tuning sweeps).
 // U: 16-byte vectors per input stream per thread per iteration; BPC:
 // workgroups launched per CU. Chosen by timing the whole aggregator pass,
-// not the op alone. GELU runs fastest with one vector per thread and 32
-// workgroups per CU; it must keep non-temporal stores, because with plain
-// stores its output occupies the cache and the LayerNorm after it slows by
-// a third.
+// not the op alone. Both ops run fastest with one vector per stream per
+// thread and many workgroups (GELU 64 per CU, ~5 vectors per thread at
+// S=32; LayerScale 32 per CU, ~3); GELU must keep non-temporal
+// stores, because with plain stores its output occupies the cache and the
+// LayerNorm after it slows by a third.
 #ifndef HS_GELU_U
 #define HS_GELU_U 1
 #endif
 #ifndef HS_GELU_BPC
-#define HS_GELU_BPC 32
+#define HS_GELU_BPC 64
 #endif
 #ifndef HS_GELU_NTL
 #define HS_GELU_NTL (HS_NT != 0)  // non-temporal loads of the fc1 output
@@ -35,10 +36,10 @@ namespace {
 #define HS_GELU_NTS (HS_NT != 0)  // non-temporal stores of the activation
 #endif
 #ifndef HS_LS_U
-#define HS_LS_U 2
+#define HS_LS_U 1
 #endif
 #ifndef HS_LS_BPC
-#define HS_LS_BPC 8
+#define HS_LS_BPC 32
 #endif
 #ifndef HS_EW_BPC
 #define HS_EW_BPC 4  // cast and tiled add
