@@ -159,6 +159,26 @@ def test_qknorm_rope_pair(ctx, dtype, case, norm, use_rope):
     check(back(gk), want, what + " k oracle", stages=2 if (norm and use_rope) else 1)
 
 
+def test_qknorm_rope_pair_unaligned_and_shared_input(ctx):
+    """Pointers off the 16-byte grid take the generic kernel for both halves;
+    q and k may be the same buffer. Each half still equals its single call."""
+    s, t, h, d, prefix, grid = 2, 11, 16, 64, 5, (2, 3)
+    n = s * t * h * d
+    buf = dev(host(O.normal(37, (n + 8,)), torch.float16))
+    q = buf[1:1 + n].view(s * t, h * d)           # 2 bytes past a 16-byte boundary
+    qn = tuple(dev(a) for a in (O.normal(38, (d,), 1.0, 0.02), O.normal(39, (d,), 0.0, 0.02)))
+    kn = tuple(dev(a) for a in (O.normal(40, (d,), 1.0, 0.02), O.normal(41, (d,), 0.0, 0.02)))
+    sin, cos = _tables(t, prefix, grid, d)
+    rp = (dev(sin), dev(cos), prefix)
+    gq, gk = ctx.qknorm_rope_pair(q, q, s, t, h, d, qn=qn, kn=kn, rope=rp, eps=1e-6)
+    wq = ctx.qknorm_rope(q, s, t, h, d, norm=qn, rope=rp, eps=1e-6)
+    wk = ctx.qknorm_rope(q, s, t, h, d, norm=kn, rope=rp, eps=1e-6)
+    assert_bit_exact(back(gq), back(wq), "pair unaligned q")
+    assert_bit_exact(back(gk), back(wk), "pair unaligned k")
+    want = O.qknorm_rope(back(q), *(back(a) for a in kn), sin, cos, s, t, h, d, prefix, 1e-6)
+    check(back(gk), want, "pair unaligned k oracle", stages=2)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_qknorm_rope_prefix_equals_t(ctx, dtype):
     s, t, h, d = 2, 5, 16, 64
