@@ -14,6 +14,9 @@
 // fastest at 44k rows, alone (69.5% of peak against 65.5%) and inside the
 // aggregator pass (72.1% against 69.7%).
 //
+// Narrow path (rows of 8 or 16 vectors, e.g. 64-wide f16 QK-norm rows):
+// several rows per wave, each reduced within its group of lanes.
+//
 // Generic path: any dim, one wave per row, strided over the row three
 // times (mean, variance, output) with the second and third reads served by
 // the cache.
@@ -107,6 +110,64 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
     }
 }
 
+// Narrow rows (dim = G vectors of 16 bytes, G = 8 or 16: a 64-wide f16 row
+// such as the reference's QK-norm over head_dim, model/block.rs:136-142):
+// a row lives in a group of G lanes, one 16-byte vector per lane, so a wave
+// holds 64 / G rows per load instruction and reduces each over its group
+// with DPP permutes. Each wave takes U such row groups, all loads issued
+// before any row is reduced.
+template <typename T, int G, int U>
+__global__ __launch_bounds__(kBlock) void ln_small_kernel(const T* x, const float* __restrict__ w,
+                                                          const float* __restrict__ b, T* out,
+                                                          int64_t rows, float eps) {
+    constexpr int V = Vec<T>::N;
+    constexpr int DIM = G * V;
+    constexpr int RPW = 64 / G;  // rows per load instruction
+    const int lane = lane_id();
+    const int piece = lane % G;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+    float wr[V], br[V];
+#pragma unroll
+    for (int k = 0; k < V; k += 4) {
+        const float4 w4 = ld_f32x4(w + piece * V + k), b4 = ld_f32x4(b + piece * V + k);
+        wr[k] = w4.x, wr[k + 1] = w4.y, wr[k + 2] = w4.z, wr[k + 3] = w4.w;
+        br[k] = b4.x, br[k + 1] = b4.y, br[k + 2] = b4.z, br[k + 3] = b4.w;
+    }
+    for (int64_t r0 = wave * (U * RPW); r0 < rows; r0 += nwaves * (U * RPW)) {
+        // every lane of a group shares its row, so the bounds test is uniform
+        // across the group that the reductions read
+        u32x4 raw[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t row = r0 + u * RPW + lane / G;
+            raw[u] = u32x4{0, 0, 0, 0};
+            if (row < rows) raw[u] = ld_stream(x + row * DIM + piece * V);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int64_t row = r0 + u * RPW + lane / G;
+            float f[V];
+            unpack(raw[u], f, T{});
+            float s = 0.0f;
+#pragma unroll
+            for (int k = 0; k < V; k++) s += f[k];
+            const float mean = group_sum<G>(s) / static_cast<float>(DIM);
+            float q = 0.0f;
+#pragma unroll
+            for (int k = 0; k < V; k++) {
+                const float d = f[k] - mean;
+                q += d * d;
+            }
+            const float inv = rsqrtf(group_sum<G>(q) / static_cast<float>(DIM) + eps);
+            float y[V];
+#pragma unroll
+            for (int k = 0; k < V; k++) y[k] = (f[k] - mean) * inv * wr[k] + br[k];
+            if (row < rows) st_stream(out + row * DIM + piece * V, pack(y, T{}));
+        }
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(kBlock) void ln_generic_kernel(const T* x, const float* __restrict__ w,
                                                             const float* __restrict__ b, T* out,
@@ -164,6 +225,20 @@ hs_status launch(hipStream_t st, const void* x, const float* w, const float* b, 
             case 4: return launch_vec<T, 4>(st, x, w, b, out, rows, eps);
             default: break;
         }
+    }
+    const bool small_ok = aligned16(x) && aligned16(out) && aligned16(w) && aligned16(b) &&
+                          (dim == 8 * V || dim == 16 * V);
+    if (small_ok) {
+        constexpr int U = 2;
+        const int64_t want = ceil_div(ceil_div(rows, (dim == 8 * V ? 8 : 4) * U), kWavesPerBlock);
+        const int64_t blocks = want < (int64_t{1} << 22) ? want : (int64_t{1} << 22);
+        if (dim == 8 * V)
+            ln_small_kernel<T, 8, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, eps);
+        else
+            ln_small_kernel<T, 16, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, eps);
+        return check_launch("layernorm");
     }
     const int64_t blocks = persistent_blocks(rows);
     ln_generic_kernel<T><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(

@@ -57,7 +57,9 @@ def check(got: np.ndarray, want: np.ndarray, what: str, max_ulp: int = 1,
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("rows,dim", [(1, 1024), (19, 1024), (257, 1024), (19, 300), (33, 64),
-                                      (7, 512), (5, 2048), (3, 4096), (11, 100)])
+                                      (7, 512), (5, 2048), (3, 4096), (11, 100),
+                                      # narrow rows: several per wave, ragged last group
+                                      (1003, 64), (17, 128), (41, 32), (2, 64)])
 def test_layernorm(ctx, dtype, rows, dim):
     x = host(O.normal(11, (rows, dim)), dtype)
     w = O.normal(12, (dim,), 1.0, 0.02)
@@ -74,6 +76,11 @@ def test_layernorm_in_place_and_empty(ctx, dtype):
     t = dev(x)
     ctx.layernorm(t, dev(w), dev(b), eps=1e-6, out=t)
     check(back(t), O.layernorm(x, w, b, 1e-6), "layernorm in place")
+    x64 = host(O.normal(17, (45, 64)), dtype)
+    w64, b64 = O.normal(18, (64,), 1.0, 0.02), O.normal(19, (64,), 0.0, 0.02)
+    t64 = dev(x64)
+    ctx.layernorm(t64, dev(w64), dev(b64), eps=1e-6, out=t64)
+    check(back(t64), O.layernorm(x64, w64, b64, 1e-6), "layernorm 64-wide in place")
     empty = torch.empty((0, 1024), dtype=dtype, device="cuda:0")
     assert ctx.layernorm(empty, dev(w), dev(b)).shape == (0, 1024)
 
