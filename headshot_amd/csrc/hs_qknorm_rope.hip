@@ -24,9 +24,13 @@
 // takes q with its norm, the second half k): each launch pays ~4 us of
 // fill and drain at S=32, so one launch for both halves that cost.
 //
+// rope_apply on head-major tensors with head_dim 64 runs the same lane
+// layout in place (rope_vec_kernel: a wave takes a few tokens of one frame
+// across all heads, so each token's table row is read once).
+//
 // Generic path (any head_dim, either input layout): one wave per head vector,
-// lanes strided over the vector; used for rope_apply on head-major tensors
-// and for shapes the fast path does not cover.
+// lanes strided over the vector; used for shapes the fast paths do not
+// cover.
 #include "hs_common.hpp"
 
 namespace hs {
@@ -181,6 +185,66 @@ __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
         if (u + 1 >= u_end) break;
         if (u + 2 < u_end) tl.load(a, u + 2);
         tl.process(b, u + 1);
+    }
+}
+
+// In-place rotate-half RoPE on head-major (S, H, T, 64) vectors (the
+// rope_apply surface op), in the row kernel's lane layout: a vector in a
+// group of G lanes, each channel's RoPE partner in the mirror lane. A wave
+// takes TG = 64 / G consecutive tokens of one frame and walks all heads, HB
+// at a time: each load instruction covers one head's TG vectors (contiguous
+// in head-major order), and each lane reads its token's sin/cos row once
+// for all heads. Prefix tokens are neither read nor written.
+template <typename T, int HB>
+__global__ __launch_bounds__(kBlock) void rope_vec_kernel(T* x, const float* __restrict__ sin_tab,
+                                                          const float* __restrict__ cos_tab,
+                                                          int nseq, int heads, int seq,
+                                                          int prefix) {
+    constexpr int D = 64, V = Vec<T>::N, G = D / V, TG = 64 / G;
+    const int lane = lane_id();
+    const int piece = lane % G;
+    const bool upper = piece >= G / 2;
+    const int ch = upper ? 32 + (G - 1 - piece) * V : piece * V;
+    const float none[V] = {};
+    const int tiles = static_cast<int>(ceil_div(seq, TG));
+    const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
+    if (unit >= static_cast<int64_t>(nseq) * tiles) return;  // wave-uniform; no barriers
+    const int s = static_cast<int>(unit / tiles);
+    const int t = static_cast<int>(unit - static_cast<int64_t>(s) * tiles) * TG + lane / G;
+    // a group's lanes share their token, so `live` is uniform across the
+    // group that the mirror permute reads
+    const bool live = t < seq && t >= prefix;
+    float cs[V], sn[V];
+#pragma unroll
+    for (int k = 0; k < V; k++) cs[k] = sn[k] = 0.0f;
+    if (live) {
+        const int64_t row = static_cast<int64_t>(t - prefix) * D + ch;
+        const float sg = upper ? 1.0f : -1.0f;
+#pragma unroll
+        for (int k = 0; k < V; k += 4) {
+            const float4 c4 = ld_f32x4(cos_tab + row + k), s4 = ld_f32x4(sin_tab + row + k);
+            cs[k] = c4.x, cs[k + 1] = c4.y, cs[k + 2] = c4.z, cs[k + 3] = c4.w;
+            sn[k] = sg * s4.x, sn[k + 1] = sg * s4.y, sn[k + 2] = sg * s4.z, sn[k + 3] = sg * s4.w;
+        }
+    }
+    T* base = x + (static_cast<int64_t>(s) * heads * seq + t) * D + ch;
+    const int64_t hstride = static_cast<int64_t>(seq) * D;
+    for (int h0 = 0; h0 < heads; h0 += HB) {
+        u32x4 raw[HB];
+#pragma unroll
+        for (int j = 0; j < HB; j++) {
+            raw[j] = u32x4{0, 0, 0, 0};
+            if (live && h0 + j < heads) raw[j] = ld_stream(base + (h0 + j) * hstride);
+        }
+        if (!live) continue;
+#pragma unroll
+        for (int j = 0; j < HB; j++) {
+            if (h0 + j >= heads) break;  // wave-uniform
+            float f[V];
+            unpack(raw[j], f, T{});
+            qk_norm_rope_vec<T, G, false>(f, none, none, 0.0f, true, cs, sn);
+            st_stream(base + (h0 + j) * hstride, pack(f, T{}));
+        }
     }
 }
 
@@ -436,6 +500,20 @@ hs_status hs_rope_apply(hs_stream_t stream, hs_dtype dt, void* x, const float* s
     if (n == 0 || prefix == t) return HS_OK;
     if (!x || !sin_tab || !cos_tab) return fail(HS_EINVAL, "rope_apply: null buffer");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    const int tg = dt == HS_F16 ? 8 : 4;  // tokens per load instruction
+    const int64_t units = static_cast<int64_t>(s) * ceil_div(t, tg);
+    const int64_t blocks = ceil_div(units, int64_t{kWavesPerBlock});
+    if (d == 64 && aligned16(x) && aligned16(sin_tab) && aligned16(cos_tab) &&
+        blocks * kBlock < (int64_t{1} << 32)) {
+        constexpr int HB = 8;
+        if (dt == HS_F16)
+            rope_vec_kernel<f16, HB><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                static_cast<f16*>(x), sin_tab, cos_tab, s, h, t, prefix);
+        else
+            rope_vec_kernel<float, HB><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                static_cast<float*>(x), sin_tab, cos_tab, s, h, t, prefix);
+        return check_launch("rope_apply");
+    }
     return dt == HS_F16
                ? launch_generic<f16>(st, x, true, nullptr, nullptr, sin_tab, cos_tab, x, s, t, h, d, prefix, 0.0f)
                : launch_generic<float>(st, x, true, nullptr, nullptr, sin_tab, cos_tab, x, s, t, h, d, prefix, 0.0f);

@@ -213,7 +213,8 @@ def test_split_heads(ctx, dtype, shape):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", [(2, 3, 11, 64, 5, (2, 3)), (2, 4, 21, 64, 5, (4, 4)),
-                                  (1, 2, 23, 64, 17, (2, 3)), (2, 2, 7, 64, 7, (2, 3))])
+                                  (1, 2, 23, 64, 17, (2, 3)), (2, 2, 7, 64, 7, (2, 3)),
+                                  (3, 16, 137, 64, 17, (10, 12))])
 def test_rope_apply(ctx, dtype, case):
     s, h, t, d, prefix, grid = case
     sin, cos = rope.tables(rope.periods(), *grid)
