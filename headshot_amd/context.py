@@ -187,11 +187,13 @@ class HipContext:
         self._launch("copy_rows", self.lib.hs_copy_rows, _dev(src, "src"), src_row,
                      _dev(dst, "dst"), dst_row, n_rows, row_bytes)
 
-    def tiled_add(self, x, table) -> torch.Tensor:
-        """engine/ops.rs:374-389 (f32 only)."""
+    def tiled_add(self, x, table, out=None) -> torch.Tensor:
+        """engine/ops.rs:374-389 (f32 only); ``out`` may be ``x``."""
         assert x.dtype == F32 and table.dtype == F32, "tiled_add is f32"
         assert table.numel() > 0 and x.numel() % table.numel() == 0, "table must tile x"
-        out = self.empty(x.shape)
+        if out is None:
+            out = self.empty(x.shape)
+        assert out.dtype == F32 and out.numel() == x.numel(), "out shape/dtype"
         self._launch("tiled_add", self.lib.hs_tiled_add, _dev(x, "x"), _dev(table, "table"),
                      _dev(out, "out"), x.numel(), table.numel())
         return out

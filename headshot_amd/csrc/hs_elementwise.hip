@@ -240,6 +240,37 @@ __global__ __launch_bounds__(kBlock) void tiled_add_kernel(const float* x, const
         out[i] = x[i] + table[i % block];
 }
 
+// Table-stationary tiled add: thread j owns table vector j (4 floats, kept
+// in registers) and walks its total / block repetitions, two 16-byte loads
+// in flight, so the table is read once and no index needs a modulo. Used
+// when the table is a whole number of 16-byte vectors and large enough to
+// fill the GPU (a pos-embed table: P x 1024 floats); other shapes take the
+// flat kernel.
+__global__ __launch_bounds__(kBlock) void tiled_add_vec_kernel(const float* x,
+                                                               const float* __restrict__ table,
+                                                               float* out, int64_t reps,
+                                                               int64_t block4) {
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+    if (j >= block4) return;  // no barriers below
+    const float4 t = ld_f32x4(table + 4 * j);
+    const int64_t stride = block4 * 4;
+    const float* xp = x + 4 * j;
+    float* op = out + 4 * j;
+    auto add = [&](u32x4 v) {
+        u32x4 o;
+        o[0] = f2u(u2f(v[0]) + t.x), o[1] = f2u(u2f(v[1]) + t.y);
+        o[2] = f2u(u2f(v[2]) + t.z), o[3] = f2u(u2f(v[3]) + t.w);
+        return o;
+    };
+    int64_t r = 0;
+    for (; r + 2 <= reps; r += 2) {
+        const u32x4 a = ld_stream(xp + r * stride), b = ld_stream(xp + (r + 1) * stride);
+        st_stream(op + r * stride, add(a));
+        st_stream(op + (r + 1) * stride, add(b));
+    }
+    if (r < reps) st_stream(op + r * stride, add(ld_stream(xp + r * stride)));
+}
+
 int64_t flat_blocks(int64_t items) {
     const int64_t cap = static_cast<int64_t>(num_cus()) * kBlocksPerCu;
     const int64_t want = ceil_div(items, kBlock);
@@ -383,6 +414,13 @@ hs_status hs_tiled_add(hs_stream_t stream, const float* x, const float* table, f
     if (!x || !table || !out) return fail(HS_EINVAL, "tiled_add: null buffer");
     if (bad_alias(x, out, total * 4)) return fail(HS_EINVAL, "tiled_add: out partially overlaps x");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (block % 4 == 0 && block / 4 >= 65536 && block / 4 < (int64_t{1} << 31) && aligned16(x) &&
+        aligned16(table) && aligned16(out)) {
+        const int64_t block4 = block / 4;
+        tiled_add_vec_kernel<<<dim3(static_cast<uint32_t>(ceil_div(block4, kBlock))), dim3(kBlock), 0,
+                               st>>>(x, table, out, total / block, block4);
+        return check_launch("tiled_add");
+    }
     tiled_add_kernel<<<dim3(static_cast<uint32_t>(flat_blocks(total))), dim3(kBlock), 0, st>>>(
         x, table, out, total, block);
     return check_launch("tiled_add");

@@ -295,6 +295,19 @@ def test_cast_to_f16(ctx):
     assert_bit_exact(back(ctx.cast_to_f16(dev(edge))), edge.astype(np.float16), "cast edges")
 
 
+def test_tiled_add_table_stationary(ctx):
+    """A table of >= 64K 16-byte vectors takes the vector kernel: odd and even
+    repetition counts, and in place."""
+    table = O.normal(84, (65536 * 4 + 8,))
+    for reps in (1, 3, 4):
+        x = O.normal(85 + reps, (reps, table.size))
+        assert_bit_exact(back(ctx.tiled_add(dev(x), dev(table))), O.tiled_add(x, table),
+                         f"tiled_add x{reps}")
+    t = dev(x)
+    ctx.tiled_add(t, dev(table), out=t)
+    assert_bit_exact(back(t), O.tiled_add(x, table), "tiled_add in place")
+
+
 def test_tiled_add_and_copy_rows(ctx):
     x = O.normal(81, (6, 10, 4))
     table = O.normal(82, (10, 4))
