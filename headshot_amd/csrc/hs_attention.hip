@@ -15,8 +15,10 @@
 // straight back as the B operand of O^T += V^T P^T; the V^T operand comes
 // from row-major V in LDS through the gfx950 transposing read
 // ds_read_b64_tr_b16, with the key order matching the order in which the
-// score accumulator holds P^T. The output rescale is skipped when no
-// query's running max changed (the factor would be exactly 1). Workgroups
+// score accumulator holds P^T. The running max is lazy: a query keeps its
+// reference max until a tile's scores exceed it by more than 2^8, so after
+// the first tiles the output rescale (skipped whenever no query's reference
+// moved) almost never runs. Workgroups
 // are ordered XCD-aware: all query tiles of one (frame, head) run on one
 // XCD, so its K/V stream through that XCD's L2.
 //
@@ -52,6 +54,10 @@ constexpr int kBM = 32 * kQB * kWaves;  // queries per workgroup
 #define HS_ATT_BN 64  // keys per tile (a multiple of 32)
 #endif
 constexpr int kBN = HS_ATT_BN;    // keys per tile
+#ifndef HS_ATT_LAZY
+#define HS_ATT_LAZY 8.0f  // running-max slack before a rescale (log2 units)
+#endif
+constexpr float kLazyMax = HS_ATT_LAZY;
 constexpr int kKB = kBN / 32;     // 32-key blocks per tile
 // LDS row pitches (halves) of the K and V tiles, multiples of 8 so rows
 // stay 16-byte aligned. The LDS has 64 4-byte banks and serves a 16-byte
@@ -160,7 +166,13 @@ __device__ __forceinline__ float softmax_tile(const f32x16 (&s)[kKB], float c, f
         for (int r = (kb == 0 ? 1 : 0); r < 16; r += 2)
             mx = r + 1 < 16 ? fmaxf(fmaxf(mx, s[kb][r]), s[kb][r + 1]) : fmaxf(mx, s[kb][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m, mx * c);
+    // Lazy running max: a query keeps its reference value m until a tile's
+    // scores exceed it by more than kLazyMax (log2 units), so most tiles need
+    // no output rescale; the weights exp2(s c - m) then stay below
+    // 2^kLazyMax, exact in f16 to its usual relative precision, and the
+    // final O / l is unchanged mathematically (both use the same m).
+    const float m_cand = fmaxf(m, mx * c);
+    const float m_new = m_cand > m + kLazyMax ? m_cand : m;
     const float corr = __builtin_amdgcn_exp2f(m - m_new);
     // The row sum adds the f16 weights the P.V product uses, two per v_dot2.
     float ps = 0.0f;
