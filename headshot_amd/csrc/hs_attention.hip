@@ -143,6 +143,24 @@ __device__ __forceinline__ void qk_scores(f32x16 (&s)[kQB][kKB], const f16* kbuf
 }
 
 // Keys at or past t score -inf (the partial last tile).
+// The two halves of the wave (lanes l and l ^ 32) exchanged with the gfx950
+// v_permlane32_swap: applied to two copies of v it leaves lane l holding
+// (v[l], v[l + 32]) for l < 32 and (v[l - 32], v[l]) above, so the pair's
+// max or sum needs no select and no LDS round trip (ds_bpermute). Both
+// halves get the same bits.
+__device__ __forceinline__ float halves_max(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                    __builtin_bit_cast(uint32_t, v), false, false);
+    return fmaxf(__builtin_bit_cast(float, static_cast<uint32_t>(r[0])),
+                 __builtin_bit_cast(float, static_cast<uint32_t>(r[1])));
+}
+__device__ __forceinline__ float halves_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, v),
+                                                    __builtin_bit_cast(uint32_t, v), false, false);
+    return __builtin_bit_cast(float, static_cast<uint32_t>(r[0])) +
+           __builtin_bit_cast(float, static_cast<uint32_t>(r[1]));
+}
+
 __device__ __forceinline__ void mask_tail(f32x16 (&s)[kKB], int key0, int t, int hh) {
 #pragma unroll
     for (int kb = 0; kb < kKB; kb++)
@@ -165,7 +183,7 @@ __device__ __forceinline__ float softmax_tile(const f32x16 (&s)[kKB], float c, f
 #pragma unroll
         for (int r = (kb == 0 ? 1 : 0); r < 16; r += 2)
             mx = r + 1 < 16 ? fmaxf(fmaxf(mx, s[kb][r]), s[kb][r + 1]) : fmaxf(mx, s[kb][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    mx = halves_max(mx);
     // Lazy running max: a query keeps its reference value m until a tile's
     // scores exceed it by more than kLazyMax (log2 units), so most tiles need
     // no output rescale; the weights exp2(s c - m) then stay below
@@ -243,7 +261,7 @@ __device__ __forceinline__ void rescale(f32x16& o0, f32x16& o1, float corr) {
 // channel 32 mb + 8 (r / 4) + 4 hh + r % 4 of query n.
 __device__ __forceinline__ void store_out(const f32x16& o0, const f32x16& o1, float l, f16* orow,
                                           int hh) {
-    const float inv = 1.0f / (l + __shfl_xor(l, 32));
+    const float inv = 1.0f / halves_sum(l);
 #pragma unroll
     for (int r4 = 0; r4 < 4; r4++) {
         const int d0 = 8 * r4 + 4 * hh;
