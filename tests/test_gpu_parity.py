@@ -214,12 +214,15 @@ def test_split_heads(ctx, dtype, shape):
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", [(2, 3, 11, 64, 5, (2, 3)), (2, 4, 21, 64, 5, (4, 4)),
                                   (1, 2, 23, 64, 17, (2, 3)), (2, 2, 7, 64, 7, (2, 3)),
-                                  (3, 16, 137, 64, 17, (10, 12))])
+                                  (3, 16, 137, 64, 17, (10, 12)),
+                                  (2, 3, 11, 32, 5, (2, 3))])  # head_dim 32: generic kernel
 def test_rope_apply(ctx, dtype, case):
     s, h, t, d, prefix, grid = case
     sin, cos = rope.tables(rope.periods(), *grid)
     if t - prefix != sin.shape[0]:
         sin, cos = sin[: t - prefix].copy(), cos[: t - prefix].copy()
+    if d != sin.shape[1]:
+        sin, cos = np.ascontiguousarray(sin[:, :d]), np.ascontiguousarray(cos[:, :d])
     x = host(O.normal(41, (s, h, t, d)), dtype)
     g = dev(x)
     ctx.rope_apply(g, dev(sin), dev(cos), prefix)
