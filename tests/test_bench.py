@@ -1,0 +1,53 @@
+"""bench.py's contract on the CPU: the one-GPU rule, the algorithmic byte
+counts its rates divide by, and the kernel names its rocprofv3 summaries
+group by."""
+import json
+import os
+import subprocess
+import sys
+
+import bench
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_more_than_one_gpu_is_refused():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    line = json.loads(r.stdout.strip().splitlines()[-1])
+    assert "one GPU" in line["error"]
+
+
+def test_algorithmic_bytes_per_token():
+    rows, patches = 32 * 1374, 32 * 1369
+    b = bench.op_bytes(rows, 2, patches, 1369)
+    assert b["layernorm"] == rows * 4096             # 2048 R + 2048 W
+    assert b["qknorm_rope"] == rows * 8192           # q and k in one launch
+    assert b["bias_gelu"] == rows * 16384            # hidden 4096, 1R + 1W
+    assert b["bias_ls_residual"] == rows * 6144      # 2R + 1W
+    assert b["assemble"] == patches * 4096 + 1369 * 4096 + rows * 2048
+    per_block = (2 * b["layernorm"] + b["qknorm_rope"] + 2 * b["bias_ls_residual"]
+                 + b["bias_gelu"])
+    assert per_block == rows * 45056
+    # f32 storage doubles every activation term (the f32 patches and table stay)
+    b32 = bench.op_bytes(rows, 4, patches, 1369)
+    assert b32["layernorm"] == 2 * b["layernorm"]
+    assert b32["assemble"] == patches * 4096 + 1369 * 4096 + rows * 4096
+
+
+def test_kernel_names_map_to_ops():
+    names = {
+        "_ZN2hs12_GLOBAL__N_113ln_vec_kernelIDF16_Li2ELi2EEEvPKT_PKfS6_PS2_lf": "layernorm",
+        "_ZN2hs12_GLOBAL__N_114qkn_row_kernelIDF16_Li16ELb1ELb1ELi2EEEvNS0_10QknTensorsIT_EEPKfS6_liif":
+            "qknorm_rope",
+        "_ZN2hs12_GLOBAL__N_114bias_ls_kernelIDF16_Lb1ELi1EEEvPKT_S4_PKfS6_PS2_li":
+            "bias_ls_residual",
+        "_ZN2hs12_GLOBAL__N_116bias_gelu_kernelIDF16_Lb1ELi1EEEvPKT_PKfPS2_li": "bias_gelu",
+        "_ZN2hs12_GLOBAL__N_115assemble_kernelIDF16_fLi4ELi4EEEvPKT0_PKfS6_PKT_S9_PS7_iiiii":
+            "assemble",
+        "_ZN2hs12_GLOBAL__N_116flash_f16_kernelEPKDF16_S2_S2_PDF16_iiiifi": None,
+        "__amd_rocclr_copyBuffer": None,
+    }
+    for name, op in names.items():
+        assert bench.kernel_op(name) == op, name
