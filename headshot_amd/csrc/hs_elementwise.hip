@@ -4,12 +4,14 @@
 //   f32 -> f16 cast        (cast_f32_to_f16.wesl)
 //   tiled add              (tiled_add.wesl)
 //
-// The bias/GELU and LayerScale kernels are column-stationary and persistent:
+// The bias/GELU and LayerScale kernels are column-stationary grid-stride loops:
 // the grid's stride through the flat (rows, cols) tensor is a multiple of
 // cols, so each thread owns the same V consecutive columns (one 16-byte
 // vector) for every row it visits and keeps their bias/gamma in registers.
 // Each thread issues U independent 16-byte loads per tensor before it
-// computes, so a wave keeps U KiB per input stream in flight.
+// computes, so a wave keeps U KiB per input stream in flight. The tiled add
+// is table-stationary the same way for large tables (each thread owns one
+// table vector and walks its repetitions).
 #include "hs_common.hpp"
 
 namespace hs {
