@@ -73,7 +73,6 @@ struct QknRow {
     const float* __restrict__ sin_tab;
     const float* __restrict__ cos_tab;
     T* __restrict__ out;
-    int64_t tokens;
     int seq, prefix, ch, gsub;
     bool upper;
     float eps;
@@ -159,7 +158,7 @@ __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
     Row tl;
     tl.x = ts.x[which], tl.out = ts.out[which];
     tl.sin_tab = sin_tab, tl.cos_tab = cos_tab;
-    tl.tokens = tokens, tl.seq = seq, tl.prefix = prefix, tl.eps = eps;
+    tl.seq = seq, tl.prefix = prefix, tl.eps = eps;
     tl.gsub = lane / G;
     // Channels held by this lane: lower-half pieces hold [piece*V, +V), the
     // mirrored upper-half pieces hold the matching [32 + (G-1-piece)*V, +V).
