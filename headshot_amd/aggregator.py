@@ -87,10 +87,11 @@ def run_block_ops(ctx: HipContext, p: BlockParams, io: BlockIO, s: int, t: int, 
     rec = record or (lambda op: None)
     ctx.layernorm(io.x, *p.ln1, eps=eps, out=io.normed)
     rec("layernorm")
-    if p.qn is not None or rope is not None:
-        ctx.qknorm_rope_pair(io.q_raw, io.k_raw, s, t, heads, head_dim, qn=p.qn, kn=p.kn,
-                             rope=rope, eps=eps, out_q=io.q_head, out_k=io.k_head)
-        rec("qknorm_rope")
+    # always: with neither QK-norm nor RoPE this is the plain split_heads
+    # the reference runs unconditionally (model/block.rs:130-133)
+    ctx.qknorm_rope_pair(io.q_raw, io.k_raw, s, t, heads, head_dim, qn=p.qn, kn=p.kn,
+                         rope=rope, eps=eps, out_q=io.q_head, out_k=io.k_head)
+    rec("qknorm_rope")
     ctx.bias_ls_residual(io.x, io.proj_raw, p.ls1, p.proj_b, out=io.x1)
     rec("bias_ls_residual")
     ctx.layernorm(io.x1, *p.ln2, eps=eps, out=io.normed2)

@@ -36,9 +36,16 @@ def _dt(t: torch.Tensor) -> int:
     raise AssertionError(f"storage must be f32 or f16, got {t.dtype}")
 
 
+# Tensors whose pointers the op being prepared passes to the library; the
+# launch's re-issue thunk keeps them alive (a replayed launch must never
+# write into memory the caching allocator has handed out again).
+_held: list = []
+
+
 def _dev(t: torch.Tensor, what: str) -> int:
     assert t.is_cuda, f"{what} must live in device memory"
     assert t.is_contiguous(), f"{what} must be contiguous"
+    _held.append(t)
     return t.data_ptr()
 
 
@@ -65,9 +72,13 @@ class HipContext:
         self.last_launch = None
 
     def _launch(self, name: str, fn, *args) -> None:
+        held = tuple(_held)
+        _held.clear()
+
         def call():
             _lib.check(fn(torch.cuda.current_stream().cuda_stream, *args), name)
 
+        call.held = held
         call()
         self.last_launch = call
 
@@ -146,6 +157,7 @@ class HipContext:
         assert dim > 0 and x.numel() % dim == 0, "gamma must tile x"
         if out is None:
             out = self.empty_typed(res.shape, x.dtype)
+        assert out.dtype == x.dtype and out.numel() == x.numel(), "out shape/dtype"
         self._launch("residual_ls", self.lib.hs_residual_ls, _dt(x), _dev(res, "res"),
                      _dev(x, "x"), _dev(gamma, "gamma"), _dev(out, "out"), x.numel(), dim)
         return out

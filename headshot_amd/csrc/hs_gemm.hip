@@ -398,7 +398,9 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(
 
 bool fast_shape(hs_dtype dt, int N, int K, const void* x, const void* w, const float* bias,
                 const float* gamma, const void* out, const void* res) {
-    return dt == HS_F16 && N % kBN == 0 && K % kBK == 0 && aligned16(x) && aligned16(w) &&
+    // K == 0 takes the generic kernel (out = bias): the fast path's first
+    // stage would read K-tiles that do not exist
+    return dt == HS_F16 && N % kBN == 0 && K > 0 && K % kBK == 0 && aligned16(x) && aligned16(w) &&
            (!bias || aligned16(bias)) && (!gamma || aligned16(gamma)) && aligned16(out) &&
            (!res || aligned16(res));
 }

@@ -84,7 +84,7 @@ def tables(grid):
     ("config0 f32 S=2", 2, (37, 37), torch.float32, ("frame", "global")),
     ("config1 f16 S=8", 8, (37, 37), torch.float16, ("frame",)),
     ("config2 f16 S=32", 32, (37, 37), torch.float16, ("frame", "global")),
-    ("config4 f32 S=16 21x37", 16, (21, 37), torch.float32, ("frame",)),
+    ("config4 f32 S=16 21x37", 16, (21, 37), torch.float32, ("frame", "global")),
     ("config4 f16 S=16 21x37", 16, (21, 37), torch.float16, ("frame", "global")),
 ])
 def test_block_ops_full_size(ctx, cfg):
@@ -149,12 +149,14 @@ def test_non_square_tables_bit_exact_and_used(ctx):
     assert_bit_exact(got[:, :, :5], np.ascontiguousarray(xs[:, :5].transpose(0, 2, 1, 3)), "prefix")
 
 
-def test_assembly_full_size(ctx):
-    """Config 2's assembly: f32 patches + bias + pos-embed -> f16 tokens, with
-    camera/register variants for frame 0 and the rest; bit-exact."""
-    frames, p, r = 32, 1369, 4
+@pytest.mark.parametrize("frames,p", [(32, 1369), (16, 777)], ids=["config2", "config4"])
+def test_assembly_full_size(ctx, frames, p):
+    """Configs 2 and 4's assembly (37 x 37 and 21 x 37 patches): f32 patches
+    + bias + pos-embed -> f16 tokens, with camera/register variants for frame
+    0 and the rest; bit-exact."""
+    r = 4
     g = torch.Generator(device="cuda:0")
-    g.manual_seed(3)
+    g.manual_seed(3 + p)
     patches = torch.randn(frames * p, DIM, generator=g, device="cuda:0")
     pos = torch.randn(p, DIM, generator=g, device="cuda:0") * 0.02
     pb = torch.randn(DIM, generator=g, device="cuda:0") * 0.02
@@ -163,7 +165,74 @@ def test_assembly_full_size(ctx):
     got = host(ctx.assemble_tokens(patches, frames, p, cam, reg, patch_bias=pb, pos=pos))
     want = O.assemble_tokens(host(patches), host(pb), host(pos), host(cam), host(reg), frames, p,
                              r, np.float16)
-    assert_bit_exact(got, want, "assembly S=32")
+    assert_bit_exact(got, want, f"assembly S={frames} P={p}")
+
+
+def test_assembly_dino_layout_full_size(ctx):
+    """The DINO stage's assembly (model/dino.rs:76-93): per frame [cls,
+    storage x 4, patches + patch-embed bias], one token variant for every
+    frame (n_var 1), f32 in and out, at D=1024 on config 4's 16 frames of
+    21 x 37 = 777 patches; bit-exact."""
+    frames, p, r = 16, 777, 4
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(21)
+    patches = torch.randn(frames * p, DIM, generator=g, device="cuda:0")
+    pb = torch.randn(DIM, generator=g, device="cuda:0") * 0.02
+    cls = torch.randn(1, DIM, generator=g, device="cuda:0")
+    storage = torch.randn(r, DIM, generator=g, device="cuda:0")
+    print(f"[dino assembly: frames={frames} p={p} n_var=1 f32]", flush=True)
+    got = host(ctx.assemble_tokens(patches, frames, p, cls, storage, patch_bias=pb, pos=None,
+                                   out_dtype=torch.float32, n_var=1))
+    want = O.assemble_tokens(host(patches), host(pb), None, host(cls), host(storage), frames, p,
+                             r, np.float32, n_var=1)
+    assert_bit_exact(got, want, "dino assembly S=16 x 777")
+    # every frame carries the same cls and storage rows, then its own patches
+    t = 1 + r + p
+    g3 = got.reshape(frames, t, DIM)
+    assert_bit_exact(g3[:, 0], np.broadcast_to(host(cls), (frames, DIM)), "cls rows")
+    assert_bit_exact(g3[:, 1:1 + r], np.broadcast_to(host(storage), (frames, r, DIM)), "storage")
+
+
+def test_config3_frame_layout_rope(ctx):
+    """Config 3's qk-norm + RoPE2D leg: S=200 frames x 1374 tokens in the
+    frame-block layout (37 x 37 tables, prefix 5), q and k in one launch.
+    Oracle on 4 whole frames (5,496 tokens); at full size RoPE preserves
+    every pair norm of the normalised vectors and the 5 prefix tokens pass
+    through bit-exact."""
+    frames, t, prefix = 200, 1374, 5
+    rows = frames * t
+    g = torch.Generator(device="cuda:0")
+    g.manual_seed(33)
+    q = torch.randn(rows, DIM, generator=g, device="cuda:0").half()
+    k = torch.randn(rows, DIM, generator=g, device="cuda:0").half()
+    qn = (torch.randn(HD, generator=g, device="cuda:0") * 0.02 + 1,
+          torch.randn(HD, generator=g, device="cuda:0") * 0.02)
+    kn = (torch.randn(HD, generator=g, device="cuda:0") * 0.02 + 1,
+          torch.randn(HD, generator=g, device="cuda:0") * 0.02)
+    sin, cos = tables((37, 37))
+    print(f"[config3 frame layout: rows={rows}]", flush=True)
+    qh, kh = ctx.qknorm_rope_pair(q, k, frames, t, HEADS, HD, qn=qn, kn=kn,
+                                  rope=(sin, cos, prefix), eps=1e-6)
+    O.set_num_threads(min(16, os.cpu_count() or 1))
+    for name, src, nrm, got in (("q", q, qn, qh), ("k", k, kn, kh)):
+        for f in (0, 57, 123, 199):
+            x_f = host(src[f * t:(f + 1) * t])
+            want = O.qknorm_rope(x_f, host(nrm[0]), host(nrm[1]), host(sin), host(cos), 1, t,
+                                 HEADS, HD, prefix, 1e-6)
+            gate(host(got[f]), want[0], f"config3 {name} frame {f}")
+    # full size: the same normalisation without RoPE ...
+    qa, ka = ctx.qknorm_rope_pair(q, k, frames, t, HEADS, HD, qn=qn, kn=kn, rope=None, eps=1e-6)
+    for name, rot, plain in (("q", qh, qa), ("k", kh, ka)):
+        r32, p32 = rot.float(), plain.float()
+        nr = torch.hypot(r32[..., :32], r32[..., 32:])
+        np_ = torch.hypot(p32[..., :32], p32[..., 32:])
+        # rotating an f16 pair and rounding each component to f16 again
+        # moves its norm by at most 2^-11 of the norm (half an f16 ulp per
+        # component), plus f32 rounding
+        err = ((nr - np_).abs() / np_.clamp_min(1.0)).max().item()
+        assert err < 1e-3, f"config3 {name} pair norms moved by {err}"
+        assert torch.equal(rot[:, :, :prefix], plain[:, :, :prefix]), f"{name} prefix passthrough"
+        del r32, p32, nr, np_
 
 
 def test_global_block_long_sequence(ctx):
