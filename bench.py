@@ -77,7 +77,7 @@ def parse():
     ap.add_argument("--op-passes", type=int, default=3)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU work for the oracle baseline sample")
     ap.add_argument("--calibrate-copy-mib", type=int, default=512,
                     help="size of one plain torch copy launched before timing (HBM counter "
@@ -126,14 +126,18 @@ class Pass:
         self.fp.run()
 
 
-def per_op_times(bench: Pass, passes: int) -> dict:
+def per_op_times(bench: Pass, passes: int, flush=None) -> dict:
     """Mean kernel duration per op (ms) from HIP event pairs on the launch
     stream. A GPU busy-wait ahead of each pass lets the host enqueue the
     whole pass first, so the kernels run back to back as in the timed loop.
     One untimed pass runs between the busy-wait and the timed one: the first
     kernel after the wait runs slower (the assembly at S=32: 52.1 us against
     49.4 us back to back), and in the timed loop every op, the assembly
-    included, follows other work."""
+    included, follows other work.
+
+    ``flush`` (a callable enqueueing GPU work) runs untimed before every
+    timed launch: with a read of more than the last-level caches hold, no
+    input of the timed op is cache-resident (cold timing)."""
     import torch
 
     pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -146,6 +150,8 @@ def per_op_times(bench: Pass, passes: int) -> dict:
         for _, thunk in bench.seq:
             thunk()
         for (op, thunk), (a, b) in zip(bench.seq, pairs):
+            if flush is not None:
+                flush()
             a.record()
             thunk()
             b.record()
@@ -154,6 +160,35 @@ def per_op_times(bench: Pass, passes: int) -> dict:
             sums[op] += a.elapsed_time(b)
             counts[op] += 1
     return {op: sums[op] / counts[op] for op in OPS}
+
+
+FLUSH_BYTES = 1 << 30  # > the 256 MB Infinity Cache + 8 x 4 MB L2
+
+
+def cache_flusher(device):
+    """A read-only sweep of FLUSH_BYTES: torch.sum over a resident f32 buffer
+    (reads it once, writes one value), so the caches hold only clean lines
+    of that buffer afterwards."""
+    import torch
+
+    buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=device)
+    acc = torch.empty((), dtype=torch.float32, device=device)
+
+    def flush():
+        torch.sum(buf, dim=0, out=acc)
+
+    return flush
+
+
+def op_rates(bench: Pass, mean_ms: dict) -> dict:
+    per_op = {}
+    for op in OPS:
+        us = mean_ms[op] * 1e3
+        gbs = bench.bytes[op] / (us * 1e-6) / 1e9
+        per_op[op] = {"us": round(us, 2), "GB/s": round(gbs, 1),
+                      "frac": round(gbs / PEAK_GBS, 4), "bytes": bench.bytes[op],
+                      "launches_per_pass": bench.launches[op]}
+    return per_op
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix peak
@@ -392,7 +427,7 @@ def cpu_baseline_legs(frames: int) -> dict:
 
     from oracle import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    threads, _ = host_threads()
     O.set_num_threads(threads)
     rng = np.random.default_rng(3)
     t = GRID[0] * GRID[1] + PREFIX
@@ -430,16 +465,135 @@ def cpu_baseline_legs(frames: int) -> dict:
     return out
 
 
-def cpu_baseline(bench: Pass, target_s: float):
-    """Time the oracle (C restatement of the reference's f32-math kernels, run
+def host_threads() -> tuple:
+    """(threads used, cores visible): every core this process may run on
+    (sched_getaffinity), capped by OMP_NUM_THREADS where the host sets it as
+    this process's CPU share."""
+    visible = len(os.sched_getaffinity(0))
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    used = min(visible, int(share)) if share.isdigit() and int(share) > 0 else visible
+    return used, visible
+
+
+def config0_block(ctx, seed: int = 0):
+    """Config 0's workload: one frame block's fused-op sequence at S=2 frames
+    x 1374 tokens x 1024, f32, 37 x 37 RoPE grid, prefix 5, eps 1e-6, with
+    random-init parameters (LN gamma N(1,.02), beta/biases N(0,.02),
+    LayerScale 1e-5) and N(0,1) activations and GEMM outputs."""
+    import torch
+
+    from headshot_amd import rope
+    from headshot_amd.aggregator import BlockIO, BlockParams
+
+    frames, t = 2, GRID[0] * GRID[1] + PREFIX
+    rows = frames * t
+    g = torch.Generator(device=ctx.device)
+    g.manual_seed(seed)
+    n = lambda *sh: torch.randn(sh, generator=g, device=ctx.device)  # noqa: E731
+    io = BlockIO.empty_like_inputs(n(rows, DIM), n(rows, DIM), n(rows, DIM), n(rows, DIM),
+                                   n(rows, HIDDEN), n(rows, DIM))
+    p = BlockParams.random(DIM, HIDDEN, HEAD_DIM, ctx.device, g)
+    sin, cos = rope.tables(rope.periods(), *GRID)
+    tabs = (torch.from_numpy(sin).to(ctx.device), torch.from_numpy(cos).to(ctx.device), PREFIX)
+    return io, p, tabs, frames, t
+
+
+def cpu_baseline(ctx, target_s: float):
+    """The planned CPU baseline: config 0 (one frame block's fused-op
+    sequence, f32, S=2 x 1374 x 1024) through the oracle (the reference's f32
+    WGSL kernels restated in C, run in the reference's unfused dispatch
+    order: layernorm, split_heads + layernorm + rope_apply for q and k,
+    residual_ls, layernorm, gelu, residual_ls), OpenMP over rows on the host
+    cores; median of repeated runs (at least 5, about ``target_s`` seconds).
+    The same block on the GPU (HipContext, the fused ops) is timed beside it
+    on the same inputs."""
+    import numpy as np
+    import torch
+
+    from headshot_amd.aggregator import run_block_ops
+    from oracle import oracle as O
+
+    threads, visible = host_threads()
+    O.set_num_threads(threads)
+    io, p, (sin, cos, prefix), frames, t = config0_block(ctx)
+    rows = frames * t
+    nbytes = rows * 45056 * 2  # per-token algorithmic bytes of a block, f32 storage
+    h = lambda x: x.detach().cpu().numpy()  # noqa: E731
+    P = {k: tuple(h(x) for x in v) if isinstance(v, tuple) else h(v) for k, v in vars(p).items()}
+    x, q, k = h(io.x), h(io.q_raw), h(io.k_raw)
+    proj, fc1, fc2 = h(io.proj_raw), h(io.fc1_raw), h(io.fc2_raw)
+    out = dict(normed=np.empty_like(x), q_head=np.empty_like(q), k_head=np.empty_like(k),
+               x1=np.empty_like(x), normed2=np.empty_like(x), act=np.empty_like(fc1),
+               x_out=np.empty_like(x))
+    hs, hc = h(sin), h(cos)
+
+    def cpu_block():
+        O.block_ops(O.F32, x, *P["ln1"], q, k, *P["qn"], *P["kn"], hs, hc, prefix, proj,
+                    P["proj_b"], P["ls1"], *P["ln2"], fc1, P["fc1_b"], fc2, P["fc2_b"], P["ls2"],
+                    out, frames, t, DIM, HEADS, HIDDEN, EPS)
+
+    cpu_block()  # first touch of the output pages, thread pool start
+    runs = []
+    t_all = time.perf_counter()
+    while len(runs) < 5 or time.perf_counter() - t_all < target_s:
+        t0 = time.perf_counter()
+        cpu_block()
+        runs.append(time.perf_counter() - t0)
+    cpu_s = float(np.median(runs))
+
+    # the GPU, same inputs and op sequence
+    def gpu_block():
+        run_block_ops(ctx, p, io, frames, t, HEADS, HEAD_DIM, rope=(sin, cos, prefix), eps=EPS)
+
+    seq = []
+    run_block_ops(ctx, p, io, frames, t, HEADS, HEAD_DIM, rope=(sin, cos, prefix), eps=EPS,
+                  record=lambda op: seq.append(ctx.last_launch))
+    iters = 200
+    for _ in range(10):
+        gpu_block()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        for thunk in seq:
+            thunk()
+    b.record()
+    torch.cuda.synchronize()
+    gpu_ms = a.elapsed_time(b) / iters
+    gpu_gbs = nbytes / (gpu_ms * 1e-3) / 1e9
+    return {
+        "value": round(nbytes / cpu_s / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"config 0: one frame block's fused-op sequence, f32, S={frames} x {t} x "
+                   f"{DIM}, 37x37 RoPE, prefix {prefix}, through oracle/hs_oracle.c (C "
+                   f"restatement of the reference's f32 WGSL kernels, unfused reference "
+                   f"dispatch order), {threads} OpenMP threads of {visible} visible cores; "
+                   f"median of {len(runs)} runs"),
+        "ms_per_block": round(cpu_s * 1e3, 2),
+        "tokens_per_s": round(rows / cpu_s, 1),
+        "bytes_per_block": nbytes,
+        "runs": len(runs),
+        "cpu_model": cpu_model(),
+        "gpu_same_config": {"ms_per_block": round(gpu_ms, 4), "GB/s": round(gpu_gbs, 1),
+                            "frac": round(gpu_gbs / PEAK_GBS, 4),
+                            "tokens_per_s": round(rows / (gpu_ms * 1e-3), 1),
+                            "timing": f"HIP events over {iters} back-to-back blocks (6 launches "
+                                      f"each, fused ops)"},
+    }
+
+
+def cpu_pass_sample(bench: Pass, target_s: float):
+    """The oracle (C restatement of the reference's f32-math kernels, run
     with the reference's unfused dispatch sequence and f16 storage rounding)
-    on the host cores over a bounded sample of the same pass."""
+    on the host cores over a bounded sample of the benchmarked pass."""
     import numpy as np
     import torch
 
     from oracle import oracle as O
 
-    threads = min(16, os.cpu_count() or 1)
+    threads, _ = host_threads()
     O.set_num_threads(threads)
     dt = O.F16 if bench.dtype == torch.float16 else O.F32
     h = lambda t: t.cpu().numpy()  # noqa: E731
@@ -481,13 +635,9 @@ def cpu_baseline(bench: Pass, target_s: float):
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/hs_oracle.c (C restatement of the reference's WGSL kernels, unfused "
-                   f"reference dispatch order, {'f16' if dt == O.F16 else 'f32'} storage) over "
-                   f"assembly + {blocks_done} of 48 blocks at S={frames}: "
-                   f"{done_bytes / 1e9:.2f} GB algorithmic in {elapsed:.1f} s, "
-                   f"{threads} OpenMP threads"),
-        "ms_per_block": round(elapsed * 1e3 / max(blocks_done, 1), 1),
-        "cpu_model": cpu_model(),
+        "sample": (f"oracle over assembly + {blocks_done} of 48 blocks of the benchmarked pass "
+                   f"at S={frames}, {'f16' if dt == O.F16 else 'f32'} storage: "
+                   f"{done_bytes / 1e9:.2f} GB algorithmic in {elapsed:.1f} s, {threads} threads"),
     }
 
 
@@ -805,15 +955,12 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
 
-    per_op, roofline, ops_ms = {}, None, None
+    per_op, per_op_cold, roofline, ops_ms = {}, None, None, None
     if args.op_passes > 0:
-        mean = per_op_times(bench, args.op_passes)
-        for op in OPS:
-            us = mean[op] * 1e3
-            gbs = bench.bytes[op] / (us * 1e-6) / 1e9
-            per_op[op] = {"us": round(us, 2), "GB/s": round(gbs, 1),
-                          "frac": round(gbs / PEAK_GBS, 4), "bytes": bench.bytes[op],
-                          "launches_per_pass": bench.launches[op]}
+        per_op = op_rates(bench, per_op_times(bench, args.op_passes))
+        flush = cache_flusher(ctx.device)
+        per_op_cold = op_rates(bench, per_op_times(bench, args.op_passes, flush=flush))
+        del flush
         ops_ms = round(sum(per_op[op]["us"] * bench.launches[op] for op in OPS) / 1e3, 3)
         dominant = max(OPS, key=lambda op: per_op[op]["us"] * bench.launches[op])
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": per_op[dominant]["GB/s"],
@@ -849,6 +996,7 @@ def main():
         "tokens_per_s": round(bench.rows / (ms * 1e-3), 1),
         "ops_ms_per_step": ops_ms,
         "ops": per_op,
+        "ops_cold": per_op_cold,
         "roofline": roofline,
     }
     if args.attention_iters > 0:
@@ -860,9 +1008,11 @@ def main():
         if trunk_iters > 0:
             line["trunk"] = trunk_times(ctx, args.frames, trunk_iters)
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(bench, args.cpu_seconds)
+        line["cpu_baseline"] = cpu_baseline(ctx, args.cpu_seconds)
+        legs = {"pass_sample": cpu_pass_sample(bench, args.cpu_seconds / 2)}
         if args.attention_iters > 0:
-            line["cpu_baseline_legs"] = cpu_baseline_legs(args.frames)
+            legs.update(cpu_baseline_legs(args.frames))
+        line["cpu_baseline_legs"] = legs
     print(json.dumps(line), flush=True)
 
 

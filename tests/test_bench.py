@@ -51,3 +51,13 @@ def test_kernel_names_map_to_ops():
     }
     for name, op in names.items():
         assert bench.kernel_op(name) == op, name
+
+
+def test_host_threads_uses_the_visible_cores_within_the_share(monkeypatch):
+    visible = len(os.sched_getaffinity(0))
+    monkeypatch.delenv("OMP_NUM_THREADS", raising=False)
+    assert bench.host_threads() == (visible, visible)
+    monkeypatch.setenv("OMP_NUM_THREADS", "1")
+    assert bench.host_threads() == (1, visible)
+    monkeypatch.setenv("OMP_NUM_THREADS", str(visible + 100))
+    assert bench.host_threads() == (visible, visible)
