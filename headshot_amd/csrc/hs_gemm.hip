@@ -14,8 +14,8 @@
 // Fast path (f16, N % kBN == 0, K % kBK == 0): matrix-core GEMM. A workgroup
 // of kWaves waves computes a 256 (rows) x kBN (columns) tile of out, K in
 // steps of kBK staged through LDS (double-buffered; the next step's tiles go straight
-// from global memory into LDS with global_load_lds_dwordx4 while the current
-// one computes, with no registers in between). Both operands are K-contiguous
+// from global memory into LDS with buffer_load_dwordx4 ... lds while the
+// current one computes, with no registers in between). Both operands are K-contiguous
 // rows (x rows, w rows), which is exactly the operand layout of
 // v_mfma_f32_32x32x16_f16, so both come from LDS with 16-byte reads. Each
 // wave owns 128 rows x 64 columns and computes the transposed tile
@@ -89,16 +89,23 @@ constexpr int kBK = HS_GEMM_BK;
 constexpr int kRowChunks = kBK / 8;      // 16-byte chunks per LDS row
 constexpr int kRowsPerInstr = 64 / kRowChunks;
 constexpr int kRowsPer256B = 128 / kBK;  // LDS rows per 64-bank period
-// Stages are filled with global_load_lds_dwordx4: one wave instruction puts
-// its 64 lanes' 16-byte chunks into 1 KiB of LDS in lane order, i.e.
-// kRowsPerInstr unpadded rows. Lane L of instruction j supplies row
-// kRowsPerInstr * j + L / kRowChunks at physical chunk L % kRowChunks, which
-// holds logical chunk (L % kRowChunks) ^ swz(row), swz(row) = (row /
+// Stages are filled by buffer_load_dwordx4 ... lds (LDS-DMA): one wave
+// instruction puts its 64 lanes' 16-byte chunks into 1 KiB of LDS in lane
+// order, i.e. kRowsPerInstr unpadded rows. Lane L of instruction j supplies
+// row kRowsPerInstr * j + L / kRowChunks at physical chunk L % kRowChunks,
+// which holds logical chunk (L % kRowChunks) ^ swz(row), swz(row) = (row /
 // kRowsPer256B) % kRowChunks: with that XOR swizzle the operand reads (16
 // consecutive rows, one logical chunk) hit 16 distinct 16-byte bank groups.
+// The buffer form (a descriptor in scalar registers, a per-lane offset fixed
+// for the tile, the stage's column in the scalar offset) costs no vector
+// instruction per load, and unlike the global (FLAT-encoded) form it lets
+// the compiler wait for the operand reads of one k-slice with lgkmcnt(n)
+// while the next slice's reads are in flight.
 constexpr int kXInstr = kBM * kBK / 8 / 64;  // wave instructions per x stage
 constexpr int kWInstr = kBN * kBK / 8 / 64;  // per w stage
+constexpr int kLoads = kXInstr / kWaves + kWInstr / kWaves;  // per wave and stage
 static_assert(kXInstr % kWaves == 0 && kWInstr % kWaves == 0, "stage split");
+static_assert((kBK / 16) % 2 == 0, "operand register sets alternate within a stage");
 
 struct GemmSmem {
     f16 x[2][kBM * kBK];
@@ -118,30 +125,49 @@ typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ int swz(int row) { return (row / kRowsPer256B) % kRowChunks; }
 
-// Issues this wave's direct-to-LDS loads of one stage (x rows past M read
-// row M - 1; their outputs are masked).
-__device__ __forceinline__ void issue_stage(GemmSmem& sm, int buf, const f16* x, const f16* w,
-                                            int64_t m0, int64_t n0, int M, int K, int k0,
-                                            int wave, int lane) {
+// Per-lane byte offsets of this wave's stage loads within the tile's x and
+// w row blocks; x rows past M read row M - 1 (their outputs are masked).
+struct StageOffsets {
+    uint32_t x[kXInstr / kWaves];
+    uint32_t w[kWInstr / kWaves];
+};
+
+__device__ __forceinline__ StageOffsets stage_offsets(int64_t m0, int M, int K, int wave,
+                                                     int lane) {
+    StageOffsets o;
     const int prow = lane / kRowChunks, pc = lane % kRowChunks;
 #pragma unroll
     for (int i = 0; i < kXInstr / kWaves; i++) {
-        const int j = wave + kWaves * i;
-        const int row = kRowsPerInstr * j + prow;
-        const int64_t grow = min(m0 + row, static_cast<int64_t>(M) - 1);
-        const int c = pc ^ swz(row);
-        __builtin_amdgcn_global_load_lds(x + grow * K + k0 + 8 * c,
-                                         (lds_void*)(&sm.x[buf][j * 512]), 16, 0, 0);
+        const int row = kRowsPerInstr * (wave + kWaves * i) + prow;
+        const int lrow = static_cast<int>(min(m0 + row, static_cast<int64_t>(M) - 1) - m0);
+        o.x[i] = static_cast<uint32_t>(lrow * K * 2 + 16 * (pc ^ swz(row)));
     }
 #pragma unroll
     for (int i = 0; i < kWInstr / kWaves; i++) {
-        const int j = wave + kWaves * i;
-        const int row = kRowsPerInstr * j + prow;
-        const int c = pc ^ swz(row);
-        __builtin_amdgcn_global_load_lds(w + (n0 + row) * K + k0 + 8 * c,
-                                         (lds_void*)(&sm.w[buf][j * 512]), 16, 0, 0);
+        const int row = kRowsPerInstr * (wave + kWaves * i) + prow;
+        o.w[i] = static_cast<uint32_t>(row * K * 2 + 16 * (pc ^ swz(row)));
     }
+    return o;
 }
+
+// Issues this wave's LDS-DMA loads of one stage from the buffer resources
+// covering the tile's x and w rows; koff = the stage's first column, in
+// bytes.
+__device__ __forceinline__ void issue_stage(GemmSmem& sm, int buf, __amdgpu_buffer_rsrc_t xr,
+                                            __amdgpu_buffer_rsrc_t wr, int koff,
+                                            const StageOffsets& o, int wave) {
+#pragma unroll
+    for (int i = 0; i < kXInstr / kWaves; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            xr, (lds_void*)(&sm.x[buf][(wave + kWaves * i) * 512]), 16, o.x[i], koff, 0, 0);
+#pragma unroll
+    for (int i = 0; i < kWInstr / kWaves; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            wr, (lds_void*)(&sm.w[buf][(wave + kWaves * i) * 512]), 16, o.w[i], koff, 0, 0);
+}
+
+// Buffer descriptor word 3 for raw (unstructured, stride 0) buffers on gfx950.
+constexpr int kRawBufferFlags = 0x00020000;
 
 // Operand read: logical chunk k of LDS row `row` (rows of kBK halves).
 __device__ __forceinline__ h8 ld_op(const f16* buf, int row, int k) {
@@ -253,31 +279,63 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
         for (int b = 0; b < 4; b++) acc[a][b] = f32x16{};
 
     const int nsteps = K / kBK;
-    issue_stage(sm, 0, x, w, m0, n0, M, K, 0, wave, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    const int wv = wave_in_block();
+    const StageOffsets so = stage_offsets(m0, M, K, wv, lane);
+    const int xrows = static_cast<int>(min(static_cast<int64_t>(kBM), M - m0));
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16*>(x + m0 * K), 0, xrows * K * 2, kRawBufferFlags);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<f16*>(w + n0 * K), 0, kBN * K * 2, kRawBufferFlags);
+    // Both buffers start filled (stages 0 and 1). The waits below are
+    // explicit: vmcnt counts this wave's LDS-DMA loads, which complete in
+    // order, and the barrier then covers every wave's.
+    issue_stage(sm, 0, xr, wr, 0, so, wv);
+    if (nsteps > 1) {
+        issue_stage(sm, 1, xr, wr, 2 * kBK, so, wv);
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kLoads) : "memory");
+    } else {
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    // Operand registers in two sets: the next 16-wide k slice is read from
+    // LDS while the current one multiplies, across stage boundaries too.
+    h8 A[2][2], B[2][4];
+#pragma unroll
+    for (int a = 0; a < 2; a++) A[0][a] = ld_op(sm.w[0], wn + 32 * a + l32, hh);
+#pragma unroll
+    for (int b = 0; b < 4; b++) B[0][b] = ld_op(sm.x[0], wm + 32 * b + l32, hh);
     for (int s = 0; s < nsteps; s++) {
         const int cur = s & 1;
-        // the other buffer was last read in step s - 1, closed by its barrier
-        if (s + 1 < nsteps) issue_stage(sm, cur ^ 1, x, w, m0, n0, M, K, (s + 1) * kBK, wave, lane);
 #pragma unroll
         for (int ks = 0; ks < kBK / 16; ks++) {
-            const int kc = 2 * ks + hh;
-            h8 A[2], B[4];
+            const int p = ks & 1;  // kBK / 16 is even: set 0 holds slice 0 of every stage
+            if (ks + 1 < kBK / 16) {
+                const int kc = 2 * (ks + 1) + hh;
 #pragma unroll
-            for (int a = 0; a < 2; a++) A[a] = ld_op(sm.w[cur], wn + 32 * a + l32, kc);
+                for (int a = 0; a < 2; a++) A[p ^ 1][a] = ld_op(sm.w[cur], wn + 32 * a + l32, kc);
 #pragma unroll
-            for (int b = 0; b < 4; b++) B[b] = ld_op(sm.x[cur], wm + 32 * b + l32, kc);
+                for (int b = 0; b < 4; b++) B[p ^ 1][b] = ld_op(sm.x[cur], wm + 32 * b + l32, kc);
+            } else {
+                // every wave's reads of stage s are done and stage s + 1
+                // (the only load in flight) has landed
+                asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                // buffer cur is free: refill it with stage s + 2
+                if (s + 2 < nsteps) issue_stage(sm, cur, xr, wr, 2 * (s + 2) * kBK, so, wv);
+                if (s + 1 < nsteps) {
+#pragma unroll
+                    for (int a = 0; a < 2; a++) A[p ^ 1][a] = ld_op(sm.w[cur ^ 1], wn + 32 * a + l32, hh);
+#pragma unroll
+                    for (int b = 0; b < 4; b++) B[p ^ 1][b] = ld_op(sm.x[cur ^ 1], wm + 32 * b + l32, hh);
+                }
+            }
 #pragma unroll
             for (int a = 0; a < 2; a++)
 #pragma unroll
                 for (int b = 0; b < 4; b++)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[a], B[b], acc[a][b], 0, 0, 0);
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[p][a], B[p][b], acc[a][b], 0, 0, 0);
+            // keep the reads above ahead of these multiplies
+            __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // LDS reads
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // MFMAs
         }
-        // the next stage's loads have landed in LDS (this wave's), then
-        // every wave's (barrier)
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
     }
 
     // Epilogue, in two phases so that global memory sees whole rows.
@@ -400,7 +458,8 @@ bool fast_shape(hs_dtype dt, int N, int K, const void* x, const void* w, const f
                 const float* gamma, const void* out, const void* res) {
     // K == 0 takes the generic kernel (out = bias): the fast path's first
     // stage would read K-tiles that do not exist
-    return dt == HS_F16 && N % kBN == 0 && K > 0 && K % kBK == 0 && aligned16(x) && aligned16(w) &&
+    // K <= 2^20 keeps a tile's byte offsets (256 rows x K x 2) in 32 bits
+    return dt == HS_F16 && N % kBN == 0 && K > 0 && K % kBK == 0 && K <= (1 << 20) && aligned16(x) && aligned16(w) &&
            (!bias || aligned16(bias)) && (!gamma || aligned16(gamma)) && aligned16(out) &&
            (!res || aligned16(res));
 }
