@@ -158,6 +158,14 @@ fn i32_of(v: usize, what: &str) -> i32 {
     i32::try_from(v).unwrap_or_else(|_| panic!("{what} {v} exceeds i32"))
 }
 
+/// A linear layer with the LayerNorm before it folded in
+/// ([`HipContext::fold_layernorm`]).
+pub struct FoldedLinear {
+    pub w_fold: HipTensor,
+    pub colsum: HipTensor,
+    pub shift: HipTensor,
+}
+
 /// One device's op surface on one HIP stream.
 pub struct HipContext {
     stream: ffi::HsStream,
@@ -584,6 +592,101 @@ impl HipContext {
                                      i32_of(s, "S"), i32_of(t, "T"), i32_of(h, "H"),
                                      i32_of(d, "d"), i32_of(k, "k"), prefix, eps)
         }, "linear_qkv_heads");
+        let [q, kk, v] = outs;
+        (q, kk, v)
+    }
+
+    /// The statistics half of `layernorm`: (rows, 2) f32 mean and
+    /// rsqrt(var + eps) per row.
+    pub fn layernorm_stats(&self, x: &HipTensor, eps: f32) -> HipTensor {
+        let (rows, dim) = x.dims();
+        let out = self.empty(&[rows, 2]);
+        check(unsafe {
+            ffi::hs_layernorm_stats(self.stream, x.dtype.raw(), x.cptr(), out.mptr() as *mut f32,
+                                    rows as i64, i32_of(dim, "dim"), eps)
+        }, "layernorm_stats");
+        out
+    }
+
+    /// Folds a LayerNorm (norm weight and bias) into the linear layer after
+    /// it, once at load time.
+    pub fn fold_layernorm(&self, weight: &HipTensor, bias: Option<&HipTensor>,
+                          ln_w: &HipTensor, ln_b: &HipTensor) -> FoldedLinear {
+        let (n, k) = weight.dims();
+        let w_fold = self.empty_typed(&weight.shape, weight.dtype);
+        let colsum = self.empty(&[n]);
+        let shift = self.empty(&[n]);
+        check(unsafe {
+            ffi::hs_fold_layernorm(self.stream, weight.dtype.raw(), weight.cptr(),
+                                   opt_f32(bias, n, "bias"), opt_f32(Some(ln_w), k, "norm weight"),
+                                   opt_f32(Some(ln_b), k, "norm bias"), w_fold.mptr(),
+                                   colsum.mptr() as *mut f32, shift.mptr() as *mut f32,
+                                   i32_of(n, "n"), i32_of(k, "k"))
+        }, "fold_layernorm");
+        FoldedLinear { w_fold, colsum, shift }
+    }
+
+    fn folded(&self, x: &HipTensor, f: &FoldedLinear) -> (usize, usize, usize, HipTensor) {
+        let (m, k) = x.dims();
+        let (n, wk) = f.w_fold.dims();
+        assert_eq!(wk, k, "folded weight k");
+        assert_eq!(f.w_fold.dtype, x.dtype, "folded weight dtype");
+        assert_eq!(f.colsum.len(), n, "colsum length");
+        assert_eq!(f.shift.len(), n, "shift length");
+        (m, n, k, self.empty(&[m, 2]))
+    }
+
+    /// linear(layernorm(x)) on folded weights (model/block.rs:128-131).
+    pub fn linear_ln(&self, x: &HipTensor, f: &FoldedLinear, eps: f32) -> HipTensor {
+        let (m, n, k, ws) = self.folded(x, f);
+        let out = self.empty_typed(&[m, n], x.dtype);
+        check(unsafe {
+            ffi::hs_linear_ln(self.stream, x.dtype.raw(), x.cptr(), f.w_fold.cptr(),
+                              f.colsum.f32p("colsum"), f.shift.f32p("shift"),
+                              ws.mptr() as *mut f32, out.mptr(), m as i64, i32_of(n, "n"),
+                              i32_of(k, "k"), eps)
+        }, "linear_ln");
+        out
+    }
+
+    /// gelu(linear(layernorm(x))) on folded weights (LN2, fc1, GELU).
+    pub fn linear_ln_gelu(&self, x: &HipTensor, f: &FoldedLinear, eps: f32) -> HipTensor {
+        let (m, n, k, ws) = self.folded(x, f);
+        let out = self.empty_typed(&[m, n], x.dtype);
+        check(unsafe {
+            ffi::hs_linear_ln_gelu(self.stream, x.dtype.raw(), x.cptr(), f.w_fold.cptr(),
+                                   f.colsum.f32p("colsum"), f.shift.f32p("shift"),
+                                   ws.mptr() as *mut f32, out.mptr(), m as i64, i32_of(n, "n"),
+                                   i32_of(k, "k"), eps)
+        }, "linear_ln_gelu");
+        out
+    }
+
+    /// LN1 + the q|k|v projection with heads, QK-norm and RoPE
+    /// (model/block.rs:128-146) on the folded q|k|v weight.
+    #[allow(clippy::too_many_arguments)]
+    pub fn linear_ln_qkv_heads(&self, x: &HipTensor, f: &FoldedLinear, s: usize, t: usize,
+                               h: usize, norms: Option<[(&HipTensor, &HipTensor); 2]>,
+                               rope: Option<Rope>, eps: f32) -> (HipTensor, HipTensor, HipTensor) {
+        let (m, n3, k, ws) = self.folded(x, f);
+        assert_eq!(m, s * t, "x rows must be S*T");
+        assert_eq!(n3 % (3 * h), 0, "w_fold rows must be 3 * H * d");
+        let d = n3 / (3 * h);
+        let mut p = [ptr::null::<f32>(); 4];
+        if let Some([(qw, qb), (kw, kb)]) = norms {
+            p = [opt_f32(Some(qw), d, "q-norm weight"), opt_f32(Some(qb), d, "q-norm bias"),
+                 opt_f32(Some(kw), d, "k-norm weight"), opt_f32(Some(kb), d, "k-norm bias")];
+        }
+        let (sn, cs, prefix) = rope_ptrs(rope.as_ref(), t, d);
+        let outs = [0, 1, 2].map(|_| self.empty_typed(&[s, h, t, d], x.dtype));
+        check(unsafe {
+            ffi::hs_linear_ln_qkv_heads(self.stream, x.dtype.raw(), x.cptr(), f.w_fold.cptr(),
+                                        f.colsum.f32p("colsum"), f.shift.f32p("shift"), p[0],
+                                        p[1], p[2], p[3], sn, cs, ws.mptr() as *mut f32,
+                                        outs[0].mptr(), outs[1].mptr(), outs[2].mptr(),
+                                        i32_of(s, "S"), i32_of(t, "T"), i32_of(h, "H"),
+                                        i32_of(d, "d"), i32_of(k, "k"), prefix, eps)
+        }, "linear_ln_qkv_heads");
         let [q, kk, v] = outs;
         (q, kk, v)
     }

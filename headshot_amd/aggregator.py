@@ -18,7 +18,7 @@ from dataclasses import dataclass
 import torch
 
 from . import rope as _rope
-from .context import HipContext
+from .context import FoldedLinear, HipContext
 
 DIM, HEADS, HEAD_DIM, HIDDEN = 1024, 16, 64, 4096
 
@@ -210,6 +210,17 @@ class BlockWeights:
     proj_w: torch.Tensor  # (dim, dim)
     fc1_w: torch.Tensor   # (hidden, dim)
     fc2_w: torch.Tensor   # (dim, hidden)
+    # LN1 folded into the q|k|v projection, LN2 into fc1 (fold_layernorms)
+    qkv_fold: FoldedLinear | None = None
+    fc1_fold: FoldedLinear | None = None
+
+    def fold_layernorms(self, ctx: HipContext) -> "BlockWeights":
+        """Prepares the LayerNorm-prologue path of ``block_forward`` once at
+        load time: LN1's affine parameters folded into the q|k|v weight and
+        bias, LN2's into fc1's (HipContext.fold_layernorm)."""
+        self.qkv_fold = ctx.fold_layernorm(self.qkv_w, self.qkv_b, *self.p.ln1)
+        self.fc1_fold = ctx.fold_layernorm(self.fc1_w, self.p.fc1_b, *self.p.ln2)
+        return self
 
     def _third(self, t, i):
         dim = self.qkv_w.shape[1]
@@ -265,21 +276,38 @@ class BlockWeights:
 
 
 def block_forward(ctx: HipContext, wts: BlockWeights, x, s: int, t: int, heads: int = HEADS,
-                  rope=None, eps: float = 1e-6):
+                  rope=None, eps: float = 1e-6, fold_ln2: bool = False, fold_ln1: bool = False):
     """Block::forward (model/block.rs:118-193) with every op on HIP and the
     epilogues fused: LN1 -> the q|k|v linear with split_heads, QK-norm and
     RoPE in its epilogue -> attention written token-major -> proj +
     LayerScale + residual -> LN2 -> fc1 + GELU -> fc2 + LayerScale +
     residual (7 launches). ``rope`` = (sin, cos, prefix) or None (global
-    blocks). Returns the block output (S*T, dim)."""
+    blocks). With the weights prepared by ``BlockWeights.fold_layernorms``,
+    ``fold_ln2`` folds LN2 into fc1 and ``fold_ln1`` LN1 into the q|k|v
+    projection: a row-statistics pass replaces the LayerNorm pass and the
+    normalised activation never reaches memory. Folding LN2 stays within the
+    f16 gate of the reference's sequence; folding LN1 rounds the q|k|v
+    product at another point than the reference, which QK-norm magnifies
+    beyond that gate for a few q and k values in 10^4 (as accurate against
+    float64 math as the reference's own sequence), so it is opt-in.
+    Returns the block output (S*T, dim)."""
     p = wts.p
-    normed = ctx.layernorm(x, *p.ln1, eps=eps)
-    q, k, v = ctx.linear_qkv_heads(normed, wts.qkv_w, wts.qkv_b, s, t, heads, qn=p.qn, kn=p.kn,
-                                   rope=rope, eps=eps)
+    if fold_ln1 or fold_ln2:
+        assert wts.qkv_fold is not None and wts.fc1_fold is not None, "fold_layernorms first"
+    if fold_ln1:
+        q, k, v = ctx.linear_ln_qkv_heads(x, wts.qkv_fold, s, t, heads, qn=p.qn, kn=p.kn,
+                                          rope=rope, eps=eps)
+    else:
+        normed = ctx.layernorm(x, *p.ln1, eps=eps)
+        q, k, v = ctx.linear_qkv_heads(normed, wts.qkv_w, wts.qkv_b, s, t, heads, qn=p.qn,
+                                       kn=p.kn, rope=rope, eps=eps)
     attn = ctx.attention_merged(q, k, v)
     x1 = ctx.linear_ls_residual(attn, wts.proj_w, p.ls1, x, p.proj_b)
-    normed2 = ctx.layernorm(x1, *p.ln2, eps=eps)
-    act = ctx.linear_gelu(normed2, wts.fc1_w, p.fc1_b)
+    if fold_ln2:
+        act = ctx.linear_ln_gelu(x1, wts.fc1_fold, eps=eps)
+    else:
+        normed2 = ctx.layernorm(x1, *p.ln2, eps=eps)
+        act = ctx.linear_gelu(normed2, wts.fc1_w, p.fc1_b)
     return ctx.linear_ls_residual(act, wts.fc2_w, p.ls2, x1, p.fc2_b)
 
 

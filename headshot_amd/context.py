@@ -18,6 +18,7 @@ stream (for launch loops and graph capture without per-call Python checks).
 from __future__ import annotations
 
 import math
+from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -57,6 +58,16 @@ def _param(t, n: int, what: str) -> int:
 
 def _opt(t, n: int, what: str):
     return None if t is None else _param(t, n, what)
+
+
+@dataclass
+class FoldedLinear:
+    """A linear layer with the LayerNorm before it folded in
+    (``HipContext.fold_layernorm``): ``w_fold`` (n, k) in the storage dtype,
+    ``colsum`` and ``shift`` (n) f32."""
+    w_fold: torch.Tensor
+    colsum: torch.Tensor
+    shift: torch.Tensor
 
 
 class HipContext:
@@ -365,6 +376,100 @@ class HipContext:
             assert o.dtype == x.dtype and o.numel() == s * t * hd, "out shape/dtype"
         self._launch("linear_qkv_heads", self.lib.hs_linear_qkv_heads, _dt(x), _dev(x, "x"),
                      _dev(w_qkv, "w_qkv"), b, qw, qb, kw, kb, sn, cs, _dev(out[0], "q out"),
+                     _dev(out[1], "k out"), _dev(out[2], "v out"), s, t, h, d, k, prefix, eps)
+        return tuple(out)
+
+    def layernorm_stats(self, x, eps: float = 1e-5, out=None) -> torch.Tensor:
+        """The statistics half of ``layernorm`` (engine/ops.rs:130-153): (rows,
+        2) f32 holding each row's mean and rsqrt(var + eps), bit-identical to
+        what ``layernorm`` normalises with."""
+        dim = x.shape[-1]
+        rows = x.numel() // dim if dim else 0
+        if out is None:
+            out = self.empty_typed((rows, 2), F32)
+        assert out.dtype == F32 and out.numel() == 2 * rows, "out shape/dtype"
+        self._launch("layernorm_stats", self.lib.hs_layernorm_stats, _dt(x), _dev(x, "x"),
+                     _dev(out, "stats"), rows, dim, eps)
+        return out
+
+    def fold_layernorm(self, weight, bias, ln_w, ln_b) -> FoldedLinear:
+        """Folds the LayerNorm (``ln_w``, ``ln_b``) that feeds a linear layer
+        (``weight`` (n, k), ``bias`` (n) or None) into it, once at load time;
+        ``linear_ln*`` then compute linear(layernorm(x)) from raw x."""
+        n, k = weight.shape
+        b = _opt(bias, n, "bias")
+        w_fold = torch.empty_like(weight)
+        colsum = self.empty_typed((n,), F32)
+        shift = self.empty_typed((n,), F32)
+        self._launch("fold_layernorm", self.lib.hs_fold_layernorm, _dt(weight),
+                     _dev(weight, "weight"), b, _param(ln_w, k, "norm weight"),
+                     _param(ln_b, k, "norm bias"), _dev(w_fold, "w_fold"), _dev(colsum, "colsum"),
+                     _dev(shift, "shift"), n, k)
+        return FoldedLinear(w_fold, colsum, shift)
+
+    def _folded_args(self, x, folded: FoldedLinear, workspace):
+        k = x.shape[-1]
+        m = x.numel() // k if k else 0
+        w = folded.w_fold
+        assert w.dim() == 2 and w.shape[1] == k, "weight k mismatch"
+        assert w.dtype == x.dtype, "weight/activation dtype"
+        n = w.shape[0]
+        if workspace is None:
+            workspace = self.empty_typed((m, 2), F32)
+        assert workspace.dtype == F32 and workspace.numel() >= 2 * m, "workspace shape/dtype"
+        return m, n, k, (_dev(w, "w_fold"), _param(folded.colsum, n, "colsum"),
+                         _param(folded.shift, n, "shift"), _dev(workspace, "workspace"))
+
+    def linear_ln(self, x, folded: FoldedLinear, eps: float = 1e-5, out=None,
+                  workspace=None) -> torch.Tensor:
+        """linear(layernorm(x)) (model/block.rs:128-131) on folded weights,
+        without materialising the normalised activation."""
+        m, n, k, (w, cs, sh, ws) = self._folded_args(x, folded, workspace)
+        if out is None:
+            out = self.empty_typed((m, n), x.dtype)
+        assert out.dtype == x.dtype and out.numel() == m * n, "out shape/dtype"
+        self._launch("linear_ln", self.lib.hs_linear_ln, _dt(x), _dev(x, "x"), w, cs, sh, ws,
+                     _dev(out, "out"), m, n, k, eps)
+        return out
+
+    def linear_ln_gelu(self, x, folded: FoldedLinear, eps: float = 1e-5, out=None,
+                       workspace=None) -> torch.Tensor:
+        """gelu(linear(layernorm(x))) (model/block.rs:153, 172-176: LN2, fc1,
+        GELU) in one product on folded weights."""
+        m, n, k, (w, cs, sh, ws) = self._folded_args(x, folded, workspace)
+        if out is None:
+            out = self.empty_typed((m, n), x.dtype)
+        assert out.dtype == x.dtype and out.numel() == m * n, "out shape/dtype"
+        self._launch("linear_ln_gelu", self.lib.hs_linear_ln_gelu, _dt(x), _dev(x, "x"), w, cs,
+                     sh, ws, _dev(out, "out"), m, n, k, eps)
+        return out
+
+    def linear_ln_qkv_heads(self, x, folded: FoldedLinear, s: int, t: int, h: int, qn=None,
+                            kn=None, rope=None, eps: float = 1e-5, out=None, workspace=None):
+        """LN1 + the q|k|v projection with split_heads, QK-norm and RoPE
+        (model/block.rs:128-146) on the folded q|k|v weight: returns
+        head-major (q, k, v). ``eps`` serves both norms."""
+        m, n3, k, (w, cs, sh, ws) = self._folded_args(x, folded, workspace)
+        assert m == s * t, "x rows must be S*T"
+        assert n3 % (3 * h) == 0, "w_fold rows must be 3 * H * d"
+        d = n3 // (3 * h)
+        qw = qb = kw = kb = sn = cs_ = None
+        prefix = 0
+        if qn is not None:
+            qw, qb = _param(qn[0], d, "q-norm weight"), _param(qn[1], d, "q-norm bias")
+        if kn is not None:
+            kw, kb = _param(kn[0], d, "k-norm weight"), _param(kn[1], d, "k-norm bias")
+        if rope is not None:
+            sin, cos, prefix = rope
+            assert 0 <= prefix <= t, "prefix"
+            sn = _param(sin, (t - prefix) * d, "rope sin table")
+            cs_ = _param(cos, (t - prefix) * d, "rope cos table")
+        if out is None:
+            out = tuple(self.empty_typed((s, h, t, d), x.dtype) for _ in range(3))
+        for o in out:
+            assert o.dtype == x.dtype and o.numel() == s * t * h * d, "out shape/dtype"
+        self._launch("linear_ln_qkv_heads", self.lib.hs_linear_ln_qkv_heads, _dt(x),
+                     _dev(x, "x"), w, cs, sh, qw, qb, kw, kb, sn, cs_, ws, _dev(out[0], "q out"),
                      _dev(out[1], "k out"), _dev(out[2], "v out"), s, t, h, d, k, prefix, eps)
         return tuple(out)
 

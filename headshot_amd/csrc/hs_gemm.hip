@@ -52,6 +52,14 @@ struct QkvArgs {
     float eps;
 };
 
+// The LayerNorm folded into the product (hs_linear_ln*): stats holds each x
+// row's (mean, rsqrt(var + eps)), colsum each output column's sum of the
+// folded weight; the bias argument carries the folded shift.
+struct LnArgs {
+    const float* stats;
+    const float* colsum;
+};
+
 // Exact-erf GELU in the A&S 7.1.26 form used by the elementwise GELU kernel
 // (gelu.wesl:18-38 with the 1/sqrt(2) folded into the constants).
 __device__ __forceinline__ float gelu_erf(float v) {
@@ -242,11 +250,11 @@ __device__ __forceinline__ void qkv_heads_out(const f16* stage, const QkvArgs& q
 
 // Grid: tiles_m * tiles_n workgroups, column tiles fastest, so workgroups
 // running together share their x rows.
-template <int EPI>
+template <int EPI, bool LN>
 __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     const f16* __restrict__ x, const f16* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ gamma, const f16* res, f16* out, int M, int N, int K,
-    int tiles_n, int ntiles, QkvArgs qa) {
+    int tiles_n, int ntiles, QkvArgs qa, LnArgs la) {
     __shared__ __align__(16) unsigned char smem_raw[kSmemBytes];
     GemmSmem& sm = *reinterpret_cast<GemmSmem*>(smem_raw);
     const int tid = threadIdx.x;
@@ -344,18 +352,38 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     //    f16(acc + bias) (for GELU: f16(gelu(acc + bias))), and writes it
     //    to the wave's staging block in LDS (free once every wave has left
     //    the main loop).
+    //    With the LayerNorm folded in, the stored value is f16((acc -
+    //    mean * colsum) * rstd + shift), shift in the bias slot.
     f16* stage = reinterpret_cast<f16*>(smem_raw) + wave * kEpiWave;
+    f32x2 rs[4];  // (mean, rstd) of this lane's rows wm + 32 b + l32
+    if constexpr (LN) {
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const int64_t row = min(m0 + wm + 32 * b + l32, static_cast<int64_t>(M) - 1);
+            rs[b] = *reinterpret_cast<const f32x2*>(la.stats + 2 * row);
+        }
+    }
 #pragma unroll
     for (int a = 0; a < 2; a++)
 #pragma unroll
         for (int r4 = 0; r4 < 4; r4++) {
             const int cl = 32 * a + 8 * r4 + 4 * hh;  // column within the wave's block
             const float4 bv = bias ? ld_f32x4(bias + n0 + wn + cl) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            float4 cv = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (LN) cv = ld_f32x4(la.colsum + n0 + wn + cl);
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 float v[4];
-                v[0] = acc[a][b][4 * r4] + bv.x, v[1] = acc[a][b][4 * r4 + 1] + bv.y;
-                v[2] = acc[a][b][4 * r4 + 2] + bv.z, v[3] = acc[a][b][4 * r4 + 3] + bv.w;
+                if constexpr (LN) {
+                    const float mu = rs[b][0], rstd = rs[b][1];
+                    v[0] = fmaf(fmaf(-mu, cv.x, acc[a][b][4 * r4]), rstd, bv.x);
+                    v[1] = fmaf(fmaf(-mu, cv.y, acc[a][b][4 * r4 + 1]), rstd, bv.y);
+                    v[2] = fmaf(fmaf(-mu, cv.z, acc[a][b][4 * r4 + 2]), rstd, bv.z);
+                    v[3] = fmaf(fmaf(-mu, cv.w, acc[a][b][4 * r4 + 3]), rstd, bv.w);
+                } else {
+                    v[0] = acc[a][b][4 * r4] + bv.x, v[1] = acc[a][b][4 * r4 + 1] + bv.y;
+                    v[2] = acc[a][b][4 * r4 + 2] + bv.z, v[3] = acc[a][b][4 * r4 + 3] + bv.w;
+                }
                 if constexpr (EPI == EPI_GELU) {
 #pragma unroll
                     for (int e = 0; e < 4; e++) v[e] = gelu_erf(v[e]);
@@ -406,10 +434,11 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
 
 constexpr int kGT = 64, kGK = 16;
 
-template <typename T, int EPI>
+template <typename T, int EPI, bool LN>
 __global__ __launch_bounds__(256) void gemm_generic_kernel(
     const T* __restrict__ x, const T* __restrict__ w, const float* __restrict__ bias,
-    const float* __restrict__ gamma, const T* res, T* out, int M, int N, int K, int tiles_n) {
+    const float* __restrict__ gamma, const T* res, T* out, int M, int N, int K, int tiles_n,
+    LnArgs la) {
     __shared__ float xs[kGK][kGT + 1];
     __shared__ float ws[kGK][kGT + 1];
     const int64_t m0 = static_cast<int64_t>(blockIdx.x / tiles_n) * kGT;
@@ -446,6 +475,9 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(
             const int64_t n = n0 + tc * 4 + j;
             if (n >= N) continue;
             float v = acc[i][j] + (bias ? bias[n] : 0.0f);
+            if constexpr (LN)
+                v = fmaf(fmaf(-la.stats[2 * m], la.colsum[n], acc[i][j]), la.stats[2 * m + 1],
+                         bias ? bias[n] : 0.0f);
             if constexpr (EPI == EPI_GELU) v = gelu_erf(v);
             if constexpr (EPI == EPI_LS)
                 v = static_cast<float>(res[m * N + n]) + gamma[n] * storage_round(v, T{});
@@ -464,18 +496,18 @@ bool fast_shape(hs_dtype dt, int N, int K, const void* x, const void* w, const f
            (!res || aligned16(res));
 }
 
-template <int EPI>
+template <int EPI, bool LN = false>
 hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, const float* bias,
                  const float* gamma, const void* res, void* out, int M, int N, int K,
-                 const char* op, const QkvArgs& qa = QkvArgs{}) {
-    if (fast_shape(dt, N, K, x, w, bias, gamma, out, res)) {
+                 const char* op, const QkvArgs& qa = QkvArgs{}, const LnArgs& la = LnArgs{}) {
+    if (fast_shape(dt, N, K, x, w, bias, gamma, out, res) && (!LN || aligned16(la.colsum))) {
         const int tiles_n = N / kBN;
         const int64_t ntiles = ceil_div(M, kBM) * tiles_n;
         const int64_t blocks = HS_GEMM_XCD ? ceil_div(ntiles, 8) * 8 : ntiles;
-        gemm_f16_kernel<EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st>>>(
+        gemm_f16_kernel<EPI, LN><<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st>>>(
             static_cast<const f16*>(x), static_cast<const f16*>(w), bias, gamma,
             static_cast<const f16*>(res), static_cast<f16*>(out), M, N, K, tiles_n,
-            static_cast<int>(ntiles), qa);
+            static_cast<int>(ntiles), qa, la);
         return check_launch(op);
     }
     if constexpr (EPI == EPI_QKV) {
@@ -485,13 +517,13 @@ hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, cons
         const int tiles_n = static_cast<int>(ceil_div(N, kGT));
         const int64_t blocks = ceil_div(M, kGT) * tiles_n;
         if (dt == HS_F16)
-            gemm_generic_kernel<f16, EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, st>>>(
+            gemm_generic_kernel<f16, EPI, LN><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, st>>>(
                 static_cast<const f16*>(x), static_cast<const f16*>(w), bias, gamma,
-                static_cast<const f16*>(res), static_cast<f16*>(out), M, N, K, tiles_n);
+                static_cast<const f16*>(res), static_cast<f16*>(out), M, N, K, tiles_n, la);
         else
-            gemm_generic_kernel<float, EPI><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, st>>>(
+            gemm_generic_kernel<float, EPI, LN><<<dim3(static_cast<uint32_t>(blocks)), dim3(256), 0, st>>>(
                 static_cast<const float*>(x), static_cast<const float*>(w), bias, gamma,
-                static_cast<const float*>(res), static_cast<float*>(out), M, N, K, tiles_n);
+                static_cast<const float*>(res), static_cast<float*>(out), M, N, K, tiles_n, la);
         return check_launch(op);
     }
 }
@@ -546,15 +578,18 @@ extern "C" hs_status hs_linear_ls_residual(hs_stream_t stream, hs_dtype dt, cons
                           static_cast<int>(m), n, k, "linear_ls_residual");
 }
 
-extern "C" hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x,
-                                         const void* w_qkv, const float* b_qkv, const float* qn_w,
-                                         const float* qn_b, const float* kn_w, const float* kn_b,
-                                         const float* sin_tab, const float* cos_tab, void* q_out,
-                                         void* k_out, void* v_out, int32_t S, int32_t T,
-                                         int32_t H, int32_t d, int32_t k, int32_t prefix,
-                                         float eps) {
-    using namespace hs;
-    const char* op = "linear_qkv_heads";
+namespace hs {
+namespace {
+
+// Validation and arguments of the q|k|v projection with heads (shared by
+// hs_linear_qkv_heads and hs_linear_ln_qkv_heads). Returns HS_OK with
+// *skip set for zero-size work.
+hs_status qkv_setup(const char* op, hs_dtype dt, const void* x, const void* w_qkv,
+                    const float* qn_w, const float* qn_b, const float* kn_w, const float* kn_b,
+                    const float* sin_tab, const float* cos_tab, void* q_out, void* k_out,
+                    void* v_out, int32_t S, int32_t T, int32_t H, int32_t d, int32_t k,
+                    int32_t prefix, float eps, QkvArgs* qa, bool* skip) {
+    *skip = false;
     if (!valid_dtype(dt)) return fail(HS_EINVAL, "%s: unknown dtype", op);
     if (S < 0 || T < 0 || H <= 0 || d <= 0 || k <= 0)
         return fail(HS_EINVAL, "%s: shape S=%d T=%d H=%d d=%d k=%d", op, S, T, H, d, k);
@@ -569,7 +604,10 @@ extern "C" hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const 
     if (N >= (int64_t{1} << 31) || M >= (int64_t{1} << 31) || M * N >= (int64_t{1} << 40) ||
         M * k >= (int64_t{1} << 40))
         return fail(HS_EINVAL, "%s: too large", op);
-    if (M == 0) return HS_OK;
+    if (M == 0) {
+        *skip = true;
+        return HS_OK;
+    }
     if (!x || !w_qkv || !q_out || !k_out || !v_out) return fail(HS_EINVAL, "%s: null buffer", op);
     const int64_t esz = dtype_size(dt), ob = M * H * d * esz;  // each of q, k, v
     const void* outs[3] = {q_out, k_out, v_out};
@@ -588,12 +626,170 @@ extern "C" hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const 
         if (p && !aligned16(p)) return fail(HS_EUNSUPPORTED, "%s: parameters must be 16-byte aligned", op);
     if (!aligned16(k_out) || !aligned16(v_out))
         return fail(HS_EUNSUPPORTED, "%s: outputs must be 16-byte aligned", op);
-    QkvArgs qa{};
-    qa.out[0] = static_cast<f16*>(q_out), qa.out[1] = static_cast<f16*>(k_out);
-    qa.out[2] = static_cast<f16*>(v_out);
-    qa.nw[0] = qn_w, qa.nb[0] = qn_b, qa.nw[1] = kn_w, qa.nb[1] = kn_b;
-    qa.sin_tab = sin_tab, qa.cos_tab = cos_tab;
-    qa.seq = T, qa.heads = H, qa.prefix = prefix, qa.eps = eps;
+    *qa = QkvArgs{};
+    qa->out[0] = static_cast<f16*>(q_out), qa->out[1] = static_cast<f16*>(k_out);
+    qa->out[2] = static_cast<f16*>(v_out);
+    qa->nw[0] = qn_w, qa->nb[0] = qn_b, qa->nw[1] = kn_w, qa->nb[1] = kn_b;
+    qa->sin_tab = sin_tab, qa->cos_tab = cos_tab;
+    qa->seq = T, qa->heads = H, qa->prefix = prefix, qa->eps = eps;
+    return HS_OK;
+}
+
+// The folded LayerNorm's operands: colsum and shift (n) f32, the workspace
+// for the row statistics (2 m floats, 8-byte aligned); then the statistics
+// of x go into the workspace.
+hs_status ln_prologue(const char* op, hipStream_t st, hs_dtype dt, const void* x,
+                      const float* colsum, const float* shift, float* workspace, int64_t M,
+                      int32_t K, float eps) {
+    if (!colsum || !shift || !workspace) return fail(HS_EINVAL, "%s: null buffer", op);
+    if (!(eps > 0.0f)) return fail(HS_EINVAL, "%s: eps must be positive", op);
+    if (reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
+        return fail(HS_EINVAL, "%s: workspace must be 8-byte aligned", op);
+    const int64_t xb = M * K * dtype_size(dt);
+    if (overlaps(workspace, M * 8, x, xb)) return fail(HS_EINVAL, "%s: workspace overlaps x", op);
+    // (a failure keeps the statistics launch's own message)
+    return hs_layernorm_stats(st, dt, x, workspace, M, K, eps);
+}
+
+// Folds a LayerNorm into the linear layer after it: one wave per output
+// row n of w, f32 sums in a fixed order (lane-strided, then the wave tree).
+template <typename T>
+__global__ __launch_bounds__(256) void fold_ln_kernel(const T* __restrict__ w,
+                                                      const float* __restrict__ bias,
+                                                      const float* __restrict__ ln_w,
+                                                      const float* __restrict__ ln_b,
+                                                      T* __restrict__ w_fold,
+                                                      float* __restrict__ colsum,
+                                                      float* __restrict__ shift, int n, int k) {
+    const int row = static_cast<int>(blockIdx.x) * 4 + wave_in_block();
+    if (row >= n) return;  // wave-uniform; no barriers
+    const int lane = lane_id();
+    const T* wr = w + static_cast<int64_t>(row) * k;
+    T* fr = w_fold + static_cast<int64_t>(row) * k;
+    float cs = 0.0f, sh = 0.0f;
+    for (int j = lane; j < k; j += 64) {
+        const float wv = static_cast<float>(wr[j]);
+        // the f32 product is materialised before its storage rounding (left
+        // alone, the compiler fuses the two into one single-rounding op)
+        const T f = static_cast<T>(as_f32(wv * ln_w[j]));
+        fr[j] = f;
+        cs += static_cast<float>(f);
+        sh = fmaf(ln_b[j], wv, sh);
+    }
+    cs = wave_sum(cs);
+    sh = wave_sum(sh);
+    if (lane == 0) colsum[row] = cs, shift[row] = sh + (bias ? bias[row] : 0.0f);
+}
+
+}  // namespace
+}  // namespace hs
+
+extern "C" hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x,
+                                         const void* w_qkv, const float* b_qkv, const float* qn_w,
+                                         const float* qn_b, const float* kn_w, const float* kn_b,
+                                         const float* sin_tab, const float* cos_tab, void* q_out,
+                                         void* k_out, void* v_out, int32_t S, int32_t T,
+                                         int32_t H, int32_t d, int32_t k, int32_t prefix,
+                                         float eps) {
+    using namespace hs;
+    const char* op = "linear_qkv_heads";
+    QkvArgs qa;
+    bool skip;
+    const hs_status rc = qkv_setup(op, dt, x, w_qkv, qn_w, qn_b, kn_w, kn_b, sin_tab, cos_tab,
+                                   q_out, k_out, v_out, S, T, H, d, k, prefix, eps, &qa, &skip);
+    if (rc != HS_OK || skip) return rc;
+    const int64_t M = int64_t{S} * T, N = int64_t{3} * H * d;
     return launch<EPI_QKV>(static_cast<hipStream_t>(stream), dt, x, w_qkv, b_qkv, nullptr, nullptr,
                            q_out, static_cast<int>(M), static_cast<int>(N), k, op, qa);
+}
+
+extern "C" hs_status hs_fold_layernorm(hs_stream_t stream, hs_dtype dt, const void* w,
+                                       const float* bias, const float* ln_w, const float* ln_b,
+                                       void* w_fold, float* colsum, float* shift, int32_t n,
+                                       int32_t k) {
+    using namespace hs;
+    const char* op = "fold_layernorm";
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "%s: unknown dtype", op);
+    if (n < 0 || k <= 0) return fail(HS_EINVAL, "%s: shape n=%d k=%d", op, n, k);
+    if (n == 0) return HS_OK;
+    if (!w || !ln_w || !ln_b || !w_fold || !colsum || !shift)
+        return fail(HS_EINVAL, "%s: null buffer", op);
+    const int64_t wb = int64_t{n} * k * dtype_size(dt);
+    if (overlaps(w_fold, wb, w, wb)) return fail(HS_EINVAL, "%s: w_fold overlaps w", op);
+    const dim3 grid(static_cast<uint32_t>(ceil_div(int64_t{n}, int64_t{4})));
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (dt == HS_F16)
+        fold_ln_kernel<f16><<<grid, dim3(256), 0, st>>>(static_cast<const f16*>(w), bias, ln_w,
+                                                        ln_b, static_cast<f16*>(w_fold), colsum,
+                                                        shift, n, k);
+    else
+        fold_ln_kernel<float><<<grid, dim3(256), 0, st>>>(static_cast<const float*>(w), bias, ln_w,
+                                                          ln_b, static_cast<float*>(w_fold), colsum,
+                                                          shift, n, k);
+    return check_launch(op);
+}
+
+extern "C" hs_status hs_linear_ln(hs_stream_t stream, hs_dtype dt, const void* x,
+                                  const void* w_fold, const float* colsum, const float* shift,
+                                  float* workspace, void* out, int64_t m, int32_t n, int32_t k,
+                                  float eps) {
+    using namespace hs;
+    const char* op = "linear_ln";
+    hs_status rc = check(op, dt, x, w_fold, nullptr, out, m, n, k, false);
+    if (rc != HS_OK || m == 0 || n == 0) return rc;
+    if (k == 0) return fail(HS_EINVAL, "%s: k must be positive", op);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (overlaps(workspace, m * 8, out, m * n * dtype_size(dt)))
+        return fail(HS_EINVAL, "%s: workspace overlaps out", op);
+    rc = ln_prologue(op, st, dt, x, colsum, shift, workspace, m, k, eps);
+    if (rc != HS_OK) return rc;
+    return launch<EPI_BIAS, true>(st, dt, x, w_fold, shift, nullptr, nullptr, out,
+                                  static_cast<int>(m), n, k, op, QkvArgs{}, LnArgs{workspace, colsum});
+}
+
+extern "C" hs_status hs_linear_ln_gelu(hs_stream_t stream, hs_dtype dt, const void* x,
+                                       const void* w_fold, const float* colsum, const float* shift,
+                                       float* workspace, void* out, int64_t m, int32_t n,
+                                       int32_t k, float eps) {
+    using namespace hs;
+    const char* op = "linear_ln_gelu";
+    hs_status rc = check(op, dt, x, w_fold, nullptr, out, m, n, k, false);
+    if (rc != HS_OK || m == 0 || n == 0) return rc;
+    if (k == 0) return fail(HS_EINVAL, "%s: k must be positive", op);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (overlaps(workspace, m * 8, out, m * n * dtype_size(dt)))
+        return fail(HS_EINVAL, "%s: workspace overlaps out", op);
+    rc = ln_prologue(op, st, dt, x, colsum, shift, workspace, m, k, eps);
+    if (rc != HS_OK) return rc;
+    return launch<EPI_GELU, true>(st, dt, x, w_fold, shift, nullptr, nullptr, out,
+                                  static_cast<int>(m), n, k, op, QkvArgs{}, LnArgs{workspace, colsum});
+}
+
+extern "C" hs_status hs_linear_ln_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x,
+                                            const void* w_fold, const float* colsum,
+                                            const float* shift, const float* qn_w,
+                                            const float* qn_b, const float* kn_w,
+                                            const float* kn_b, const float* sin_tab,
+                                            const float* cos_tab, float* workspace, void* q_out,
+                                            void* k_out, void* v_out, int32_t S, int32_t T,
+                                            int32_t H, int32_t d, int32_t k, int32_t prefix,
+                                            float eps) {
+    using namespace hs;
+    const char* op = "linear_ln_qkv_heads";
+    QkvArgs qa;
+    bool skip;
+    hs_status rc = qkv_setup(op, dt, x, w_fold, qn_w, qn_b, kn_w, kn_b, sin_tab, cos_tab, q_out,
+                             k_out, v_out, S, T, H, d, k, prefix, eps, &qa, &skip);
+    if (rc != HS_OK || skip) return rc;
+    const int64_t M = int64_t{S} * T, N = int64_t{3} * H * d;
+    const int64_t ob = M * H * d * dtype_size(dt);
+    const void* outs[3] = {q_out, k_out, v_out};
+    for (const void* o : outs)
+        if (overlaps(workspace, M * 8, o, ob)) return fail(HS_EINVAL, "%s: workspace overlaps an output", op);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    rc = ln_prologue(op, st, dt, x, colsum, shift, workspace, M, k, eps);
+    if (rc != HS_OK) return rc;
+    return launch<EPI_QKV, true>(st, dt, x, w_fold, shift, nullptr, nullptr, q_out,
+                                 static_cast<int>(M), static_cast<int>(N), k, op, qa,
+                                 LnArgs{workspace, colsum});
 }

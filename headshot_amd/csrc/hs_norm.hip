@@ -44,10 +44,13 @@ constexpr int kBlock = 256;  // 4 waves per workgroup
 constexpr int kWavesPerBlock = kBlock / 64;
 constexpr int kBlocksPerCu = 4;  // generic path
 
-template <typename T, int CHUNKS, int U>
+// STATS: write each row's (mean, rsqrt(var + eps)) to stats[2 r], [2 r + 1]
+// instead of the normalised row (the statistics the row would be normalised
+// with, from the same code).
+template <typename T, int CHUNKS, int U, bool STATS>
 __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float* __restrict__ w,
                                                         const float* __restrict__ b, T* out,
-                                                        int64_t rows, float eps) {
+                                                        float* stats, int64_t rows, float eps) {
     constexpr int V = Vec<T>::N;
     constexpr int DIM = 64 * V * CHUNKS;
     const int lane = lane_id();
@@ -56,7 +59,7 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
 
     float wr[CHUNKS][V], br[CHUNKS][V];
 #pragma unroll
-    for (int c = 0; c < CHUNKS; c++) {
+    for (int c = 0; c < CHUNKS && !STATS; c++) {
         const int col = c * 64 * V + lane * V;
 #pragma unroll
         for (int k = 0; k < V; k += 4) {
@@ -98,6 +101,14 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
                 }
             const float var = wave_sum(q) / static_cast<float>(DIM);
             const float inv = rsqrtf(var + eps);
+            if constexpr (STATS) {
+                if (lane == 0) {
+                    f32x2 m2;
+                    m2[0] = mean, m2[1] = inv;
+                    *reinterpret_cast<f32x2*>(stats + 2 * (r0 + u)) = m2;
+                }
+                continue;
+            }
             T* orow = out + (r0 + u) * DIM + lane * V;
 #pragma unroll
             for (int c = 0; c < CHUNKS; c++) {
@@ -168,10 +179,11 @@ __global__ __launch_bounds__(kBlock) void ln_small_kernel(const T* x, const floa
     }
 }
 
-template <typename T>
+template <typename T, bool STATS>
 __global__ __launch_bounds__(kBlock) void ln_generic_kernel(const T* x, const float* __restrict__ w,
                                                             const float* __restrict__ b, T* out,
-                                                            int64_t rows, int dim, float eps) {
+                                                            float* stats, int64_t rows, int dim,
+                                                            float eps) {
     const int lane = lane_id();
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
@@ -188,6 +200,14 @@ __global__ __launch_bounds__(kBlock) void ln_generic_kernel(const T* x, const fl
         }
         const float var = wave_sum(q) / static_cast<float>(dim);
         const float inv = rsqrtf(var + eps);
+        if constexpr (STATS) {
+            if (lane == 0) {
+                f32x2 m2;
+                m2[0] = mean, m2[1] = inv;
+                *reinterpret_cast<f32x2*>(stats + 2 * row) = m2;
+            }
+            continue;
+        }
         for (int j = lane; j < dim; j += 64)
             store_elem(orow + j, (load_elem(xr + j) - mean) * inv * w[j] + b[j]);
     }
@@ -199,17 +219,17 @@ int64_t persistent_blocks(int64_t work_waves) {
     return blocks < cap ? blocks : cap;
 }
 
-template <typename T, int CHUNKS>
+template <typename T, int CHUNKS, bool STATS = false>
 hs_status launch_vec(hipStream_t st, const void* x, const float* w, const float* b, void* out,
-                     int64_t rows, float eps) {
+                     float* stats, int64_t rows, float eps) {
     constexpr int U = HS_LN_U;
     const int64_t want = ceil_div(ceil_div(rows, U), kWavesPerBlock);
     const int64_t cap = HS_LN_BPC > 0 ? static_cast<int64_t>(num_cus()) * HS_LN_BPC
                                       : int64_t{1} << 22;
     const int64_t blocks = want < cap ? want : cap;
-    ln_vec_kernel<T, CHUNKS, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
-        static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, eps);
-    return check_launch("layernorm");
+    ln_vec_kernel<T, CHUNKS, U, STATS><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+        static_cast<const T*>(x), w, b, static_cast<T*>(out), stats, rows, eps);
+    return check_launch(STATS ? "layernorm_stats" : "layernorm");
 }
 
 template <typename T>
@@ -220,9 +240,9 @@ hs_status launch(hipStream_t st, const void* x, const float* w, const float* b, 
                         dim % (64 * V) == 0;
     if (vec_ok) {
         switch (dim / (64 * V)) {
-            case 1: return launch_vec<T, 1>(st, x, w, b, out, rows, eps);
-            case 2: return launch_vec<T, 2>(st, x, w, b, out, rows, eps);
-            case 4: return launch_vec<T, 4>(st, x, w, b, out, rows, eps);
+            case 1: return launch_vec<T, 1>(st, x, w, b, out, nullptr, rows, eps);
+            case 2: return launch_vec<T, 2>(st, x, w, b, out, nullptr, rows, eps);
+            case 4: return launch_vec<T, 4>(st, x, w, b, out, nullptr, rows, eps);
             default: break;
         }
     }
@@ -241,9 +261,29 @@ hs_status launch(hipStream_t st, const void* x, const float* w, const float* b, 
         return check_launch("layernorm");
     }
     const int64_t blocks = persistent_blocks(rows);
-    ln_generic_kernel<T><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
-        static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, dim, eps);
+    ln_generic_kernel<T, false><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+        static_cast<const T*>(x), w, b, static_cast<T*>(out), nullptr, rows, dim, eps);
     return check_launch("layernorm");
+}
+
+// Row statistics only: the same kernels (and so the same arithmetic) as the
+// normalising launch above for the vector widths, the generic kernel else.
+template <typename T>
+hs_status launch_stats(hipStream_t st, const void* x, float* stats, int64_t rows, int dim,
+                       float eps) {
+    constexpr int V = Vec<T>::N;
+    if (aligned16(x) && dim % (64 * V) == 0) {
+        switch (dim / (64 * V)) {
+            case 1: return launch_vec<T, 1, true>(st, x, nullptr, nullptr, nullptr, stats, rows, eps);
+            case 2: return launch_vec<T, 2, true>(st, x, nullptr, nullptr, nullptr, stats, rows, eps);
+            case 4: return launch_vec<T, 4, true>(st, x, nullptr, nullptr, nullptr, stats, rows, eps);
+            default: break;
+        }
+    }
+    const int64_t blocks = persistent_blocks(rows);
+    ln_generic_kernel<T, true><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+        static_cast<const T*>(x), nullptr, nullptr, nullptr, stats, rows, dim, eps);
+    return check_launch("layernorm_stats");
 }
 
 }  // namespace
@@ -264,4 +304,21 @@ extern "C" hs_status hs_layernorm(hs_stream_t stream, hs_dtype dt, const void* x
     hipStream_t st = static_cast<hipStream_t>(stream);
     return dt == HS_F16 ? launch<f16>(st, x, w, b, out, rows, dim, eps)
                         : launch<float>(st, x, w, b, out, rows, dim, eps);
+}
+
+extern "C" hs_status hs_layernorm_stats(hs_stream_t stream, hs_dtype dt, const void* x,
+                                        float* stats, int64_t rows, int32_t dim, float eps) {
+    using namespace hs;
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "layernorm_stats: unknown dtype %d", (int)dt);
+    if (rows < 0 || dim <= 0)
+        return fail(HS_EINVAL, "layernorm_stats: rows %lld / dim %d", (long long)rows, dim);
+    if (rows == 0) return HS_OK;
+    if (!x || !stats) return fail(HS_EINVAL, "layernorm_stats: null buffer");
+    if (reinterpret_cast<uintptr_t>(stats) % 8 != 0)
+        return fail(HS_EINVAL, "layernorm_stats: stats must be 8-byte aligned");
+    if (overlaps(x, rows * dim * dtype_size(dt), stats, rows * 8))
+        return fail(HS_EINVAL, "layernorm_stats: stats overlaps x");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    return dt == HS_F16 ? launch_stats<f16>(st, x, stats, rows, dim, eps)
+                        : launch_stats<float>(st, x, stats, rows, dim, eps);
 }
