@@ -117,6 +117,10 @@ extern "C" {
                              w_fold: *const c_void, colsum: *const f32, shift: *const f32,
                              workspace: *mut f32, out: *mut c_void, m: i64, n: i32, k: i32,
                              eps: f32) -> HsStatus;
+    pub fn hs_linear_ln_gelu_noalloc(stream: HsStream, dt: HsDtype, x: *const c_void,
+                                     w_fold: *const c_void, colsum: *const f32,
+                                     shift: *const f32, out: *mut c_void, m: i64, n: i32, k: i32,
+                                     eps: f32) -> HsStatus;
     pub fn hs_linear_ln_qkv_heads(stream: HsStream, dt: HsDtype, x: *const c_void,
                                   w_fold: *const c_void, colsum: *const f32, shift: *const f32,
                                   qn_w: *const f32, qn_b: *const f32, kn_w: *const f32,

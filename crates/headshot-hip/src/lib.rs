@@ -662,6 +662,25 @@ impl HipContext {
         out
     }
 
+    /// `linear_ln_gelu` into a caller's output without any device
+    /// allocation by the library (the row statistics use the library's own
+    /// per-device array): for callers that cannot allocate. At most 524,288
+    /// rows; calls that overlap on one device race.
+    pub fn linear_ln_gelu_noalloc(&self, x: &HipTensor, f: &FoldedLinear, eps: f32,
+                                  out: &HipTensor) {
+        let (m, k) = x.dims();
+        let (n, wk) = f.w_fold.dims();
+        assert_eq!(wk, k, "folded weight k");
+        assert_eq!(out.len(), m * n, "out shape");
+        assert_eq!(out.dtype, x.dtype, "out dtype");
+        check(unsafe {
+            ffi::hs_linear_ln_gelu_noalloc(self.stream, x.dtype.raw(), x.cptr(), f.w_fold.cptr(),
+                                           f.colsum.f32p("colsum"), f.shift.f32p("shift"),
+                                           out.mptr(), m as i64, i32_of(n, "n"), i32_of(k, "k"),
+                                           eps)
+        }, "linear_ln_gelu_noalloc");
+    }
+
     /// LN1 + the q|k|v projection with heads, QK-norm and RoPE
     /// (model/block.rs:128-146) on the folded q|k|v weight.
     #[allow(clippy::too_many_arguments)]

@@ -54,6 +54,7 @@ SIGNATURES = {
     "hs_fold_layernorm": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _I32]),
     "hs_linear_ln": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
     "hs_linear_ln_gelu": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
+    "hs_linear_ln_gelu_noalloc": (_S, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
     "hs_linear_ln_qkv_heads": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                     _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F]),
     "hs_concat_channels": (_S, [_P, _I32, _P, _P, _P, _I64, _I32, _I32]),

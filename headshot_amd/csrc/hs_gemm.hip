@@ -29,6 +29,8 @@
 // scalar kernel, f32 accumulation in K order.
 #include <math.h>
 
+#include <mutex>
+
 #include "hs_common.hpp"
 
 namespace hs {
@@ -792,4 +794,75 @@ extern "C" hs_status hs_linear_ln_qkv_heads(hs_stream_t stream, hs_dtype dt, con
     return launch<EPI_QKV, true>(st, dt, x, w_fold, shift, nullptr, nullptr, q_out,
                                  static_cast<int>(M), static_cast<int>(N), k, op, qa,
                                  LnArgs{workspace, colsum});
+}
+
+// ---------------------------------------------------------------------------
+// An allocation-free variant of hs_linear_ln_gelu: the row statistics live
+// in a file-scope device array instead of a caller workspace. Each device the
+// library runs on holds its own copy for the life of the process; its device
+// address comes from hipGetSymbolAddress, taken once per device (with that
+// device current) on the first call there. Every call on a device shares
+// that device's array, so calls that overlap on one device race; the array
+// keeps the last call's statistics, and each call writes every row it reads.
+
+namespace hs {
+namespace {
+
+constexpr int64_t kNoAllocMaxRows = int64_t{1} << 19;  // 524,288 rows: 4 MiB of statistics
+static __device__ __align__(256) float scratch[2 * kNoAllocMaxRows];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kScratchDevices];  // device address of `scratch` per device, once taken
+
+// The current device's address of `scratch` (nullptr with *rc and the
+// error message set on failure). The array's host-side name is not a device
+// address: only the pointer returned by hipGetSymbolAddress goes to kernels.
+float* scratch_address(const char* op, hs_status* rc) {
+    int dev = 0;
+    const hipError_t de = hipGetDevice(&dev);
+    if (de != hipSuccess) {
+        *rc = fail(HS_EHIP, "%s: hipGetDevice: %s", op, hipGetErrorString(de));
+        return nullptr;
+    }
+    if (dev < 0 || dev >= kScratchDevices) {
+        *rc = fail(HS_EUNSUPPORTED, "%s: device %d beyond the %d the library tracks", op, dev,
+                   kScratchDevices);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch[dev] == nullptr) {
+        void* ptr = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || ptr == nullptr) {
+            *rc = fail(HS_EHIP, "%s: hipGetSymbolAddress(scratch): %s", op, hipGetErrorString(e));
+            return nullptr;
+        }
+        g_scratch[dev] = static_cast<float*>(ptr);
+    }
+    return g_scratch[dev];
+}
+
+}  // namespace
+}  // namespace hs
+
+extern "C" hs_status hs_linear_ln_gelu_noalloc(hs_stream_t stream, hs_dtype dt, const void* x,
+                                               const void* w_fold, const float* colsum,
+                                               const float* shift, void* out, int64_t m,
+                                               int32_t n, int32_t k, float eps) {
+    using namespace hs;
+    const char* op = "linear_ln_gelu_noalloc";
+    if (m > kNoAllocMaxRows)
+        return fail(HS_EINVAL, "%s: m = %lld rows exceeds the statistics array's %lld", op,
+                    static_cast<long long>(m), static_cast<long long>(kNoAllocMaxRows));
+    hs_status rc = check(op, dt, x, w_fold, nullptr, out, m, n, k, false);
+    if (rc != HS_OK || m == 0 || n == 0) return rc;
+    if (k == 0) return fail(HS_EINVAL, "%s: k must be positive", op);
+    float* ws = scratch_address(op, &rc);
+    if (ws == nullptr) return rc;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    rc = ln_prologue(op, st, dt, x, colsum, shift, ws, m, k, eps);
+    if (rc != HS_OK) return rc;
+    return launch<EPI_GELU, true>(st, dt, x, w_fold, shift, nullptr, nullptr, out,
+                                  static_cast<int>(m), n, k, op, QkvArgs{}, LnArgs{ws, colsum});
 }

@@ -302,6 +302,17 @@ hs_status hs_linear_ln_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x,
                                  int32_t S, int32_t T, int32_t H, int32_t d, int32_t k,
                                  int32_t prefix, float eps);
 
+/* hs_linear_ln_gelu without a workspace, for callers that cannot allocate
+ * device memory (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc); no counterpart in the reference. The row statistics go
+ * to a 4 MiB array the library holds in each device's memory for the life
+ * of the process, so m is at most 524,288 rows (HS_EINVAL beyond), and calls
+ * that overlap on one device race on that array. It calls no allocating
+ * routine. */
+hs_status hs_linear_ln_gelu_noalloc(hs_stream_t stream, hs_dtype dt, const void* x,
+                                    const void* w_fold, const float* colsum, const float* shift,
+                                    void* out, int64_t m, int32_t n, int32_t k, float eps);
+
 /* ---------------------------------------------------------------------- */
 /* Attention                                                                */
 
