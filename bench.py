@@ -336,6 +336,59 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
         del x, w, o
     out["ms_per_block"] = round(total_ms, 3)
     out["ms_per_pass"] = round(total_ms * (N_FRAME_BLOCKS + N_GLOBAL_BLOCKS), 2)
+    out["layernorm_folded"] = ln_fold_times(ctx, m, timed, g)
+    return out
+
+
+def ln_fold_times(ctx, m: int, timed, g) -> dict:
+    """The pre-norm LayerNorm folded into the product after it
+    (hs_layernorm_stats + hs_linear_ln_gelu / hs_linear_ln_qkv_heads on
+    weights folded by hs_fold_layernorm) against layernorm then the fused
+    product, at the block's LN2 -> fc1 + GELU and LN1 -> q|k|v (heads,
+    QK-norm, RoPE) shapes. Times include the statistics pass."""
+    import torch
+
+    from headshot_amd import rope as _rope
+
+    t = GRID[0] * GRID[1] + PREFIX
+    frames = m // t
+    x = torch.randn((m, DIM), generator=g).half().to(ctx.device)
+    lw = (1 + 0.02 * torch.randn(DIM, generator=g)).to(ctx.device)
+    lb = (0.02 * torch.randn(DIM, generator=g)).to(ctx.device)
+    normed = ctx.layernorm(x, lw, lb, eps=EPS)
+    ln_call = ctx.last_launch
+    ws = torch.empty((m, 2), dtype=torch.float32, device=ctx.device)
+    out = {"layernorm_us": round(timed(ln_call) * 1e3, 1)}
+    ctx.layernorm_stats(x, eps=EPS, out=ws)
+    out["stats_us"] = round(timed(ctx.last_launch) * 1e3, 1)
+    sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(_rope.periods(), *GRID))
+    nrm = (torch.ones(HEAD_DIM, device=ctx.device), torch.zeros(HEAD_DIM, device=ctx.device))
+    for name, n in (("fc1", HIDDEN), ("qkv", 3 * DIM)):
+        w = (torch.randn((n, DIM), generator=g) / DIM ** 0.5).half().to(ctx.device)
+        b = (torch.randn(n, generator=g) * 0.02).to(ctx.device)
+        f = ctx.fold_layernorm(w, b, lw, lb)
+        if name == "fc1":
+            o = torch.empty((m, n), dtype=torch.float16, device=ctx.device)
+            ctx.linear_gelu(normed, w, b, out=o)
+            plain = ctx.last_launch
+            ctx.linear_ln_gelu(x, f, eps=EPS, out=o, workspace=ws)
+            folded = ctx.last_launch
+        else:
+            o = tuple(torch.empty((frames, HEADS, t, HEAD_DIM), dtype=torch.float16,
+                                  device=ctx.device) for _ in range(3))
+            ctx.linear_qkv_heads(normed, w, b, frames, t, HEADS, qn=nrm, kn=nrm,
+                                 rope=(sin, cos, PREFIX), eps=EPS, out=o)
+            plain = ctx.last_launch
+            ctx.linear_ln_qkv_heads(x, f, frames, t, HEADS, qn=nrm, kn=nrm,
+                                    rope=(sin, cos, PREFIX), eps=EPS, out=o, workspace=ws)
+            folded = ctx.last_launch
+        ms_plain = timed(lambda: (ln_call(), plain()))
+        ms_fold = timed(folded)
+        fl = 2.0 * m * n * DIM
+        out[name] = {"layernorm_then_product_ms": round(ms_plain, 3),
+                     "folded_ms": round(ms_fold, 3),
+                     "folded_TFLOP/s": round(fl / (ms_fold * 1e-3) / 1e12, 1)}
+        del w, o
     return out
 
 
@@ -353,13 +406,19 @@ def block_times(ctx, frames: int, iters: int) -> dict:
     t = GRID[0] * GRID[1] + PREFIX
     gen = torch.Generator(device=ctx.device).manual_seed(17)
     wts = BlockWeights.random(DIM, HIDDEN, HEAD_DIM, torch.float16, ctx.device, gen)
+    wts.fold_layernorms(ctx)
     x = torch.randn((frames * t, DIM), generator=gen, device=ctx.device).half()
     sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(_rope.periods(), *GRID))
     out = {}
+
+    def folded(*a, **kw):
+        return block_forward(*a, fold_ln2=True, fold_ln1=True, **kw)
+
     for kind, (s, tt, rope) in {"frame": (frames, t, (sin, cos, PREFIX)),
                                 "global": (1, frames * t, None)}.items():
         res = {}
-        for name, fn in (("fused", block_forward), ("reference_sequence", block_forward_reference)):
+        for name, fn in (("fused", block_forward), ("reference_sequence", block_forward_reference),
+                         ("fused_layernorm_folded", folded)):
             fn(ctx, wts, x, s, tt, rope=rope, eps=EPS)
             torch.cuda.synchronize()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -375,6 +434,9 @@ def block_times(ctx, frames: int, iters: int) -> dict:
     out["aggregator_reference_sequence_ms"] = round(
         N_FRAME_BLOCKS * out["frame"]["reference_sequence_ms"]
         + N_GLOBAL_BLOCKS * out["global"]["reference_sequence_ms"], 1)
+    out["aggregator_layernorm_folded_ms"] = round(
+        N_FRAME_BLOCKS * out["frame"]["fused_layernorm_folded_ms"]
+        + N_GLOBAL_BLOCKS * out["global"]["fused_layernorm_folded_ms"], 1)
     return out
 
 
