@@ -30,6 +30,12 @@ dispatch sequence through the same library) and a ``trunk`` section (one
 whole aggregator trunk forward from DINO tokens to the head-input caches,
 the same two ways).
 
+``ceilings``: each fused op beside a data-movement probe that moves the same
+bytes in the same access pattern with no arithmetic (bench_ceiling.hip:
+copy, two-input add, the token-major to head-major copy of the QK-norm pair
+kernel, f32 to f16 cast), warm and cold, with the op's rate as a fraction of
+the probe's.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--frames S]
 """
 from __future__ import annotations
@@ -77,6 +83,8 @@ def parse():
     ap.add_argument("--op-passes", type=int, default=3)
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-ceilings", action="store_true",
+                    help="skip the data-movement probes timed beside each op")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="target CPU work for the oracle baseline sample")
     ap.add_argument("--calibrate-copy-mib", type=int, default=512,
@@ -192,6 +200,134 @@ def op_rates(bench: Pass, mean_ms: dict) -> dict:
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix peak
+
+
+CEILING_SRC = os.path.join(ROOT, "bench_ceiling.hip")
+CEILING_LIB = os.path.join(ROOT, "bench_ceiling.so")
+
+
+def build_ceiling() -> str:
+    """Compile bench_ceiling.hip (the data-movement probes) for gfx950 with
+    the library's flags into bench_ceiling.so."""
+    from headshot_amd import build as hs_build
+
+    tmp = CEILING_LIB + ".tmp"
+    hs_build._run([hs_build.HIPCC, *hs_build.HIP_FLAGS, "-shared", "-o", tmp, CEILING_SRC])
+    os.replace(tmp, CEILING_LIB)
+    return CEILING_LIB
+
+
+def load_ceiling():
+    import ctypes
+
+    lib = ctypes.CDLL(CEILING_LIB)
+    lib.hsc_run.restype = ctypes.c_int
+    lib.hsc_run.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 4 + \
+        [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
+    return lib
+
+
+# op -> (probe kernel, what it moves)
+CEILING_PROBES = {
+    "layernorm": ("copy", "rows x 1024 f16 read and written, contiguous"),
+    "bias_gelu": ("copy", "rows x 4096 f16 read and written, contiguous"),
+    "bias_ls_residual": ("add2", "two rows x 1024 f16 read, one written, contiguous"),
+    "qknorm_rope": ("heads", "q and k, rows x 1024 f16 each, token-major in, head-major out, "
+                             "the pair kernel's addressing (a wave per 2 tokens, 8 heads' "
+                             "128-byte vectors per store)"),
+    "assemble": ("cast", "S*P x 1024 f32 read, f16 written, contiguous (positional table "
+                         "and prefix rows not included)"),
+}
+KINDS = {"copy": 0, "add2": 1, "heads": 2, "cast": 3}
+
+
+def ceiling_times(bench: Pass, op_cold: dict, flush, iters: int = 20) -> dict:
+    """Each op beside a data-movement probe with its byte mix and access
+    pattern (bench_ceiling.hip). Warm: back-to-back launches of the probe,
+    and of the op's own first launch of the pass, over ``iters`` launches
+    each. Cold: the probe under the per-op cold method (cache flush, then a
+    HIP event pair around one launch), compared with the op's cold rate."""
+    import torch
+
+    if not os.path.exists(CEILING_LIB):
+        return {"error": "bench_ceiling.so is not built (python -c 'import bench; "
+                         "bench.build_ceiling()')"}
+    if bench.dtype != torch.float16:
+        return {"error": "the probes move f16 activations"}
+    lib = load_ceiling()
+    dev = bench.ctx.device
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rows, frames, t, p = bench.rows, bench.frames, bench.t, bench.p
+
+    def timed_warm(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters * 1e3
+
+    def timed_cold(fn):
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(iters)]
+        for a, b in ev:
+            flush()
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3
+
+    first = {}
+    for op, thunk in bench.seq:
+        first.setdefault(op, thunk)
+    out = {}
+    for op, (probe, what) in CEILING_PROBES.items():
+        f16 = torch.float16
+        if probe in ("copy", "add2"):
+            width = HIDDEN if op == "bias_gelu" else DIM
+            a = torch.ones((rows, width), device=dev, dtype=f16)
+            b = torch.ones_like(a) if probe == "add2" else None
+            o, o2 = torch.empty_like(a), None
+            n = a.numel() * 2 // 16
+            nbytes = n * 16 * (3 if probe == "add2" else 2)
+            args = (n, 0, 0)
+        elif probe == "heads":
+            a = torch.ones((rows, DIM), device=dev, dtype=f16)
+            b, o, o2 = torch.ones_like(a), torch.empty_like(a), torch.empty_like(a)
+            nbytes = 4 * a.numel() * 2
+            args = (0, frames, t)
+        else:
+            a = torch.ones((frames * p, DIM), device=dev, dtype=torch.float32)
+            b, o, o2 = None, torch.empty((frames * p, DIM), device=dev, dtype=f16), None
+            nbytes = a.numel() * 6
+            args = (a.numel(), 0, 0)
+        ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
+
+        def run(kind=KINDS[probe], bufs=(ptr(a), ptr(b), ptr(o), ptr(o2)), args=args):
+            rc = lib.hsc_run(kind, *bufs, *args, stream)
+            if rc != 0:
+                raise RuntimeError(f"hsc_run({probe}) returned {rc}")
+
+        us, cold_us = timed_warm(run), timed_cold(run)
+        op_us = timed_warm(first[op])
+        gbs, cold_gbs = nbytes / us / 1e3, nbytes / cold_us / 1e3
+        op_gbs = bench.bytes[op] / op_us / 1e3
+        entry = {"probe": probe, "moves": what, "bytes": nbytes,
+                 "us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                 "cold_us": round(cold_us, 2), "cold_GB/s": round(cold_gbs, 1),
+                 "cold_frac": round(cold_gbs / PEAK_GBS, 4),
+                 "op_back_to_back_us": round(op_us, 2), "op_back_to_back_GB/s": round(op_gbs, 1),
+                 "op_frac_of_probe": round(op_gbs / gbs, 4)}
+        if op_cold:
+            entry["op_cold_frac_of_probe"] = round(op_cold[op]["GB/s"] / cold_gbs, 4)
+        out[op] = entry
+        del a, b, o, o2
+    torch.cuda.synchronize()
+    return out
 
 
 def attention_times(ctx, frames: int, iters: int) -> dict:
@@ -1017,11 +1153,13 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
 
-    per_op, per_op_cold, roofline, ops_ms = {}, None, None, None
+    per_op, per_op_cold, roofline, ops_ms, ceilings = {}, None, None, None, None
     if args.op_passes > 0:
         per_op = op_rates(bench, per_op_times(bench, args.op_passes))
         flush = cache_flusher(ctx.device)
         per_op_cold = op_rates(bench, per_op_times(bench, args.op_passes, flush=flush))
+        if not args.no_ceilings:
+            ceilings = ceiling_times(bench, per_op_cold, flush)
         del flush
         ops_ms = round(sum(per_op[op]["us"] * bench.launches[op] for op in OPS) / 1e3, 3)
         dominant = max(OPS, key=lambda op: per_op[op]["us"] * bench.launches[op])
@@ -1059,6 +1197,7 @@ def main():
         "ops_ms_per_step": ops_ms,
         "ops": per_op,
         "ops_cold": per_op_cold,
+        "ceilings": ceilings,
         "roofline": roofline,
     }
     if args.attention_iters > 0:

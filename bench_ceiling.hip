@@ -1,0 +1,165 @@
+// Data-movement ceilings for bench.py: each kernel moves the same bytes as
+// one of the fused ops, in that op's access pattern, with no arithmetic
+// beyond what the byte mix needs. Timed beside the op, the pair says how
+// much of the op's distance from the 8 TB/s HBM peak is the memory system's
+// own limit for that pattern and how much is the op's.
+//
+//   copy   1 read : 1 write, contiguous            (layernorm, bias_gelu)
+//   add2   2 reads : 1 write, contiguous           (bias_ls_residual)
+//   heads  token-major (S*T, 16*64) f16 -> head-major (S, 16, T, 64), two
+//          tensors in one launch, a wave per two tokens and 8 heads' 128-byte
+//          vectors per store: the addressing of the fused QK-norm + RoPE
+//          pair kernel (qknorm_rope)
+//   cast   f32 rows in, f16 rows out, contiguous   (assembly's byte mix)
+//
+// Loads and stores are the library's streaming (non-temporal) forms. Not
+// part of libheadshot_hip: built into bench_ceiling.so next to bench.py.
+#include "hs_common.hpp"
+
+namespace {
+
+using hs::f16;
+using hs::u32x4;
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;  // 16-byte vectors per lane
+
+// Vectors [w * 256, w * 256 + 256) for wave w: four wave-contiguous 1 KiB
+// pieces per wave.
+__global__ __launch_bounds__(kBlock) void copy_kernel(const u32x4* __restrict__ a,
+                                                      u32x4* __restrict__ o, int64_t n) {
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kUnroll +
+                         (threadIdx.x & 63);
+    u32x4 r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++)
+        if (base + u * 64 < n) r[u] = hs::ld_stream(a + base + u * 64);
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++)
+        if (base + u * 64 < n) hs::st_stream(o + base + u * 64, r[u]);
+}
+
+__global__ __launch_bounds__(kBlock) void add2_kernel(const u32x4* __restrict__ a,
+                                                      const u32x4* __restrict__ b,
+                                                      u32x4* __restrict__ o, int64_t n) {
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kUnroll +
+                         (threadIdx.x & 63);
+    u32x4 ra[kUnroll], rb[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++)
+        if (base + u * 64 < n) ra[u] = hs::ld_stream(a + base + u * 64), rb[u] = hs::ld_stream(b + base + u * 64);
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++)
+        if (base + u * 64 < n) hs::st_stream(o + base + u * 64, ra[u] + rb[u]);
+}
+
+// Two tensors: waves [0, W) copy the first, [W, 2W) the second, W =
+// ceil(tokens / 2). A load covers one token's 8 heads (1 KiB contiguous),
+// a store writes those 8 heads' vectors to their head-major rows.
+__global__ __launch_bounds__(kBlock) void heads_kernel(const f16* __restrict__ x0,
+                                                       const f16* __restrict__ x1,
+                                                       f16* __restrict__ o0, f16* __restrict__ o1,
+                                                       int64_t tokens, int seq) {
+    constexpr int H = 16, D = 64, K = 2;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + hs::wave_in_block();
+    const int64_t per = (tokens + K - 1) / K;
+    const int which = wave >= per ? 1 : 0;
+    const int64_t u0 = (wave - which * per) * K;
+    if (which > 1 || u0 >= tokens) return;
+    const f16* x = which ? x1 : x0;
+    f16* o = which ? o1 : o0;
+    const int lane = hs::lane_id(), gsub = lane >> 3, ch = (lane & 7) * 8;
+    u32x4 r[K][2];
+#pragma unroll
+    for (int k = 0; k < K; k++)
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+            if (u0 + k < tokens) r[k][c] = hs::ld_stream(x + (u0 + k) * (H * D) + (c * 8 + gsub) * D + ch);
+#pragma unroll
+    for (int k = 0; k < K; k++) {
+        const int64_t tok = u0 + k;
+        if (tok >= tokens) break;
+        const int64_t s = tok / seq, t = tok - s * seq;
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+            hs::st_stream(o + ((s * H + c * 8 + gsub) * seq + t) * D + ch, r[k][c]);
+    }
+}
+
+// n f32 -> f16, four elements (16 bytes in, 8 out) per lane per step.
+__global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ a,
+                                                      f16* __restrict__ o, int64_t n) {
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kUnroll +
+                         (threadIdx.x & 63);
+    u32x4 r[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++)
+        if ((base + u * 64) * 4 < n) r[u] = hs::ld_stream(a + (base + u * 64) * 4);
+#pragma unroll
+    for (int u = 0; u < kUnroll; u++) {
+        if ((base + u * 64) * 4 >= n) continue;
+        hs::f16x2 lo, hi;
+        lo.x = static_cast<f16>(hs::u2f(r[u][0])), lo.y = static_cast<f16>(hs::u2f(r[u][1]));
+        hi.x = static_cast<f16>(hs::u2f(r[u][2])), hi.y = static_cast<f16>(hs::u2f(r[u][3]));
+        hs::u32x2 v;
+        v[0] = hs::h22u(lo), v[1] = hs::h22u(hi);
+        hs::st_stream_as(reinterpret_cast<hs::u32x2*>(o + (base + u * 64) * 4), v);
+    }
+}
+
+int64_t blocks_for(int64_t lanes_work) { return (lanes_work + kBlock - 1) / kBlock; }
+
+}  // namespace
+
+extern "C" {
+
+// kind 0 copy / 1 add2: n 16-byte vectors (a, b -> o). kind 2 heads: s
+// frames of t tokens, a and b -> o and o2. kind 3 cast: n f32 elements
+// (n % 4 == 0). Buffers are 16-byte aligned and sized by the caller.
+// Returns 0, or -1 for an argument the kernels do not take, or the HIP
+// error code of the launch.
+int hsc_run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n, int32_t s,
+            int32_t t, hipStream_t stream) {
+    if (n < 0 || s < 0 || t < 0) return -1;
+    switch (kind) {
+        case 0:
+        case 1: {
+            const int64_t blocks = blocks_for((n + kUnroll - 1) / kUnroll);
+            if (blocks == 0) return 0;
+            if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
+            if (kind == 0)
+                copy_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                    static_cast<const u32x4*>(a), static_cast<u32x4*>(o), n);
+            else
+                add2_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                    static_cast<const u32x4*>(a), static_cast<const u32x4*>(b),
+                    static_cast<u32x4*>(o), n);
+            break;
+        }
+        case 2: {
+            const int64_t tokens = static_cast<int64_t>(s) * t;
+            const int64_t waves = 2 * ((tokens + 1) / 2);
+            const int64_t blocks = (waves + 3) / 4;
+            if (blocks == 0) return 0;
+            if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
+            heads_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                static_cast<const f16*>(a), static_cast<const f16*>(b), static_cast<f16*>(o),
+                static_cast<f16*>(o2), tokens, t);
+            break;
+        }
+        case 3: {
+            if (n % 4 != 0) return -1;
+            const int64_t blocks = blocks_for((n / 4 + kUnroll - 1) / kUnroll);
+            if (blocks == 0) return 0;
+            if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
+            cast_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                static_cast<const float*>(a), static_cast<f16*>(o), n);
+            break;
+        }
+        default:
+            return -1;
+    }
+    return static_cast<int>(hipGetLastError());
+}
+
+}  // extern "C"

@@ -18,7 +18,15 @@
 // together, and a wave pipelines K consecutive rows so the next row's loads
 // are in flight while the current one is computed and stored. Each store
 // writes 64/G heads' 128-byte vectors of one token into the head-major
-// (S, H, T, 64) output that attention consumes.
+// (S, H, T, 64) output that attention consumes. (A pure copy with exactly
+// this addressing runs as fast as a contiguous copy of the same bytes.)
+//
+// RoPE tables: all 64/G head groups of a wave need the same cos/sin values
+// for a token, so per-lane table loads would fetch each row 64/G times (as
+// many bytes as the activations themselves, through the same load path;
+// measured 7% of the kernel's time at S=32). Each wave instead stages its
+// K tokens' cos and sin rows in a 1 KiB LDS slice with one 16-byte load per
+// lane (K = 2), and the lanes read their channels from there.
 //
 // hs_qknorm_rope_pair runs q and k in one launch (the first half of the grid
 // takes q with its norm, the second half k): each launch pays ~4 us of
@@ -75,6 +83,8 @@ struct QknRow {
     T* __restrict__ out;
     int seq, prefix, ch, gsub;
     bool upper;
+    const float* tab;      // this wave's LDS slice: per token, cos row then sin row
+    int64_t tab_tok0;      // token of the slice's first row
     float eps;
     float wr[V], br[V];
 
@@ -94,11 +104,12 @@ struct QknRow {
         // Two copies of the row code, chosen by a wave-uniform branch, so
         // the rotated and the unrotated results never meet in one register.
         if (ROPE && t >= prefix) {
-            const int64_t row = static_cast<int64_t>(t - prefix) * D + ch;
+            const float* trow = tab + (tok - tab_tok0) * 2 * D + ch;
             const float sg = upper ? 1.0f : -1.0f;
 #pragma unroll
             for (int k = 0; k < V; k += 4) {
-                const float4 c4 = ld_f32x4(cos_tab + row + k), s4 = ld_f32x4(sin_tab + row + k);
+                const float4 c4 = *reinterpret_cast<const float4*>(trow + k);
+                const float4 s4 = *reinterpret_cast<const float4*>(trow + D + k);
                 cs[k] = c4.x, cs[k + 1] = c4.y, cs[k + 2] = c4.z, cs[k + 3] = c4.w;
                 sn[k] = sg * s4.x, sn[k + 1] = sg * s4.y, sn[k + 2] = sg * s4.z,
                 sn[k + 3] = sg * s4.w;
@@ -175,6 +186,30 @@ __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
         }
     }
 
+    // RoPE table rows of the wave's K tokens, staged through LDS: one 16-byte
+    // load per lane covers two tokens' cos and sin rows (1 KiB), instead of
+    // every lane reading its own 64 bytes of both rows per token.
+    __shared__ float4 tab_lds[kWavesPerBlock][K * 2 * 64 / 4];
+    if constexpr (ROPE) {
+        float4* slice = tab_lds[wave_in_block()];
+#pragma unroll
+        for (int i = lane; i < K * 2 * 64 / 4; i += 64) {
+            const int k = i / 32, which_tab = (i / 16) & 1, off = (i & 15) * 4;
+            const int64_t tok = u0 + k;
+            if (tok < u_end) {
+                const int t = static_cast<int>(static_cast<uint32_t>(tok) % static_cast<uint32_t>(seq));
+                if (t >= prefix) {
+                    const float* src = which_tab ? sin_tab : cos_tab;
+                    slice[i] = ld_f32x4(src + static_cast<int64_t>(t - prefix) * 64 + off);
+                }
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        tl.tab = reinterpret_cast<const float*>(slice);
+        tl.tab_tok0 = u0;
+    }
     u32x4 a[HB], b[HB];
     tl.load(a, u0);
 #pragma unroll 1

@@ -61,3 +61,23 @@ def test_host_threads_uses_the_visible_cores_within_the_share(monkeypatch):
     assert bench.host_threads() == (1, visible)
     monkeypatch.setenv("OMP_NUM_THREADS", str(visible + 100))
     assert bench.host_threads() == (visible, visible)
+
+
+def test_ceiling_probes_cover_every_op():
+    assert set(bench.CEILING_PROBES) == set(bench.OPS)
+    assert {probe for probe, _ in bench.CEILING_PROBES.values()} == set(bench.KINDS)
+
+
+def test_ceiling_library_exports_its_entry_point():
+    import ctypes
+
+    if not os.path.exists(bench.CEILING_LIB):
+        bench.build_ceiling()
+    lib = ctypes.CDLL(bench.CEILING_LIB)
+    assert hasattr(lib, "hsc_run")
+    # argument checks run on the host, before any launch
+    run = bench.load_ceiling().hsc_run
+    assert run(7, None, None, None, None, 0, 0, 0, None) == -1       # unknown kind
+    assert run(3, None, None, None, None, 6, 0, 0, None) == -1       # cast needs n % 4 == 0
+    assert run(0, None, None, None, None, -1, 0, 0, None) == -1      # negative size
+    assert run(2, None, None, None, None, 0, 0, 5, None) == 0        # empty: no launch
