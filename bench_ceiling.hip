@@ -12,8 +12,10 @@
 //          pair kernel (qknorm_rope)
 //   cast   f32 rows in, f16 rows out, contiguous   (assembly's byte mix)
 //
-// Loads and stores are the library's streaming (non-temporal) forms. Not
-// part of libheadshot_hip: built into bench_ceiling.so next to bench.py.
+// Each kernel runs with non-temporal (streaming) or ordinary cached loads and
+// stores, the two policies the library's kernels use; the bench takes the
+// faster as the ceiling. Not part of libheadshot_hip: built into
+// bench_ceiling.so next to bench.py.
 #include "hs_common.hpp"
 
 namespace {
@@ -24,8 +26,20 @@ using hs::u32x4;
 constexpr int kBlock = 256;
 constexpr int kUnroll = 4;  // 16-byte vectors per lane
 
+template <bool NT, typename V>
+__device__ __forceinline__ V ld(const V* p) {
+    if constexpr (NT) return __builtin_nontemporal_load(p);
+    else return *p;
+}
+template <bool NT, typename V>
+__device__ __forceinline__ void st(V* p, V v) {
+    if constexpr (NT) __builtin_nontemporal_store(v, p);
+    else *p = v;
+}
+
 // Vectors [w * 256, w * 256 + 256) for wave w: four wave-contiguous 1 KiB
 // pieces per wave.
+template <bool NT>
 __global__ __launch_bounds__(kBlock) void copy_kernel(const u32x4* __restrict__ a,
                                                       u32x4* __restrict__ o, int64_t n) {
     const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kUnroll +
@@ -33,12 +47,13 @@ __global__ __launch_bounds__(kBlock) void copy_kernel(const u32x4* __restrict__ 
     u32x4 r[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; u++)
-        if (base + u * 64 < n) r[u] = hs::ld_stream(a + base + u * 64);
+        if (base + u * 64 < n) r[u] = ld<NT>(a + base + u * 64);
 #pragma unroll
     for (int u = 0; u < kUnroll; u++)
-        if (base + u * 64 < n) hs::st_stream(o + base + u * 64, r[u]);
+        if (base + u * 64 < n) st<NT>(o + base + u * 64, r[u]);
 }
 
+template <bool NT>
 __global__ __launch_bounds__(kBlock) void add2_kernel(const u32x4* __restrict__ a,
                                                       const u32x4* __restrict__ b,
                                                       u32x4* __restrict__ o, int64_t n) {
@@ -47,15 +62,16 @@ __global__ __launch_bounds__(kBlock) void add2_kernel(const u32x4* __restrict__ 
     u32x4 ra[kUnroll], rb[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; u++)
-        if (base + u * 64 < n) ra[u] = hs::ld_stream(a + base + u * 64), rb[u] = hs::ld_stream(b + base + u * 64);
+        if (base + u * 64 < n) ra[u] = ld<NT>(a + base + u * 64), rb[u] = ld<NT>(b + base + u * 64);
 #pragma unroll
     for (int u = 0; u < kUnroll; u++)
-        if (base + u * 64 < n) hs::st_stream(o + base + u * 64, ra[u] + rb[u]);
+        if (base + u * 64 < n) st<NT>(o + base + u * 64, ra[u] + rb[u]);
 }
 
 // Two tensors: waves [0, W) copy the first, [W, 2W) the second, W =
 // ceil(tokens / 2). A load covers one token's 8 heads (1 KiB contiguous),
 // a store writes those 8 heads' vectors to their head-major rows.
+template <bool NT>
 __global__ __launch_bounds__(kBlock) void heads_kernel(const f16* __restrict__ x0,
                                                        const f16* __restrict__ x1,
                                                        f16* __restrict__ o0, f16* __restrict__ o1,
@@ -74,7 +90,7 @@ __global__ __launch_bounds__(kBlock) void heads_kernel(const f16* __restrict__ x
     for (int k = 0; k < K; k++)
 #pragma unroll
         for (int c = 0; c < 2; c++)
-            if (u0 + k < tokens) r[k][c] = hs::ld_stream(x + (u0 + k) * (H * D) + (c * 8 + gsub) * D + ch);
+            if (u0 + k < tokens) r[k][c] = ld<NT>(reinterpret_cast<const u32x4*>(x + (u0 + k) * (H * D) + (c * 8 + gsub) * D + ch));
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const int64_t tok = u0 + k;
@@ -82,11 +98,12 @@ __global__ __launch_bounds__(kBlock) void heads_kernel(const f16* __restrict__ x
         const int64_t s = tok / seq, t = tok - s * seq;
 #pragma unroll
         for (int c = 0; c < 2; c++)
-            hs::st_stream(o + ((s * H + c * 8 + gsub) * seq + t) * D + ch, r[k][c]);
+            st<NT>(reinterpret_cast<u32x4*>(o + ((s * H + c * 8 + gsub) * seq + t) * D + ch), r[k][c]);
     }
 }
 
 // n f32 -> f16, four elements (16 bytes in, 8 out) per lane per step.
+template <bool NT>
 __global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ a,
                                                       f16* __restrict__ o, int64_t n) {
     const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kUnroll +
@@ -94,7 +111,7 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ 
     u32x4 r[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; u++)
-        if ((base + u * 64) * 4 < n) r[u] = hs::ld_stream(a + (base + u * 64) * 4);
+        if ((base + u * 64) * 4 < n) r[u] = ld<NT>(reinterpret_cast<const u32x4*>(a + (base + u * 64) * 4));
 #pragma unroll
     for (int u = 0; u < kUnroll; u++) {
         if ((base + u * 64) * 4 >= n) continue;
@@ -103,24 +120,15 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ 
         hi.x = static_cast<f16>(hs::u2f(r[u][2])), hi.y = static_cast<f16>(hs::u2f(r[u][3]));
         hs::u32x2 v;
         v[0] = hs::h22u(lo), v[1] = hs::h22u(hi);
-        hs::st_stream_as(reinterpret_cast<hs::u32x2*>(o + (base + u * 64) * 4), v);
+        st<NT>(reinterpret_cast<hs::u32x2*>(o + (base + u * 64) * 4), v);
     }
 }
 
 int64_t blocks_for(int64_t lanes_work) { return (lanes_work + kBlock - 1) / kBlock; }
 
-}  // namespace
-
-extern "C" {
-
-// kind 0 copy / 1 add2: n 16-byte vectors (a, b -> o). kind 2 heads: s
-// frames of t tokens, a and b -> o and o2. kind 3 cast: n f32 elements
-// (n % 4 == 0). Buffers are 16-byte aligned and sized by the caller.
-// Returns 0, or -1 for an argument the kernels do not take, or the HIP
-// error code of the launch.
-int hsc_run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n, int32_t s,
-            int32_t t, hipStream_t stream) {
-    if (n < 0 || s < 0 || t < 0) return -1;
+template <bool NT>
+int run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n, int32_t s,
+        int32_t t, hipStream_t stream) {
     switch (kind) {
         case 0:
         case 1: {
@@ -128,10 +136,10 @@ int hsc_run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n
             if (blocks == 0) return 0;
             if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
             if (kind == 0)
-                copy_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                copy_kernel<NT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                     static_cast<const u32x4*>(a), static_cast<u32x4*>(o), n);
             else
-                add2_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                add2_kernel<NT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                     static_cast<const u32x4*>(a), static_cast<const u32x4*>(b),
                     static_cast<u32x4*>(o), n);
             break;
@@ -142,7 +150,7 @@ int hsc_run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n
             const int64_t blocks = (waves + 3) / 4;
             if (blocks == 0) return 0;
             if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
-            heads_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+            heads_kernel<NT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                 static_cast<const f16*>(a), static_cast<const f16*>(b), static_cast<f16*>(o),
                 static_cast<f16*>(o2), tokens, t);
             break;
@@ -152,7 +160,7 @@ int hsc_run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n
             const int64_t blocks = blocks_for((n / 4 + kUnroll - 1) / kUnroll);
             if (blocks == 0) return 0;
             if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
-            cast_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+            cast_kernel<NT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                 static_cast<const float*>(a), static_cast<f16*>(o), n);
             break;
         }
@@ -160,6 +168,22 @@ int hsc_run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n
             return -1;
     }
     return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" {
+
+// kind 0 copy / 1 add2: n 16-byte vectors (a, b -> o). kind 2 heads: s
+// frames of t tokens, a and b -> o and o2. kind 3 cast: n f32 elements
+// (n % 4 == 0). temporal: 0 non-temporal loads and stores, 1 cached.
+// Buffers are 16-byte aligned and sized by the caller. Returns 0, or -1 for
+// an argument the kernels do not take, or the HIP error code of the launch.
+int hsc_run(int kind, int temporal, const void* a, const void* b, void* o, void* o2, int64_t n,
+            int32_t s, int32_t t, hipStream_t stream) {
+    if (n < 0 || s < 0 || t < 0 || (temporal != 0 && temporal != 1)) return -1;
+    return temporal ? run<false>(kind, a, b, o, o2, n, s, t, stream)
+                    : run<true>(kind, a, b, o, o2, n, s, t, stream);
 }
 
 }  // extern "C"

@@ -1,6 +1,7 @@
 """bench.py's data-movement probes (bench_ceiling.hip) move what they claim:
-each is checked exactly against torch on a small shape, so a ceiling the
-bench reports is the rate of a kernel that did the op's data movement."""
+each is checked exactly against torch on a small shape under both load/store
+policies, so a ceiling the bench reports is the rate of a kernel that did
+the op's data movement."""
 import os
 
 import pytest
@@ -9,6 +10,7 @@ import torch
 import bench
 
 pytestmark = pytest.mark.gpu
+POLICIES = [0, 1]  # streaming, cached
 
 
 @pytest.fixture(scope="module")
@@ -17,44 +19,50 @@ def lib():
     return bench.load_ceiling()
 
 
-def _run(lib, kind, a, b, o, o2, n, s, t):
+def _run(lib, kind, temporal, a, b, o, o2, n, s, t):
     ptr = lambda x: None if x is None else x.data_ptr()  # noqa: E731
-    rc = lib.hsc_run(bench.KINDS[kind], ptr(a), ptr(b), ptr(o), ptr(o2), n, s, t,
+    for out in (o, o2):
+        if out is not None:
+            out.zero_()
+    rc = lib.hsc_run(bench.KINDS[kind], temporal, ptr(a), ptr(b), ptr(o), ptr(o2), n, s, t,
                      torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert rc == 0
 
 
+@pytest.mark.parametrize("temporal", POLICIES)
 @pytest.mark.parametrize("rows", [1, 37, 1374])
-def test_copy_and_add2(lib, rows):
+def test_copy_and_add2(lib, rows, temporal):
     g = torch.Generator(device="cuda").manual_seed(rows)
     a = torch.randint(-2**31, 2**31 - 1, (rows, 512), device="cuda", dtype=torch.int32, generator=g)
     b = torch.randint(-2**31, 2**31 - 1, (rows, 512), device="cuda", dtype=torch.int32, generator=g)
-    o = torch.zeros_like(a)
+    o = torch.empty_like(a)
     n = a.numel() // 4
-    _run(lib, "copy", a, None, o, None, n, 0, 0)
+    _run(lib, "copy", temporal, a, None, o, None, n, 0, 0)
     assert torch.equal(o, a)
-    _run(lib, "add2", a, b, o, None, n, 0, 0)
-    want = ((a.to(torch.int64) + b.to(torch.int64)) & 0xFFFFFFFF)
+    _run(lib, "add2", temporal, a, b, o, None, n, 0, 0)
+    want = (a.to(torch.int64) + b.to(torch.int64)) & 0xFFFFFFFF
     want = torch.where(want >= 2**31, want - 2**32, want).to(torch.int32)
     assert torch.equal(o, want)
 
 
+@pytest.mark.parametrize("temporal", POLICIES)
 @pytest.mark.parametrize("s,t", [(1, 1), (2, 11), (3, 1374)])
-def test_heads_is_the_head_split(lib, s, t):
+def test_heads_is_the_head_split(lib, s, t, temporal):
     g = torch.Generator(device="cuda").manual_seed(t)
     q = torch.randn((s * t, 1024), device="cuda", generator=g).half()
     k = torch.randn((s * t, 1024), device="cuda", generator=g).half()
-    oq, ok = torch.zeros_like(q), torch.zeros_like(k)
-    _run(lib, "heads", q, k, oq, ok, 0, s, t)
+    oq, ok = torch.empty_like(q), torch.empty_like(k)
+    _run(lib, "heads", temporal, q, k, oq, ok, 0, s, t)
     split = lambda x: x.view(s, t, 16, 64).permute(0, 2, 1, 3).contiguous().view(-1, 1024)  # noqa: E731
     assert torch.equal(oq, split(q)) and torch.equal(ok, split(k))
 
 
+@pytest.mark.parametrize("temporal", POLICIES)
 @pytest.mark.parametrize("n", [4, 1024 * 37, 1369 * 1024 * 2])
-def test_cast(lib, n):
+def test_cast(lib, n, temporal):
     g = torch.Generator(device="cuda").manual_seed(n)
     x = torch.randn(n, device="cuda", generator=g) * 100
-    o = torch.zeros(n, device="cuda", dtype=torch.float16)
-    _run(lib, "cast", x, None, o, None, n, 0, 0)
+    o = torch.empty(n, device="cuda", dtype=torch.float16)
+    _run(lib, "cast", temporal, x, None, o, None, n, 0, 0)
     assert torch.equal(o, x.half())
