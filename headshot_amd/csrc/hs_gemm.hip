@@ -23,7 +23,10 @@
 // columns of one output row. The epilogue adds the bias (and applies GELU)
 // there, stages the f16 results through LDS, and then streams whole rows:
 // 16-byte reads of the residual and 16-byte writes of out. Rows past M are
-// clamped on load and masked on store.
+// clamped on load and masked on store. The writes are non-temporal: every
+// workgroup of a round stores its tile at about the same time, and streaming
+// stores drain that burst faster than write-allocating ones (fc1 + GELU at
+// S=32: 494 us against 523).
 //
 // Generic path (f32, or shapes the fast path does not cover): a tiled
 // scalar kernel, f32 accumulation in K order.
@@ -243,7 +246,7 @@ __device__ __forceinline__ void qkv_heads_out(const f16* stage, const QkvArgs& q
             qk_norm_rope_vec<f16, 8, true>(f, wr, br, qa.eps, rot, cs, sn);
         else
             qk_norm_rope_vec<f16, 8, false>(f, wr, br, qa.eps, rot, cs, sn);
-        st16(obase + (static_cast<int64_t>(s) * qa.heads * qa.seq + t) * 64, pack(f, f16{}));
+        st16_nt(obase + (static_cast<int64_t>(s) * qa.heads * qa.seq + t) * 64, pack(f, f16{}));
         m += 8;
         t += 8;
         while (t >= qa.seq) t -= qa.seq, s++;
@@ -426,7 +429,7 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
                               fmaf(gg[2 * q + 1], static_cast<float>(xv.y), static_cast<float>(rv.y)));
             }
         }
-        st16(out + m * N + n, v);
+        st16_nt(out + m * N + n, v);
     }
 }
 

@@ -193,7 +193,8 @@ __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
     if constexpr (ROPE) {
         float4* slice = tab_lds[wave_in_block()];
 #pragma unroll
-        for (int i = lane; i < K * 2 * 64 / 4; i += 64) {
+        for (int i0 = 0; i0 < K * 2 * 64 / 4; i0 += 64) {
+            const int i = i0 + lane;
             const int k = i / 32, which_tab = (i / 16) & 1, off = (i & 15) * 4;
             const int64_t tok = u0 + k;
             if (tok < u_end) {
