@@ -234,7 +234,9 @@ CEILING_PROBES = {
     "bias_ls_residual": ("add2", "two rows x 1024 f16 read, one written, contiguous"),
     "qknorm_rope": ("heads", "q and k, rows x 1024 f16 each, token-major in, head-major out, "
                              "the pair kernel's addressing (a wave per 2 tokens, 8 heads' "
-                             "128-byte vectors per store)"),
+                             "128-byte vectors per store); the mean of the frame-block "
+                             "layout (S frames of T) and the global-block layout (one "
+                             "sequence of S*T), as the pass runs 24 of each"),
     "assemble": ("cast", "S*P x 1024 f32 read, f16 written, contiguous (positional table "
                          "and prefix rows not included)"),
 }
@@ -288,12 +290,8 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
     def ptrs(bufs):
         return tuple(None if x is None else x.data_ptr() for x in bufs[:4])
 
-    out = {}
-    for op, (probe, what) in CEILING_PROBES.items():
-        first = buffers(op, probe)
-        nbytes, args = first[4], first[5]
-        sets = [first] + [buffers(op, probe) for _ in range(max(1, -(-ROTATE_BYTES // nbytes)) - 1)]
-
+    def timed(probe, args, sets):
+        """(warm us per policy, cold us) of one probe launch shape."""
         def launch(temporal, bufs):
             rc = lib.hsc_run(KINDS[probe], temporal, *bufs, *args, stream)
             if rc != 0:
@@ -316,10 +314,25 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
         for a, b in ev:
             flush()
             a.record()
-            launch(0, ptrs(first))
+            launch(0, ptrs(sets[0]))
             b.record()
         torch.cuda.synchronize()
-        cold_us = sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3
+        return warm, sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3
+
+    out = {}
+    for op, (probe, what) in CEILING_PROBES.items():
+        first = buffers(op, probe)
+        nbytes, args = first[4], first[5]
+        sets = [first] + [buffers(op, probe) for _ in range(max(1, -(-ROTATE_BYTES // nbytes)) - 1)]
+        warm, cold_us = timed(probe, args, sets)
+        layouts = None
+        if probe == "heads":
+            # the pass's global blocks: one sequence of S*T tokens
+            gwarm, gcold = timed(probe, (0, 1, frames * t), sets)
+            layouts = {"frame_us": round(min(warm.values()), 2), "frame_cold_us": round(cold_us, 2),
+                       "global_us": round(min(gwarm.values()), 2), "global_cold_us": round(gcold, 2)}
+            warm = {k: (warm[k] + gwarm[k]) / 2 for k in warm}
+            cold_us = (cold_us + gcold) / 2
         policy = min(warm, key=warm.get)
         us = warm[policy]
         gbs, cold_gbs = nbytes / us / 1e3, nbytes / cold_us / 1e3
@@ -328,6 +341,8 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
                  "policy": policy,
                  "cold_us": round(cold_us, 2), "cold_GB/s": round(cold_gbs, 1),
                  "cold_frac": round(cold_gbs / PEAK_GBS, 4)}
+        if layouts:
+            entry["layouts"] = layouts
         if op_warm:
             entry["op_frac_of_probe"] = round(op_warm[op]["GB/s"] / gbs, 4)
         if op_cold:
