@@ -905,7 +905,8 @@ def summarize_counters(paths) -> None:
     """Per matrix-core kernel and launch shape, the mean of each shader
     counter over its dispatches, and ratios derived from them (MI355X: 8
     XCDs, 256 CUs, 1024 SIMDs; rocprofv3 reports GRBM_GUI_ACTIVE summed over
-    the XCDs, so one XCD's busy cycles are an eighth of it)."""
+    the XCDs, so one XCD's busy cycles are an eighth of it, and that over the
+    dispatch's duration is the clock the kernel ran at)."""
     import csv
     import statistics as st
     from collections import defaultdict
@@ -926,9 +927,11 @@ def summarize_counters(paths) -> None:
             key = (op, int(r["Grid_Size"]))
             vals[key][r["Counter_Name"]].append(float(r["Counter_Value"]))
             dur[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9)
-    out = ["| kernel | grid work-items | dispatches | matrix core busy | VALU co-issue with MFMA "
+    out = ["| kernel | grid work-items | dispatches | mean us | shader clock GHz "
+           "| matrix core busy | VALU co-issue with MFMA "
            "| cycles / MFMA | VALU / MFMA | transcendental / MFMA | LDS busy "
-           "| bank-conflict cycles / LDS instr |", "|---|---|---|---|---|---|---|---|---|---|"]
+           "| bank-conflict cycles / LDS instr |",
+           "|---|---|---|---|---|---|---|---|---|---|---|---|"]
     for key in sorted(vals):
         c = {k: st.mean(v) for k, v in vals[key].items()}
         cyc = c.get("GRBM_GUI_ACTIVE", 0.0) / 8.0
@@ -941,8 +944,10 @@ def summarize_counters(paths) -> None:
             except (KeyError, ZeroDivisionError):
                 return "-"
         mf = c.get("SQ_INSTS_MFMA", 0.0)
+        mean_s = st.mean(dur[key])
         out.append("| " + " | ".join([
             key[0], str(key[1]), str(len(dur[key]) // max(1, len(vals[key]))),
+            format(mean_s * 1e6, ".1f"), format(cyc / mean_s / 1e9, ".2f"),
             f(lambda: c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * 1024), ".1%"),
             f(lambda: c["SQ_VALU_MFMA_COEXEC_CYCLES"] / (cyc * 1024), ".1%"),
             f(lambda: c["SQ_VALU_MFMA_BUSY_CYCLES"] / mf, ".1f"),
