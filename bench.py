@@ -443,8 +443,10 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
     heads, QK-norm and RoPE of a frame block), proj (bias + LayerScale +
     residual), fc1 (bias + exact GELU), fc2 (bias + LayerScale + residual).
     flops = 2*m*n*k. For reference the same shapes' plain product through
-    torch (the ROCm BLAS library, no bias or epilogue) is timed beside them;
-    it is not part of this library."""
+    torch (the ROCm BLAS library, no bias or epilogue) is timed beside them
+    (not part of this library), and so is this library's standalone op that
+    each fused epilogue replaces, so library_plus_op_ms is the unfused
+    alternative."""
     from headshot_amd import rope as _rope
     import torch
 
@@ -487,10 +489,28 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
         call = ctx.last_launch
         ms = timed(call)
         ms_lib = timed(lambda: torch.nn.functional.linear(x, w))
+        # the standalone op that the fused epilogue replaces, on a product-
+        # shaped input: the q and k heads (QK-norm + RoPE pair), LayerScale +
+        # residual, or bias + GELU
+        y = torch.randn((m, DIM if name == "qkv" else n), generator=g).half().to(ctx.device)
+        if name == "qkv":
+            y2 = torch.randn((m, DIM), generator=g).half().to(ctx.device)
+            ctx.qknorm_rope_pair(y, y2, frames, t, HEADS, HEAD_DIM, qn=nrm, kn=nrm,
+                                 rope=(sin, cos, PREFIX), eps=EPS, out_q=qkv[0], out_k=qkv[1])
+            op_name = "qknorm_rope_pair"
+        elif name == "fc1":
+            ctx.bias_gelu(y, b, out=o)
+            op_name = "bias_gelu"
+        else:
+            ctx.bias_ls_residual(res, y, gam, b, out=o)
+            op_name = "bias_ls_residual"
+        ms_op = timed(ctx.last_launch)
         fl = 2.0 * m * n * k
         tf = fl / (ms * 1e-3) / 1e12
         out[name] = {"m": m, "n": n, "k": k, "ms": round(ms, 3), "TFLOP/s": round(tf, 1),
-                     "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "library_gemm_ms": round(ms_lib, 3)}
+                     "frac": round(tf / MFMA_PEAK_TFLOPS, 4), "library_gemm_ms": round(ms_lib, 3),
+                     "standalone_op": op_name, "standalone_op_ms": round(ms_op, 3),
+                     "library_plus_op_ms": round(ms_lib + ms_op, 3)}
         total_ms += ms
         del x, w, o
     out["ms_per_block"] = round(total_ms, 3)
