@@ -573,6 +573,79 @@ class HipContext {
         return out;
     }
 
+    // A linear layer with the LayerNorm before it folded in (LN1 -> q|k|v,
+    // model/block.rs:128-131; LN2 -> fc1, :153-173): w_fold = (w * ln_w)
+    // rounded to w's storage type, colsum = each folded row's sum, shift =
+    // w ln_b + bias. Prepared once, at load time.
+    struct FoldedLinear {
+        HipTensor w_fold, colsum, shift;
+    };
+    FoldedLinear fold_layernorm(const HipTensor& w, const HipTensor* bias, const HipTensor& ln_w,
+                                const HipTensor& ln_b) const {
+        HS_REQUIRE(w.shape().size() == 2, "fold_layernorm: weight must be (n, k)");
+        const size_t n = w.shape()[0], k = w.shape()[1];
+        HS_REQUIRE(ln_w.dtype() == Dtype::F32 && ln_w.len() == k && ln_b.dtype() == Dtype::F32 &&
+                       ln_b.len() == k,
+                   "fold_layernorm: norm parameters must be f32 (k)");
+        HS_REQUIRE(!bias || (bias->dtype() == Dtype::F32 && bias->len() == n),
+                   "fold_layernorm: bias must be f32 (n)");
+        FoldedLinear f{empty_typed({n, k}, w.dtype()), empty_typed({n}, Dtype::F32),
+                       empty_typed({n}, Dtype::F32)};
+        check(hs_fold_layernorm(stream_, hs_dtype(w.dtype()), w.data(), bias ? bias->f32() : nullptr,
+                                ln_w.f32(), ln_b.f32(), f.w_fold.data(),
+                                static_cast<float*>(f.colsum.data()),
+                                static_cast<float*>(f.shift.data()), i32(n), i32(k)),
+              "fold_layernorm");
+        return f;
+    }
+
+    // linear(layernorm(x)) on folded weights; the row statistics go to a
+    // workspace owned by the call.
+    HipTensor linear_ln(const HipTensor& x, const FoldedLinear& f, float eps = 1e-5f) const {
+        return folded_call(x, f, eps, false);
+    }
+    // gelu(linear(layernorm(x))): LN2, fc1 with its bias, GELU
+    HipTensor linear_ln_gelu(const HipTensor& x, const FoldedLinear& f, float eps = 1e-5f) const {
+        return folded_call(x, f, eps, true);
+    }
+    // LN1 and the q|k|v projection with heads, QK-norm and RoPE
+    // (model/block.rs:128-146) on the folded q|k|v weight (f16, d = 64)
+    Qkv linear_ln_qkv_heads(const HipTensor& x, const FoldedLinear& f, size_t s, size_t t, size_t h,
+                            const Norm* qn, const Norm* kn, const Rope* rope,
+                            float eps = 1e-5f) const {
+        const auto& sh = f.w_fold.shape();
+        HS_REQUIRE(sh.size() == 2 && sh[0] % (3 * h) == 0, "w_fold shape");
+        const size_t n3 = sh[0], k = sh[1], d = n3 / (3 * h);
+        HS_REQUIRE(x.len() == s * t * k && x.dtype() == f.w_fold.dtype(), "x shape/dtype");
+        const float *qw = nullptr, *qb = nullptr, *kw = nullptr, *kb = nullptr;
+        const float *sn = nullptr, *cs = nullptr;
+        size_t prefix = 0;
+        for (const auto& [n, w, b] : {std::tuple{qn, &qw, &qb}, std::tuple{kn, &kw, &kb}}) {
+            if (!n) continue;
+            HS_REQUIRE(n->weight->len() == d && n->bias->len() == d, "qk-norm length");
+            HS_REQUIRE(n->weight->dtype() == Dtype::F32 && n->bias->dtype() == Dtype::F32,
+                       "qk-norm parameters must be f32");
+            *w = n->weight->f32(), *b = n->bias->f32();
+        }
+        if (rope) {
+            prefix = rope->prefix;
+            HS_REQUIRE(prefix <= t, "prefix");
+            HS_REQUIRE(rope->sin->len() == (t - prefix) * d && rope->cos->len() == rope->sin->len(),
+                       "table size");
+            sn = rope->sin->f32(), cs = rope->cos->f32();
+        }
+        HipTensor ws = empty_typed({2 * s * t}, Dtype::F32);
+        Qkv out{empty_typed({s, h, t, d}, x.dtype()), empty_typed({s, h, t, d}, x.dtype()),
+                empty_typed({s, h, t, d}, x.dtype())};
+        check(hs_linear_ln_qkv_heads(stream_, hs_dtype(x.dtype()), x.data(), f.w_fold.data(),
+                                     f.colsum.f32(), f.shift.f32(), qw, qb, kw, kb, sn, cs,
+                                     static_cast<float*>(ws.data()), out.q.data(), out.k.data(),
+                                     out.v.data(), i32(s), i32(t), i32(h), i32(d), i32(k),
+                                     i32(prefix), eps),
+              "linear_ln_qkv_heads");
+        return out;
+    }
+
     // fc1 bias epilogue + GELU (model/block.rs:173-174)
     HipTensor bias_gelu(const HipTensor& x, const HipTensor* bias) const {
         const size_t cols = x.last();
@@ -622,6 +695,23 @@ class HipContext {
 
    private:
     static ::hs_dtype hs_dtype(Dtype dt) { return static_cast<::hs_dtype>(static_cast<int>(dt)); }
+    HipTensor folded_call(const HipTensor& x, const FoldedLinear& f, float eps, bool gelu) const {
+        const auto& sh = f.w_fold.shape();
+        HS_REQUIRE(sh.size() == 2, "w_fold must be (n, k)");
+        const size_t n = sh[0], k = sh[1];
+        HS_REQUIRE(x.last() == k && x.dtype() == f.w_fold.dtype(),
+                   "x must be (m, k) in w_fold's dtype");
+        const size_t m = x.len() / k;
+        HS_REQUIRE(f.colsum.len() == n && f.shift.len() == n, "colsum/shift length");
+        HipTensor ws = empty_typed({2 * m}, Dtype::F32);
+        HipTensor out = empty_typed({m, n}, x.dtype());
+        check((gelu ? hs_linear_ln_gelu : hs_linear_ln)(
+                  stream_, hs_dtype(x.dtype()), x.data(), f.w_fold.data(), f.colsum.f32(),
+                  f.shift.f32(), static_cast<float*>(ws.data()), out.data(),
+                  static_cast<int64_t>(m), i32(n), i32(k), eps),
+              gelu ? "linear_ln_gelu" : "linear_ln");
+        return out;
+    }
     static void linear_shape(const HipTensor& x, const HipTensor& w, const HipTensor* bias, size_t& m,
                              size_t& n, size_t& k) {
         k = x.last();

@@ -434,6 +434,71 @@ void qknorm_rope_pair_equals_two_calls(HipContext& ctx) {
         }
 }
 
+// The LayerNorm folded into the product == layernorm then the product:
+// f32 within f32 summation error; f16 within twice the f16 gate (the fold
+// rounds w * gamma once where the sequence rounds the normalised row), and
+// the same for the GELU and q|k|v-heads forms.
+void folded_layernorm_equals_sequence(HipContext& ctx) {
+    auto twice_gate = [](const std::vector<float>& a, const std::vector<float>& e, const std::string& what) {
+        if (a.size() != e.size()) throw Failure(what + ": length");
+        for (size_t i = 0; i < a.size(); i++)
+            if (!(std::fabs(a[i] - e[i]) <= 4e-3f * std::fmax(1.0f, std::fabs(e[i]))))
+                throw Failure(what + "[" + std::to_string(i) + "]: got " + std::to_string(a[i]) +
+                              ", want " + std::to_string(e[i]));
+    };
+    for (auto [m, k, n] : {std::array<size_t, 3>{37, 128, 256}, std::array<size_t, 3>{19, 96, 48}}) {
+        Rng rng{17 + n};
+        auto x = rng.vec(m * k), w = rng.vec(n * k), b = rng.vec(n), g = rng.vec(k), be = rng.vec(k);
+        for (auto& e : w) e *= 0.1f;
+        for (auto& e : g) e = 1.0f + 0.1f * e;
+        for (auto& e : be) e *= 0.1f;
+        auto gg = ctx.tensor_from_slice({k}, g), gbe = ctx.tensor_from_slice({k}, be);
+        auto gb = ctx.tensor_from_slice({n}, b);
+        for (Dtype dt : {Dtype::F32, Dtype::F16}) {
+            auto gx = ctx.tensor_from_f32({m, k}, x, dt), gw = ctx.tensor_from_f32({n, k}, w, dt);
+            auto f = ctx.fold_layernorm(gw, &gb, gg, gbe);
+            auto seq = ctx.linear(ctx.layernorm(gx, gg, gbe, 1e-6f), gw, &gb);
+            auto got = ctx.download(ctx.linear_ln(gx, f, 1e-6f));
+            auto want = ctx.download(seq);
+            auto got_g = ctx.download(ctx.linear_ln_gelu(gx, f, 1e-6f));
+            auto want_g = ctx.download(ctx.gelu(seq));
+            if (dt == Dtype::F32) {
+                assert_close(got, want, 1e-4f, "linear_ln f32");
+                assert_close(got_g, want_g, 1e-4f, "linear_ln_gelu f32");
+            } else {
+                twice_gate(got, want, "linear_ln f16");
+                twice_gate(got_g, want_g, "linear_ln_gelu f16");
+            }
+        }
+    }
+    // LN1 + q|k|v with heads, QK-norm and RoPE == layernorm then linear_qkv_heads.
+    // Zero-mean weights and bias, as trained projections are: a common offset
+    // in every head vector would let the QK-norm's mean removal magnify the
+    // two forms' rounding difference far beyond what real layers see.
+    Rng rng{23};
+    const size_t s = 2, h = 16, d = 64, prefix = 5, t = 6 + prefix, k = 128, n3 = 3 * h * d;
+    auto x = rng.vec(s * t * k), w = rng.vec(n3 * k), b = rng.vec(n3), g = rng.vec(k), be = rng.vec(k);
+    for (auto& e : w) e = 0.1f * (e - 1.0f);
+    for (auto& e : b) e = 0.1f * (e - 1.0f);
+    for (auto& e : g) e = 1.0f + 0.1f * e;
+    for (auto& e : be) e *= 0.1f;
+    auto [sin, cos] = hs::rope::tables(hs::rope::periods(), 2, 3);
+    auto nw = ctx.tensor_from_slice({d}, rng.vec(d)), nb = ctx.tensor_from_slice({d}, rng.vec(d));
+    auto st = ctx.tensor_from_slice({t - prefix, d}, sin), ct = ctx.tensor_from_slice({t - prefix, d}, cos);
+    hs::Norm norm{&nw, &nb};
+    hs::Rope rope{&st, &ct, prefix};
+    auto gg = ctx.tensor_from_slice({k}, g), gbe = ctx.tensor_from_slice({k}, be);
+    auto gb = ctx.tensor_from_slice({n3}, b);
+    auto gx = ctx.tensor_from_f32({s * t, k}, x, Dtype::F16), gw = ctx.tensor_from_f32({n3, k}, w, Dtype::F16);
+    auto f = ctx.fold_layernorm(gw, &gb, gg, gbe);
+    auto fused = ctx.linear_ln_qkv_heads(gx, f, s, t, h, &norm, &norm, &rope, 1e-6f);
+    auto seq = ctx.linear_qkv_heads(ctx.layernorm(gx, gg, gbe, 1e-6f), gw, &gb, s, t, h, &norm, &norm,
+                                    &rope, 1e-6f);
+    twice_gate(ctx.download(fused.q), ctx.download(seq.q), "linear_ln_qkv_heads q");
+    twice_gate(ctx.download(fused.k), ctx.download(seq.k), "linear_ln_qkv_heads k");
+    twice_gate(ctx.download(fused.v), ctx.download(seq.v), "linear_ln_qkv_heads v");
+}
+
 void contract_violations_throw(HipContext& ctx) {
     auto x = ctx.tensor_from_slice({4, 8}, std::vector<float>(32, 1.0f));
     auto w = ctx.tensor_from_slice({7}, std::vector<float>(7, 1.0f));
@@ -471,6 +536,7 @@ int main(int argc, char** argv) {
         {"linear_matches_cpu", linear_matches_cpu},
         {"qkv_heads_equal_sequence", qkv_heads_equal_sequence},
         {"qknorm_rope_pair_equals_two_calls", qknorm_rope_pair_equals_two_calls},
+        {"folded_layernorm_equals_sequence", folded_layernorm_equals_sequence},
         {"contract_violations_throw", contract_violations_throw},
     };
     HipContext ctx;
