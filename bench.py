@@ -627,7 +627,9 @@ def trunk_times(ctx, frames: int, iters: int) -> dict:
     register gather/scatter and the 4 head-input caches. Random-init f16
     weights in the checkpoint's layout (fused q|k|v), generated on the
     device. Beside it the reference's dispatch sequence through the same
-    library's single ops (Trunk.forward(fused=False))."""
+    library's single ops (Trunk.forward(fused=False)), and the fused trunk
+    with every block's LayerNorms folded into the products after them
+    (Trunk.forward(fold_ln=True))."""
     import torch
 
     from headshot_amd.aggregator import BlockWeights
@@ -645,13 +647,15 @@ def trunk_times(ctx, frames: int, iters: int) -> dict:
     p = GRID[0] * GRID[1]
     tokens = torch.randn((frames * p, TDIM), generator=gen, device=ctx.device)
     out = {"frames": frames, "tokens_per_frame": p + 17}
-    for name, fused in (("fused", True), ("reference_sequence", False)):
-        trunk.forward(ctx, tokens, frames, *GRID, fused=fused)
+    trunk.fold_layernorms(ctx)
+    for name, fused, fold in (("fused", True, False), ("reference_sequence", False, False),
+                              ("fused_layernorm_folded", True, True)):
+        trunk.forward(ctx, tokens, frames, *GRID, fused=fused, fold_ln=fold)
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(iters):
-            trunk.forward(ctx, tokens, frames, *GRID, fused=fused)
+            trunk.forward(ctx, tokens, frames, *GRID, fused=fused, fold_ln=fold)
         b.record()
         torch.cuda.synchronize()
         out[name + "_ms"] = round(a.elapsed_time(b) / iters, 1)

@@ -448,11 +448,24 @@ class HipContext:
                             kn=None, rope=None, eps: float = 1e-5, out=None, workspace=None):
         """LN1 + the q|k|v projection with split_heads, QK-norm and RoPE
         (model/block.rs:128-146) on the folded q|k|v weight: returns
-        head-major (q, k, v). ``eps`` serves both norms."""
+        head-major (q, k, v). ``eps`` serves both norms. Shapes the fused
+        kernel does not cover (f32, head dim other than 64) run
+        ``linear_ln`` then ``qknorm_rope`` per third."""
         m, n3, k, (w, cs, sh, ws) = self._folded_args(x, folded, workspace)
         assert m == s * t, "x rows must be S*T"
         assert n3 % (3 * h) == 0, "w_fold rows must be 3 * H * d"
         d = n3 // (3 * h)
+        hd = h * d
+        if not (x.dtype == F16 and d == 64 and n3 % 256 == 0 and k % 64 == 0):
+            outs = []
+            for i, norm in enumerate((qn, kn, None)):
+                rows = slice(i * hd, (i + 1) * hd)
+                third = FoldedLinear(folded.w_fold[rows], folded.colsum[rows], folded.shift[rows])
+                proj = self.linear_ln(x, third, eps=eps, workspace=workspace)
+                outs.append(self.qknorm_rope(proj, s, t, h, d, norm=norm,
+                                             rope=rope if i < 2 else None, eps=eps,
+                                             out=None if out is None else out[i]))
+            return tuple(outs)
         qw = qb = kw = kb = sn = cs_ = None
         prefix = 0
         if qn is not None:

@@ -609,14 +609,34 @@ class HipContext {
         return folded_call(x, f, eps, true);
     }
     // LN1 and the q|k|v projection with heads, QK-norm and RoPE
-    // (model/block.rs:128-146) on the folded q|k|v weight (f16, d = 64)
+    // (model/block.rs:128-146) on the folded q|k|v weight. Shapes the fused
+    // kernel does not cover (f32, d != 64) run linear_ln then qknorm_rope
+    // per third.
     Qkv linear_ln_qkv_heads(const HipTensor& x, const FoldedLinear& f, size_t s, size_t t, size_t h,
                             const Norm* qn, const Norm* kn, const Rope* rope,
                             float eps = 1e-5f) const {
         const auto& sh = f.w_fold.shape();
         HS_REQUIRE(sh.size() == 2 && sh[0] % (3 * h) == 0, "w_fold shape");
-        const size_t n3 = sh[0], k = sh[1], d = n3 / (3 * h);
+        const size_t n3 = sh[0], k = sh[1], d = n3 / (3 * h), hd = h * d;
         HS_REQUIRE(x.len() == s * t * k && x.dtype() == f.w_fold.dtype(), "x shape/dtype");
+        if (!(x.dtype() == Dtype::F16 && d == 64 && n3 % 256 == 0 && k % 64 == 0)) {
+            Qkv out;
+            HipTensor* dst[3] = {&out.q, &out.k, &out.v};
+            const Norm* norms[3] = {qn, kn, nullptr};
+            const size_t esz = dtype_size(x.dtype());
+            HipTensor ws = empty_typed({2 * s * t}, Dtype::F32);
+            for (int i = 0; i < 3; i++) {
+                HipTensor proj = empty_typed({s * t, hd}, x.dtype());
+                check(hs_linear_ln(stream_, hs_dtype(x.dtype()), x.data(),
+                                   static_cast<const char*>(f.w_fold.data()) + i * hd * k * esz,
+                                   f.colsum.f32() + i * hd, f.shift.f32() + i * hd,
+                                   static_cast<float*>(ws.data()), proj.data(),
+                                   static_cast<int64_t>(s * t), i32(hd), i32(k), eps),
+                      "linear_ln");
+                *dst[i] = qknorm_rope(proj, s, t, h, d, norms[i], i < 2 ? rope : nullptr, eps);
+            }
+            return out;
+        }
         const float *qw = nullptr, *qb = nullptr, *kw = nullptr, *kb = nullptr;
         const float *sn = nullptr, *cs = nullptr;
         size_t prefix = 0;

@@ -489,14 +489,23 @@ void folded_layernorm_equals_sequence(HipContext& ctx) {
     hs::Rope rope{&st, &ct, prefix};
     auto gg = ctx.tensor_from_slice({k}, g), gbe = ctx.tensor_from_slice({k}, be);
     auto gb = ctx.tensor_from_slice({n3}, b);
-    auto gx = ctx.tensor_from_f32({s * t, k}, x, Dtype::F16), gw = ctx.tensor_from_f32({n3, k}, w, Dtype::F16);
-    auto f = ctx.fold_layernorm(gw, &gb, gg, gbe);
-    auto fused = ctx.linear_ln_qkv_heads(gx, f, s, t, h, &norm, &norm, &rope, 1e-6f);
-    auto seq = ctx.linear_qkv_heads(ctx.layernorm(gx, gg, gbe, 1e-6f), gw, &gb, s, t, h, &norm, &norm,
-                                    &rope, 1e-6f);
-    twice_gate(ctx.download(fused.q), ctx.download(seq.q), "linear_ln_qkv_heads q");
-    twice_gate(ctx.download(fused.k), ctx.download(seq.k), "linear_ln_qkv_heads k");
-    twice_gate(ctx.download(fused.v), ctx.download(seq.v), "linear_ln_qkv_heads v");
+    for (Dtype dt : {Dtype::F16, Dtype::F32}) {  // f32 takes the per-third fallback
+        auto gx = ctx.tensor_from_f32({s * t, k}, x, dt), gw = ctx.tensor_from_f32({n3, k}, w, dt);
+        auto f = ctx.fold_layernorm(gw, &gb, gg, gbe);
+        auto fused = ctx.linear_ln_qkv_heads(gx, f, s, t, h, &norm, &norm, &rope, 1e-6f);
+        auto seq = ctx.linear_qkv_heads(ctx.layernorm(gx, gg, gbe, 1e-6f), gw, &gb, s, t, h, &norm,
+                                        &norm, &rope, 1e-6f);
+        const HipTensor* got[3] = {&fused.q, &fused.k, &fused.v};
+        const HipTensor* want[3] = {&seq.q, &seq.k, &seq.v};
+        for (int i = 0; i < 3; i++) {
+            const std::string what = std::string("linear_ln_qkv_heads ") + "qkv"[i] +
+                                     (dt == Dtype::F16 ? " f16" : " f32");
+            if (dt == Dtype::F16)
+                twice_gate(ctx.download(*got[i]), ctx.download(*want[i]), what);
+            else
+                assert_close(ctx.download(*got[i]), ctx.download(*want[i]), 1e-4f, what);
+        }
+    }
 }
 
 void contract_violations_throw(HipContext& ctx) {
