@@ -15,10 +15,12 @@
 // straight back as the B operand of O^T += V^T P^T; the V^T operand comes
 // from row-major V in LDS through the gfx950 transposing read
 // ds_read_b64_tr_b16, with the key order matching the order in which the
-// score accumulator holds P^T. The running max is lazy: a query keeps its
-// reference max until a tile's scores exceed it by more than 2^8, so after
-// the first tiles the output rescale (skipped whenever no query's reference
-// moved) almost never runs. Workgroups
+// score accumulator holds P^T. The running max is lazy: after the first
+// tile a query keeps its reference max m and a tile's weights are computed
+// against it without the tile max; only when a lane's row sum over the tile
+// exceeds 2^15 (a weight might then overflow f16) does the tile take the
+// max path, which moves m if the tile's scores exceed it by more than 2^8
+// and rescales the output. Workgroups
 // are ordered XCD-aware: all query tiles of one (frame, head) run on one
 // XCD, so its K/V stream through that XCD's L2.
 //
@@ -171,9 +173,35 @@ __device__ __forceinline__ void mask_tail(f32x16 (&s)[kKB], int key0, int t, int
         }
 }
 
-// Online-softmax update for one tile's scores (already masked): returns
-// P^T as f16 B operands (registers 8 kk .. 8 kk + 7 of s[kb] in p[kb][kk])
-// and the factor the running output must be scaled by.
+// The tile's weights against reference m: P^T as f16 B operands
+// (registers 8 kk .. 8 kk + 7 of s[kb] in p[kb][kk]) and their row sum over
+// this lane's keys, which adds the f16 weights the P.V product uses, two per
+// v_dot2. Masked keys weigh exp2(-inf) = 0.
+__device__ __forceinline__ float weights_tile(const f32x16 (&s)[kKB], float c, float m,
+                                              u32x4 (&p)[kKB][2]) {
+    float ps = 0.0f;
+    const f16x2 one2 = {static_cast<f16>(1.0f), static_cast<f16>(1.0f)};
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+        for (int w = 0; w < 4; w++)
+#pragma unroll
+            for (int kb = 0; kb < kKB; kb++) {
+                const int r = 8 * kk + 2 * w;
+                p[kb][kk][w] = pk_f16(__builtin_amdgcn_exp2f(fmaf(s[kb][r], c, -m)),
+                                      __builtin_amdgcn_exp2f(fmaf(s[kb][r + 1], c, -m)));
+                ps = __builtin_amdgcn_fdot2(u2h2(p[kb][kk][w]), one2, ps, false);
+            }
+    return ps;
+}
+
+// A lane's row sum over one tile above which its weights take the max path:
+// every weight is then at most 2^15, inside f16's range.
+constexpr float kRowSumMax = 32768.0f;
+
+// Online-softmax update for one tile's scores (already masked) through the
+// tile max: returns the weights in p and the factor the running output must
+// be scaled by.
 __device__ __forceinline__ float softmax_tile(const f32x16 (&s)[kKB], float c, float& m, float& l,
                                               u32x4 (&p)[kKB][2]) {
     // a sequential chain, which the compiler turns into v_max3_f32
@@ -184,28 +212,14 @@ __device__ __forceinline__ float softmax_tile(const f32x16 (&s)[kKB], float c, f
         for (int r = (kb == 0 ? 1 : 0); r < 16; r += 2)
             mx = r + 1 < 16 ? fmaxf(fmaxf(mx, s[kb][r]), s[kb][r + 1]) : fmaxf(mx, s[kb][r]);
     mx = halves_max(mx);
-    // Lazy running max: a query keeps its reference value m until a tile's
-    // scores exceed it by more than kLazyMax (log2 units), so most tiles need
-    // no output rescale; the weights exp2(s c - m) then stay below
+    // The reference moves only when the tile's scores exceed it by more than
+    // kLazyMax (log2 units): the weights exp2(s c - m) then stay below
     // 2^kLazyMax, exact in f16 to its usual relative precision, and the
     // final O / l is unchanged mathematically (both use the same m).
     const float m_cand = fmaxf(m, mx * c);
     const float m_new = m_cand > m + kLazyMax ? m_cand : m;
     const float corr = __builtin_amdgcn_exp2f(m - m_new);
-    // The row sum adds the f16 weights the P.V product uses, two per v_dot2.
-    float ps = 0.0f;
-    const f16x2 one2 = {static_cast<f16>(1.0f), static_cast<f16>(1.0f)};
-#pragma unroll
-    for (int kk = 0; kk < 2; kk++)
-#pragma unroll
-        for (int w = 0; w < 4; w++)
-#pragma unroll
-            for (int kb = 0; kb < kKB; kb++) {
-                const int r = 8 * kk + 2 * w;
-                p[kb][kk][w] = pk_f16(__builtin_amdgcn_exp2f(fmaf(s[kb][r], c, -m_new)),
-                                      __builtin_amdgcn_exp2f(fmaf(s[kb][r + 1], c, -m_new)));
-                ps = __builtin_amdgcn_fdot2(u2h2(p[kb][kk][w]), one2, ps, false);
-            }
+    const float ps = weights_tile(s, c, m_new, p);
     l = fmaf(l, corr, ps);
     m = m_new;
     return corr;
@@ -348,8 +362,20 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
 #pragma unroll
         for (int b = 0; b < kQB; b++) {
             if ((j + 1) * kBN > t) mask_tail(sc[b], j * kBN, t, hh);
-            const float corr = softmax_tile(sc[b], c, m[b], l[b], p[b]);
-            rescale(o[b][0], o[b][1], corr);
+            // After the first tile, weights against the kept reference; the
+            // max path only when some lane's sum says a weight may exceed
+            // 2^15 (a row sum above 2^15 means a weight above 2^10, more
+            // than kLazyMax over m, so that path then moves m).
+            bool max_path = j == 0;
+            if (!max_path) {
+                const float ps = weights_tile(sc[b], c, m[b], p[b]);
+                max_path = __any(!(ps <= kRowSumMax));
+                if (!max_path) l[b] += ps;
+            }
+            if (max_path) {
+                const float corr = softmax_tile(sc[b], c, m[b], l[b], p[b]);
+                rescale(o[b][0], o[b][1], corr);
+            }
         }
         pv_update(o, sm.v[cur], p, n, hh);
         if (j + 1 < ntiles) {

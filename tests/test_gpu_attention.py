@@ -118,6 +118,32 @@ def test_attention_f16_score_range(ctx, scale):
     check(got, O.attention(q, k, v), f"attention score scale {scale}")
 
 
+@pytest.mark.parametrize("case", ["ramp", "spike", "mixed"])
+def test_attention_f16_reference_moves(ctx, case):
+    """Scores that rise from tile to tile, so that later 64-key tiles take the
+    max path (a tile's weights against the kept reference would overflow
+    f16): "ramp" raises every tile's scores by ~18 (log2 units), "spike" puts
+    one dominant key in the last tile, "mixed" gives half the queries of each
+    wave a rising and half a falling ramp (the max path then runs for the
+    whole wave while half its queries keep their reference)."""
+    rng = np.random.default_rng(5)
+    s, h, t = 1, 2, 300
+    q = np.zeros((s, h, t, 64))
+    k = 0.5 * rng.standard_normal((s, h, t, 64))
+    v = rng.standard_normal((s, h, t, 64))
+    q[..., 0] = 8.0  # score = k[..., 0] (q.k / 8)
+    if case == "spike":
+        k[..., 0] += 2.0 * rng.standard_normal((s, h, t))
+        k[:, :, t - 3, 0] = 120.0
+    else:
+        k[..., 0] += 12.5 * (np.arange(t) // 64)  # 12.5 * log2(e) = 18 per tile
+        if case == "mixed":
+            q[:, :, 1::2, 0] = -8.0  # odd queries: scores fall tile to tile
+    q, k, v = O.to_f16(q), O.to_f16(k), O.to_f16(v)
+    got = back(ctx.attention(dev(q), dev(k), dev(v)))
+    check(got, O.attention(q, k, v), f"attention reference moves ({case})")
+
+
 def test_attention_d128_f32(ctx):
     """The camera head's head_dim 128 (f32 only, engine/ops.rs:233-238)."""
     rng = np.random.default_rng(128)
