@@ -437,6 +437,19 @@ def cache_times(ctx, frames: int, iters: int) -> dict:
             "calls_per_pass": CACHED_LAYERS}
 
 
+def alternating_best(fns: dict, timed, rounds: int = 3) -> dict:
+    """Times each contestant (name -> callable) with timed(fn) -> ms in
+    `rounds` rounds that take them in turn, rotating which goes first, and
+    keeps each one's fastest round: no contestant always runs first (right
+    after its inputs were made, on a clock the others then warm up)."""
+    best = {k: float("inf") for k in fns}
+    names = list(fns)
+    for r in range(rounds):
+        for k in names[r % len(names):] + names[:r % len(names)]:
+            best[k] = min(best[k], timed(fns[k]))
+    return best
+
+
 def gemm_times(ctx, frames: int, iters: int) -> dict:
     """The aggregator block's four linear layers at this S (S*1374 rows, f16),
     each with the epilogue the block applies fused in: qkv (bias, split into
@@ -446,7 +459,7 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
     torch (the ROCm BLAS library, no bias or epilogue) is timed beside them
     (not part of this library), and so is this library's standalone op that
     each fused epilogue replaces, so library_plus_op_ms is the unfused
-    alternative."""
+    alternative. Each figure is its fastest of three alternating rounds."""
     from headshot_amd import rope as _rope
     import torch
 
@@ -487,8 +500,6 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
             gam = torch.full((n,), 1e-5, device=ctx.device)
             ctx.linear_ls_residual(x, w, gam, res, b, out=o)
         call = ctx.last_launch
-        ms = timed(call)
-        ms_lib = timed(lambda: torch.nn.functional.linear(x, w))
         # the standalone op that the fused epilogue replaces, on a product-
         # shaped input: the q and k heads (QK-norm + RoPE pair), LayerScale +
         # residual, or bias + GELU
@@ -504,7 +515,10 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
         else:
             ctx.bias_ls_residual(res, y, gam, b, out=o)
             op_name = "bias_ls_residual"
-        ms_op = timed(ctx.last_launch)
+        op_call = ctx.last_launch
+        best = alternating_best({"fused": call, "library": lambda: torch.nn.functional.linear(x, w),
+                                 "op": op_call}, timed)
+        ms, ms_lib, ms_op = best["fused"], best["library"], best["op"]
         fl = 2.0 * m * n * k
         tf = fl / (ms * 1e-3) / 1e12
         out[name] = {"m": m, "n": n, "k": k, "ms": round(ms, 3), "TFLOP/s": round(tf, 1),
@@ -524,7 +538,8 @@ def ln_fold_times(ctx, m: int, timed, g) -> dict:
     (hs_layernorm_stats + hs_linear_ln_gelu / hs_linear_ln_qkv_heads on
     weights folded by hs_fold_layernorm) against layernorm then the fused
     product, at the block's LN2 -> fc1 + GELU and LN1 -> q|k|v (heads,
-    QK-norm, RoPE) shapes. Times include the statistics pass."""
+    QK-norm, RoPE) shapes. Times include the statistics pass; each is its
+    fastest of three alternating rounds."""
     import torch
 
     from headshot_amd import rope as _rope
@@ -537,9 +552,9 @@ def ln_fold_times(ctx, m: int, timed, g) -> dict:
     normed = ctx.layernorm(x, lw, lb, eps=EPS)
     ln_call = ctx.last_launch
     ws = torch.empty((m, 2), dtype=torch.float32, device=ctx.device)
-    out = {"layernorm_us": round(timed(ln_call) * 1e3, 1)}
     ctx.layernorm_stats(x, eps=EPS, out=ws)
-    out["stats_us"] = round(timed(ctx.last_launch) * 1e3, 1)
+    best = alternating_best({"layernorm": ln_call, "stats": ctx.last_launch}, timed)
+    out = {"layernorm_us": round(best["layernorm"] * 1e3, 1), "stats_us": round(best["stats"] * 1e3, 1)}
     sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(_rope.periods(), *GRID))
     nrm = (torch.ones(HEAD_DIM, device=ctx.device), torch.zeros(HEAD_DIM, device=ctx.device))
     for name, n in (("fc1", HIDDEN), ("qkv", 3 * DIM)):
@@ -561,8 +576,8 @@ def ln_fold_times(ctx, m: int, timed, g) -> dict:
             ctx.linear_ln_qkv_heads(x, f, frames, t, HEADS, qn=nrm, kn=nrm,
                                     rope=(sin, cos, PREFIX), eps=EPS, out=o, workspace=ws)
             folded = ctx.last_launch
-        ms_plain = timed(lambda: (ln_call(), plain()))
-        ms_fold = timed(folded)
+        best = alternating_best({"plain": lambda: (ln_call(), plain()), "folded": folded}, timed)
+        ms_plain, ms_fold = best["plain"], best["folded"]
         fl = 2.0 * m * n * DIM
         out[name] = {"layernorm_then_product_ms": round(ms_plain, 3),
                      "folded_ms": round(ms_fold, 3),
@@ -576,7 +591,8 @@ def block_times(ctx, frames: int, iters: int) -> dict:
     HIP (headshot_amd.aggregator.block_forward: linears with fused
     epilogues, fused QK-norm/RoPE, attention written token-major), and the
     reference's unfused dispatch sequence through the same library's single
-    ops beside it (block_forward_reference). Random-init f16 weights."""
+    ops beside it (block_forward_reference). Random-init f16 weights. Each
+    figure is its fastest of three alternating rounds."""
     import torch
 
     from headshot_amd import rope as _rope
@@ -595,19 +611,21 @@ def block_times(ctx, frames: int, iters: int) -> dict:
 
     for kind, (s, tt, rope) in {"frame": (frames, t, (sin, cos, PREFIX)),
                                 "global": (1, frames * t, None)}.items():
-        res = {}
-        for name, fn in (("fused", block_forward), ("reference_sequence", block_forward_reference),
-                         ("fused_layernorm_folded", folded)):
-            fn(ctx, wts, x, s, tt, rope=rope, eps=EPS)
+        def timed(fn):
+            fn()
             torch.cuda.synchronize()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             for _ in range(iters):
-                fn(ctx, wts, x, s, tt, rope=rope, eps=EPS)
+                fn()
             b.record()
             torch.cuda.synchronize()
-            res[name + "_ms"] = round(a.elapsed_time(b) / iters, 3)
-        out[kind] = res
+            return a.elapsed_time(b) / iters
+
+        fns = {name: (lambda f=f: f(ctx, wts, x, s, tt, rope=rope, eps=EPS))
+               for name, f in (("fused", block_forward), ("reference_sequence", block_forward_reference),
+                               ("fused_layernorm_folded", folded))}
+        out[kind] = {name + "_ms": round(ms, 3) for name, ms in alternating_best(fns, timed).items()}
     out["aggregator_ms"] = round(N_FRAME_BLOCKS * out["frame"]["fused_ms"]
                                  + N_GLOBAL_BLOCKS * out["global"]["fused_ms"], 1)
     out["aggregator_reference_sequence_ms"] = round(
@@ -629,7 +647,8 @@ def trunk_times(ctx, frames: int, iters: int) -> dict:
     device. Beside it the reference's dispatch sequence through the same
     library's single ops (Trunk.forward(fused=False)), and the fused trunk
     with every block's LayerNorms folded into the products after them
-    (Trunk.forward(fold_ln=True))."""
+    (Trunk.forward(fold_ln=True)). Each figure is its fastest of three
+    alternating rounds."""
     import torch
 
     from headshot_amd.aggregator import BlockWeights
@@ -648,17 +667,22 @@ def trunk_times(ctx, frames: int, iters: int) -> dict:
     tokens = torch.randn((frames * p, TDIM), generator=gen, device=ctx.device)
     out = {"frames": frames, "tokens_per_frame": p + 17}
     trunk.fold_layernorms(ctx)
-    for name, fused, fold in (("fused", True, False), ("reference_sequence", False, False),
-                              ("fused_layernorm_folded", True, True)):
-        trunk.forward(ctx, tokens, frames, *GRID, fused=fused, fold_ln=fold)
+    def timed(fn):
+        fn()
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
         for _ in range(iters):
-            trunk.forward(ctx, tokens, frames, *GRID, fused=fused, fold_ln=fold)
+            fn()
         b.record()
         torch.cuda.synchronize()
-        out[name + "_ms"] = round(a.elapsed_time(b) / iters, 1)
+        return a.elapsed_time(b) / iters
+
+    fns = {name: (lambda fu=fused, fo=fold: trunk.forward(ctx, tokens, frames, *GRID, fused=fu, fold_ln=fo))
+           for name, fused, fold in (("fused", True, False), ("reference_sequence", False, False),
+                                     ("fused_layernorm_folded", True, True))}
+    for name, ms in alternating_best(fns, timed).items():
+        out[name + "_ms"] = round(ms, 1)
     out["frames_per_s"] = round(frames / (out["fused_ms"] * 1e-3), 1)
     return out
 
