@@ -241,6 +241,9 @@ CEILING_PROBES = {
                          "and prefix rows not included)"),
 }
 KINDS = {"copy": 0, "add2": 1, "heads": 2, "cast": 3}
+# hsc_run shape flags: bit 0 cached loads/stores (else streaming), bit 1 one
+# 16-byte vector per lane / one token per wave (else four / two)
+CEILING_SHAPES = {"streaming x4": 0, "cached x4": 1, "streaming x1": 2, "cached x1": 3}
 
 
 ROTATE_BYTES = 768 << 20  # > the 256 MB Infinity Cache: no reuse across launches
@@ -252,10 +255,11 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
 
     Warm: ``iters`` back-to-back launches that rotate over as many buffer
     sets as make ROTATE_BYTES, so no launch finds its inputs in a cache and
-    each pays for its own write-back (streaming and cached loads/stores both
-    run; the faster is the ceiling). Compared with the op's rate inside the
-    pass. Cold: the per-op cold method (cache flush, then a HIP event pair
-    around one launch) with streaming stores only: cached stores leave their
+    each pays for its own write-back (streaming and cached loads/stores, each
+    with four and with one 16-byte vector per lane; the fastest is the
+    ceiling). Compared with the op's rate inside the pass. Cold: the per-op
+    cold method (cache flush, then a HIP event pair around one launch) with
+    streaming stores only, the faster launch shape: cached stores leave their
     write-back for after the end event, so their cold time undercounts.
     Compared with the op's cold rate."""
     import torch
@@ -292,32 +296,35 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
 
     def timed(probe, args, sets):
         """(warm us per policy, cold us) of one probe launch shape."""
-        def launch(temporal, bufs):
-            rc = lib.hsc_run(KINDS[probe], temporal, *bufs, *args, stream)
+        def launch(shape, bufs):
+            rc = lib.hsc_run(KINDS[probe], shape, *bufs, *args, stream)
             if rc != 0:
                 raise RuntimeError(f"hsc_run({probe}) returned {rc}")
 
         warm = {}
-        for policy, temporal in (("streaming", 0), ("cached", 1)):
+        for policy, shape in CEILING_SHAPES.items():
             for bufs in sets:
-                launch(temporal, ptrs(bufs))
+                launch(shape, ptrs(bufs))
             torch.cuda.synchronize()
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             a.record()
             for i in range(iters):
-                launch(temporal, ptrs(sets[i % len(sets)]))
+                launch(shape, ptrs(sets[i % len(sets)]))
             b.record()
             torch.cuda.synchronize()
             warm[policy] = a.elapsed_time(b) / iters * 1e3
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(iters)]
-        for a, b in ev:
-            flush()
-            a.record()
-            launch(0, ptrs(sets[0]))
-            b.record()
-        torch.cuda.synchronize()
-        return warm, sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3
+        cold = []
+        for shape in (s for s in CEILING_SHAPES.values() if not s & 1):  # streaming stores only
+            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+                  for _ in range(iters)]
+            for a, b in ev:
+                flush()
+                a.record()
+                launch(shape, ptrs(sets[0]))
+                b.record()
+            torch.cuda.synchronize()
+            cold.append(sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3)
+        return warm, min(cold)
 
     out = {}
     for op, (probe, what) in CEILING_PROBES.items():

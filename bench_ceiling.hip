@@ -7,15 +7,19 @@
 //   copy   1 read : 1 write, contiguous            (layernorm, bias_gelu)
 //   add2   2 reads : 1 write, contiguous           (bias_ls_residual)
 //   heads  token-major (S*T, 16*64) f16 -> head-major (S, 16, T, 64), two
-//          tensors in one launch, a wave per two tokens and 8 heads' 128-byte
-//          vectors per store: the addressing of the fused QK-norm + RoPE
-//          pair kernel (qknorm_rope)
+//          tensors in one launch, a wave per two tokens (or one) and 8 heads'
+//          128-byte vectors per store: the addressing of the fused QK-norm +
+//          RoPE pair kernel (qknorm_rope)
 //   cast   f32 rows in, f16 rows out, contiguous   (assembly's byte mix)
 //
 // Each kernel runs with non-temporal (streaming) or ordinary cached loads and
-// stores, the two policies the library's kernels use; the bench takes the
-// faster as the ceiling. Not part of libheadshot_hip: built into
-// bench_ceiling.so next to bench.py.
+// stores, the two policies the library's kernels use, and in two launch
+// shapes: four 16-byte vectors per lane (two tokens per wave for heads) or
+// one (one token per wave); the bench takes the fastest as the ceiling (a
+// bare copy is fastest with one vector per lane, 82% of peak against 78%
+// with four, while the ops, with their arithmetic, run best with their own
+// shapes). Not part of libheadshot_hip: built into bench_ceiling.so next to
+// bench.py.
 #include "hs_common.hpp"
 
 namespace {
@@ -24,7 +28,6 @@ using hs::f16;
 using hs::u32x4;
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;  // 16-byte vectors per lane
 
 template <bool NT, typename V>
 __device__ __forceinline__ V ld(const V* p) {
@@ -37,46 +40,46 @@ __device__ __forceinline__ void st(V* p, V v) {
     else *p = v;
 }
 
-// Vectors [w * 256, w * 256 + 256) for wave w: four wave-contiguous 1 KiB
+// Vectors [w * 64 U, (w + 1) * 64 U) for wave w: U wave-contiguous 1 KiB
 // pieces per wave.
-template <bool NT>
+template <bool NT, int U>
 __global__ __launch_bounds__(kBlock) void copy_kernel(const u32x4* __restrict__ a,
                                                       u32x4* __restrict__ o, int64_t n) {
-    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kUnroll +
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * U +
                          (threadIdx.x & 63);
-    u32x4 r[kUnroll];
+    u32x4 r[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++)
+    for (int u = 0; u < U; u++)
         if (base + u * 64 < n) r[u] = ld<NT>(a + base + u * 64);
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++)
+    for (int u = 0; u < U; u++)
         if (base + u * 64 < n) st<NT>(o + base + u * 64, r[u]);
 }
 
-template <bool NT>
+template <bool NT, int U>
 __global__ __launch_bounds__(kBlock) void add2_kernel(const u32x4* __restrict__ a,
                                                       const u32x4* __restrict__ b,
                                                       u32x4* __restrict__ o, int64_t n) {
-    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kUnroll +
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * U +
                          (threadIdx.x & 63);
-    u32x4 ra[kUnroll], rb[kUnroll];
+    u32x4 ra[U], rb[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++)
+    for (int u = 0; u < U; u++)
         if (base + u * 64 < n) ra[u] = ld<NT>(a + base + u * 64), rb[u] = ld<NT>(b + base + u * 64);
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++)
+    for (int u = 0; u < U; u++)
         if (base + u * 64 < n) st<NT>(o + base + u * 64, ra[u] + rb[u]);
 }
 
 // Two tensors: waves [0, W) copy the first, [W, 2W) the second, W =
-// ceil(tokens / 2). A load covers one token's 8 heads (1 KiB contiguous),
+// ceil(tokens / K). A load covers one token's 8 heads (1 KiB contiguous),
 // a store writes those 8 heads' vectors to their head-major rows.
-template <bool NT>
+template <bool NT, int K>
 __global__ __launch_bounds__(kBlock) void heads_kernel(const f16* __restrict__ x0,
                                                        const f16* __restrict__ x1,
                                                        f16* __restrict__ o0, f16* __restrict__ o1,
                                                        int64_t tokens, int seq) {
-    constexpr int H = 16, D = 64, K = 2;
+    constexpr int H = 16, D = 64;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + hs::wave_in_block();
     const int64_t per = (tokens + K - 1) / K;
     const int which = wave >= per ? 1 : 0;
@@ -103,17 +106,17 @@ __global__ __launch_bounds__(kBlock) void heads_kernel(const f16* __restrict__ x
 }
 
 // n f32 -> f16, four elements (16 bytes in, 8 out) per lane per step.
-template <bool NT>
+template <bool NT, int U>
 __global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ a,
                                                       f16* __restrict__ o, int64_t n) {
-    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kUnroll +
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * U +
                          (threadIdx.x & 63);
-    u32x4 r[kUnroll];
+    u32x4 r[U];
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++)
+    for (int u = 0; u < U; u++)
         if ((base + u * 64) * 4 < n) r[u] = ld<NT>(reinterpret_cast<const u32x4*>(a + (base + u * 64) * 4));
 #pragma unroll
-    for (int u = 0; u < kUnroll; u++) {
+    for (int u = 0; u < U; u++) {
         if ((base + u * 64) * 4 >= n) continue;
         hs::f16x2 lo, hi;
         lo.x = static_cast<f16>(hs::u2f(r[u][0])), lo.y = static_cast<f16>(hs::u2f(r[u][1]));
@@ -126,41 +129,43 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ 
 
 int64_t blocks_for(int64_t lanes_work) { return (lanes_work + kBlock - 1) / kBlock; }
 
-template <bool NT>
+// U: 16-byte vectors per lane (copy, add2, cast) or tokens per wave (heads).
+template <bool NT, int U>
 int run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n, int32_t s,
         int32_t t, hipStream_t stream) {
     switch (kind) {
         case 0:
         case 1: {
-            const int64_t blocks = blocks_for((n + kUnroll - 1) / kUnroll);
+            const int64_t blocks = blocks_for((n + U - 1) / U);
             if (blocks == 0) return 0;
             if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
             if (kind == 0)
-                copy_kernel<NT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                copy_kernel<NT, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                     static_cast<const u32x4*>(a), static_cast<u32x4*>(o), n);
             else
-                add2_kernel<NT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                add2_kernel<NT, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                     static_cast<const u32x4*>(a), static_cast<const u32x4*>(b),
                     static_cast<u32x4*>(o), n);
             break;
         }
         case 2: {
+            constexpr int K = U == 1 ? 1 : 2;
             const int64_t tokens = static_cast<int64_t>(s) * t;
-            const int64_t waves = 2 * ((tokens + 1) / 2);
+            const int64_t waves = 2 * ((tokens + K - 1) / K);
             const int64_t blocks = (waves + 3) / 4;
             if (blocks == 0) return 0;
             if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
-            heads_kernel<NT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+            heads_kernel<NT, K><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                 static_cast<const f16*>(a), static_cast<const f16*>(b), static_cast<f16*>(o),
                 static_cast<f16*>(o2), tokens, t);
             break;
         }
         case 3: {
             if (n % 4 != 0) return -1;
-            const int64_t blocks = blocks_for((n / 4 + kUnroll - 1) / kUnroll);
+            const int64_t blocks = blocks_for((n / 4 + U - 1) / U);
             if (blocks == 0) return 0;
             if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
-            cast_kernel<NT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+            cast_kernel<NT, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                 static_cast<const float*>(a), static_cast<f16*>(o), n);
             break;
         }
@@ -176,14 +181,20 @@ extern "C" {
 
 // kind 0 copy / 1 add2: n 16-byte vectors (a, b -> o). kind 2 heads: s
 // frames of t tokens, a and b -> o and o2. kind 3 cast: n f32 elements
-// (n % 4 == 0). temporal: 0 non-temporal loads and stores, 1 cached.
-// Buffers are 16-byte aligned and sized by the caller. Returns 0, or -1 for
-// an argument the kernels do not take, or the HIP error code of the launch.
-int hsc_run(int kind, int temporal, const void* a, const void* b, void* o, void* o2, int64_t n,
+// (n % 4 == 0). shape: bit 0 set = cached loads and stores (clear:
+// non-temporal), bit 1 set = one 16-byte vector per lane / one token per
+// wave (clear: four / two). Buffers are 16-byte aligned and sized by the
+// caller. Returns 0, or -1 for an argument the kernels do not take, or the
+// HIP error code of the launch.
+int hsc_run(int kind, int shape, const void* a, const void* b, void* o, void* o2, int64_t n,
             int32_t s, int32_t t, hipStream_t stream) {
-    if (n < 0 || s < 0 || t < 0 || (temporal != 0 && temporal != 1)) return -1;
-    return temporal ? run<false>(kind, a, b, o, o2, n, s, t, stream)
-                    : run<true>(kind, a, b, o, o2, n, s, t, stream);
+    if (n < 0 || s < 0 || t < 0 || shape < 0 || shape > 3) return -1;
+    switch (shape) {
+        case 0: return run<true, 4>(kind, a, b, o, o2, n, s, t, stream);
+        case 1: return run<false, 4>(kind, a, b, o, o2, n, s, t, stream);
+        case 2: return run<true, 1>(kind, a, b, o, o2, n, s, t, stream);
+        default: return run<false, 1>(kind, a, b, o, o2, n, s, t, stream);
+    }
 }
 
 }  // extern "C"

@@ -78,7 +78,9 @@ def test_ceiling_library_exports_its_entry_point():
     # argument checks run on the host, before any launch
     run = bench.load_ceiling().hsc_run
     assert run(7, 0, None, None, None, None, 0, 0, 0, None) == -1    # unknown kind
-    assert run(0, 2, None, None, None, None, 0, 0, 0, None) == -1    # unknown policy
+    assert run(0, 4, None, None, None, None, 0, 0, 0, None) == -1    # unknown shape
+    assert run(0, -1, None, None, None, None, 0, 0, 0, None) == -1   # unknown shape
     assert run(3, 1, None, None, None, None, 6, 0, 0, None) == -1    # cast needs n % 4 == 0
     assert run(0, 0, None, None, None, None, -1, 0, 0, None) == -1   # negative size
     assert run(2, 1, None, None, None, None, 0, 0, 5, None) == 0     # empty: no launch
+    assert run(0, 3, None, None, None, None, 0, 0, 0, None) == 0     # empty: no launch

@@ -1,7 +1,7 @@
 """bench.py's data-movement probes (bench_ceiling.hip) move what they claim:
 each is checked exactly against torch on a small shape under both load/store
-policies, so a ceiling the bench reports is the rate of a kernel that did
-the op's data movement."""
+policies and both launch shapes, so a ceiling the bench reports is the rate
+of a kernel that did the op's data movement."""
 import os
 
 import pytest
@@ -10,7 +10,9 @@ import torch
 import bench
 
 pytestmark = pytest.mark.gpu
-POLICIES = [0, 1]  # streaming, cached
+# shape flags: bit 0 cached (else streaming), bit 1 one vector per lane /
+# one token per wave (else four / two)
+POLICIES = [0, 1, 2, 3]
 
 
 @pytest.fixture(scope="module")
