@@ -1010,6 +1010,22 @@ def summarize_counters(paths) -> None:
             f(lambda: c["SQ_INSTS_VALU_TRANS_F32"] / mf, ".2f"),
             f(lambda: c["SQ_LDS_IDX_ACTIVE"] / (cyc * 256), ".1%"),
             f(lambda: c["SQ_LDS_BANK_CONFLICT"] / c["SQ_INSTS_LDS"], ".2f")]) + " |")
+    # Wave stall breakdown, when a pass collected it: SQ_WAVE_CYCLES and the
+    # SQ_WAIT_* counters all count quad-cycles per resident wave.
+    stall = ["", "| kernel | grid work-items | waves resident per SIMD | waiting on a dependency "
+             "| ready, waiting for issue | waiting for LDS issue |", "|---|---|---|---|---|---|"]
+    for key in sorted(vals):
+        c = {k: st.mean(v) for k, v in vals[key].items()}
+        cyc = c.get("GRBM_GUI_ACTIVE", 0.0) / 8.0
+        w = c.get("SQ_WAVE_CYCLES", 0.0)
+        if not cyc or not w or "SQ_WAIT_ANY" not in c or not c.get("SQ_INSTS_MFMA"):
+            continue
+        stall.append("| " + " | ".join([
+            key[0], str(key[1]), format(4 * w / (cyc * 1024), ".2f"),
+            format(c["SQ_WAIT_ANY"] / w, ".1%"), format(c.get("SQ_WAIT_INST_ANY", 0.0) / w, ".1%"),
+            format(c.get("SQ_WAIT_INST_LDS", 0.0) / w, ".1%")]) + " |")
+    if len(stall) > 3:
+        out += stall
     print("\n".join(out))
 
 

@@ -84,3 +84,19 @@ def test_ceiling_library_exports_its_entry_point():
     assert run(0, 0, None, None, None, None, -1, 0, 0, None) == -1   # negative size
     assert run(2, 1, None, None, None, None, 0, 0, 5, None) == 0     # empty: no launch
     assert run(0, 3, None, None, None, None, 0, 0, 0, None) == 0     # empty: no launch
+
+
+def test_summarize_counters_stall_table(tmp_path, capsys):
+    """The counter summary adds the stall table when a pass collected the
+    SQ_WAIT counters: shares are quad-cycle counts over SQ_WAVE_CYCLES."""
+    head = "Kernel_Name,Grid_Size,Counter_Name,Counter_Value,Start_Timestamp,End_Timestamp\n"
+    name = "void hs::(anonymous namespace)::flash_f16_kernel(x)"
+    rows = [("SQ_INSTS_MFMA", 100), ("SQ_INSTS_VALU", 800), ("SQ_VALU_MFMA_BUSY_CYCLES", 3200),
+            ("GRBM_GUI_ACTIVE", 8000), ("SQ_WAVE_CYCLES", 512000), ("SQ_WAIT_ANY", 128000),
+            ("SQ_WAIT_INST_ANY", 204800), ("SQ_WAIT_INST_LDS", 25600)]
+    path = tmp_path / "c.csv"
+    path.write_text(head + "".join(f'"{name}",4096,{k},{v},0,1000\n' for k, v in rows))
+    bench.summarize_counters([str(path)])
+    out = capsys.readouterr().out
+    # 1000 cycles per XCD, 1024 SIMDs: 4 x 512000 quad-cycles = 2 waves per SIMD
+    assert "| flash_f16_kernel | 4096 | 2.00 | 25.0% | 40.0% | 5.0% |" in out
