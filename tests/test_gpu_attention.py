@@ -144,6 +144,35 @@ def test_attention_f16_reference_moves(ctx, case):
     check(got, O.attention(q, k, v), f"attention reference moves ({case})")
 
 
+@pytest.mark.parametrize("case", range(24))
+def test_attention_f16_random_sweep(ctx, case):
+    """Seeded random shapes and score statistics against float32 torch: T
+    from 1 to 3000 (partial tiles of every size), 1-4 sequences x 1-5
+    heads, score scales from flat to peaked, and in half the cases a drift
+    that raises or lowers the scores along the keys by a random amount per
+    64-key tile, so that the max path runs at random tiles and not only at
+    the first."""
+    rng = np.random.default_rng(1000 + case)
+    s, h = int(rng.integers(1, 5)), int(rng.integers(1, 6))
+    t = int(rng.integers(1, 3001))
+    scale = float(rng.choice([0.1, 0.5, 1.0, 2.0, 4.0]))
+    q = scale * rng.standard_normal((s, h, t, 64))
+    k = rng.standard_normal((s, h, t, 64))
+    v = rng.standard_normal((s, h, t, 64))
+    if case % 2:
+        # every query leans on one direction u; key j moves along u by a
+        # random walk over the tiles, so its scores move by ~2 * drift
+        u = rng.standard_normal(64)
+        u /= np.linalg.norm(u)
+        q = q + 2.0 * u
+        drift = rng.normal(0.0, 6.0, -(-t // 64)).cumsum()
+        k = k + (4.0 * drift[np.arange(t) // 64])[None, None, :, None] * u
+    q, k, v = (dev(O.to_f16(a)) for a in (q, k, v))
+    got = back(ctx.attention(q, k, v)).astype(np.float32)
+    ref = back(torch_attention32(q, k, v))
+    f16_close(got, ref, f"attention sweep case {case}: s={s} h={h} t={t} scale={scale}")
+
+
 def test_attention_d128_f32(ctx):
     """The camera head's head_dim 128 (f32 only, engine/ops.rs:233-238)."""
     rng = np.random.default_rng(128)
