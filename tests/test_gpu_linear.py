@@ -117,6 +117,33 @@ def test_linear_full_size(ctx, name):
         check(back(got)[rows], O.linear(xs, ws, back(b), rows), f"full-size {name} vs oracle")
 
 
+@pytest.mark.parametrize("case", range(16))
+def test_linear_epilogues_random_sweep(ctx, case):
+    """Seeded random shapes on the matrix-core path (n a multiple of 256, k
+    of 64) and off it, each epilogue against float32 torch of the
+    reference's sequence: bias; bias then GELU of the stored (f16) value;
+    bias then LayerScale + residual of the stored value. m from 1 to 3000
+    covers every remainder of the 256-row tile."""
+    rng = np.random.default_rng(500 + case)
+    m = int(rng.integers(1, 3001))
+    fast = case % 4 != 3
+    n = int(rng.choice([256, 512, 768, 1024])) if fast else int(rng.integers(1, 300))
+    k = int(rng.choice([64, 128, 192, 512, 1024])) if fast else int(rng.integers(1, 200))
+    g = torch.Generator(device="cpu").manual_seed(500 + case)
+    x = torch.randn((m, k), generator=g).half().to("cuda:0")
+    w = (torch.randn((n, k), generator=g) / k ** 0.5).half().to("cuda:0")
+    b = (torch.randn(n, generator=g) * 0.02).to("cuda:0")
+    stored = ((x.float() @ w.float().t().contiguous()) + b).half().float()
+    what = f"sweep case {case}: m={m} n={n} k={k}"
+    f16_close(back(ctx.linear(x, w, b)).astype(np.float32), back(stored), what + " bias")
+    f16_close(back(ctx.linear_gelu(x, w, b)).astype(np.float32),
+              back(torch.nn.functional.gelu(stored)), what + " gelu")
+    res = torch.randn((m, n), generator=g).half().to("cuda:0")
+    gam = (torch.randn(n, generator=g) * 0.1).to("cuda:0")
+    f16_close(back(ctx.linear_ls_residual(x, w, gam, res, b)).astype(np.float32),
+              back(res.float() + gam * stored), what + " layerscale")
+
+
 def test_linear_contract(ctx):
     x = torch.zeros((4, 32), dtype=torch.float16, device="cuda:0")
     with pytest.raises(AssertionError):
