@@ -349,3 +349,72 @@ def test_assemble_tokens(ctx, out_dtype, patch_dtype, s, grid, r, d, n_var, bias
                              s, p, r, nout, n_var)
     what = f"assemble {out_dtype}<-{patch_dtype} s={s} p={p} r={r} d={d}"
     assert_bit_exact(got, want, what)
+
+
+# ------------------------------------------------------------ random sweep
+
+@pytest.mark.parametrize("case", range(12))
+def test_fused_ops_random_sweep(ctx, case):
+    """Seeded random shapes for every fused per-layer op against the oracle,
+    to the bars above: LayerNorm at random rows and widths; the QK-norm +
+    RoPE pair at a random grid, prefix, frame count and head count (bit-exact
+    against two single calls as well); bias + GELU and bias + LayerScale +
+    residual at random shapes; token assembly at random frame counts, grids,
+    register counts, widths and variant counts (bit-exact)."""
+    rng = np.random.default_rng(700 + case)
+    dtype = DTYPES[case % 2]
+    tag = f"sweep case {case} {dtype}"
+
+    rows = int(rng.integers(1, 3001))
+    dim = int(rng.choice([64, 96, 128, 300, 512, 1024, 2048]))
+    x = host(O.normal(701 + case, (rows, dim)), dtype)
+    w, b = O.normal(702, (dim,), 1.0, 0.02), O.normal(703, (dim,), 0.0, 0.02)
+    check(back(ctx.layernorm(dev(x), dev(w), dev(b), eps=1e-6)), O.layernorm(x, w, b, 1e-6),
+          f"{tag} layernorm {rows}x{dim}")
+
+    grid = (int(rng.integers(1, 9)), int(rng.integers(1, 9)))
+    prefix = int(rng.integers(0, 18))
+    s, h, d = int(rng.integers(1, 6)), int(rng.choice([4, 5, 8, 16, 32])), 64
+    t = grid[0] * grid[1] + prefix
+    q = host(O.normal(711 + case, (s * t, h * d)), dtype)
+    k = host(O.normal(712 + case, (s * t, h * d)), dtype)
+    qn = (O.normal(713, (d,), 1.0, 0.02), O.normal(714, (d,), 0.0, 0.02))
+    kn = (O.normal(715, (d,), 1.0, 0.02), O.normal(716, (d,), 0.0, 0.02))
+    sin, cos = _tables(t, prefix, grid, d)
+    rp = (dev(sin), dev(cos), prefix)
+    dq, dk = dev(q), dev(k)
+    gq, gk = ctx.qknorm_rope_pair(dq, dk, s, t, h, d, qn=tuple(dev(a) for a in qn),
+                                  kn=tuple(dev(a) for a in kn), rope=rp, eps=1e-6)
+    what = f"{tag} qknorm_rope_pair s={s} t={t} h={h} grid={grid} prefix={prefix}"
+    assert_bit_exact(back(gq), back(ctx.qknorm_rope(dq, s, t, h, d, norm=tuple(dev(a) for a in qn),
+                                                    rope=rp, eps=1e-6)), what + " q")
+    check(back(gk), O.qknorm_rope(k, *kn, sin, cos, s, t, h, d, prefix, 1e-6), what + " k oracle",
+          stages=2)
+
+    rows, cols = int(rng.integers(1, 2001)), int(rng.choice([8, 24, 1000, 1024, 4096]))
+    x = host(O.normal(721 + case, (rows, cols)) * np.float32(2.0), dtype)
+    bg = O.normal(722, (cols,), 0.0, 0.02)
+    check(back(ctx.bias_gelu(dev(x), dev(bg))), O.bias_gelu(x, bg, round_bias=False),
+          f"{tag} bias_gelu {rows}x{cols}")
+    res = host(O.normal(723 + case, (rows, cols)), dtype)
+    g = O.normal(724, (cols,))
+    check(back(ctx.bias_ls_residual(dev(res), dev(x), dev(g), dev(bg))),
+          O.bias_ls_residual(res, x, bg, g), f"{tag} bias_ls_residual {rows}x{cols}")
+
+    s, grid = int(rng.integers(1, 7)), (int(rng.integers(1, 6)), int(rng.integers(1, 6)))
+    r, d, n_var = int(rng.integers(0, 9)), int(rng.choice([96, 256, 1024])), int(rng.integers(1, 3))
+    p = grid[0] * grid[1]
+    patch_dtype = DTYPES[(case // 2) % 2]
+    patches = host(O.normal(731 + case, (s * p, d)), patch_dtype)
+    cam = host(O.normal(732, (n_var, d)), dtype)
+    reg = host(O.normal(733, (n_var * r, d)), dtype) if r else None
+    pb = O.normal(734, (d,), 0.0, 0.02) if case % 3 else None
+    pe = O.normal(735, (p, d), 0.0, 0.02) if case % 4 else None
+    got = back(ctx.assemble_tokens(dev(patches), s, p, dev(cam), None if reg is None else dev(reg),
+                                   patch_bias=None if pb is None else dev(pb),
+                                   pos=None if pe is None else dev(pe), out_dtype=dtype,
+                                   n_var=n_var))
+    want = O.assemble_tokens(patches, pb, pe, cam,
+                             reg if reg is not None else np.zeros((0, d), NP[dtype]),
+                             s, p, r, NP[dtype], n_var)
+    assert_bit_exact(got, want, f"{tag} assemble s={s} p={p} r={r} d={d} n_var={n_var}")
