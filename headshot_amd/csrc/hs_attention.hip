@@ -20,7 +20,9 @@
 // against it without the tile max; only when a lane's row sum over the tile
 // exceeds 2^15 (a weight might then overflow f16) does the tile take the
 // max path, which moves m if the tile's scores exceed it by more than 2^8
-// and rescales the output. Workgroups
+// and rescales the output. When many sequences have a partial last query
+// tile (the frame blocks), those tiles run as a second launch in which the
+// waves whose queries all lie past T skip the arithmetic. Workgroups
 // are ordered XCD-aware: all query tiles of one (frame, head) run on one
 // XCD, so its K/V stream through that XCD's L2.
 //
@@ -291,17 +293,20 @@ __device__ __forceinline__ void store_out(const f32x16& o0, const f32x16& o1, fl
 
 // grid.x = kXcds * ceil(SH / kXcds) * QT workgroups; workgroup b runs on XCD
 // b % kXcds and takes (frame*head) index sh = (b / kXcds / QT) * kXcds +
-// b % kXcds, query tile (b / kXcds) % QT.
+// b % kXcds, query tile qt0 + (b / kXcds) % QT.
+// TAIL: the launch of the partial last query tiles (qt0 = their index),
+// whose waves with every query past T only stage K and V.
+template <bool TAIL>
 __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
     const f16* __restrict__ q, const f16* __restrict__ k, const f16* __restrict__ v,
     f16* __restrict__ out, int sh_count, int heads, int t, int qtiles, float c,
-    int token_major) {
+    int token_major, int qt0) {
     __shared__ FlashSmem sm;
     const int b = blockIdx.x;
     const int slot = b / kXcds;
     const int sh = (slot / qtiles) * kXcds + b % kXcds;
     if (sh >= sh_count) return;  // workgroup-uniform, before any barrier
-    const int qt = slot % qtiles;
+    const int qt = qt0 + slot % qtiles;
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = tid >> 6;
@@ -356,6 +361,7 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
             load_rows(pk, kb, (j + 1) * kBN, t, tid);
             load_rows(pv, vb, (j + 1) * kBN, t, tid);
         }
+        if (!TAIL || qt * kBM + wave * kQB * 32 < t) {
         f32x16 sc[kQB][kKB];
         qk_scores(sc, sm.k[cur], qa, n, hh);
         u32x4 p[kQB][kKB][2];
@@ -378,6 +384,7 @@ __global__ __launch_bounds__(kThreads) void flash_f16_kernel(
             }
         }
         pv_update(o, sm.v[cur], p, n, hh);
+        }
         if (j + 1 < ntiles) {
             store_rows<kKPitch>(pk, sm.k[cur ^ 1], tid);
             store_rows<kVPitch>(pv, sm.v[cur ^ 1], tid);
@@ -534,9 +541,24 @@ hs_status launch_attention(hipStream_t st, hs_dtype dt, const void* q, const voi
         const int64_t blocks = static_cast<int64_t>(kXcds) * ceil_div(sh, kXcds) * qtiles;
         if (blocks < (int64_t{1} << 31) / kThreads) {
             const float c = scale * 1.4426950408889634f;  // scores enter exp2
-            flash_f16_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), 0, st>>>(
+            // A partial last query tile runs as a launch of its own when
+            // there are enough of them to fill the chip (two workgroups per
+            // CU, e.g. 32 frames x 16 heads of 1374 tokens): its waves past
+            // T then leave their SIMDs to the live ones. With fewer (one
+            // long sequence) they stay in the main launch, where they
+            // overlap the other tiles.
+            const bool split = t % kBM != 0 && qtiles > 1 && sh >= 2 * num_cus();
+            const int main_tiles = split ? qtiles - 1 : qtiles;
+            const int64_t mblocks = static_cast<int64_t>(kXcds) * ceil_div(sh, kXcds) * main_tiles;
+            flash_f16_kernel<false><<<dim3(static_cast<uint32_t>(mblocks)), dim3(kThreads), 0, st>>>(
                 static_cast<const f16*>(q), static_cast<const f16*>(k), static_cast<const f16*>(v),
-                static_cast<f16*>(out), sh, h, t, qtiles, c, token_major);
+                static_cast<f16*>(out), sh, h, t, main_tiles, c, token_major, 0);
+            if (split) {
+                const int64_t tblocks = static_cast<int64_t>(kXcds) * ceil_div(sh, kXcds);
+                flash_f16_kernel<true><<<dim3(static_cast<uint32_t>(tblocks)), dim3(kThreads), 0, st>>>(
+                    static_cast<const f16*>(q), static_cast<const f16*>(k), static_cast<const f16*>(v),
+                    static_cast<f16*>(out), sh, h, t, 1, c, token_major, qtiles - 1);
+            }
             return check_launch("attention");
         }
     }

@@ -173,6 +173,20 @@ def test_attention_f16_random_sweep(ctx, case):
     f16_close(got, ref, f"attention sweep case {case}: s={s} h={h} t={t} scale={scale}")
 
 
+@pytest.mark.parametrize("t", [257, 300, 511])
+def test_attention_partial_tile_launch(ctx, t):
+    """32 sequences x 16 heads with a partial last 256-query tile: the tile
+    runs as its own launch with the waves past T idle (t = 257 leaves one
+    live query in it), plain and merged outputs against float32 torch."""
+    s, h = 32, 16
+    q, k, v = rand_qkv(t, (s, h, t, 64), torch.float16)
+    got = ctx.attention(q, k, v)
+    f16_close(back(got).astype(np.float32), back(torch_attention32(q, k, v)),
+              f"partial-tile launch t={t}")
+    assert_bit_exact(back(ctx.attention_merged(q, k, v)), back(ctx.attn_merge(got)),
+                     f"partial-tile launch merged t={t}")
+
+
 def test_attention_d128_f32(ctx):
     """The camera head's head_dim 128 (f32 only, engine/ops.rs:233-238)."""
     rng = np.random.default_rng(128)
