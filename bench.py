@@ -1069,6 +1069,9 @@ def summarize(args) -> None:
     # Attention (the benchmark's attention leg): the flash kernel, told apart by
     # grid size: one workgroup of 8 waves (512 work-items) per 256 queries of
     # one (sequence, head), the (sequence, head) count rounded up to the 8 XCDs.
+    # When the last query tile is partial and there are at least two such
+    # tiles per CU (256 CUs), the call is two launches (the full tiles, then
+    # the partial ones); its time is their sum.
     att = defaultdict(list)
     t_tok = GRID[0] * GRID[1] + PREFIX
     for r in csv.DictReader(open(legs)):
@@ -1076,20 +1079,29 @@ def summarize(args) -> None:
             att[int(r["Grid_Size_X"])].append(
                 (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     shapes = {"frame": (args.frames, t_tok), "global": (1, args.frames * t_tok)}
-    att_grid = {name: 8 * -(-(s_ * HEADS) // 8) * -(-tt // 256) * 512
-                for name, (s_, tt) in shapes.items()}
-    if any(att_grid[n] in att for n in shapes):
+
+    def att_grids(s_, tt):
+        """(main launch grid, tail launch grid or None) in work-items."""
+        sh, qt = s_ * HEADS, -(-tt // 256)
+        per_tile = 8 * -(-sh // 8) * 512
+        if tt % 256 and qt > 1 and sh >= 2 * 256:
+            return per_tile * (qt - 1), per_tile
+        return per_tile * qt, None
+
+    att_grid = {name: att_grids(s_, tt) for name, (s_, tt) in shapes.items()}
+    if any(att_grid[n][0] in att for n in shapes):
         out += ["", "## Attention (flash_f16_kernel, f16, 16 heads of 64)", "",
                 "| call | grid work-items | kernel calls | mean us | TFLOP/s | of 2.5 PFLOP/s |",
                 "|---|---|---|---|---|---|"]
         for name, (s_, tt) in shapes.items():
-            grid = att_grid[name]
+            grid, tail = att_grid[name]
             durs = att.get(grid)
             if not durs:
                 continue
-            m = st.mean(durs)
+            m = st.mean(durs) + (st.mean(att[tail]) if tail and att.get(tail) else 0.0)
             tf = 4.0 * tt * tt * HEAD_DIM * s_ * HEADS / (m * 1e-6) / 1e12
-            out.append(f"| {name} (S={s_}, T={tt}) | {grid} | {len(durs)} | {m:.1f} | {tf:.0f} | "
+            shown = f"{grid} + {tail}" if tail else str(grid)
+            out.append(f"| {name} (S={s_}, T={tt}) | {shown} | {len(durs)} | {m:.1f} | {tf:.0f} | "
                        f"{tf / MFMA_PEAK_TFLOPS:.1%} |")
     cache = [(int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
              for r in csv.DictReader(open(legs))
