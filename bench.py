@@ -242,7 +242,8 @@ CEILING_PROBES = {
 }
 KINDS = {"copy": 0, "add2": 1, "heads": 2, "cast": 3}
 # hsc_run shape flags: bit 0 cached loads/stores (else streaming), bit 1 one
-# 16-byte vector per lane / one token per wave (else four / two)
+# 16-byte vector per lane / one token's 8-head chunk per wave, chunk by chunk
+# (else four / two whole rows)
 CEILING_SHAPES = {"streaming x4": 0, "cached x4": 1, "streaming x1": 2, "cached x1": 3}
 
 
@@ -334,11 +335,15 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
         warm, cold_us = timed(probe, args, sets)
         layouts = None
         if probe == "heads":
-            # the pass's global blocks: one sequence of S*T tokens
+            # the pass's global blocks: one sequence of S*T tokens; each
+            # layout takes its own fastest shape, as the op picks its order
+            # by sequence length
             gwarm, gcold = timed(probe, (0, 1, frames * t), sets)
-            layouts = {"frame_us": round(min(warm.values()), 2), "frame_cold_us": round(cold_us, 2),
-                       "global_us": round(min(gwarm.values()), 2), "global_cold_us": round(gcold, 2)}
-            warm = {k: (warm[k] + gwarm[k]) / 2 for k in warm}
+            fpol, gpol = min(warm, key=warm.get), min(gwarm, key=gwarm.get)
+            layouts = {"frame_us": round(warm[fpol], 2), "frame_cold_us": round(cold_us, 2),
+                       "frame_policy": fpol, "global_us": round(gwarm[gpol], 2),
+                       "global_cold_us": round(gcold, 2), "global_policy": gpol}
+            warm = {f"{fpol} / {gpol}": (warm[fpol] + gwarm[gpol]) / 2}
             cold_us = (cold_us + gcold) / 2
         policy = min(warm, key=warm.get)
         us = warm[policy]

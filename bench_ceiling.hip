@@ -7,15 +7,17 @@
 //   copy   1 read : 1 write, contiguous            (layernorm, bias_gelu)
 //   add2   2 reads : 1 write, contiguous           (bias_ls_residual)
 //   heads  token-major (S*T, 16*64) f16 -> head-major (S, 16, T, 64), two
-//          tensors in one launch, a wave per two tokens (or one) and 8 heads'
-//          128-byte vectors per store: the addressing of the fused QK-norm +
-//          RoPE pair kernel (qknorm_rope)
+//          tensors in one launch, 8 heads' 128-byte vectors per store, a
+//          wave per two whole rows or per one token's 8-head chunk (chunk
+//          by chunk): the fused QK-norm + RoPE pair kernel's two orders
+//          (qknorm_rope)
 //   cast   f32 rows in, f16 rows out, contiguous   (assembly's byte mix)
 //
 // Each kernel runs with non-temporal (streaming) or ordinary cached loads and
 // stores, the two policies the library's kernels use, and in two launch
-// shapes: four 16-byte vectors per lane (two tokens per wave for heads) or
-// one (one token per wave); the bench takes the fastest as the ceiling (a
+// shapes: four 16-byte vectors per lane (two whole rows per wave for heads)
+// or one (one token's 8-head chunk per wave); the bench takes the fastest as
+// the ceiling (a
 // bare copy is fastest with one vector per lane, 82% of peak against 78%
 // with four, while the ops, with their arithmetic, run best with their own
 // shapes). Not part of libheadshot_hip: built into bench_ceiling.so next to
@@ -71,37 +73,50 @@ __global__ __launch_bounds__(kBlock) void add2_kernel(const u32x4* __restrict__ 
         if (base + u * 64 < n) st<NT>(o + base + u * 64, ra[u] + rb[u]);
 }
 
-// Two tensors: waves [0, W) copy the first, [W, 2W) the second, W =
-// ceil(tokens / K). A load covers one token's 8 heads (1 KiB contiguous),
-// a store writes those 8 heads' vectors to their head-major rows.
-template <bool NT, int K>
+// Two tensors, K tokens per wave. Whole rows (SPLIT false): waves [0, W)
+// copy the first tensor, [W, 2W) the second, W = ceil(tokens / K), each
+// token's two 1 KiB loads (8 heads each). SPLIT: a wave takes one 1 KiB
+// chunk (8 heads) of its tokens and the grid runs (chunk, tensor) units
+// chunk by chunk, the order the QK-norm pair uses for long sequences. A
+// store writes 8 heads' vectors to their head-major rows.
+template <bool NT, int K, bool SPLIT>
 __global__ __launch_bounds__(kBlock) void heads_kernel(const f16* __restrict__ x0,
                                                        const f16* __restrict__ x1,
                                                        f16* __restrict__ o0, f16* __restrict__ o1,
                                                        int64_t tokens, int seq) {
-    constexpr int H = 16, D = 64;
+    constexpr int H = 16, D = 64, NC = SPLIT ? 1 : 2;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * (kBlock / 64) + hs::wave_in_block();
     const int64_t per = (tokens + K - 1) / K;
-    const int which = wave >= per ? 1 : 0;
-    const int64_t u0 = (wave - which * per) * K;
-    if (which > 1 || u0 >= tokens) return;
+    int which, c0 = 0;
+    int64_t u0;
+    if constexpr (SPLIT) {
+        const int64_t unit = wave / per;
+        if (unit > 3) return;
+        c0 = static_cast<int>(unit / 2), which = static_cast<int>(unit % 2);
+        u0 = (wave - unit * per) * K;
+    } else {
+        which = wave >= per ? 1 : 0;
+        u0 = (wave - which * per) * K;
+        if (wave >= 2 * per) return;
+    }
+    if (u0 >= tokens) return;
     const f16* x = which ? x1 : x0;
     f16* o = which ? o1 : o0;
     const int lane = hs::lane_id(), gsub = lane >> 3, ch = (lane & 7) * 8;
-    u32x4 r[K][2];
+    u32x4 r[K][NC];
 #pragma unroll
     for (int k = 0; k < K; k++)
 #pragma unroll
-        for (int c = 0; c < 2; c++)
-            if (u0 + k < tokens) r[k][c] = ld<NT>(reinterpret_cast<const u32x4*>(x + (u0 + k) * (H * D) + (c * 8 + gsub) * D + ch));
+        for (int c = 0; c < NC; c++)
+            if (u0 + k < tokens) r[k][c] = ld<NT>(reinterpret_cast<const u32x4*>(x + (u0 + k) * (H * D) + ((c0 + c) * 8 + gsub) * D + ch));
 #pragma unroll
     for (int k = 0; k < K; k++) {
         const int64_t tok = u0 + k;
         if (tok >= tokens) break;
         const int64_t s = tok / seq, t = tok - s * seq;
 #pragma unroll
-        for (int c = 0; c < 2; c++)
-            st<NT>(reinterpret_cast<u32x4*>(o + ((s * H + c * 8 + gsub) * seq + t) * D + ch), r[k][c]);
+        for (int c = 0; c < NC; c++)
+            st<NT>(reinterpret_cast<u32x4*>(o + ((s * H + (c0 + c) * 8 + gsub) * seq + t) * D + ch), r[k][c]);
     }
 }
 
@@ -149,13 +164,16 @@ int run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n, in
             break;
         }
         case 2: {
+            // four vectors per lane: two whole rows per wave; one: one token's
+            // 1 KiB chunk per wave, chunk by chunk
             constexpr int K = U == 1 ? 1 : 2;
+            constexpr bool SPLIT = U == 1;
             const int64_t tokens = static_cast<int64_t>(s) * t;
-            const int64_t waves = 2 * ((tokens + K - 1) / K);
+            const int64_t waves = (SPLIT ? 4 : 2) * ((tokens + K - 1) / K);
             const int64_t blocks = (waves + 3) / 4;
             if (blocks == 0) return 0;
             if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
-            heads_kernel<NT, K><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+            heads_kernel<NT, K, SPLIT><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
                 static_cast<const f16*>(a), static_cast<const f16*>(b), static_cast<f16*>(o),
                 static_cast<f16*>(o2), tokens, t);
             break;
@@ -182,8 +200,8 @@ extern "C" {
 // kind 0 copy / 1 add2: n 16-byte vectors (a, b -> o). kind 2 heads: s
 // frames of t tokens, a and b -> o and o2. kind 3 cast: n f32 elements
 // (n % 4 == 0). shape: bit 0 set = cached loads and stores (clear:
-// non-temporal), bit 1 set = one 16-byte vector per lane / one token per
-// wave (clear: four / two). Buffers are 16-byte aligned and sized by the
+// non-temporal), bit 1 set = one 16-byte vector per lane / one token's
+// 8-head chunk per wave (clear: four / two whole rows). Buffers are 16-byte aligned and sized by the
 // caller. Returns 0, or -1 for an argument the kernels do not take, or the
 // HIP error code of the launch.
 int hsc_run(int kind, int shape, const void* a, const void* b, void* o, void* o2, int64_t n,

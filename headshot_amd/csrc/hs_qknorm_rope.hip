@@ -19,7 +19,15 @@
 // are in flight while the current one is computed and stored. Each store
 // writes 64/G heads' 128-byte vectors of one token into the head-major
 // (S, H, T, 64) output that attention consumes. (A pure copy with exactly
-// this addressing runs as fast as a contiguous copy of the same bytes.)
+// this addressing runs as fast as a contiguous copy of the same bytes when
+// T is a frame's 1374 tokens.) For long sequences (T >= kSplitSeq, the
+// global blocks' 43,968 tokens) the output's head regions lie megabytes
+// apart and writing all of them at once costs: there a wave takes one
+// 1 KiB load chunk (64/G heads) of each row and the grid runs chunk by
+// chunk, so half as many regions receive writes at a time (S=32 global
+// layout, q and k: 61.5 us against 66.0; a pure copy in that order 75% of
+// the HBM peak against 67%; in the frame layout the split is slower, 66 us
+// against 59).
 //
 // RoPE tables: all 64/G head groups of a wave need the same cos/sin values
 // for a token, so per-lane table loads would fetch each row 64/G times (as
@@ -51,6 +59,9 @@ namespace {
 #ifndef HS_QK_BPC
 #define HS_QK_BPC 8  // resident workgroups per CU (generic path)
 #endif
+// Sequence length from which a wave takes one load chunk of each row
+// instead of the whole row (see above).
+constexpr int kSplitSeq = 8192;
 
 constexpr int kBlock = 256;
 constexpr int kWavesPerBlock = kBlock / 64;
@@ -67,7 +78,7 @@ int64_t persistent_blocks(int64_t work_waves) {
 // loads; the token index, its frame and the RoPE decision are wave-uniform
 // (scalar divide, uniform branch), and each store writes HPI heads' vectors
 // of one token (HPI separate 128-byte pieces of the head-major output).
-template <typename T, int H, bool NORM, bool ROPE>
+template <typename T, int H, bool NORM, bool ROPE, bool SPLIT>
 struct QknRow {
     static constexpr int D = 64;
     static constexpr int V = Vec<T>::N;
@@ -75,7 +86,8 @@ struct QknRow {
     static constexpr int HPI = 64 / G;
     static constexpr int CH = H / HPI;
     static_assert(H % HPI == 0, "whole load instructions per row");
-    static constexpr int HB = CH;  // loads per unit (buffer size)
+    static constexpr int NCH = SPLIT ? 1 : CH;  // load chunks per wave and row
+    static constexpr int HB = NCH;              // loads per unit (buffer size)
 
     const T* __restrict__ x;
     const float* __restrict__ sin_tab;
@@ -87,11 +99,12 @@ struct QknRow {
     int64_t tab_tok0;      // token of the slice's first row
     float eps;
     float wr[V], br[V];
+    int c0;                // first load chunk of the row this wave takes
 
     __device__ __forceinline__ void load(u32x4 (&raw)[HB], int64_t tok) const {
         const T* xr = x + tok * (H * D) + gsub * D + ch;
 #pragma unroll
-        for (int c = 0; c < CH; c++) raw[c] = ld_stream(xr + c * HPI * D);
+        for (int c = 0; c < NCH; c++) raw[c] = ld_stream(xr + (c0 + c) * HPI * D);
     }
 
     __device__ __forceinline__ void process(const u32x4 (&raw)[HB], int64_t tok) const {
@@ -126,18 +139,19 @@ struct QknRow {
     __device__ __forceinline__ void emit(const u32x4 (&raw)[HB], T* obase, const float (&cs)[V],
                                          const float (&sn)[V]) const {
 #pragma unroll
-        for (int c = 0; c < CH; c++) {
+        for (int c = 0; c < NCH; c++) {
             float f[V];
             unpack(raw[c], f, T{});
             qk_norm_rope_vec<T, G, NORM>(f, wr, br, eps, ROT, cs, sn);
-            st_stream(obase + static_cast<int64_t>(c) * HPI * seq * D, pack(f, T{}));
+            st_stream(obase + static_cast<int64_t>(c0 + c) * HPI * seq * D, pack(f, T{}));
         }
     }
 };
 
 // One or two tensors of the same shape that share the RoPE tables and one
 // launch (q and k of a block): waves [0, W) take the first, [W, 2W) the
-// second, W = ceil(tokens / K).
+// second, W = ceil(tokens / K); with SPLIT the units (chunk, tensor) run
+// chunk-major, W waves each.
 template <typename T>
 struct QknTensors {
     const T* x[2];
@@ -151,22 +165,32 @@ struct QknTensors {
 // the loads of unit i+1 are in flight while unit i is normalised, rotated
 // and stored, so waves overlap memory with arithmetic instead of alternating
 // between them in lockstep.
-template <typename T, int H, bool NORM, bool ROPE, int K>
+template <typename T, int H, bool NORM, bool ROPE, int K, bool SPLIT>
 __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
     QknTensors<T> ts, const float* __restrict__ sin_tab, const float* __restrict__ cos_tab,
     int64_t tokens, int seq, int prefix, float eps) {
-    using Row = QknRow<T, H, NORM, ROPE>;
+    using Row = QknRow<T, H, NORM, ROPE, SPLIT>;
     constexpr int G = Row::G, V = Row::V, HB = Row::HB;
     const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
     const int64_t per_tensor = ceil_div(tokens, int64_t{K});
-    const int which = wave >= per_tensor ? 1 : 0;
-    if (which >= ts.n) return;  // wave-uniform: the kernel has no barriers
-    const int64_t u0 = (wave - which * per_tensor) * K;
+    int which, chunk = 0;
+    int64_t u0;
+    if constexpr (SPLIT) {
+        const int64_t unit = wave / per_tensor;
+        chunk = static_cast<int>(unit / ts.n), which = static_cast<int>(unit % ts.n);
+        if (chunk >= Row::CH) return;  // wave-uniform: the kernel has no barriers
+        u0 = (wave - unit * per_tensor) * K;
+    } else {
+        which = wave >= per_tensor ? 1 : 0;
+        if (which >= ts.n) return;  // wave-uniform: the kernel has no barriers
+        u0 = (wave - which * per_tensor) * K;
+    }
     if (u0 >= tokens) return;  // the grid's last workgroup may run past the second tensor
     const int64_t u_end = u0 + K < tokens ? u0 + K : tokens;
     const int lane = lane_id();
     const int piece = lane % G;
     Row tl;
+    tl.c0 = chunk;
     tl.x = ts.x[which], tl.out = ts.out[which];
     tl.sin_tab = sin_tab, tl.cos_tab = cos_tab;
     tl.seq = seq, tl.prefix = prefix, tl.eps = eps;
@@ -347,14 +371,27 @@ __global__ __launch_bounds__(kBlock) void qkn_generic_kernel(
     }
 }
 
+// Row waves of a launch: K tokens per wave and tensor, times the load
+// chunks of a row when each wave takes one.
+template <typename T>
+int64_t row_waves(int64_t tokens, int n, int h, int seq) {
+    const int64_t parts = seq >= kSplitSeq ? h / Vec<T>::N : 1;
+    return ceil_div(tokens, int64_t{HS_QK_K}) * n * parts;
+}
+
 template <typename T, int H, bool NORM, bool ROPE>
 hs_status launch_rows(hipStream_t st, const QknTensors<T>& ts, const float* sn, const float* cs,
                       int64_t tokens, int seq, int prefix, float eps) {
     constexpr int K = HS_QK_K;
-    const int64_t blocks = ceil_div(ceil_div(tokens, int64_t{K}) * ts.n, int64_t{kWavesPerBlock});
-    qkn_row_kernel<T, H, NORM, ROPE, K>
-        <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(ts, sn, cs, tokens, seq,
-                                                                      prefix, eps);
+    const int64_t blocks = ceil_div(row_waves<T>(tokens, ts.n, H, seq), int64_t{kWavesPerBlock});
+    if (seq >= kSplitSeq)
+        qkn_row_kernel<T, H, NORM, ROPE, K, true>
+            <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(ts, sn, cs, tokens, seq,
+                                                                          prefix, eps);
+    else
+        qkn_row_kernel<T, H, NORM, ROPE, K, false>
+            <<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(ts, sn, cs, tokens, seq,
+                                                                          prefix, eps);
     return check_launch("qknorm_rope");
 }
 
@@ -394,8 +431,7 @@ hs_status dispatch_tok(hipStream_t st, const QknTensors<T>& ts, const float* sn,
     // The dispatch packet counts work-items in 32 bits: the row grid has one
     // wave per K tokens per tensor; beyond that the persistent generic
     // kernel runs.
-    const int64_t row_blocks =
-        ceil_div(ceil_div(tokens, int64_t{HS_QK_K}) * ts.n, int64_t{kWavesPerBlock});
+    const int64_t row_blocks = ceil_div(row_waves<T>(tokens, ts.n, h, t), int64_t{kWavesPerBlock});
     const bool grid_ok = row_blocks * kBlock < (int64_t{1} << 32);
     if (d == 64 && ptrs_ok && grid_ok) {
         switch (h) {

@@ -11,7 +11,7 @@ import bench
 
 pytestmark = pytest.mark.gpu
 # shape flags: bit 0 cached (else streaming), bit 1 one vector per lane /
-# one token per wave (else four / two)
+# one token's 8-head chunk per wave (else four / two whole rows)
 POLICIES = [0, 1, 2, 3]
 
 

@@ -187,6 +187,37 @@ def test_qknorm_rope_pair_unaligned_and_shared_input(ctx):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("h", [8, 16, 32])
+@pytest.mark.parametrize("norm,use_rope", [(True, True), (False, False)])
+def test_qknorm_rope_long_sequence(ctx, dtype, h, norm, use_rope):
+    """A sequence of 8286 tokens (91x91 grid, prefix 5): from 8192 tokens the
+    row kernel gives each wave one load chunk of every row and runs the
+    chunks one after another. The pair against the oracle and bit-exact
+    against two single calls."""
+    s, grid, prefix, d = 1, (91, 91), 5, 64
+    t = grid[0] * grid[1] + prefix
+    q = host(O.normal(41, (s * t, h * d)), dtype)
+    k = host(O.normal(42, (s * t, h * d)), dtype)
+    qn = (O.normal(43, (d,), 1.0, 0.02), O.normal(44, (d,), 0.0, 0.02))
+    kn = (O.normal(45, (d,), 1.0, 0.02), O.normal(46, (d,), 0.0, 0.02))
+    sin, cos = _tables(t, prefix, grid, d)
+    rp = (dev(sin), dev(cos), prefix) if use_rope else None
+    dq, dk = dev(q), dev(k)
+    kw = dict(qn=tuple(dev(a) for a in qn) if norm else None,
+              kn=tuple(dev(a) for a in kn) if norm else None)
+    gq, gk = ctx.qknorm_rope_pair(dq, dk, s, t, h, d, rope=rp, eps=1e-6, **kw)
+    what = f"qknorm_rope long {dtype} h={h} norm={norm} rope={use_rope}"
+    assert_bit_exact(back(gq), back(ctx.qknorm_rope(dq, s, t, h, d, norm=kw["qn"], rope=rp,
+                                                    eps=1e-6)), what + " q")
+    want = O.qknorm_rope(k, *(kn if norm else (None, None)), sin if use_rope else None,
+                         cos if use_rope else None, s, t, h, d, prefix, 1e-6)
+    if not norm and not use_rope:
+        assert_bit_exact(back(gk), want, what + " k")
+    else:
+        check(back(gk), want, what + " k oracle", stages=2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_qknorm_rope_prefix_equals_t(ctx, dtype):
     s, t, h, d = 2, 5, 16, 64
     x = host(O.normal(24, (s * t, h * d)), dtype)
