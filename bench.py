@@ -370,7 +370,10 @@ def attention_times(ctx, frames: int, iters: int) -> dict:
     (hs_attention_merged, as model/block.rs:148-149 consumes it): frame
     blocks run S sequences of 1374 tokens, global blocks one sequence of
     S*1374, 16 heads of 64, f16. Kernel time from HIP events on the launch
-    stream; flops = 4*T^2*D per (sequence, head)."""
+    stream; flops = 4*T^2*D per (sequence, head). For reference torch's own
+    fused attention (scaled_dot_product_attention, the backend it picks on
+    ROCm; head-major output, no merge; not part of this library) is timed
+    beside it in alternating rounds, each figure its fastest of three."""
     import torch
 
     out = {}
@@ -383,19 +386,29 @@ def attention_times(ctx, frames: int, iters: int) -> dict:
         o = torch.empty((s * tt, h * HEAD_DIM), dtype=torch.float16, device=ctx.device)
         ctx.attention_merged(q, k, v, out=o)
         call = ctx.last_launch
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(iters):
-            call()
-        b.record()
-        torch.cuda.synchronize()
-        ms = a.elapsed_time(b) / iters
+
+        def timed(fn):
+            fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(iters):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / iters
+
+        best = alternating_best(
+            {"hip": call,
+             "library": lambda: torch.nn.functional.scaled_dot_product_attention(q, k, v)}, timed)
+        ms, ms_lib = best["hip"], best["library"]
         flops = 4.0 * tt * tt * HEAD_DIM * s * h
         tf = flops / (ms * 1e-3) / 1e12
         out[name] = {"shape_SHTD": [s, h, tt, HEAD_DIM], "ms": round(ms, 3),
                      "TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
-                     "calls_per_pass": N_FRAME_BLOCKS if name == "frame" else N_GLOBAL_BLOCKS}
+                     "calls_per_pass": N_FRAME_BLOCKS if name == "frame" else N_GLOBAL_BLOCKS,
+                     "library_sdpa_ms": round(ms_lib, 3),
+                     "library_sdpa_TFLOP/s": round(flops / (ms_lib * 1e-3) / 1e12, 1)}
         del q, k, v, o
     out["roofline"] = {"bound": "mfma", "kernel": "flash_f16_kernel (global)",
                        "achieved": out["global"]["TFLOP/s"], "peak": MFMA_PEAK_TFLOPS,
