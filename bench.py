@@ -134,11 +134,66 @@ class Pass:
         self.fp.run()
 
 
+class KernelEvent:
+    """A HIP timing event recorded without the system-scope release
+    (hipEventCreateWithFlags with hipEventDisableSystemFence), with
+    torch.cuda.Event's record/elapsed_time surface, on torch's current
+    stream. A default event's record releases to system scope, writing back
+    and invalidating the GPU caches: between two back-to-back kernels that
+    adds ~1.7 us to every event pair (S=32 pass: the ops' event durations
+    fall from 48.4 / 30.8 / 63.8 / 42.4 / 122.3 us to 46.5 / 29.1 / 62.2 /
+    40.7 / 120.7 us, against 45.8 / 28.7 / 61.4 / 39.8 / 120.8 in the kernel
+    trace) and empties the L2 that the next kernel would otherwise find as
+    the graph-replayed pass leaves it. The HIP runtime is the one torch
+    loaded (same soname, so the same handle)."""
+
+    _hip = None
+
+    def __init__(self):
+        import ctypes
+
+        if KernelEvent._hip is None:
+            hip = ctypes.CDLL("libamdhip64.so.7")
+            hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                ctypes.c_void_p]
+            hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            KernelEvent._hip = hip
+        self._ev = ctypes.c_void_p()
+        rc = self._hip.hipEventCreateWithFlags(ctypes.byref(self._ev), 0x20000000)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags returned {rc}")
+
+    def record(self):
+        import ctypes
+
+        import torch
+
+        rc = self._hip.hipEventRecord(self._ev, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord returned {rc}")
+
+    def elapsed_time(self, end: "KernelEvent") -> float:
+        import ctypes
+
+        ms = ctypes.c_float()
+        rc = self._hip.hipEventElapsedTime(ctypes.byref(ms), self._ev, end._ev)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime returned {rc}")
+        return ms.value
+
+    def __del__(self):
+        if self._hip is not None and self._ev:
+            self._hip.hipEventDestroy(self._ev)
+
+
 def per_op_times(bench: Pass, passes: int, flush=None) -> dict:
-    """Mean kernel duration per op (ms) from HIP event pairs on the launch
-    stream. A GPU busy-wait ahead of each pass lets the host enqueue the
-    whole pass first, so the kernels run back to back as in the timed loop.
-    One untimed pass runs between the busy-wait and the timed one: the first
+    """Mean kernel duration per op (ms) from event pairs on the launch
+    stream (KernelEvent: no cache flush at each record). A GPU busy-wait
+    ahead of each pass lets the host enqueue the whole pass first, so the
+    kernels run back to back as in the timed loop. One untimed pass runs
+    between the busy-wait and the timed one: the first
     kernel after the wait runs slower (the assembly at S=32: 52.1 us against
     49.4 us back to back), and in the timed loop every op, the assembly
     included, follows other work.
@@ -148,8 +203,7 @@ def per_op_times(bench: Pass, passes: int, flush=None) -> dict:
     input of the timed op is cache-resident (cold timing)."""
     import torch
 
-    pairs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             for _ in bench.seq]
+    pairs = [(KernelEvent(), KernelEvent()) for _ in bench.seq]
     sums = {op: 0.0 for op in OPS}
     counts = {op: 0 for op in OPS}
     for _ in range(passes):
@@ -307,7 +361,7 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
             for bufs in sets:
                 launch(shape, ptrs(bufs))
             torch.cuda.synchronize()
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a, b = KernelEvent(), KernelEvent()
             a.record()
             for i in range(iters):
                 launch(shape, ptrs(sets[i % len(sets)]))
@@ -316,8 +370,7 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
             warm[policy] = a.elapsed_time(b) / iters * 1e3
         cold = []
         for shape in (s for s in CEILING_SHAPES.values() if not s & 1):  # streaming stores only
-            ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-                  for _ in range(iters)]
+            ev = [(KernelEvent(), KernelEvent()) for _ in range(iters)]
             for a, b in ev:
                 flush()
                 a.record()
