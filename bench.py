@@ -184,8 +184,11 @@ class KernelEvent:
         return ms.value
 
     def __del__(self):
-        if self._hip is not None and self._ev:
-            self._hip.hipEventDestroy(self._ev)
+        try:
+            if self._hip is not None and self._ev:
+                self._hip.hipEventDestroy(self._ev)
+        except Exception:  # interpreter shutdown: the runtime may be gone
+            pass
 
 
 def per_op_times(bench: Pass, passes: int, flush=None) -> dict:
