@@ -68,3 +68,22 @@ def test_cast(lib, n, temporal):
     o = torch.empty(n, device="cuda", dtype=torch.float16)
     _run(lib, "cast", temporal, x, None, o, None, n, 0, 0)
     assert torch.equal(o, x.half())
+
+
+def test_kernel_event_times_what_torch_events_time():
+    """bench.KernelEvent (no system-scope release at record) measures the
+    same interval as torch's default events around a fixed-length GPU
+    busy-wait: within the ~2 us the default events' cache flush adds."""
+    torch.cuda.synchronize()
+    pairs = {"kernel": (bench.KernelEvent(), bench.KernelEvent()),
+             "torch": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))}
+    ms = {}
+    for name, (a, b) in pairs.items():
+        torch.cuda._sleep(1_000_000)  # untimed: the timed wait follows other work
+        a.record()
+        torch.cuda._sleep(5_000_000)
+        b.record()
+        torch.cuda.synchronize()
+        ms[name] = a.elapsed_time(b)
+    assert ms["kernel"] > 0.5, ms  # a ~5 M-cycle wait is milliseconds long
+    assert abs(ms["kernel"] - ms["torch"]) < 0.01 + 0.05 * ms["torch"], ms
