@@ -182,7 +182,7 @@ __device__ __forceinline__ void mask_tail(f32x16 (&s)[kKB], int key0, int t, int
 // addition rounded to f16, at most 2^-11 relative) and four v_dot2 into
 // f32. Beside MFMAs a v_dot2 costs ~6 cycles that do not overlap them (an
 // issue-rate probe), so the packed additions replace twelve of the sixteen
-// (global calls 1.5% faster, frame calls 2-3%). Masked keys weigh exp2(-inf) = 0; a weight or partial sum past
+// (global calls 3% faster, frame calls 2%). Masked keys weigh exp2(-inf) = 0; a weight or partial sum past
 // f16's range gives an infinite sum, which takes the max path.
 __device__ __forceinline__ float weights_tile(const f32x16 (&s)[kKB], float c, float m,
                                               u32x4 (&p)[kKB][2]) {
