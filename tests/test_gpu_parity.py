@@ -449,3 +449,35 @@ def test_fused_ops_random_sweep(ctx, case):
                              reg if reg is not None else np.zeros((0, d), NP[dtype]),
                              s, p, r, NP[dtype], n_var)
     assert_bit_exact(got, want, f"{tag} assemble s={s} p={p} r={r} d={d} n_var={n_var}")
+
+
+# ------------------------------------------------------------ empty inputs
+
+def test_every_op_accepts_empty_inputs(ctx):
+    """Zero rows, tokens or frames through every op of the surface: each
+    returns an empty result of the right shape and launches nothing that
+    touches memory (no fault, HS_OK)."""
+    f16, f32 = torch.float16, torch.float32
+    d = "cuda:0"
+    e = lambda *shape, dt=f16: torch.empty(shape, dtype=dt, device=d)  # noqa: E731
+    ones = lambda n: torch.ones(n, dtype=f32, device=d)  # noqa: E731
+    assert ctx.bias_gelu(e(0, 4096), ones(4096)).shape == (0, 4096)
+    assert ctx.gelu(e(0, 64)).shape == (0, 64)
+    assert ctx.bias_ls_residual(e(0, 1024), e(0, 1024), ones(1024), ones(1024)).shape == (0, 1024)
+    assert ctx.residual_ls(e(0, 1024), e(0, 1024), ones(1024)).shape == (0, 1024)
+    assert ctx.layernorm_stats(e(0, 1024), eps=1e-6).numel() == 0
+    q = ctx.qknorm_rope(e(0, 1024), 0, 1374, 16, 64, norm=(ones(64), ones(64)))
+    assert q.numel() == 0
+    qh, kh = ctx.qknorm_rope_pair(e(0, 1024), e(0, 1024), 0, 1374, 16, 64)
+    assert qh.numel() == 0 and kh.numel() == 0
+    cam, reg = e(2, 1024), e(2 * 4, 1024)
+    assert ctx.assemble_tokens(e(0, 1024, dt=f32), 0, 1369, cam, reg).shape == (0, 1024)
+    for s, h, t in ((0, 16, 1374), (2, 16, 0)):
+        assert ctx.attention(e(s, h, t, 64), e(s, h, t, 64), e(s, h, t, 64)).numel() == 0
+        assert ctx.attention_merged(e(s, h, t, 64), e(s, h, t, 64), e(s, h, t, 64)).numel() == 0
+    w = torch.zeros((256, 1024), dtype=f16, device=d)
+    assert ctx.linear(e(0, 1024), w, ones(256)).shape == (0, 256)
+    assert ctx.linear_gelu(e(0, 1024), w, ones(256)).shape == (0, 256)
+    assert ctx.linear_ls_residual(e(0, 1024), w, ones(256), e(0, 256), ones(256)).shape == (0, 256)
+    assert ctx.cache_build(e(0, 1024), e(0, 1024)).shape == (0, 2048)
+    torch.cuda.synchronize()
