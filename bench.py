@@ -81,6 +81,10 @@ def parse():
     ap.add_argument("--frames", type=int, default=32)
     ap.add_argument("--dtype", choices=["f16", "f32"], default="f16")
     ap.add_argument("--op-passes", type=int, default=3)
+    ap.add_argument("--shared-inputs", action="store_true",
+                    help="all blocks read one set of raw GEMM outputs (default: each its own)")
+    ap.add_argument("--no-workloads", action="store_true",
+                    help="skip the other workloads' legs (S=2, 8, 200, 16 at 21x37)")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of a graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-ceilings", action="store_true",
@@ -113,22 +117,25 @@ def parse():
 
 class Pass:
     """One aggregator fused-op pass (headshot_amd.aggregator.FusedOpPass)
-    plus its algorithmic byte counts."""
+    plus its algorithmic byte counts. ``distinct``: each block reads raw
+    GEMM outputs of its own (48 x 720 MB at S=32)."""
 
-    def __init__(self, ctx, frames: int, dtype):
+    def __init__(self, ctx, frames: int, dtype, grid=GRID, n_frame: int = N_FRAME_BLOCKS,
+                 n_global: int = N_GLOBAL_BLOCKS, distinct: bool = True):
         import torch
 
         from headshot_amd.aggregator import FusedOpPass
 
-        self.fp = fp = FusedOpPass(ctx, frames, grid=GRID, n_reg=N_REG, n_frame=N_FRAME_BLOCKS,
-                                   n_global=N_GLOBAL_BLOCKS, dtype=dtype, eps=EPS)
+        self.fp = fp = FusedOpPass(ctx, frames, grid=grid, n_reg=N_REG, n_frame=n_frame,
+                                   n_global=n_global, dtype=dtype, eps=EPS,
+                                   distinct_inputs=distinct)
         self.ctx, self.frames, self.dtype = ctx, frames, dtype
         self.p, self.t, self.rows = fp.p, fp.t, fp.rows
         self.seq = fp.seq
         esz = 2 if dtype == torch.float16 else 4
         self.bytes = op_bytes(self.rows, esz, frames * fp.p, fp.p)
         self.launches = fp.launches()
-        self.pass_bytes = sum(self.bytes[k] * self.launches[k] for k in OPS)
+        self.pass_bytes = sum(self.bytes[k] * self.launches.get(k, 0) for k in OPS)
 
     def run(self):
         self.fp.run()
@@ -254,6 +261,74 @@ def op_rates(bench: Pass, mean_ms: dict) -> dict:
                       "frac": round(gbs / PEAK_GBS, 4), "bytes": bench.bytes[op],
                       "launches_per_pass": bench.launches[op]}
     return per_op
+
+
+def pass_from_ops(bench: Pass, per_op: dict) -> dict:
+    """The pass rate that the per-op kernel times imply: pass bytes / the sum
+    of each op's mean duration x its launches (with cold per-op times: every
+    launch finding none of its inputs in a cache)."""
+    ms = sum(per_op[op]["us"] * bench.launches.get(op, 0) for op in OPS) / 1e3
+    gbs = bench.pass_bytes / (ms * 1e-3) / 1e9
+    return {"ms": round(ms, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+
+
+# The op sequence's other workloads, each timed like the headline pass:
+# key -> (frames, (patch rows, patch columns), storage, frame blocks, global
+# blocks). A frame block runs S sequences of T tokens with RoPE; a global
+# block one sequence of S*T tokens without.
+WORKLOADS = {
+    "s2_f32_frame_global": (2, (37, 37), "f32", 1, 1),
+    "s8_f16_frame": (8, (37, 37), "f16", 1, 0),
+    "s200_f16_global": (200, (37, 37), "f16", 0, 1),
+    "s200_f16_frame": (200, (37, 37), "f16", 1, 0),
+    "s16_21x37_f32_frame_global": (16, (21, 37), "f32", 1, 1),
+    "s16_21x37_f16_frame_global": (16, (21, 37), "f16", 1, 1),
+}
+
+
+def workload_legs(ctx, op_passes: int, flush, min_launches: int = 64, replays: int = 10) -> dict:
+    """Each workload's sequence (assembly, then its blocks' fused ops, every
+    block with raw GEMM outputs of its own) captured in a HIP graph,
+    repeated until the graph holds at least ``min_launches`` launches (so a
+    few short kernels are not timed against one graph launch), replayed
+    ``replays`` times: ms per sequence, GB/s of its algorithmic bytes,
+    tokens/s (S*T tokens per sequence); and each op's kernel time warm and
+    cold (event pairs, as the headline's ``ops``)."""
+    import torch
+
+    out = {}
+    for key, (frames, grid, dt, nf, ng) in WORKLOADS.items():
+        dtype = torch.float16 if dt == "f16" else torch.float32
+        b = Pass(ctx, frames, dtype, grid=grid, n_frame=nf, n_global=ng, distinct=True)
+        reps = max(1, -(-min_launches // len(b.fp.seq)))
+        b.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                b.run()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(replays):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / (replays * reps)
+        gbs = b.pass_bytes / (ms * 1e-3) / 1e9
+        warm = op_rates(b, per_op_times(b, op_passes))
+        cold = op_rates(b, per_op_times(b, op_passes, flush=flush))
+        out[key] = {"frames": frames, "tokens_per_frame": b.t, "grid": f"{grid[0]}x{grid[1]}",
+                    "dtype": dt, "frame_blocks": nf, "global_blocks": ng, "rows": b.rows,
+                    "ms_per_sequence": round(ms, 4), "bytes_per_sequence": b.pass_bytes,
+                    "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                    "tokens_per_s": round(b.rows / (ms * 1e-3), 1),
+                    "pass_cold": pass_from_ops(b, cold), "ops": warm, "ops_cold": cold,
+                    "graph_repeats": reps}
+        del graph, b
+        torch.cuda.empty_cache()
+    return out
 
 
 MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense f16 matrix peak
@@ -610,17 +685,17 @@ def gemm_times(ctx, frames: int, iters: int) -> dict:
         del x, w, o
     out["ms_per_block"] = round(total_ms, 3)
     out["ms_per_pass"] = round(total_ms * (N_FRAME_BLOCKS + N_GLOBAL_BLOCKS), 2)
-    out["layernorm_folded"] = ln_fold_times(ctx, m, timed, g)
+    out["layernorm_prologue"] = ln_prologue_times(ctx, m, timed, g)
     return out
 
 
-def ln_fold_times(ctx, m: int, timed, g) -> dict:
-    """The pre-norm LayerNorm folded into the product after it
-    (hs_layernorm_stats + hs_linear_ln_gelu / hs_linear_ln_qkv_heads on
-    weights folded by hs_fold_layernorm) against layernorm then the fused
-    product, at the block's LN2 -> fc1 + GELU and LN1 -> q|k|v (heads,
-    QK-norm, RoPE) shapes. Times include the statistics pass; each is its
-    fastest of three alternating rounds."""
+def ln_prologue_times(ctx, m: int, timed, g) -> dict:
+    """The pre-norm LayerNorm as the prologue of the product after it
+    (hs_layernorm_stats + hs_linear_ln_gelu / hs_linear_ln_qkv_heads, which
+    normalise the x tiles in LDS; bit-identical results) against layernorm
+    then the fused product, at the block's LN2 -> fc1 + GELU and LN1 ->
+    q|k|v (heads, QK-norm, RoPE) shapes. Times include the statistics pass;
+    each is its fastest of three alternating rounds."""
     import torch
 
     from headshot_amd import rope as _rope
@@ -641,28 +716,29 @@ def ln_fold_times(ctx, m: int, timed, g) -> dict:
     for name, n in (("fc1", HIDDEN), ("qkv", 3 * DIM)):
         w = (torch.randn((n, DIM), generator=g) / DIM ** 0.5).half().to(ctx.device)
         b = (torch.randn(n, generator=g) * 0.02).to(ctx.device)
-        f = ctx.fold_layernorm(w, b, lw, lb)
         if name == "fc1":
             o = torch.empty((m, n), dtype=torch.float16, device=ctx.device)
             ctx.linear_gelu(normed, w, b, out=o)
             plain = ctx.last_launch
-            ctx.linear_ln_gelu(x, f, eps=EPS, out=o, workspace=ws)
-            folded = ctx.last_launch
+            ctx.linear_ln_gelu(x, (lw, lb), w, b, eps=EPS, out=o, workspace=ws)
+            fused = ctx.last_launch
         else:
             o = tuple(torch.empty((frames, HEADS, t, HEAD_DIM), dtype=torch.float16,
                                   device=ctx.device) for _ in range(3))
             ctx.linear_qkv_heads(normed, w, b, frames, t, HEADS, qn=nrm, kn=nrm,
                                  rope=(sin, cos, PREFIX), eps=EPS, out=o)
             plain = ctx.last_launch
-            ctx.linear_ln_qkv_heads(x, f, frames, t, HEADS, qn=nrm, kn=nrm,
+            ctx.linear_ln_qkv_heads(x, (lw, lb), w, b, frames, t, HEADS, qn=nrm, kn=nrm,
                                     rope=(sin, cos, PREFIX), eps=EPS, out=o, workspace=ws)
-            folded = ctx.last_launch
-        best = alternating_best({"plain": lambda: (ln_call(), plain()), "folded": folded}, timed)
-        ms_plain, ms_fold = best["plain"], best["folded"]
+            fused = ctx.last_launch
+        best = alternating_best({"plain": lambda: (ln_call(), plain()), "prologue": fused,
+                                 "plain_product": plain}, timed)
+        ms_plain, ms_pro = best["plain"], best["prologue"]
         fl = 2.0 * m * n * DIM
         out[name] = {"layernorm_then_product_ms": round(ms_plain, 3),
-                     "folded_ms": round(ms_fold, 3),
-                     "folded_TFLOP/s": round(fl / (ms_fold * 1e-3) / 1e12, 1)}
+                     "product_alone_ms": round(best["plain_product"], 3),
+                     "prologue_ms": round(ms_pro, 3),
+                     "prologue_TFLOP/s": round(fl / (ms_pro * 1e-3) / 1e12, 1)}
         del w, o
     return out
 
@@ -682,13 +758,12 @@ def block_times(ctx, frames: int, iters: int) -> dict:
     t = GRID[0] * GRID[1] + PREFIX
     gen = torch.Generator(device=ctx.device).manual_seed(17)
     wts = BlockWeights.random(DIM, HIDDEN, HEAD_DIM, torch.float16, ctx.device, gen)
-    wts.fold_layernorms(ctx)
     x = torch.randn((frames * t, DIM), generator=gen, device=ctx.device).half()
     sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(_rope.periods(), *GRID))
     out = {}
 
-    def folded(*a, **kw):
-        return block_forward(*a, fold_ln2=True, fold_ln1=True, **kw)
+    def ln_passes(*a, **kw):
+        return block_forward(*a, fuse_ln=False, **kw)
 
     for kind, (s, tt, rope) in {"frame": (frames, t, (sin, cos, PREFIX)),
                                 "global": (1, frames * t, None)}.items():
@@ -705,16 +780,16 @@ def block_times(ctx, frames: int, iters: int) -> dict:
 
         fns = {name: (lambda f=f: f(ctx, wts, x, s, tt, rope=rope, eps=EPS))
                for name, f in (("fused", block_forward), ("reference_sequence", block_forward_reference),
-                               ("fused_layernorm_folded", folded))}
+                               ("fused_layernorm_passes", ln_passes))}
         out[kind] = {name + "_ms": round(ms, 3) for name, ms in alternating_best(fns, timed).items()}
     out["aggregator_ms"] = round(N_FRAME_BLOCKS * out["frame"]["fused_ms"]
                                  + N_GLOBAL_BLOCKS * out["global"]["fused_ms"], 1)
     out["aggregator_reference_sequence_ms"] = round(
         N_FRAME_BLOCKS * out["frame"]["reference_sequence_ms"]
         + N_GLOBAL_BLOCKS * out["global"]["reference_sequence_ms"], 1)
-    out["aggregator_layernorm_folded_ms"] = round(
-        N_FRAME_BLOCKS * out["frame"]["fused_layernorm_folded_ms"]
-        + N_GLOBAL_BLOCKS * out["global"]["fused_layernorm_folded_ms"], 1)
+    out["aggregator_layernorm_passes_ms"] = round(
+        N_FRAME_BLOCKS * out["frame"]["fused_layernorm_passes_ms"]
+        + N_GLOBAL_BLOCKS * out["global"]["fused_layernorm_passes_ms"], 1)
     return out
 
 
@@ -726,10 +801,8 @@ def trunk_times(ctx, frames: int, iters: int) -> dict:
     register gather/scatter and the 4 head-input caches. Random-init f16
     weights in the checkpoint's layout (fused q|k|v), generated on the
     device. Beside it the reference's dispatch sequence through the same
-    library's single ops (Trunk.forward(fused=False)), and the fused trunk
-    with every block's LayerNorms folded into the products after them
-    (Trunk.forward(fold_ln=True)). Each figure is its fastest of three
-    alternating rounds."""
+    library's single ops (Trunk.forward(fused=False)). Each figure is its
+    fastest of three alternating rounds."""
     import torch
 
     from headshot_amd.aggregator import BlockWeights
@@ -747,7 +820,7 @@ def trunk_times(ctx, frames: int, iters: int) -> dict:
     p = GRID[0] * GRID[1]
     tokens = torch.randn((frames * p, TDIM), generator=gen, device=ctx.device)
     out = {"frames": frames, "tokens_per_frame": p + 17}
-    trunk.fold_layernorms(ctx)
+
     def timed(fn):
         fn()
         torch.cuda.synchronize()
@@ -759,9 +832,8 @@ def trunk_times(ctx, frames: int, iters: int) -> dict:
         torch.cuda.synchronize()
         return a.elapsed_time(b) / iters
 
-    fns = {name: (lambda fu=fused, fo=fold: trunk.forward(ctx, tokens, frames, *GRID, fused=fu, fold_ln=fo))
-           for name, fused, fold in (("fused", True, False), ("reference_sequence", False, False),
-                                     ("fused_layernorm_folded", True, True))}
+    fns = {name: (lambda fu=fused: trunk.forward(ctx, tokens, frames, *GRID, fused=fu))
+           for name, fused in (("fused", True), ("reference_sequence", False))}
     for name, ms in alternating_best(fns, timed).items():
         out[name + "_ms"] = round(ms, 1)
     out["frames_per_s"] = round(frames / (out["fused_ms"] * 1e-3), 1)
@@ -898,18 +970,27 @@ def cpu_baseline(ctx, target_s: float):
     seq = []
     run_block_ops(ctx, p, io, frames, t, HEADS, HEAD_DIM, rope=(sin, cos, prefix), eps=EPS,
                   record=lambda op: seq.append(ctx.last_launch))
-    iters = 200
     for _ in range(10):
         gpu_block()
     torch.cuda.synchronize()
+    # a HIP graph of `reps` back-to-back blocks, replayed: the kernels' time,
+    # not the host's launch rate (6 small launches per block)
+    reps, replays = 64, 5
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(reps):
+            for thunk in seq:
+                thunk()
+    graph.replay()
+    torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for _ in range(iters):
-        for thunk in seq:
-            thunk()
+    for _ in range(replays):
+        graph.replay()
     b.record()
     torch.cuda.synchronize()
-    gpu_ms = a.elapsed_time(b) / iters
+    gpu_ms = a.elapsed_time(b) / (reps * replays)
+    del graph
     gpu_gbs = nbytes / (gpu_ms * 1e-3) / 1e9
     return {
         "value": round(nbytes / cpu_s / 1e9, 3),
@@ -929,8 +1010,8 @@ def cpu_baseline(ctx, target_s: float):
         "gpu_same_config": {"ms_per_block": round(gpu_ms, 4), "GB/s": round(gpu_gbs, 1),
                             "frac": round(gpu_gbs / PEAK_GBS, 4),
                             "tokens_per_s": round(rows / (gpu_ms * 1e-3), 1),
-                            "timing": f"HIP events over {iters} back-to-back blocks (6 launches "
-                                      f"each, fused ops)"},
+                            "timing": f"HIP graph of {reps} back-to-back blocks (6 launches "
+                                      f"each, fused ops), {replays} replays"},
     }
 
 
@@ -1294,7 +1375,7 @@ def main():
 
     dtype = torch.float16 if args.dtype == "f16" else torch.float32
     ctx = HipContext("cuda:0")
-    bench = Pass(ctx, args.frames, dtype)
+    bench = Pass(ctx, args.frames, dtype, distinct=not args.shared_inputs)
     torch.cuda.synchronize()
 
     # HBM counter calibration: one plain copy of known size (outside timing).
@@ -1338,13 +1419,17 @@ def main():
     torch.cuda.synchronize()
     ms = start.elapsed_time(end) / args.steps
 
-    per_op, per_op_cold, roofline, ops_ms, ceilings = {}, None, None, None, None
+    per_op, per_op_cold, roofline, ops_ms, ceilings, pass_cold = {}, None, None, None, None, None
+    workloads = None
     if args.op_passes > 0:
         per_op = op_rates(bench, per_op_times(bench, args.op_passes))
         flush = cache_flusher(ctx.device)
         per_op_cold = op_rates(bench, per_op_times(bench, args.op_passes, flush=flush))
         if not args.no_ceilings:
             ceilings = ceiling_times(bench, per_op, per_op_cold, flush)
+        pass_cold = pass_from_ops(bench, per_op_cold)
+        if not args.no_workloads:
+            workloads = workload_legs(ctx, args.op_passes, flush)
         del flush
         ops_ms = round(sum(per_op[op]["us"] * bench.launches[op] for op in OPS) / 1e3, 3)
         dominant = max(OPS, key=lambda op: per_op[op]["us"] * bench.launches[op])
@@ -1373,6 +1458,7 @@ def main():
                 "(LN gamma N(1,.02), beta/biases/pos N(0,.02), LayerScale 1e-5)",
         "config": {"workload": f"aggregator fused-op pass: assembly + {N_FRAME_BLOCKS} frame + "
                                f"{N_GLOBAL_BLOCKS} global blocks",
+                   "block_inputs": "shared" if args.shared_inputs else "per block",
                    "frames": args.frames, "tokens_per_frame": bench.t, "dim": DIM,
                    "heads": HEADS, "head_dim": HEAD_DIM, "hidden": HIDDEN, "prefix": PREFIX,
                    "grid": f"{GRID[0]}x{GRID[1]}", "eps": EPS, "launch": launch},
@@ -1380,10 +1466,12 @@ def main():
         "pass_bytes": bench.pass_bytes,
         "tokens_per_s": round(bench.rows / (ms * 1e-3), 1),
         "ops_ms_per_step": ops_ms,
+        "pass_cold": pass_cold,
         "ops": per_op,
         "ops_cold": per_op_cold,
         "ceilings": ceilings,
         "roofline": roofline,
+        "workloads": workloads,
     }
     if args.attention_iters > 0:
         line["attention"] = attention_times(ctx, args.frames, args.attention_iters)

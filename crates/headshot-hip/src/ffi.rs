@@ -104,30 +104,28 @@ extern "C" {
                                k_out: *mut c_void, v_out: *mut c_void, S: i32, T: i32, H: i32,
                                d: i32, k: i32, prefix: i32, eps: f32) -> HsStatus;
 
-    // LayerNorm folded into the linear layer after it
+    // LayerNorm as the prologue of the linear layer after it
     pub fn hs_layernorm_stats(stream: HsStream, dt: HsDtype, x: *const c_void, stats: *mut f32,
                               rows: i64, dim: i32, eps: f32) -> HsStatus;
-    pub fn hs_fold_layernorm(stream: HsStream, dt: HsDtype, w: *const c_void, bias: *const f32,
-                             ln_w: *const f32, ln_b: *const f32, w_fold: *mut c_void,
-                             colsum: *mut f32, shift: *mut f32, n: i32, k: i32) -> HsStatus;
-    pub fn hs_linear_ln(stream: HsStream, dt: HsDtype, x: *const c_void, w_fold: *const c_void,
-                        colsum: *const f32, shift: *const f32, workspace: *mut f32,
-                        out: *mut c_void, m: i64, n: i32, k: i32, eps: f32) -> HsStatus;
-    pub fn hs_linear_ln_gelu(stream: HsStream, dt: HsDtype, x: *const c_void,
-                             w_fold: *const c_void, colsum: *const f32, shift: *const f32,
+    pub fn hs_linear_ln(stream: HsStream, dt: HsDtype, x: *const c_void, ln_w: *const f32,
+                        ln_b: *const f32, w: *const c_void, bias: *const f32,
+                        workspace: *mut f32, out: *mut c_void, m: i64, n: i32, k: i32, eps: f32)
+                        -> HsStatus;
+    pub fn hs_linear_ln_gelu(stream: HsStream, dt: HsDtype, x: *const c_void, ln_w: *const f32,
+                             ln_b: *const f32, w: *const c_void, bias: *const f32,
                              workspace: *mut f32, out: *mut c_void, m: i64, n: i32, k: i32,
                              eps: f32) -> HsStatus;
-    pub fn hs_linear_ln_gelu_noalloc(stream: HsStream, dt: HsDtype, x: *const c_void,
-                                     w_fold: *const c_void, colsum: *const f32,
-                                     shift: *const f32, out: *mut c_void, m: i64, n: i32, k: i32,
-                                     eps: f32) -> HsStatus;
     pub fn hs_linear_ln_qkv_heads(stream: HsStream, dt: HsDtype, x: *const c_void,
-                                  w_fold: *const c_void, colsum: *const f32, shift: *const f32,
-                                  qn_w: *const f32, qn_b: *const f32, kn_w: *const f32,
-                                  kn_b: *const f32, sin_tab: *const f32, cos_tab: *const f32,
-                                  workspace: *mut f32, q_out: *mut c_void, k_out: *mut c_void,
-                                  v_out: *mut c_void, S: i32, T: i32, H: i32, d: i32, k: i32,
-                                  prefix: i32, eps: f32) -> HsStatus;
+                                  ln_w: *const f32, ln_b: *const f32, w_qkv: *const c_void,
+                                  b_qkv: *const f32, qn_w: *const f32, qn_b: *const f32,
+                                  kn_w: *const f32, kn_b: *const f32, sin_tab: *const f32,
+                                  cos_tab: *const f32, workspace: *mut f32, q_out: *mut c_void,
+                                  k_out: *mut c_void, v_out: *mut c_void, S: i32, T: i32, H: i32,
+                                  d: i32, k: i32, prefix: i32, eps: f32) -> HsStatus;
+    pub fn hs_linear_ln_gelu_noalloc(stream: HsStream, dt: HsDtype, x: *const c_void,
+                                     ln_w: *const f32, ln_b: *const f32, w: *const c_void,
+                                     bias: *const f32, out: *mut c_void, m: i64, n: i32, k: i32,
+                                     eps: f32) -> HsStatus;
 
     // attention
     pub fn hs_attention(stream: HsStream, dt: HsDtype, q: *const c_void, k: *const c_void,

@@ -158,14 +158,6 @@ fn i32_of(v: usize, what: &str) -> i32 {
     i32::try_from(v).unwrap_or_else(|_| panic!("{what} {v} exceeds i32"))
 }
 
-/// A linear layer with the LayerNorm before it folded in
-/// ([`HipContext::fold_layernorm`]).
-pub struct FoldedLinear {
-    pub w_fold: HipTensor,
-    pub colsum: HipTensor,
-    pub shift: HipTensor,
-}
-
 /// One device's op surface on one HIP stream.
 pub struct HipContext {
     stream: ffi::HsStream,
@@ -608,56 +600,44 @@ impl HipContext {
         out
     }
 
-    /// Folds a LayerNorm (norm weight and bias) into the linear layer after
-    /// it, once at load time.
-    pub fn fold_layernorm(&self, weight: &HipTensor, bias: Option<&HipTensor>,
-                          ln_w: &HipTensor, ln_b: &HipTensor) -> FoldedLinear {
-        let (n, k) = weight.dims();
-        let w_fold = self.empty_typed(&weight.shape, weight.dtype);
-        let colsum = self.empty(&[n]);
-        let shift = self.empty(&[n]);
-        check(unsafe {
-            ffi::hs_fold_layernorm(self.stream, weight.dtype.raw(), weight.cptr(),
-                                   opt_f32(bias, n, "bias"), opt_f32(Some(ln_w), k, "norm weight"),
-                                   opt_f32(Some(ln_b), k, "norm bias"), w_fold.mptr(),
-                                   colsum.mptr() as *mut f32, shift.mptr() as *mut f32,
-                                   i32_of(n, "n"), i32_of(k, "k"))
-        }, "fold_layernorm");
-        FoldedLinear { w_fold, colsum, shift }
-    }
-
-    fn folded(&self, x: &HipTensor, f: &FoldedLinear) -> (usize, usize, usize, HipTensor) {
+    /// Operands of the `linear_ln*` calls: x (m, k), the LayerNorm's weight
+    /// and bias (k, f32), the linear weight (n, k); a statistics workspace.
+    fn ln_operands(&self, x: &HipTensor, ln: (&HipTensor, &HipTensor), weight: &HipTensor)
+                   -> (usize, usize, usize, *const f32, *const f32, HipTensor) {
         let (m, k) = x.dims();
-        let (n, wk) = f.w_fold.dims();
-        assert_eq!(wk, k, "folded weight k");
-        assert_eq!(f.w_fold.dtype, x.dtype, "folded weight dtype");
-        assert_eq!(f.colsum.len(), n, "colsum length");
-        assert_eq!(f.shift.len(), n, "shift length");
-        (m, n, k, self.empty(&[m, 2]))
+        let (n, wk) = weight.dims();
+        assert_eq!(wk, k, "linear_ln weight k");
+        assert_eq!(weight.dtype, x.dtype, "linear_ln weight dtype");
+        let lw = opt_f32(Some(ln.0), k, "norm weight");
+        let lb = opt_f32(Some(ln.1), k, "norm bias");
+        (m, n, k, lw, lb, self.empty(&[m, 2]))
     }
 
-    /// linear(layernorm(x)) on folded weights (model/block.rs:128-131).
-    pub fn linear_ln(&self, x: &HipTensor, f: &FoldedLinear, eps: f32) -> HipTensor {
-        let (m, n, k, ws) = self.folded(x, f);
+    /// layernorm(x) then linear(weight, bias) (model/block.rs:128-131) in one
+    /// product: the normalised rows, rounded to the storage type as
+    /// `layernorm` stores them, exist only on the way to the matrix cores.
+    pub fn linear_ln(&self, x: &HipTensor, ln: (&HipTensor, &HipTensor), weight: &HipTensor,
+                     bias: Option<&HipTensor>, eps: f32) -> HipTensor {
+        let (m, n, k, lw, lb, ws) = self.ln_operands(x, ln, weight);
         let out = self.empty_typed(&[m, n], x.dtype);
         check(unsafe {
-            ffi::hs_linear_ln(self.stream, x.dtype.raw(), x.cptr(), f.w_fold.cptr(),
-                              f.colsum.f32p("colsum"), f.shift.f32p("shift"),
-                              ws.mptr() as *mut f32, out.mptr(), m as i64, i32_of(n, "n"),
-                              i32_of(k, "k"), eps)
+            ffi::hs_linear_ln(self.stream, x.dtype.raw(), x.cptr(), lw, lb, weight.cptr(),
+                              opt_f32(bias, n, "bias"), ws.mptr() as *mut f32, out.mptr(),
+                              m as i64, i32_of(n, "n"), i32_of(k, "k"), eps)
         }, "linear_ln");
         out
     }
 
-    /// gelu(linear(layernorm(x))) on folded weights (LN2, fc1, GELU).
-    pub fn linear_ln_gelu(&self, x: &HipTensor, f: &FoldedLinear, eps: f32) -> HipTensor {
-        let (m, n, k, ws) = self.folded(x, f);
+    /// gelu(linear(layernorm(x))) in one product (LN2, fc1, GELU,
+    /// model/block.rs:153, 172-176).
+    pub fn linear_ln_gelu(&self, x: &HipTensor, ln: (&HipTensor, &HipTensor), weight: &HipTensor,
+                          bias: Option<&HipTensor>, eps: f32) -> HipTensor {
+        let (m, n, k, lw, lb, ws) = self.ln_operands(x, ln, weight);
         let out = self.empty_typed(&[m, n], x.dtype);
         check(unsafe {
-            ffi::hs_linear_ln_gelu(self.stream, x.dtype.raw(), x.cptr(), f.w_fold.cptr(),
-                                   f.colsum.f32p("colsum"), f.shift.f32p("shift"),
-                                   ws.mptr() as *mut f32, out.mptr(), m as i64, i32_of(n, "n"),
-                                   i32_of(k, "k"), eps)
+            ffi::hs_linear_ln_gelu(self.stream, x.dtype.raw(), x.cptr(), lw, lb, weight.cptr(),
+                                   opt_f32(bias, n, "bias"), ws.mptr() as *mut f32, out.mptr(),
+                                   m as i64, i32_of(n, "n"), i32_of(k, "k"), eps)
         }, "linear_ln_gelu");
         out
     }
@@ -666,30 +646,34 @@ impl HipContext {
     /// allocation by the library (the row statistics use the library's own
     /// per-device array): for callers that cannot allocate. At most 524,288
     /// rows; calls that overlap on one device race.
-    pub fn linear_ln_gelu_noalloc(&self, x: &HipTensor, f: &FoldedLinear, eps: f32,
+    pub fn linear_ln_gelu_noalloc(&self, x: &HipTensor, ln: (&HipTensor, &HipTensor),
+                                  weight: &HipTensor, bias: Option<&HipTensor>, eps: f32,
                                   out: &HipTensor) {
         let (m, k) = x.dims();
-        let (n, wk) = f.w_fold.dims();
-        assert_eq!(wk, k, "folded weight k");
+        let (n, wk) = weight.dims();
+        assert_eq!(wk, k, "linear_ln weight k");
+        assert_eq!(weight.dtype, x.dtype, "linear_ln weight dtype");
         assert_eq!(out.len(), m * n, "out shape");
         assert_eq!(out.dtype, x.dtype, "out dtype");
         check(unsafe {
-            ffi::hs_linear_ln_gelu_noalloc(self.stream, x.dtype.raw(), x.cptr(), f.w_fold.cptr(),
-                                           f.colsum.f32p("colsum"), f.shift.f32p("shift"),
-                                           out.mptr(), m as i64, i32_of(n, "n"), i32_of(k, "k"),
-                                           eps)
+            ffi::hs_linear_ln_gelu_noalloc(self.stream, x.dtype.raw(), x.cptr(),
+                                           opt_f32(Some(ln.0), k, "norm weight"),
+                                           opt_f32(Some(ln.1), k, "norm bias"), weight.cptr(),
+                                           opt_f32(bias, n, "bias"), out.mptr(), m as i64,
+                                           i32_of(n, "n"), i32_of(k, "k"), eps)
         }, "linear_ln_gelu_noalloc");
     }
 
     /// LN1 + the q|k|v projection with heads, QK-norm and RoPE
-    /// (model/block.rs:128-146) on the folded q|k|v weight.
+    /// (model/block.rs:128-146) in one product.
     #[allow(clippy::too_many_arguments)]
-    pub fn linear_ln_qkv_heads(&self, x: &HipTensor, f: &FoldedLinear, s: usize, t: usize,
+    pub fn linear_ln_qkv_heads(&self, x: &HipTensor, ln: (&HipTensor, &HipTensor),
+                               w_qkv: &HipTensor, b_qkv: Option<&HipTensor>, s: usize, t: usize,
                                h: usize, norms: Option<[(&HipTensor, &HipTensor); 2]>,
                                rope: Option<Rope>, eps: f32) -> (HipTensor, HipTensor, HipTensor) {
-        let (m, n3, k, ws) = self.folded(x, f);
+        let (m, n3, k, lw, lb, ws) = self.ln_operands(x, ln, w_qkv);
         assert_eq!(m, s * t, "x rows must be S*T");
-        assert_eq!(n3 % (3 * h), 0, "w_fold rows must be 3 * H * d");
+        assert_eq!(n3 % (3 * h), 0, "w_qkv rows must be 3 * H * d");
         let d = n3 / (3 * h);
         let mut p = [ptr::null::<f32>(); 4];
         if let Some([(qw, qb), (kw, kb)]) = norms {
@@ -699,12 +683,12 @@ impl HipContext {
         let (sn, cs, prefix) = rope_ptrs(rope.as_ref(), t, d);
         let outs = [0, 1, 2].map(|_| self.empty_typed(&[s, h, t, d], x.dtype));
         check(unsafe {
-            ffi::hs_linear_ln_qkv_heads(self.stream, x.dtype.raw(), x.cptr(), f.w_fold.cptr(),
-                                        f.colsum.f32p("colsum"), f.shift.f32p("shift"), p[0],
-                                        p[1], p[2], p[3], sn, cs, ws.mptr() as *mut f32,
-                                        outs[0].mptr(), outs[1].mptr(), outs[2].mptr(),
-                                        i32_of(s, "S"), i32_of(t, "T"), i32_of(h, "H"),
-                                        i32_of(d, "d"), i32_of(k, "k"), prefix, eps)
+            ffi::hs_linear_ln_qkv_heads(self.stream, x.dtype.raw(), x.cptr(), lw, lb, w_qkv.cptr(),
+                                        opt_f32(b_qkv, n3, "qkv bias"), p[0], p[1], p[2], p[3],
+                                        sn, cs, ws.mptr() as *mut f32, outs[0].mptr(),
+                                        outs[1].mptr(), outs[2].mptr(), i32_of(s, "S"),
+                                        i32_of(t, "T"), i32_of(h, "H"), i32_of(d, "d"),
+                                        i32_of(k, "k"), prefix, eps)
         }, "linear_ln_qkv_heads");
         let [q, kk, v] = outs;
         (q, kk, v)

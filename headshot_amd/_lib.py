@@ -51,12 +51,11 @@ SIGNATURES = {
     "hs_linear_qkv_heads": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                  _I32, _I32, _I32, _I32, _I32, _I32, _F]),
     "hs_layernorm_stats": (_S, [_P, _I32, _P, _P, _I64, _I32, _F]),
-    "hs_fold_layernorm": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _I32, _I32]),
-    "hs_linear_ln": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
-    "hs_linear_ln_gelu": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
-    "hs_linear_ln_gelu_noalloc": (_S, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
+    "hs_linear_ln": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
+    "hs_linear_ln_gelu": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
+    "hs_linear_ln_gelu_noalloc": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _I64, _I32, _I32, _F]),
     "hs_linear_ln_qkv_heads": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
-                                    _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F]),
+                                    _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _F]),
     "hs_concat_channels": (_S, [_P, _I32, _P, _P, _P, _I64, _I32, _I32]),
     "hs_cast_f16_to_f32": (_S, [_P, _P, _P, _I64]),
     "hs_cache_build": (_S, [_P, _I32, _P, _P, _P, _I64, _I32, _I32]),

@@ -18,7 +18,7 @@ from dataclasses import dataclass
 import torch
 
 from . import rope as _rope
-from .context import FoldedLinear, HipContext
+from .context import HipContext
 
 DIM, HEADS, HEAD_DIM, HIDDEN = 1024, 16, 64, 4096
 
@@ -107,11 +107,15 @@ class FusedOpPass:
     assembly, then ``n_frame`` frame blocks (QK-norm + RoPE, ``prefix``
     unrotated tokens) alternating with ``n_global`` global blocks (QK-norm,
     no RoPE). Inputs are synthetic: seeded N(0,1) activations and GEMM
-    outputs, random-init parameters (``BlockParams.random``)."""
+    outputs, random-init parameters (``BlockParams.random``). With
+    ``distinct_inputs`` every block reads raw GEMM outputs of its own (as
+    in the trunk, where each block's products are new data); otherwise all
+    blocks share one set."""
 
     def __init__(self, ctx: HipContext, frames: int, grid=(37, 37), n_reg: int = 4,
                  n_frame: int = 24, n_global: int = 24, dtype=torch.float16, eps: float = 1e-6,
-                 dim: int = DIM, heads: int = HEADS, hidden: int = HIDDEN, seed: int = 42):
+                 dim: int = DIM, heads: int = HEADS, hidden: int = HIDDEN, seed: int = 42,
+                 distinct_inputs: bool = False):
         self.ctx, self.frames, self.dtype, self.eps = ctx, frames, dtype, eps
         self.dim, self.heads, self.hidden = dim, heads, hidden
         self.head_dim = dim // heads
@@ -133,18 +137,12 @@ class FusedOpPass:
         self.patch_bias = normal((dim,), 0.0, 0.02)
         self.cam = normal((2, dim), dt=dtype)
         self.reg = normal((2 * n_reg, dim), dt=dtype)
-        q_raw, k_raw = normal((rows, dim), dt=dtype), normal((rows, dim), dt=dtype)
-        proj_raw, fc2_raw = normal((rows, dim), dt=dtype), normal((rows, dim), dt=dtype)
-        fc1_raw = normal((rows, hidden), dt=dtype)
-        x0 = torch.empty((rows, dim), device=dev, dtype=dtype)
-        x_b = torch.empty_like(x0)
-        io = BlockIO.empty_like_inputs(x0, q_raw, k_raw, proj_raw, fc1_raw, fc2_raw)
-        io.x_out = x_b
-        self.io = io
-        self.x = [x0, x_b]
-        sin, cos = _rope.tables(_rope.periods(), *grid)
-        self.sin = torch.from_numpy(sin).to(dev)
-        self.cos = torch.from_numpy(cos).to(dev)
+        def raw_outputs():
+            """q, k (qkv bias added), proj, fc1, fc2 products of one block."""
+            return (normal((rows, dim), dt=dtype), normal((rows, dim), dt=dtype),
+                    normal((rows, dim), dt=dtype), normal((rows, hidden), dt=dtype),
+                    normal((rows, dim), dt=dtype))
+
         kinds = []
         for i in range(max(n_frame, n_global)):
             if i < n_frame:
@@ -152,6 +150,17 @@ class FusedOpPass:
             if i < n_global:
                 kinds.append("global")
         self.kinds = kinds
+        raws = [raw_outputs()] * len(kinds) if not distinct_inputs else [raw_outputs() for _ in kinds]
+        self.raws = raws
+        x0 = torch.empty((rows, dim), device=dev, dtype=dtype)
+        x_b = torch.empty_like(x0)
+        io = BlockIO.empty_like_inputs(x0, *raws[0][:3], raws[0][3], raws[0][4])
+        io.x_out = x_b
+        self.io = io
+        self.x = [x0, x_b]
+        sin, cos = _rope.tables(_rope.periods(), *grid)
+        self.sin = torch.from_numpy(sin).to(dev)
+        self.cos = torch.from_numpy(cos).to(dev)
         self.blocks = [BlockParams.random(dim, hidden, self.head_dim, dev, g) for _ in kinds]
         self.seq = self._record()
 
@@ -170,7 +179,8 @@ class FusedOpPass:
                           out=self.x[0])
         rec("assemble")
         x = self.x[0]
-        for kind, p in zip(self.kinds, self.blocks):
+        for kind, p, raw in zip(self.kinds, self.blocks, self.raws):
+            io.q_raw, io.k_raw, io.proj_raw, io.fc1_raw, io.fc2_raw = raw
             io.x = x
             io.x_out = self.x[1] if x is self.x[0] else self.x[0]
             if kind == "frame":
@@ -210,17 +220,6 @@ class BlockWeights:
     proj_w: torch.Tensor  # (dim, dim)
     fc1_w: torch.Tensor   # (hidden, dim)
     fc2_w: torch.Tensor   # (dim, hidden)
-    # LN1 folded into the q|k|v projection, LN2 into fc1 (fold_layernorms)
-    qkv_fold: FoldedLinear | None = None
-    fc1_fold: FoldedLinear | None = None
-
-    def fold_layernorms(self, ctx: HipContext) -> "BlockWeights":
-        """Prepares the LayerNorm-prologue path of ``block_forward`` once at
-        load time: LN1's affine parameters folded into the q|k|v weight and
-        bias, LN2's into fc1's (HipContext.fold_layernorm)."""
-        self.qkv_fold = ctx.fold_layernorm(self.qkv_w, self.qkv_b, *self.p.ln1)
-        self.fc1_fold = ctx.fold_layernorm(self.fc1_w, self.p.fc1_b, *self.p.ln2)
-        return self
 
     def _third(self, t, i):
         dim = self.qkv_w.shape[1]
@@ -276,35 +275,31 @@ class BlockWeights:
 
 
 def block_forward(ctx: HipContext, wts: BlockWeights, x, s: int, t: int, heads: int = HEADS,
-                  rope=None, eps: float = 1e-6, fold_ln2: bool = False, fold_ln1: bool = False):
+                  rope=None, eps: float = 1e-6, fuse_ln: bool = False):
     """Block::forward (model/block.rs:118-193) with every op on HIP and the
     epilogues fused: LN1 -> the q|k|v linear with split_heads, QK-norm and
     RoPE in its epilogue -> attention written token-major -> proj +
     LayerScale + residual -> LN2 -> fc1 + GELU -> fc2 + LayerScale +
-    residual (7 launches). ``rope`` = (sin, cos, prefix) or None (global
-    blocks). With the weights prepared by ``BlockWeights.fold_layernorms``,
-    ``fold_ln2`` folds LN2 into fc1 and ``fold_ln1`` LN1 into the q|k|v
-    projection: a row-statistics pass replaces the LayerNorm pass and the
-    normalised activation never reaches memory. Folding LN2 stays within the
-    f16 gate of the reference's sequence; folding LN1 rounds the q|k|v
-    product at another point than the reference, which QK-norm magnifies
-    beyond that gate for a few q and k values in 10^4 (as accurate against
-    float64 math as the reference's own sequence), so it is opt-in.
+    residual. ``rope`` = (sin, cos, prefix) or None (global blocks). With
+    ``fuse_ln`` each LayerNorm runs as the prologue of the product after it
+    (``linear_ln_qkv_heads``, ``linear_ln_gelu``): a row-statistics pass
+    replaces the LayerNorm pass and the normalised rows never reach memory.
+    The result is bit-identical either way; the LayerNorm pass is the
+    default because it is faster (every 256-column tile of the product
+    normalises the same x rows again, 12-16 times the pass's arithmetic).
     Returns the block output (S*T, dim)."""
     p = wts.p
-    if fold_ln1 or fold_ln2:
-        assert wts.qkv_fold is not None and wts.fc1_fold is not None, "fold_layernorms first"
-    if fold_ln1:
-        q, k, v = ctx.linear_ln_qkv_heads(x, wts.qkv_fold, s, t, heads, qn=p.qn, kn=p.kn,
-                                          rope=rope, eps=eps)
+    if fuse_ln:
+        q, k, v = ctx.linear_ln_qkv_heads(x, p.ln1, wts.qkv_w, wts.qkv_b, s, t, heads, qn=p.qn,
+                                          kn=p.kn, rope=rope, eps=eps)
     else:
         normed = ctx.layernorm(x, *p.ln1, eps=eps)
         q, k, v = ctx.linear_qkv_heads(normed, wts.qkv_w, wts.qkv_b, s, t, heads, qn=p.qn,
                                        kn=p.kn, rope=rope, eps=eps)
     attn = ctx.attention_merged(q, k, v)
     x1 = ctx.linear_ls_residual(attn, wts.proj_w, p.ls1, x, p.proj_b)
-    if fold_ln2:
-        act = ctx.linear_ln_gelu(x1, wts.fc1_fold, eps=eps)
+    if fuse_ln:
+        act = ctx.linear_ln_gelu(x1, p.ln2, wts.fc1_w, p.fc1_b, eps=eps)
     else:
         normed2 = ctx.layernorm(x1, *p.ln2, eps=eps)
         act = ctx.linear_gelu(normed2, wts.fc1_w, p.fc1_b)

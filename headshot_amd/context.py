@@ -18,7 +18,6 @@ stream (for launch loops and graph capture without per-call Python checks).
 from __future__ import annotations
 
 import math
-from dataclasses import dataclass
 
 import numpy as np
 import torch
@@ -37,17 +36,19 @@ def _dt(t: torch.Tensor) -> int:
     raise AssertionError(f"storage must be f32 or f16, got {t.dtype}")
 
 
-# Tensors whose pointers the op being prepared passes to the library; the
-# launch's re-issue thunk keeps them alive (a replayed launch must never
-# write into memory the caching allocator has handed out again).
-_held: list = []
+class _Ptr(int):
+    """A device address passed to the library, holding its tensor: a launch's
+    re-issue thunk keeps the tensors of its own arguments alive (a replayed
+    launch must never write into memory the caching allocator has handed
+    out again). Nothing is shared between calls or threads."""
 
 
 def _dev(t: torch.Tensor, what: str) -> int:
     assert t.is_cuda, f"{what} must live in device memory"
     assert t.is_contiguous(), f"{what} must be contiguous"
-    _held.append(t)
-    return t.data_ptr()
+    p = _Ptr(t.data_ptr())
+    p.tensor = t
+    return p
 
 
 def _param(t, n: int, what: str) -> int:
@@ -58,16 +59,6 @@ def _param(t, n: int, what: str) -> int:
 
 def _opt(t, n: int, what: str):
     return None if t is None else _param(t, n, what)
-
-
-@dataclass
-class FoldedLinear:
-    """A linear layer with the LayerNorm before it folded in
-    (``HipContext.fold_layernorm``): ``w_fold`` (n, k) in the storage dtype,
-    ``colsum`` and ``shift`` (n) f32."""
-    w_fold: torch.Tensor
-    colsum: torch.Tensor
-    shift: torch.Tensor
 
 
 class HipContext:
@@ -83,8 +74,7 @@ class HipContext:
         self.last_launch = None
 
     def _launch(self, name: str, fn, *args) -> None:
-        held = tuple(_held)
-        _held.clear()
+        held = tuple(a.tensor for a in args if isinstance(a, _Ptr))
 
         def call():
             _lib.check(fn(torch.cuda.current_stream().cuda_stream, *args), name)
@@ -392,81 +382,66 @@ class HipContext:
                      _dev(out, "stats"), rows, dim, eps)
         return out
 
-    def fold_layernorm(self, weight, bias, ln_w, ln_b) -> FoldedLinear:
-        """Folds the LayerNorm (``ln_w``, ``ln_b``) that feeds a linear layer
-        (``weight`` (n, k), ``bias`` (n) or None) into it, once at load time;
-        ``linear_ln*`` then compute linear(layernorm(x)) from raw x."""
-        n, k = weight.shape
-        b = _opt(bias, n, "bias")
-        w_fold = torch.empty_like(weight)
-        colsum = self.empty_typed((n,), F32)
-        shift = self.empty_typed((n,), F32)
-        self._launch("fold_layernorm", self.lib.hs_fold_layernorm, _dt(weight),
-                     _dev(weight, "weight"), b, _param(ln_w, k, "norm weight"),
-                     _param(ln_b, k, "norm bias"), _dev(w_fold, "w_fold"), _dev(colsum, "colsum"),
-                     _dev(shift, "shift"), n, k)
-        return FoldedLinear(w_fold, colsum, shift)
-
-    def _folded_args(self, x, folded: FoldedLinear, workspace):
+    def _ln_args(self, x, ln, weight, bias, workspace):
+        """Operands of the ``linear_ln*`` calls: ``ln`` = (weight, bias) of the
+        LayerNorm over x's last dim, ``weight`` (n, k) and ``bias`` (n) or
+        None of the linear layer, ``workspace`` (m, 2) f32 or None."""
         k = x.shape[-1]
         m = x.numel() // k if k else 0
-        w = folded.w_fold
-        assert w.dim() == 2 and w.shape[1] == k, "weight k mismatch"
-        assert w.dtype == x.dtype, "weight/activation dtype"
-        n = w.shape[0]
+        assert weight.dim() == 2 and weight.shape[1] == k, "weight k mismatch"
+        assert weight.dtype == x.dtype, "weight/activation dtype"
+        n = weight.shape[0]
+        lw, lb = _param(ln[0], k, "norm weight"), _param(ln[1], k, "norm bias")
+        b = _opt(bias, n, "bias")
         if workspace is None:
             workspace = self.empty_typed((m, 2), F32)
         assert workspace.dtype == F32 and workspace.numel() >= 2 * m, "workspace shape/dtype"
-        return m, n, k, (_dev(w, "w_fold"), _param(folded.colsum, n, "colsum"),
-                         _param(folded.shift, n, "shift"), _dev(workspace, "workspace"))
+        return m, n, k, lw, lb, b, _dev(workspace, "workspace")
 
-    def linear_ln(self, x, folded: FoldedLinear, eps: float = 1e-5, out=None,
+    def linear_ln(self, x, ln, weight, bias=None, eps: float = 1e-5, out=None,
                   workspace=None) -> torch.Tensor:
-        """linear(layernorm(x)) (model/block.rs:128-131) on folded weights,
-        without materialising the normalised activation."""
-        m, n, k, (w, cs, sh, ws) = self._folded_args(x, folded, workspace)
+        """layernorm(x, *ln) then linear(weight, bias) (model/block.rs:128-131)
+        in one product: the normalised rows, rounded to the storage type as
+        ``layernorm`` stores them, exist only on the way to the matrix cores.
+        Bit-identical to ``linear(layernorm(x))``."""
+        m, n, k, lw, lb, b, ws = self._ln_args(x, ln, weight, bias, workspace)
         if out is None:
             out = self.empty_typed((m, n), x.dtype)
         assert out.dtype == x.dtype and out.numel() == m * n, "out shape/dtype"
-        self._launch("linear_ln", self.lib.hs_linear_ln, _dt(x), _dev(x, "x"), w, cs, sh, ws,
-                     _dev(out, "out"), m, n, k, eps)
+        self._launch("linear_ln", self.lib.hs_linear_ln, _dt(x), _dev(x, "x"), lw, lb,
+                     _dev(weight, "weight"), b, ws, _dev(out, "out"), m, n, k, eps)
         return out
 
-    def linear_ln_gelu(self, x, folded: FoldedLinear, eps: float = 1e-5, out=None,
+    def linear_ln_gelu(self, x, ln, weight, bias=None, eps: float = 1e-5, out=None,
                        workspace=None) -> torch.Tensor:
         """gelu(linear(layernorm(x))) (model/block.rs:153, 172-176: LN2, fc1,
-        GELU) in one product on folded weights."""
-        m, n, k, (w, cs, sh, ws) = self._folded_args(x, folded, workspace)
+        GELU) in one product, bit-identical to ``linear_gelu(layernorm(x))``
+        under the conditions of ``linear_ln``."""
+        m, n, k, lw, lb, b, ws = self._ln_args(x, ln, weight, bias, workspace)
         if out is None:
             out = self.empty_typed((m, n), x.dtype)
         assert out.dtype == x.dtype and out.numel() == m * n, "out shape/dtype"
-        self._launch("linear_ln_gelu", self.lib.hs_linear_ln_gelu, _dt(x), _dev(x, "x"), w, cs,
-                     sh, ws, _dev(out, "out"), m, n, k, eps)
+        self._launch("linear_ln_gelu", self.lib.hs_linear_ln_gelu, _dt(x), _dev(x, "x"), lw, lb,
+                     _dev(weight, "weight"), b, ws, _dev(out, "out"), m, n, k, eps)
         return out
 
-    def linear_ln_qkv_heads(self, x, folded: FoldedLinear, s: int, t: int, h: int, qn=None,
+    def linear_ln_qkv_heads(self, x, ln, w_qkv, b_qkv, s: int, t: int, h: int, qn=None,
                             kn=None, rope=None, eps: float = 1e-5, out=None, workspace=None):
         """LN1 + the q|k|v projection with split_heads, QK-norm and RoPE
-        (model/block.rs:128-146) on the folded q|k|v weight: returns
-        head-major (q, k, v). ``eps`` serves both norms. Shapes the fused
-        kernel does not cover (f32, head dim other than 64) run
-        ``linear_ln`` then ``qknorm_rope`` per third."""
-        m, n3, k, (w, cs, sh, ws) = self._folded_args(x, folded, workspace)
-        assert m == s * t, "x rows must be S*T"
-        assert n3 % (3 * h) == 0, "w_fold rows must be 3 * H * d"
+        (model/block.rs:128-146) in one product: returns head-major (q, k,
+        v), bit-identical to ``linear_qkv_heads(layernorm(x))``. ``eps``
+        serves both norms. Shapes the fused kernel does not cover (f32, head
+        dim other than 64) run ``layernorm`` then ``linear_qkv_heads``."""
+        n3, k = w_qkv.shape
+        assert n3 % (3 * h) == 0, "w_qkv rows must be 3 * H * d"
         d = n3 // (3 * h)
-        hd = h * d
+        assert x.numel() == s * t * k and x.dtype == w_qkv.dtype, "x shape/dtype"
         if not (x.dtype == F16 and d == 64 and n3 % 256 == 0 and k % 64 == 0):
-            outs = []
-            for i, norm in enumerate((qn, kn, None)):
-                rows = slice(i * hd, (i + 1) * hd)
-                third = FoldedLinear(folded.w_fold[rows], folded.colsum[rows], folded.shift[rows])
-                proj = self.linear_ln(x, third, eps=eps, workspace=workspace)
-                outs.append(self.qknorm_rope(proj, s, t, h, d, norm=norm,
-                                             rope=rope if i < 2 else None, eps=eps,
-                                             out=None if out is None else out[i]))
-            return tuple(outs)
-        qw = qb = kw = kb = sn = cs_ = None
+            xn = self.layernorm(x, ln[0], ln[1], eps=eps)
+            return self.linear_qkv_heads(xn, w_qkv, b_qkv, s, t, h, qn=qn, kn=kn, rope=rope,
+                                         eps=eps, out=out)
+        m, _, _, lw, lb, b, ws = self._ln_args(x, ln, w_qkv, b_qkv, workspace)
+        qw = qb = kw = kb = sn = cs = None
         prefix = 0
         if qn is not None:
             qw, qb = _param(qn[0], d, "q-norm weight"), _param(qn[1], d, "q-norm bias")
@@ -476,14 +451,15 @@ class HipContext:
             sin, cos, prefix = rope
             assert 0 <= prefix <= t, "prefix"
             sn = _param(sin, (t - prefix) * d, "rope sin table")
-            cs_ = _param(cos, (t - prefix) * d, "rope cos table")
+            cs = _param(cos, (t - prefix) * d, "rope cos table")
         if out is None:
             out = tuple(self.empty_typed((s, h, t, d), x.dtype) for _ in range(3))
         for o in out:
             assert o.dtype == x.dtype and o.numel() == s * t * h * d, "out shape/dtype"
         self._launch("linear_ln_qkv_heads", self.lib.hs_linear_ln_qkv_heads, _dt(x),
-                     _dev(x, "x"), w, cs, sh, qw, qb, kw, kb, sn, cs_, ws, _dev(out[0], "q out"),
-                     _dev(out[1], "k out"), _dev(out[2], "v out"), s, t, h, d, k, prefix, eps)
+                     _dev(x, "x"), lw, lb, _dev(w_qkv, "w_qkv"), b, qw, qb, kw, kb, sn, cs, ws,
+                     _dev(out[0], "q out"), _dev(out[1], "k out"), _dev(out[2], "v out"), s, t,
+                     h, d, k, prefix, eps)
         return tuple(out)
 
     def linear_gelu(self, x, weight, bias=None, out=None) -> torch.Tensor:

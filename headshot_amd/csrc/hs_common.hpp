@@ -162,6 +162,16 @@ __device__ __forceinline__ float storage_round(float v, f16) {
 }
 __device__ __forceinline__ float storage_round(float v, float) { return v; }
 
+// One LayerNorm output value before its storage rounding: (x - mean) * inv *
+// w + b, the multiply-add spelled as fmaf and the f32 result materialised.
+// Every kernel that normalises a row (the LayerNorm kernels and the linear
+// layers' LayerNorm prologue) computes it through this helper, so a row
+// normalised inside a product is bit-identical to the row hs_layernorm
+// stores.
+__device__ __forceinline__ float ln_affine(float x, float mean, float inv, float w, float b) {
+    return as_f32(fmaf((x - mean) * inv, w, b));
+}
+
 template <typename T>
 __device__ __forceinline__ float load_elem(const T* p) {
     return static_cast<float>(*p);

@@ -32,7 +32,9 @@
 // scalar kernel, f32 accumulation in K order.
 #include <math.h>
 
+#include <initializer_list>
 #include <mutex>
+#include <type_traits>
 
 #include "hs_common.hpp"
 
@@ -57,12 +59,14 @@ struct QkvArgs {
     float eps;
 };
 
-// The LayerNorm folded into the product (hs_linear_ln*): stats holds each x
-// row's (mean, rsqrt(var + eps)), colsum each output column's sum of the
-// folded weight; the bias argument carries the folded shift.
+// The LayerNorm prologue (hs_linear_ln*): stats holds each x row's (mean,
+// rsqrt(var + eps)) from hs_layernorm_stats, ln_w / ln_b the LayerNorm's
+// affine parameters over the K input columns. The product reads each x
+// element as hs_layernorm would have stored it.
 struct LnArgs {
     const float* stats;
-    const float* colsum;
+    const float* ln_w;
+    const float* ln_b;
 };
 
 // Exact-erf GELU in the A&S 7.1.26 form used by the elementwise GELU kernel
@@ -124,13 +128,19 @@ struct GemmSmem {
     f16 x[2][kBM * kBK];
     f16 w[2][kBN * kBK];
 };
+// With the LayerNorm prologue, x stages land in `raw` one stage ahead of
+// their use and are normalised from there into x[]: raw follows GemmSmem.
+constexpr size_t kRawBytes = size_t{2} * kBM * kBK;
 // Epilogue staging: each wave's 128 x 64 output block as f16 rows of
 // kEpiPitch halves (144 B: 16-byte aligned rows, spread over the banks).
 constexpr int kEpiPitch = 64 + 8;
 constexpr int kEpiWave = 128 * kEpiPitch;  // halves per wave
-constexpr size_t kSmemBytes = sizeof(GemmSmem) > size_t{2} * kWaves * kEpiWave
-                                  ? sizeof(GemmSmem)
-                                  : size_t{2} * kWaves * kEpiWave;
+constexpr size_t smem_bytes(bool ln) {
+    const size_t loop = sizeof(GemmSmem) + (ln ? kRawBytes : 0);
+    const size_t epi = size_t{2} * kWaves * kEpiWave;
+    return loop > epi ? loop : epi;
+}
+static_assert(smem_bytes(true) <= 160 * 1024, "gfx950 has 160 KiB of LDS per workgroup");
 
 __device__ __forceinline__ h8 as_h8(u32x4 v) { return __builtin_bit_cast(h8, v); }
 
@@ -163,20 +173,112 @@ __device__ __forceinline__ StageOffsets stage_offsets(int64_t m0, int M, int K, 
     return o;
 }
 
-// Issues this wave's LDS-DMA loads of one stage from the buffer resources
-// covering the tile's x and w rows; koff = the stage's first column, in
-// bytes.
-__device__ __forceinline__ void issue_stage(GemmSmem& sm, int buf, __amdgpu_buffer_rsrc_t xr,
-                                            __amdgpu_buffer_rsrc_t wr, int koff,
-                                            const StageOffsets& o, int wave) {
+// Issue this wave's LDS-DMA loads of one stage's x (or w) rows from the
+// buffer resource covering the tile's rows into dst; koff = the stage's
+// first column, in bytes.
+__device__ __forceinline__ void issue_x(f16* dst, __amdgpu_buffer_rsrc_t xr, int koff,
+                                        const StageOffsets& o, int wave) {
 #pragma unroll
     for (int i = 0; i < kXInstr / kWaves; i++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            xr, (lds_void*)(&sm.x[buf][(wave + kWaves * i) * 512]), 16, o.x[i], koff, 0, 0);
+            xr, (lds_void*)(dst + (wave + kWaves * i) * 512), 16, o.x[i], koff, 0, 0);
+}
+__device__ __forceinline__ void issue_w(f16* dst, __amdgpu_buffer_rsrc_t wr, int koff,
+                                        const StageOffsets& o, int wave) {
 #pragma unroll
     for (int i = 0; i < kWInstr / kWaves; i++)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            wr, (lds_void*)(&sm.w[buf][(wave + kWaves * i) * 512]), 16, o.w[i], koff, 0, 0);
+            wr, (lds_void*)(dst + (wave + kWaves * i) * 512), 16, o.w[i], koff, 0, 0);
+}
+__device__ __forceinline__ void issue_stage(GemmSmem& sm, int buf, __amdgpu_buffer_rsrc_t xr,
+                                            __amdgpu_buffer_rsrc_t wr, int koff,
+                                            const StageOffsets& o, int wave) {
+    issue_x(sm.x[buf], xr, koff, o, wave);
+    issue_w(sm.w[buf], wr, koff, o, wave);
+}
+
+// The LayerNorm prologue. Lane L of a wave normalises exactly the 16-byte
+// pieces that its own x loads put into LDS: instruction i's piece, at
+// halves (wave + kWaves i) * 512 + 8 L, is row kRowsPerInstr (wave + kWaves
+// i) + L / kRowChunks of the tile, logical chunk lc = (L % kRowChunks) ^
+// swz(row), and swz(row) does not depend on i. So a lane needs only its own
+// loads to have landed (vmcnt, no barrier), its rows' statistics stay in
+// registers for the whole product, and each stage's parameters are the 8
+// columns 8 lc of that stage.
+constexpr int kLnRows = kXInstr / kWaves;  // x pieces per lane and stage
+static_assert((kRowsPerInstr * kWaves / kRowsPer256B) % kRowChunks == 0,
+              "a lane's x pieces share one logical chunk");
+constexpr int kLnParamLoads = 4;            // 16-byte loads of ln_w / ln_b per stage
+#ifndef HS_GEMM_LN_SLICES
+#define HS_GEMM_LN_SLICES 2  // k slices of a step over which the next stage is normalised
+#endif
+#ifndef HS_GEMM_LN_VALU
+#define HS_GEMM_LN_VALU 8  // vector instructions scheduled after each of those slices' MFMAs
+#endif
+#ifndef HS_GEMM_LN_FIRST
+#define HS_GEMM_LN_FIRST 1  // the first of those slices (the pieces are read at slice 0)
+#endif
+#ifndef HS_GEMM_LN_HINTS
+#define HS_GEMM_LN_HINTS 1  // interleave by scheduling groups (0: the compiler's order)
+#endif
+constexpr int kLnSlices = HS_GEMM_LN_SLICES;
+constexpr int kLnFirst = HS_GEMM_LN_FIRST;
+constexpr bool kLnHints = HS_GEMM_LN_HINTS != 0;
+constexpr int kLnValuPerMfma = HS_GEMM_LN_VALU;
+static_assert(kLnRows % kLnSlices == 0 && kLnFirst >= 0 && kLnFirst + kLnSlices < kBK / 16,
+              "LayerNorm slices: the next stage's parameters load in a later slice");
+
+struct LnLane {
+    f32x2 st[kLnRows];  // (mean, rstd) of the lane's rows
+    int col;            // first column of the lane's chunk within a stage
+};
+
+__device__ __forceinline__ LnLane ln_lane(const LnArgs& la, int64_t m0, int M, int wave, int lane) {
+    LnLane ll;
+#pragma unroll
+    for (int i = 0; i < kLnRows; i++) {
+        const int row = kRowsPerInstr * (wave + kWaves * i) + lane / kRowChunks;
+        // rows past M were loaded from row M - 1 and are normalised with its
+        // statistics (their products are masked)
+        const int64_t r = min(m0 + row, static_cast<int64_t>(M) - 1);
+        ll.st[i] = *reinterpret_cast<const f32x2*>(la.stats + 2 * r);
+    }
+    ll.col = 8 * ((lane % kRowChunks) ^ swz(kRowsPerInstr * wave + lane / kRowChunks));
+    return ll;
+}
+
+// The LayerNorm parameters of the lane's 8 columns of the stage at column k0.
+__device__ __forceinline__ void ln_params(const LnArgs& la, const LnLane& ll, int k0,
+                                          float4 (&gb)[kLnParamLoads]) {
+    const int c = k0 + ll.col;
+    gb[0] = ld_f32x4(la.ln_w + c), gb[1] = ld_f32x4(la.ln_w + c + 4);
+    gb[2] = ld_f32x4(la.ln_b + c), gb[3] = ld_f32x4(la.ln_b + c + 4);
+}
+
+// Halves offset of the lane's piece i within an x stage.
+__device__ __forceinline__ int ln_off(int i, int wave, int lane) {
+    return (wave + kWaves * i) * 512 + 8 * lane;
+}
+
+// One normalised piece: the 8 f16 values of v, with the row's (mean, rstd)
+// and the lane's column parameters gb (ln_w then ln_b), rounded to f16 as
+// hs_layernorm stores them.
+__device__ __forceinline__ u32x4 ln_piece(u32x4 v, f32x2 st, const float4 (&gb)[kLnParamLoads]) {
+    const float g[8] = {gb[0].x, gb[0].y, gb[0].z, gb[0].w, gb[1].x, gb[1].y, gb[1].z, gb[1].w};
+    const float b[8] = {gb[2].x, gb[2].y, gb[2].z, gb[2].w, gb[3].x, gb[3].y, gb[3].z, gb[3].w};
+    float f[8];
+    unpack(v, f, f16{});
+#pragma unroll
+    for (int j = 0; j < 8; j++) f[j] = ln_affine(f[j], st[0], st[1], g[j], b[j]);
+    return pack(f, f16{});
+}
+
+// Normalises all of the lane's pieces of the stage in `raw` into `dst`.
+__device__ __forceinline__ void ln_stage(const f16* raw, f16* dst, const LnLane& ll,
+                                         const float4 (&gb)[kLnParamLoads], int wave, int lane) {
+#pragma unroll
+    for (int i = 0; i < kLnRows; i++)
+        st16(dst + ln_off(i, wave, lane), ln_piece(ld16(raw + ln_off(i, wave, lane)), ll.st[i], gb));
 }
 
 // Buffer descriptor word 3 for raw (unstructured, stride 0) buffers on gfx950.
@@ -260,8 +362,9 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     const f16* __restrict__ x, const f16* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ gamma, const f16* res, f16* out, int M, int N, int K,
     int tiles_n, int ntiles, QkvArgs qa, LnArgs la) {
-    __shared__ __align__(16) unsigned char smem_raw[kSmemBytes];
+    __shared__ __align__(16) unsigned char smem_raw[smem_bytes(LN)];
     GemmSmem& sm = *reinterpret_cast<GemmSmem*>(smem_raw);
+    f16* const raw = reinterpret_cast<f16*>(smem_raw + sizeof(GemmSmem));  // LN only
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = tid >> 6;
@@ -300,14 +403,42 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<f16*>(w + n0 * K), 0, kBN * K * 2, kRawBufferFlags);
     // Both buffers start filled (stages 0 and 1). The waits below are
-    // explicit: vmcnt counts this wave's LDS-DMA loads, which complete in
-    // order, and the barrier then covers every wave's.
-    issue_stage(sm, 0, xr, wr, 0, so, wv);
-    if (nsteps > 1) {
-        issue_stage(sm, 1, xr, wr, 2 * kBK, so, wv);
-        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kLoads) : "memory");
+    // explicit: vmcnt counts this wave's loads, which complete in order, and
+    // the barrier then covers every wave's.
+    //
+    // With the LayerNorm prologue, stage s's x lands in raw during step s - 2
+    // (its parameters loaded just before it) and is normalised into x[s & 1]
+    // by its own lanes during step s - 1, beside that step's multiplies; w
+    // keeps the schedule above. Per wave, in issue order: params(s + 2),
+    // x(s + 2) in the middle of step s, w(s + 2) after its closing barrier.
+    constexpr int kXL = kXInstr / kWaves, kWL = kWInstr / kWaves;
+    LnLane ll;
+    float4 gb[kLnParamLoads];
+    if constexpr (LN) {
+        ll = ln_lane(la, m0, M, wv, lane);
+        ln_params(la, ll, 0, gb);
+        issue_x(raw, xr, 0, so, wv);
+        issue_w(sm.w[0], wr, 0, so, wv);
+        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kWL) : "memory");  // params(0), x(0)
+        ln_stage(raw, sm.x[0], ll, gb, wv, lane);
+        if (nsteps > 1) {
+            ln_params(la, ll, kBK, gb);
+            issue_x(raw, xr, 2 * kBK, so, wv);
+            issue_w(sm.w[1], wr, 2 * kBK, so, wv);
+            // w(0) landed; x[0]'s normalised pieces written
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kLnParamLoads + kXL + kWL)
+                         : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
     } else {
-        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        issue_stage(sm, 0, xr, wr, 0, so, wv);
+        if (nsteps > 1) {
+            issue_stage(sm, 1, xr, wr, 2 * kBK, so, wv);
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(kLoads) : "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        }
     }
     // Operand registers in two sets: the next 16-wide k slice is read from
     // LDS while the current one multiplies, across stage boundaries too.
@@ -316,6 +447,104 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     for (int a = 0; a < 2; a++) A[0][a] = ld_op(sm.w[0], wn + 32 * a + l32, hh);
 #pragma unroll
     for (int b = 0; b < 4; b++) B[0][b] = ld_op(sm.x[0], wm + 32 * b + l32, hh);
+    if constexpr (LN) {
+        // One step of the product with the prologue: the multiplies of stage
+        // s and, beside them, NORM: stage s + 1's LayerNorm from raw into
+        // x[cur ^ 1] (last read in step s - 1, before the barrier that
+        // closed it), ISSUE: the loads of stage s + 2. The flags are
+        // compile-time, so each step is one basic block in which the
+        // scheduler can place the LayerNorm's vector work between the
+        // multiplies. The lane's kLnRows pieces are read at slice 0 and
+        // normalised over the first kLnSlices slices; raw is refilled at
+        // slice 1, once the pieces are in registers, and the next stage's
+        // parameters load at slice kLnSlices, once these are used.
+        auto step = [&](int s, auto norm_c, auto issue_c) {
+            constexpr bool NORM = decltype(norm_c)::value, ISSUE = decltype(issue_c)::value;
+            const int cur = s & 1;
+            u32x4 rw[kLnRows];
+#pragma unroll
+            for (int ks = 0; ks < kBK / 16; ks++) {
+                const int p = ks & 1;  // kBK / 16 is even: set 0 holds slice 0 of every stage
+                if constexpr (ISSUE) {
+                    if (ks == 1) {
+                        // the lane's raw pieces (read at slice 0) are in
+                        // registers: refill raw with x(s + 2)
+                        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                        issue_x(raw, xr, 2 * (s + 2) * kBK, so, wv);
+                    }
+                }
+                if (ks + 1 < kBK / 16) {
+                    const int kc = 2 * (ks + 1) + hh;
+#pragma unroll
+                    for (int a = 0; a < 2; a++) A[p ^ 1][a] = ld_op(sm.w[cur], wn + 32 * a + l32, kc);
+#pragma unroll
+                    for (int b = 0; b < 4; b++) B[p ^ 1][b] = ld_op(sm.x[cur], wm + 32 * b + l32, kc);
+                }
+                if constexpr (NORM) {
+                    if (ks == 0) {
+                        // params(s + 1), x(s + 1) landed; w(s + 1) may be in flight
+                        asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kWL) : "memory");
+#pragma unroll
+                        for (int i = 0; i < kLnRows; i++) rw[i] = ld16(raw + ln_off(i, wv, lane));
+                    }
+                    if (ks >= kLnFirst && ks < kLnFirst + kLnSlices) {
+                        constexpr int per = kLnRows / kLnSlices;
+#pragma unroll
+                        for (int i = (ks - kLnFirst) * per; i < (ks - kLnFirst + 1) * per; i++)
+                            st16(sm.x[cur ^ 1] + ln_off(i, wv, lane), ln_piece(rw[i], ll.st[i], gb));
+                    }
+                    if constexpr (ISSUE) {
+                        if (ks == kLnFirst + kLnSlices) ln_params(la, ll, (s + 2) * kBK, gb);
+                    }
+                }
+                if (ks + 1 == kBK / 16) {
+                    // every wave's reads of stage s are done; w(s + 1) and
+                    // the normalised x(s + 1) have landed (params(s + 2) and
+                    // x(s + 2) may be in flight)
+                    if constexpr (ISSUE)
+                        asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(kLnParamLoads + kXL)
+                                     : "memory");
+                    else
+                        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                    // w[cur] is free: refill it with stage s + 2
+                    if constexpr (ISSUE) issue_w(sm.w[cur], wr, 2 * (s + 2) * kBK, so, wv);
+                    if constexpr (NORM) {
+#pragma unroll
+                        for (int a = 0; a < 2; a++) A[p ^ 1][a] = ld_op(sm.w[cur ^ 1], wn + 32 * a + l32, hh);
+#pragma unroll
+                        for (int b = 0; b < 4; b++) B[p ^ 1][b] = ld_op(sm.x[cur ^ 1], wm + 32 * b + l32, hh);
+                    }
+                }
+#pragma unroll
+                for (int a = 0; a < 2; a++)
+#pragma unroll
+                    for (int b = 0; b < 4; b++)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(A[p][a], B[p][b], acc[a][b], 0, 0, 0);
+                if (NORM && !kLnHints) {
+                    // the scheduler's own order
+                } else if (NORM && ks == 0 && kLnFirst > 0) {
+                    // the operand and raw reads ahead of the multiplies
+                    __builtin_amdgcn_sched_group_barrier(0x100, 6 + kLnRows, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+                } else if (NORM && ks >= kLnFirst && ks < kLnFirst + kLnSlices) {
+                    // the LayerNorm's vector work between the multiplies
+                    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+                    for (int q = 0; q < 8; q++) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // an MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x002, kLnValuPerMfma, 0);  // VALU
+                    }
+                } else {
+                    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);  // LDS reads
+                    __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // MFMAs
+                }
+            }
+        };
+        int s = 0;
+        for (; s + 2 < nsteps; s++) step(s, std::true_type{}, std::true_type{});
+        if (s + 1 < nsteps) step(s++, std::true_type{}, std::false_type{});
+        step(s, std::false_type{}, std::false_type{});
+    } else {
     for (int s = 0; s < nsteps; s++) {
         const int cur = s & 1;
 #pragma unroll
@@ -350,6 +579,7 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
             __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // MFMAs
         }
     }
+    }
 
     // Epilogue, in two phases so that global memory sees whole rows.
     // 1. Each lane turns its accumulators (row l32 of block b, columns
@@ -357,38 +587,18 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
     //    f16(acc + bias) (for GELU: f16(gelu(acc + bias))), and writes it
     //    to the wave's staging block in LDS (free once every wave has left
     //    the main loop).
-    //    With the LayerNorm folded in, the stored value is f16((acc -
-    //    mean * colsum) * rstd + shift), shift in the bias slot.
     f16* stage = reinterpret_cast<f16*>(smem_raw) + wave * kEpiWave;
-    f32x2 rs[4];  // (mean, rstd) of this lane's rows wm + 32 b + l32
-    if constexpr (LN) {
-#pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const int64_t row = min(m0 + wm + 32 * b + l32, static_cast<int64_t>(M) - 1);
-            rs[b] = *reinterpret_cast<const f32x2*>(la.stats + 2 * row);
-        }
-    }
 #pragma unroll
     for (int a = 0; a < 2; a++)
 #pragma unroll
         for (int r4 = 0; r4 < 4; r4++) {
             const int cl = 32 * a + 8 * r4 + 4 * hh;  // column within the wave's block
             const float4 bv = bias ? ld_f32x4(bias + n0 + wn + cl) : float4{0.0f, 0.0f, 0.0f, 0.0f};
-            float4 cv = {0.0f, 0.0f, 0.0f, 0.0f};
-            if constexpr (LN) cv = ld_f32x4(la.colsum + n0 + wn + cl);
 #pragma unroll
             for (int b = 0; b < 4; b++) {
                 float v[4];
-                if constexpr (LN) {
-                    const float mu = rs[b][0], rstd = rs[b][1];
-                    v[0] = fmaf(fmaf(-mu, cv.x, acc[a][b][4 * r4]), rstd, bv.x);
-                    v[1] = fmaf(fmaf(-mu, cv.y, acc[a][b][4 * r4 + 1]), rstd, bv.y);
-                    v[2] = fmaf(fmaf(-mu, cv.z, acc[a][b][4 * r4 + 2]), rstd, bv.z);
-                    v[3] = fmaf(fmaf(-mu, cv.w, acc[a][b][4 * r4 + 3]), rstd, bv.w);
-                } else {
-                    v[0] = acc[a][b][4 * r4] + bv.x, v[1] = acc[a][b][4 * r4 + 1] + bv.y;
-                    v[2] = acc[a][b][4 * r4 + 2] + bv.z, v[3] = acc[a][b][4 * r4 + 3] + bv.w;
-                }
+                v[0] = acc[a][b][4 * r4] + bv.x, v[1] = acc[a][b][4 * r4 + 1] + bv.y;
+                v[2] = acc[a][b][4 * r4 + 2] + bv.z, v[3] = acc[a][b][4 * r4 + 3] + bv.w;
                 if constexpr (EPI == EPI_GELU) {
 #pragma unroll
                     for (int e = 0; e < 4; e++) v[e] = gelu_erf(v[e]);
@@ -455,7 +665,15 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(
             const int kk = i % kGK, rr = i / kGK;
             const int64_t xm = m0 + rr, wn = n0 + rr;
             const int kidx = k0 + kk;
-            xs[kk][rr] = (xm < M && kidx < K) ? static_cast<float>(x[xm * K + kidx]) : 0.0f;
+            float xv = (xm < M && kidx < K) ? static_cast<float>(x[xm * K + kidx]) : 0.0f;
+            if constexpr (LN) {
+                // the element as hs_layernorm stores it
+                if (xm < M && kidx < K)
+                    xv = storage_round(ln_affine(xv, la.stats[2 * xm], la.stats[2 * xm + 1],
+                                                 la.ln_w[kidx], la.ln_b[kidx]),
+                                       T{});
+            }
+            xs[kk][rr] = xv;
             ws[kk][rr] = (wn < N && kidx < K) ? static_cast<float>(w[wn * K + kidx]) : 0.0f;
         }
         __syncthreads();
@@ -480,9 +698,6 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(
             const int64_t n = n0 + tc * 4 + j;
             if (n >= N) continue;
             float v = acc[i][j] + (bias ? bias[n] : 0.0f);
-            if constexpr (LN)
-                v = fmaf(fmaf(-la.stats[2 * m], la.colsum[n], acc[i][j]), la.stats[2 * m + 1],
-                         bias ? bias[n] : 0.0f);
             if constexpr (EPI == EPI_GELU) v = gelu_erf(v);
             if constexpr (EPI == EPI_LS)
                 v = static_cast<float>(res[m * N + n]) + gamma[n] * storage_round(v, T{});
@@ -501,11 +716,19 @@ bool fast_shape(hs_dtype dt, int N, int K, const void* x, const void* w, const f
            (!res || aligned16(res));
 }
 
+// Fast-path eligibility of a call, decided before anything is enqueued.
+template <bool LN>
+bool takes_fast_path(hs_dtype dt, int N, int K, const void* x, const void* w, const float* bias,
+                     const float* gamma, const void* out, const void* res, const LnArgs& la) {
+    return fast_shape(dt, N, K, x, w, bias, gamma, out, res) &&
+           (!LN || (aligned16(la.ln_w) && aligned16(la.ln_b)));
+}
+
 template <int EPI, bool LN = false>
 hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, const float* bias,
                  const float* gamma, const void* res, void* out, int M, int N, int K,
                  const char* op, const QkvArgs& qa = QkvArgs{}, const LnArgs& la = LnArgs{}) {
-    if (fast_shape(dt, N, K, x, w, bias, gamma, out, res) && (!LN || aligned16(la.colsum))) {
+    if (takes_fast_path<LN>(dt, N, K, x, w, bias, gamma, out, res, la)) {
         const int tiles_n = N / kBN;
         const int64_t ntiles = ceil_div(M, kBM) * tiles_n;
         const int64_t blocks = HS_GEMM_XCD ? ceil_div(ntiles, 8) * 8 : ntiles;
@@ -640,50 +863,51 @@ hs_status qkv_setup(const char* op, hs_dtype dt, const void* x, const void* w_qk
     return HS_OK;
 }
 
-// The folded LayerNorm's operands: colsum and shift (n) f32, the workspace
-// for the row statistics (2 m floats, 8-byte aligned); then the statistics
-// of x go into the workspace.
-hs_status ln_prologue(const char* op, hipStream_t st, hs_dtype dt, const void* x,
-                      const float* colsum, const float* shift, float* workspace, int64_t M,
-                      int32_t K, float eps) {
-    if (!colsum || !shift || !workspace) return fail(HS_EINVAL, "%s: null buffer", op);
+// A byte range that the LayerNorm prologue's workspace must not overlap.
+struct Span {
+    const void* p;
+    int64_t bytes;
+};
+
+// Checks of the LayerNorm prologue's operands: ln_w and ln_b (k f32 each)
+// and the workspace (2 m floats, 8-byte aligned), which receives each x
+// row's (mean, rstd) and so must not overlap any buffer the call reads or
+// writes (`spans`).
+hs_status ln_check(const char* op, const float* ln_w, const float* ln_b, const float* workspace,
+                   int64_t M, int32_t K, float eps, std::initializer_list<Span> spans) {
+    if (!ln_w || !ln_b || !workspace) return fail(HS_EINVAL, "%s: null buffer", op);
     if (!(eps > 0.0f)) return fail(HS_EINVAL, "%s: eps must be positive", op);
     if (reinterpret_cast<uintptr_t>(workspace) % 8 != 0)
         return fail(HS_EINVAL, "%s: workspace must be 8-byte aligned", op);
-    const int64_t xb = M * K * dtype_size(dt);
-    if (overlaps(workspace, M * 8, x, xb)) return fail(HS_EINVAL, "%s: workspace overlaps x", op);
-    // (a failure keeps the statistics launch's own message)
-    return hs_layernorm_stats(st, dt, x, workspace, M, K, eps);
+    const int64_t wsb = M * 8;
+    if (overlaps(workspace, wsb, ln_w, int64_t{K} * 4) ||
+        overlaps(workspace, wsb, ln_b, int64_t{K} * 4))
+        return fail(HS_EINVAL, "%s: workspace overlaps the LayerNorm parameters", op);
+    for (const Span& sp : spans)
+        if (sp.p && overlaps(workspace, wsb, sp.p, sp.bytes))
+            return fail(HS_EINVAL, "%s: workspace overlaps an operand", op);
+    return HS_OK;
 }
 
-// Folds a LayerNorm into the linear layer after it: one wave per output
-// row n of w, f32 sums in a fixed order (lane-strided, then the wave tree).
-template <typename T>
-__global__ __launch_bounds__(256) void fold_ln_kernel(const T* __restrict__ w,
-                                                      const float* __restrict__ bias,
-                                                      const float* __restrict__ ln_w,
-                                                      const float* __restrict__ ln_b,
-                                                      T* __restrict__ w_fold,
-                                                      float* __restrict__ colsum,
-                                                      float* __restrict__ shift, int n, int k) {
-    const int row = static_cast<int>(blockIdx.x) * 4 + wave_in_block();
-    if (row >= n) return;  // wave-uniform; no barriers
-    const int lane = lane_id();
-    const T* wr = w + static_cast<int64_t>(row) * k;
-    T* fr = w_fold + static_cast<int64_t>(row) * k;
-    float cs = 0.0f, sh = 0.0f;
-    for (int j = lane; j < k; j += 64) {
-        const float wv = static_cast<float>(wr[j]);
-        // the f32 product is materialised before its storage rounding (left
-        // alone, the compiler fuses the two into one single-rounding op)
-        const T f = static_cast<T>(as_f32(wv * ln_w[j]));
-        fr[j] = f;
-        cs += static_cast<float>(f);
-        sh = fmaf(ln_b[j], wv, sh);
-    }
-    cs = wave_sum(cs);
-    sh = wave_sum(sh);
-    if (lane == 0) colsum[row] = cs, shift[row] = sh + (bias ? bias[row] : 0.0f);
+// hs_linear_ln / hs_linear_ln_gelu (and the allocation-free variant): the
+// row statistics into ws, then the product with the LayerNorm prologue.
+template <int EPI>
+hs_status linear_ln_entry(const char* op, hipStream_t st, hs_dtype dt, const void* x,
+                          const float* ln_w, const float* ln_b, const void* w, const float* bias,
+                          float* ws, void* out, int64_t m, int32_t n, int32_t k, float eps) {
+    hs_status rc = check(op, dt, x, w, nullptr, out, m, n, k, false);
+    if (rc != HS_OK || m == 0 || n == 0) return rc;
+    if (k == 0) return fail(HS_EINVAL, "%s: k must be positive", op);
+    const int64_t esz = dtype_size(dt);
+    rc = ln_check(op, ln_w, ln_b, ws, m, k, eps,
+                  {{x, m * k * esz}, {w, int64_t{n} * k * esz}, {bias, int64_t{n} * 4},
+                   {out, m * n * esz}});
+    if (rc != HS_OK) return rc;
+    // (a failure keeps the statistics launch's own message)
+    rc = hs_layernorm_stats(st, dt, x, ws, m, k, eps);
+    if (rc != HS_OK) return rc;
+    return launch<EPI, true>(st, dt, x, w, bias, nullptr, nullptr, out, static_cast<int>(m), n, k,
+                             op, QkvArgs{}, LnArgs{ws, ln_w, ln_b});
 }
 
 }  // namespace
@@ -708,95 +932,57 @@ extern "C" hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const 
                            q_out, static_cast<int>(M), static_cast<int>(N), k, op, qa);
 }
 
-extern "C" hs_status hs_fold_layernorm(hs_stream_t stream, hs_dtype dt, const void* w,
-                                       const float* bias, const float* ln_w, const float* ln_b,
-                                       void* w_fold, float* colsum, float* shift, int32_t n,
-                                       int32_t k) {
-    using namespace hs;
-    const char* op = "fold_layernorm";
-    if (!valid_dtype(dt)) return fail(HS_EINVAL, "%s: unknown dtype", op);
-    if (n < 0 || k <= 0) return fail(HS_EINVAL, "%s: shape n=%d k=%d", op, n, k);
-    if (n == 0) return HS_OK;
-    if (!w || !ln_w || !ln_b || !w_fold || !colsum || !shift)
-        return fail(HS_EINVAL, "%s: null buffer", op);
-    const int64_t wb = int64_t{n} * k * dtype_size(dt);
-    if (overlaps(w_fold, wb, w, wb)) return fail(HS_EINVAL, "%s: w_fold overlaps w", op);
-    const dim3 grid(static_cast<uint32_t>(ceil_div(int64_t{n}, int64_t{4})));
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (dt == HS_F16)
-        fold_ln_kernel<f16><<<grid, dim3(256), 0, st>>>(static_cast<const f16*>(w), bias, ln_w,
-                                                        ln_b, static_cast<f16*>(w_fold), colsum,
-                                                        shift, n, k);
-    else
-        fold_ln_kernel<float><<<grid, dim3(256), 0, st>>>(static_cast<const float*>(w), bias, ln_w,
-                                                          ln_b, static_cast<float*>(w_fold), colsum,
-                                                          shift, n, k);
-    return check_launch(op);
-}
-
 extern "C" hs_status hs_linear_ln(hs_stream_t stream, hs_dtype dt, const void* x,
-                                  const void* w_fold, const float* colsum, const float* shift,
-                                  float* workspace, void* out, int64_t m, int32_t n, int32_t k,
-                                  float eps) {
-    using namespace hs;
-    const char* op = "linear_ln";
-    hs_status rc = check(op, dt, x, w_fold, nullptr, out, m, n, k, false);
-    if (rc != HS_OK || m == 0 || n == 0) return rc;
-    if (k == 0) return fail(HS_EINVAL, "%s: k must be positive", op);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (overlaps(workspace, m * 8, out, m * n * dtype_size(dt)))
-        return fail(HS_EINVAL, "%s: workspace overlaps out", op);
-    rc = ln_prologue(op, st, dt, x, colsum, shift, workspace, m, k, eps);
-    if (rc != HS_OK) return rc;
-    return launch<EPI_BIAS, true>(st, dt, x, w_fold, shift, nullptr, nullptr, out,
-                                  static_cast<int>(m), n, k, op, QkvArgs{}, LnArgs{workspace, colsum});
+                                  const float* ln_w, const float* ln_b, const void* w,
+                                  const float* bias, float* workspace, void* out, int64_t m,
+                                  int32_t n, int32_t k, float eps) {
+    return hs::linear_ln_entry<hs::EPI_BIAS>("linear_ln", static_cast<hipStream_t>(stream), dt, x,
+                                             ln_w, ln_b, w, bias, workspace, out, m, n, k, eps);
 }
 
 extern "C" hs_status hs_linear_ln_gelu(hs_stream_t stream, hs_dtype dt, const void* x,
-                                       const void* w_fold, const float* colsum, const float* shift,
-                                       float* workspace, void* out, int64_t m, int32_t n,
-                                       int32_t k, float eps) {
-    using namespace hs;
-    const char* op = "linear_ln_gelu";
-    hs_status rc = check(op, dt, x, w_fold, nullptr, out, m, n, k, false);
-    if (rc != HS_OK || m == 0 || n == 0) return rc;
-    if (k == 0) return fail(HS_EINVAL, "%s: k must be positive", op);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    if (overlaps(workspace, m * 8, out, m * n * dtype_size(dt)))
-        return fail(HS_EINVAL, "%s: workspace overlaps out", op);
-    rc = ln_prologue(op, st, dt, x, colsum, shift, workspace, m, k, eps);
-    if (rc != HS_OK) return rc;
-    return launch<EPI_GELU, true>(st, dt, x, w_fold, shift, nullptr, nullptr, out,
-                                  static_cast<int>(m), n, k, op, QkvArgs{}, LnArgs{workspace, colsum});
+                                       const float* ln_w, const float* ln_b, const void* w,
+                                       const float* bias, float* workspace, void* out, int64_t m,
+                                       int32_t n, int32_t k, float eps) {
+    return hs::linear_ln_entry<hs::EPI_GELU>("linear_ln_gelu", static_cast<hipStream_t>(stream), dt,
+                                             x, ln_w, ln_b, w, bias, workspace, out, m, n, k, eps);
 }
 
 extern "C" hs_status hs_linear_ln_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x,
-                                            const void* w_fold, const float* colsum,
-                                            const float* shift, const float* qn_w,
-                                            const float* qn_b, const float* kn_w,
-                                            const float* kn_b, const float* sin_tab,
-                                            const float* cos_tab, float* workspace, void* q_out,
-                                            void* k_out, void* v_out, int32_t S, int32_t T,
-                                            int32_t H, int32_t d, int32_t k, int32_t prefix,
-                                            float eps) {
+                                            const float* ln_w, const float* ln_b,
+                                            const void* w_qkv, const float* b_qkv,
+                                            const float* qn_w, const float* qn_b,
+                                            const float* kn_w, const float* kn_b,
+                                            const float* sin_tab, const float* cos_tab,
+                                            float* workspace, void* q_out, void* k_out,
+                                            void* v_out, int32_t S, int32_t T, int32_t H,
+                                            int32_t d, int32_t k, int32_t prefix, float eps) {
     using namespace hs;
     const char* op = "linear_ln_qkv_heads";
     QkvArgs qa;
     bool skip;
-    hs_status rc = qkv_setup(op, dt, x, w_fold, qn_w, qn_b, kn_w, kn_b, sin_tab, cos_tab, q_out,
+    hs_status rc = qkv_setup(op, dt, x, w_qkv, qn_w, qn_b, kn_w, kn_b, sin_tab, cos_tab, q_out,
                              k_out, v_out, S, T, H, d, k, prefix, eps, &qa, &skip);
     if (rc != HS_OK || skip) return rc;
     const int64_t M = int64_t{S} * T, N = int64_t{3} * H * d;
-    const int64_t ob = M * H * d * dtype_size(dt);
-    const void* outs[3] = {q_out, k_out, v_out};
-    for (const void* o : outs)
-        if (overlaps(workspace, M * 8, o, ob)) return fail(HS_EINVAL, "%s: workspace overlaps an output", op);
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    rc = ln_prologue(op, st, dt, x, colsum, shift, workspace, M, k, eps);
+    const int64_t esz = dtype_size(dt), ob = M * H * d * esz;
+    const int64_t tab = int64_t{T - prefix} * d * 4;
+    rc = ln_check(op, ln_w, ln_b, workspace, M, k, eps,
+                  {{x, M * k * esz}, {w_qkv, N * k * esz}, {b_qkv, N * 4}, {qn_w, d * 4},
+                   {qn_b, d * 4}, {kn_w, d * 4}, {kn_b, d * 4}, {sin_tab, tab}, {cos_tab, tab},
+                   {q_out, ob}, {k_out, ob}, {v_out, ob}});
     if (rc != HS_OK) return rc;
-    return launch<EPI_QKV, true>(st, dt, x, w_fold, shift, nullptr, nullptr, q_out,
-                                 static_cast<int>(M), static_cast<int>(N), k, op, qa,
-                                 LnArgs{workspace, colsum});
+    const LnArgs la{workspace, ln_w, ln_b};
+    // the q|k|v epilogue exists on the matrix-core path only: refuse other
+    // calls before the statistics are enqueued
+    if (!takes_fast_path<true>(dt, static_cast<int>(N), k, x, w_qkv, b_qkv, nullptr, q_out,
+                               nullptr, la))
+        return fail(HS_EUNSUPPORTED, "%s: needs K %% %d == 0 and 16-byte aligned buffers", op, kBK);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    rc = hs_layernorm_stats(st, dt, x, workspace, M, k, eps);
+    if (rc != HS_OK) return rc;
+    return launch<EPI_QKV, true>(st, dt, x, w_qkv, b_qkv, nullptr, nullptr, q_out,
+                                 static_cast<int>(M), static_cast<int>(N), k, op, qa, la);
 }
 
 // ---------------------------------------------------------------------------
@@ -850,22 +1036,20 @@ float* scratch_address(const char* op, hs_status* rc) {
 }  // namespace hs
 
 extern "C" hs_status hs_linear_ln_gelu_noalloc(hs_stream_t stream, hs_dtype dt, const void* x,
-                                               const void* w_fold, const float* colsum,
-                                               const float* shift, void* out, int64_t m,
-                                               int32_t n, int32_t k, float eps) {
+                                               const float* ln_w, const float* ln_b,
+                                               const void* w, const float* bias, void* out,
+                                               int64_t m, int32_t n, int32_t k, float eps) {
     using namespace hs;
     const char* op = "linear_ln_gelu_noalloc";
     if (m > kNoAllocMaxRows)
         return fail(HS_EINVAL, "%s: m = %lld rows exceeds the statistics array's %lld", op,
                     static_cast<long long>(m), static_cast<long long>(kNoAllocMaxRows));
-    hs_status rc = check(op, dt, x, w_fold, nullptr, out, m, n, k, false);
-    if (rc != HS_OK || m == 0 || n == 0) return rc;
-    if (k == 0) return fail(HS_EINVAL, "%s: k must be positive", op);
+    if (m <= 0 || n <= 0)  // the shape checks and zero-size returns of the workspace entry
+        return linear_ln_entry<EPI_GELU>(op, static_cast<hipStream_t>(stream), dt, x, ln_w, ln_b,
+                                         w, bias, nullptr, out, m, n, k, eps);
+    hs_status rc = HS_OK;
     float* ws = scratch_address(op, &rc);
     if (ws == nullptr) return rc;
-    hipStream_t st = static_cast<hipStream_t>(stream);
-    rc = ln_prologue(op, st, dt, x, colsum, shift, ws, m, k, eps);
-    if (rc != HS_OK) return rc;
-    return launch<EPI_GELU, true>(st, dt, x, w_fold, shift, nullptr, nullptr, out,
-                                  static_cast<int>(m), n, k, op, QkvArgs{}, LnArgs{ws, colsum});
+    return linear_ln_entry<EPI_GELU>(op, static_cast<hipStream_t>(stream), dt, x, ln_w, ln_b, w,
+                                     bias, ws, out, m, n, k, eps);
 }

@@ -114,7 +114,7 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
             for (int c = 0; c < CHUNKS; c++) {
                 float y[V];
 #pragma unroll
-                for (int k = 0; k < V; k++) y[k] = (f[c][k] - mean) * inv * wr[c][k] + br[c][k];
+                for (int k = 0; k < V; k++) y[k] = ln_affine(f[c][k], mean, inv, wr[c][k], br[c][k]);
                 st_stream(orow + c * 64 * V, pack(y, T{}));
             }
         }
@@ -127,10 +127,10 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
 // holds 64 / G rows per load instruction and reduces each over its group
 // with DPP permutes. Each wave takes U such row groups, all loads issued
 // before any row is reduced.
-template <typename T, int G, int U>
+template <typename T, int G, int U, bool STATS = false>
 __global__ __launch_bounds__(kBlock) void ln_small_kernel(const T* x, const float* __restrict__ w,
                                                           const float* __restrict__ b, T* out,
-                                                          int64_t rows, float eps) {
+                                                          float* stats, int64_t rows, float eps) {
     constexpr int V = Vec<T>::N;
     constexpr int DIM = G * V;
     constexpr int RPW = 64 / G;  // rows per load instruction
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kBlock) void ln_small_kernel(const T* x, const floa
     const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
     float wr[V], br[V];
 #pragma unroll
-    for (int k = 0; k < V; k += 4) {
+    for (int k = 0; k < V && !STATS; k += 4) {
         const float4 w4 = ld_f32x4(w + piece * V + k), b4 = ld_f32x4(b + piece * V + k);
         wr[k] = w4.x, wr[k + 1] = w4.y, wr[k + 2] = w4.z, wr[k + 3] = w4.w;
         br[k] = b4.x, br[k + 1] = b4.y, br[k + 2] = b4.z, br[k + 3] = b4.w;
@@ -171,9 +171,17 @@ __global__ __launch_bounds__(kBlock) void ln_small_kernel(const T* x, const floa
                 q += d * d;
             }
             const float inv = rsqrtf(group_sum<G>(q) / static_cast<float>(DIM) + eps);
+            if constexpr (STATS) {
+                if (piece == 0 && row < rows) {
+                    f32x2 m2;
+                    m2[0] = mean, m2[1] = inv;
+                    *reinterpret_cast<f32x2*>(stats + 2 * row) = m2;
+                }
+                continue;
+            }
             float y[V];
 #pragma unroll
-            for (int k = 0; k < V; k++) y[k] = (f[k] - mean) * inv * wr[k] + br[k];
+            for (int k = 0; k < V; k++) y[k] = ln_affine(f[k], mean, inv, wr[k], br[k]);
             if (row < rows) st_stream(out + row * DIM + piece * V, pack(y, T{}));
         }
     }
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void ln_generic_kernel(const T* x, const fl
             continue;
         }
         for (int j = lane; j < dim; j += 64)
-            store_elem(orow + j, (load_elem(xr + j) - mean) * inv * w[j] + b[j]);
+            store_elem(orow + j, ln_affine(load_elem(xr + j), mean, inv, w[j], b[j]));
     }
 }
 
@@ -232,6 +240,22 @@ hs_status launch_vec(hipStream_t st, const void* x, const float* w, const float*
     return check_launch(STATS ? "layernorm_stats" : "layernorm");
 }
 
+template <typename T, bool STATS = false>
+hs_status launch_small(hipStream_t st, const void* x, const float* w, const float* b, void* out,
+                       float* stats, int64_t rows, int dim, float eps) {
+    constexpr int V = Vec<T>::N;
+    constexpr int U = 2;
+    const int64_t want = ceil_div(ceil_div(rows, (dim == 8 * V ? 8 : 4) * U), kWavesPerBlock);
+    const int64_t blocks = want < (int64_t{1} << 22) ? want : (int64_t{1} << 22);
+    if (dim == 8 * V)
+        ln_small_kernel<T, 8, U, STATS><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+            static_cast<const T*>(x), w, b, static_cast<T*>(out), stats, rows, eps);
+    else
+        ln_small_kernel<T, 16, U, STATS><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+            static_cast<const T*>(x), w, b, static_cast<T*>(out), stats, rows, eps);
+    return check_launch(STATS ? "layernorm_stats" : "layernorm");
+}
+
 template <typename T>
 hs_status launch(hipStream_t st, const void* x, const float* w, const float* b, void* out,
                  int64_t rows, int dim, float eps) {
@@ -248,26 +272,16 @@ hs_status launch(hipStream_t st, const void* x, const float* w, const float* b, 
     }
     const bool small_ok = aligned16(x) && aligned16(out) && aligned16(w) && aligned16(b) &&
                           (dim == 8 * V || dim == 16 * V);
-    if (small_ok) {
-        constexpr int U = 2;
-        const int64_t want = ceil_div(ceil_div(rows, (dim == 8 * V ? 8 : 4) * U), kWavesPerBlock);
-        const int64_t blocks = want < (int64_t{1} << 22) ? want : (int64_t{1} << 22);
-        if (dim == 8 * V)
-            ln_small_kernel<T, 8, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
-                static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, eps);
-        else
-            ln_small_kernel<T, 16, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
-                static_cast<const T*>(x), w, b, static_cast<T*>(out), rows, eps);
-        return check_launch("layernorm");
-    }
+    if (small_ok) return launch_small<T>(st, x, w, b, out, nullptr, rows, dim, eps);
     const int64_t blocks = persistent_blocks(rows);
     ln_generic_kernel<T, false><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
         static_cast<const T*>(x), w, b, static_cast<T*>(out), nullptr, rows, dim, eps);
     return check_launch("layernorm");
 }
 
-// Row statistics only: the same kernels (and so the same arithmetic) as the
-// normalising launch above for the vector widths, the generic kernel else.
+// Row statistics only: the kernel (and so the arithmetic) that the
+// normalising launch above picks for the same x when the other buffers are
+// 16-byte aligned too.
 template <typename T>
 hs_status launch_stats(hipStream_t st, const void* x, float* stats, int64_t rows, int dim,
                        float eps) {
@@ -280,6 +294,8 @@ hs_status launch_stats(hipStream_t st, const void* x, float* stats, int64_t rows
             default: break;
         }
     }
+    if (aligned16(x) && (dim == 8 * V || dim == 16 * V))
+        return launch_small<T, true>(st, x, nullptr, nullptr, nullptr, stats, rows, dim, eps);
     const int64_t blocks = persistent_blocks(rows);
     ln_generic_kernel<T, true><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
         static_cast<const T*>(x), nullptr, nullptr, nullptr, stats, rows, dim, eps);

@@ -21,10 +21,7 @@ QK-norm + RoPE, matrix-core attention written token-major). With
 ``fused=False`` the same trunk runs the reference's dispatch sequence
 through this library's single ops instead (``block_forward_reference``,
 one ``copy_rows`` per frame, concat then cast), the comparison path of the
-parity tests. With ``fold_ln=True`` (after ``fold_layernorms``) every block
-folds both LayerNorms into the products after them (``block_forward``'s
-``fold_ln1``/``fold_ln2``): as accurate against float32 math, but not the
-reference's rounding pattern, so it is opt-in.
+parity tests.
 """
 from __future__ import annotations
 
@@ -57,13 +54,6 @@ class Trunk:
     def depth(self) -> int:
         return len(self.frame_blocks)
 
-    def fold_layernorms(self, ctx: HipContext) -> "Trunk":
-        """Prepares ``forward(fold_ln=True)`` once: every block's LN1 folded
-        into its q|k|v weight, LN2 into its fc1 weight."""
-        for b in self.frame_blocks + self.inter_blocks:
-            b.fold_layernorms(ctx)
-        return self
-
     @staticmethod
     def load(weights, precision, device, depth: int = 24) -> "Trunk":
         """trunk.rs:28-47. ``depth`` < 24 loads the first block pairs only
@@ -81,7 +71,7 @@ class Trunk:
                      precision)
 
     def forward(self, ctx: HipContext, dino_tokens, n: int, h_p: int, w_p: int, tap=None,
-                fused: bool = True, fold_ln: bool = False) -> list:
+                fused: bool = True) -> list:
         """dino_tokens (N*P, 1024) f32 -> the head-input caches, each
         (N*T, 2048) f32, T = P + 17 (trunk.rs:49-146). ``tap(name, tensor)``
         sees "trunk.frame.NN" (N*T, 1024), "trunk.inter.NN" (N*T rows, or
@@ -105,12 +95,7 @@ class Trunk:
                 ctx.copy_rows(toks, i * p, x, i * t + PREFIX, p)
 
         sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(self.periods, h_p, w_p))
-        assert fused or not fold_ln, "the LayerNorm fold is a fused-path option"
-        if fold_ln:
-            def block(*a, **kw):
-                return block_forward(*a, **kw, fold_ln1=True, fold_ln2=True)
-        else:
-            block = block_forward if fused else block_forward_reference
+        block = block_forward if fused else block_forward_reference
         caches = []
         for k in range(self.depth):
             frame_out = block(ctx, self.frame_blocks[k], x, n, t, HEADS, rope=(sin, cos, PREFIX),

@@ -246,61 +246,55 @@ hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x, co
                               int32_t prefix, float eps);
 
 /* ---------------------------------------------------------------------- */
-/* LayerNorm folded into the linear layer after it (the pre-norm blocks'    */
-/* layernorm -> linear pairs, model/block.rs:128-131 and 153-173)            */
+/* LayerNorm fused into the linear layer after it (the pre-norm blocks'     */
+/* layernorm -> linear pairs, model/block.rs:128-131 and 153, 172-174)       */
 
 /* The statistics half of GpuContext::layernorm (engine/ops.rs:130-153):
  * stats[2 r] = mean of row r of x (rows, dim), stats[2 r + 1] = rsqrt(var +
- * eps), f32, from the same kernels and arithmetic as hs_layernorm
- * normalises with (bit-identical). stats is 8-byte aligned, 2 * rows floats,
- * and must not overlap x. */
+ * eps), f32, from the kernel and arithmetic that hs_layernorm normalises
+ * the same x with (bit-identical when hs_layernorm's buffers are 16-byte
+ * aligned). stats is 8-byte aligned, 2 * rows floats, and must not overlap
+ * x. */
 hs_status hs_layernorm_stats(hs_stream_t stream, hs_dtype dt, const void* x, float* stats,
                              int64_t rows, int32_t dim, float eps);
 
-/* Folds a LayerNorm's affine parameters (ln_w, ln_b, k) into the weight w
- * (n, k) and bias (n, nullable) of the linear layer that consumes its
- * output, once at load time (as Block::load prepares its weights,
- * model/block.rs:60-110):
- *   w_fold[i, j] = dt(w[i, j] * ln_w[j])
- *   colsum[i]    = sum_j w_fold[i, j]            (f32, of the stored values)
- *   shift[i]     = sum_j ln_b[j] * w[i, j] + bias[i]
- * Then linear(layernorm(x), w, bias) = (x @ w_fold^T - mean * colsum) *
- * rstd + shift per row, which the hs_linear_ln* calls compute without
- * materialising the normalised activation. w_fold must not overlap w. */
-hs_status hs_fold_layernorm(hs_stream_t stream, hs_dtype dt, const void* w, const float* bias,
-                            const float* ln_w, const float* ln_b, void* w_fold, float* colsum,
-                            float* shift, int32_t n, int32_t k);
+/* GpuContext::layernorm (engine/ops.rs:130-153) then GpuContext::linear
+ * (engine/ops.rs:81-128) as Block::forward pairs them (LN1 -> q|k|v,
+ * model/block.rs:128-131): out (m, n) = dt(layernorm(x, ln_w, ln_b, eps)) @
+ * w^T + bias, where each element of the normalised row is rounded to the
+ * storage type exactly as hs_layernorm stores it (shaders/layernorm.wesl:76
+ * stores Elem) before the product reads it. The normalised row never
+ * reaches memory: each row's mean and rstd go to workspace (2 * m floats,
+ * 8-byte aligned; it must not overlap x, w, bias, ln_w, ln_b or out), and
+ * the product normalises its x tiles on the way to the matrix cores. With
+ * 16-byte aligned buffers the result is bit-identical to hs_layernorm then
+ * hs_linear. ln_w, ln_b (k) f32; bias (n) f32 may be NULL; k > 0. */
+hs_status hs_linear_ln(hs_stream_t stream, hs_dtype dt, const void* x, const float* ln_w,
+                       const float* ln_b, const void* w, const float* bias, float* workspace,
+                       void* out, int64_t m, int32_t n, int32_t k, float eps);
 
-/* layernorm(x, eps) then linear (block.rs:128-131 / 153-173) on the folded
- * weights of hs_fold_layernorm: out (m, n) = (x @ w_fold^T - mean * colsum)
- * * rstd + shift, with each row's mean and rstd first computed into
- * workspace (2 * m floats, 8-byte aligned, must not overlap x or out). The
- * normalised activation never reaches memory; the result equals layernorm
- * then hs_linear up to rounding (the reference rounds the normalised row to
- * the storage type before its product; here the folded weight is rounded
- * instead). */
-hs_status hs_linear_ln(hs_stream_t stream, hs_dtype dt, const void* x, const void* w_fold,
-                       const float* colsum, const float* shift, float* workspace, void* out,
-                       int64_t m, int32_t n, int32_t k, float eps);
-
-/* hs_linear_ln then GELU (block.rs:153 and 172-176: layernorm, fc1 with its
- * bias, gelu) in one product: out = gelu(...), rounded once. */
-hs_status hs_linear_ln_gelu(hs_stream_t stream, hs_dtype dt, const void* x, const void* w_fold,
-                            const float* colsum, const float* shift, float* workspace, void* out,
-                            int64_t m, int32_t n, int32_t k, float eps);
+/* hs_linear_ln then GELU (LN2 -> fc1 -> gelu, model/block.rs:153, 172-176):
+ * out = dt(gelu(dt(layernorm(x)) @ w^T + bias)), the sum kept in f32 and
+ * rounded once, as hs_linear_gelu. Bit-identical to hs_layernorm then
+ * hs_linear_gelu under the same conditions as hs_linear_ln. */
+hs_status hs_linear_ln_gelu(hs_stream_t stream, hs_dtype dt, const void* x, const float* ln_w,
+                            const float* ln_b, const void* w, const float* bias, float* workspace,
+                            void* out, int64_t m, int32_t n, int32_t k, float eps);
 
 /* hs_linear_ln then the q|k|v heads epilogue of hs_linear_qkv_heads
- * (block.rs:128-146: layernorm, the q|k|v projection, split_heads, QK-norm,
- * RoPE): w_fold (3*H*d, k) is the folded q|k|v weight, shift the folded
- * q|k|v bias; eps serves the LayerNorm and the QK-norm (the block uses
- * one). Same shape rules as hs_linear_qkv_heads; workspace as hs_linear_ln. */
+ * (model/block.rs:128-146: LN1, the q|k|v projection, split_heads,
+ * QK-norm, RoPE): bit-identical to hs_layernorm then hs_linear_qkv_heads
+ * under the conditions of both. eps serves the LayerNorm and the QK-norm
+ * (the block uses one). Same shape rules as hs_linear_qkv_heads (fast path
+ * only, checked before anything is enqueued; ln_w, ln_b 16-byte aligned);
+ * workspace as hs_linear_ln. */
 hs_status hs_linear_ln_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x,
-                                 const void* w_fold, const float* colsum, const float* shift,
-                                 const float* qn_w, const float* qn_b, const float* kn_w,
-                                 const float* kn_b, const float* sin_tab, const float* cos_tab,
-                                 float* workspace, void* q_out, void* k_out, void* v_out,
-                                 int32_t S, int32_t T, int32_t H, int32_t d, int32_t k,
-                                 int32_t prefix, float eps);
+                                 const float* ln_w, const float* ln_b, const void* w_qkv,
+                                 const float* b_qkv, const float* qn_w, const float* qn_b,
+                                 const float* kn_w, const float* kn_b, const float* sin_tab,
+                                 const float* cos_tab, float* workspace, void* q_out, void* k_out,
+                                 void* v_out, int32_t S, int32_t T, int32_t H, int32_t d,
+                                 int32_t k, int32_t prefix, float eps);
 
 /* hs_linear_ln_gelu without a workspace, for callers that cannot allocate
  * device memory (code under HIP graph capture, serving loops, harnesses that
@@ -310,8 +304,9 @@ hs_status hs_linear_ln_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x,
  * that overlap on one device race on that array. It calls no allocating
  * routine. */
 hs_status hs_linear_ln_gelu_noalloc(hs_stream_t stream, hs_dtype dt, const void* x,
-                                    const void* w_fold, const float* colsum, const float* shift,
-                                    void* out, int64_t m, int32_t n, int32_t k, float eps);
+                                    const float* ln_w, const float* ln_b, const void* w,
+                                    const float* bias, void* out, int64_t m, int32_t n, int32_t k,
+                                    float eps);
 
 /* ---------------------------------------------------------------------- */
 /* Attention                                                                */

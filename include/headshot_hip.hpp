@@ -148,7 +148,8 @@ struct Rope {
     size_t prefix;
 };
 
-// QK-norm weight and bias (model/block.rs:35-40, one side).
+// A LayerNorm's weight and bias: one side's QK-norm (model/block.rs:35-40)
+// or a pre-norm (LN1, LN2).
 struct Norm {
     const HipTensor* weight;
     const HipTensor* bias;
@@ -573,70 +574,34 @@ class HipContext {
         return out;
     }
 
-    // A linear layer with the LayerNorm before it folded in (LN1 -> q|k|v,
-    // model/block.rs:128-131; LN2 -> fc1, :153-173): w_fold = (w * ln_w)
-    // rounded to w's storage type, colsum = each folded row's sum, shift =
-    // w ln_b + bias. Prepared once, at load time.
-    struct FoldedLinear {
-        HipTensor w_fold, colsum, shift;
-    };
-    FoldedLinear fold_layernorm(const HipTensor& w, const HipTensor* bias, const HipTensor& ln_w,
-                                const HipTensor& ln_b) const {
-        HS_REQUIRE(w.shape().size() == 2, "fold_layernorm: weight must be (n, k)");
-        const size_t n = w.shape()[0], k = w.shape()[1];
-        HS_REQUIRE(ln_w.dtype() == Dtype::F32 && ln_w.len() == k && ln_b.dtype() == Dtype::F32 &&
-                       ln_b.len() == k,
-                   "fold_layernorm: norm parameters must be f32 (k)");
-        HS_REQUIRE(!bias || (bias->dtype() == Dtype::F32 && bias->len() == n),
-                   "fold_layernorm: bias must be f32 (n)");
-        FoldedLinear f{empty_typed({n, k}, w.dtype()), empty_typed({n}, Dtype::F32),
-                       empty_typed({n}, Dtype::F32)};
-        check(hs_fold_layernorm(stream_, hs_dtype(w.dtype()), w.data(), bias ? bias->f32() : nullptr,
-                                ln_w.f32(), ln_b.f32(), f.w_fold.data(),
-                                static_cast<float*>(f.colsum.data()),
-                                static_cast<float*>(f.shift.data()), i32(n), i32(k)),
-              "fold_layernorm");
-        return f;
-    }
-
-    // linear(layernorm(x)) on folded weights; the row statistics go to a
-    // workspace owned by the call.
-    HipTensor linear_ln(const HipTensor& x, const FoldedLinear& f, float eps = 1e-5f) const {
-        return folded_call(x, f, eps, false);
+    // layernorm(x, norm) then linear(w, bias) (LN1 -> q|k|v,
+    // model/block.rs:128-131) in one product: the normalised rows, rounded to
+    // the storage type as layernorm stores them, exist only on the way to the
+    // matrix cores. The row statistics go to a workspace owned by the call.
+    HipTensor linear_ln(const HipTensor& x, const Norm& norm, const HipTensor& w,
+                        const HipTensor* bias, float eps = 1e-5f) const {
+        return ln_call(x, norm, w, bias, eps, false);
     }
     // gelu(linear(layernorm(x))): LN2, fc1 with its bias, GELU
-    HipTensor linear_ln_gelu(const HipTensor& x, const FoldedLinear& f, float eps = 1e-5f) const {
-        return folded_call(x, f, eps, true);
+    // (model/block.rs:153, 172-176)
+    HipTensor linear_ln_gelu(const HipTensor& x, const Norm& norm, const HipTensor& w,
+                             const HipTensor* bias, float eps = 1e-5f) const {
+        return ln_call(x, norm, w, bias, eps, true);
     }
     // LN1 and the q|k|v projection with heads, QK-norm and RoPE
-    // (model/block.rs:128-146) on the folded q|k|v weight. Shapes the fused
-    // kernel does not cover (f32, d != 64) run linear_ln then qknorm_rope
-    // per third.
-    Qkv linear_ln_qkv_heads(const HipTensor& x, const FoldedLinear& f, size_t s, size_t t, size_t h,
-                            const Norm* qn, const Norm* kn, const Rope* rope,
-                            float eps = 1e-5f) const {
-        const auto& sh = f.w_fold.shape();
-        HS_REQUIRE(sh.size() == 2 && sh[0] % (3 * h) == 0, "w_fold shape");
-        const size_t n3 = sh[0], k = sh[1], d = n3 / (3 * h), hd = h * d;
-        HS_REQUIRE(x.len() == s * t * k && x.dtype() == f.w_fold.dtype(), "x shape/dtype");
-        if (!(x.dtype() == Dtype::F16 && d == 64 && n3 % 256 == 0 && k % 64 == 0)) {
-            Qkv out;
-            HipTensor* dst[3] = {&out.q, &out.k, &out.v};
-            const Norm* norms[3] = {qn, kn, nullptr};
-            const size_t esz = dtype_size(x.dtype());
-            HipTensor ws = empty_typed({2 * s * t}, Dtype::F32);
-            for (int i = 0; i < 3; i++) {
-                HipTensor proj = empty_typed({s * t, hd}, x.dtype());
-                check(hs_linear_ln(stream_, hs_dtype(x.dtype()), x.data(),
-                                   static_cast<const char*>(f.w_fold.data()) + i * hd * k * esz,
-                                   f.colsum.f32() + i * hd, f.shift.f32() + i * hd,
-                                   static_cast<float*>(ws.data()), proj.data(),
-                                   static_cast<int64_t>(s * t), i32(hd), i32(k), eps),
-                      "linear_ln");
-                *dst[i] = qknorm_rope(proj, s, t, h, d, norms[i], i < 2 ? rope : nullptr, eps);
-            }
-            return out;
-        }
+    // (model/block.rs:128-146) in one product. Shapes the fused kernel does
+    // not cover (f32, d != 64) run layernorm then linear_qkv_heads.
+    Qkv linear_ln_qkv_heads(const HipTensor& x, const Norm& norm, const HipTensor& w_qkv,
+                            const HipTensor* b_qkv, size_t s, size_t t, size_t h, const Norm* qn,
+                            const Norm* kn, const Rope* rope, float eps = 1e-5f) const {
+        HS_REQUIRE(w_qkv.shape().size() == 2 && w_qkv.shape()[0] % (3 * h) == 0, "w_qkv shape");
+        const size_t n3 = w_qkv.shape()[0], k = w_qkv.shape()[1], d = n3 / (3 * h);
+        HS_REQUIRE(x.len() == s * t * k && x.dtype() == w_qkv.dtype(), "x shape/dtype");
+        HS_REQUIRE(!b_qkv || (b_qkv->dtype() == Dtype::F32 && b_qkv->len() == n3), "qkv bias");
+        ln_params(norm, k);
+        if (!(x.dtype() == Dtype::F16 && d == 64 && n3 % 256 == 0 && k % 64 == 0))
+            return linear_qkv_heads(layernorm(x, *norm.weight, *norm.bias, eps), w_qkv, b_qkv, s, t,
+                                    h, qn, kn, rope, eps);
         const float *qw = nullptr, *qb = nullptr, *kw = nullptr, *kb = nullptr;
         const float *sn = nullptr, *cs = nullptr;
         size_t prefix = 0;
@@ -657,11 +622,11 @@ class HipContext {
         HipTensor ws = empty_typed({2 * s * t}, Dtype::F32);
         Qkv out{empty_typed({s, h, t, d}, x.dtype()), empty_typed({s, h, t, d}, x.dtype()),
                 empty_typed({s, h, t, d}, x.dtype())};
-        check(hs_linear_ln_qkv_heads(stream_, hs_dtype(x.dtype()), x.data(), f.w_fold.data(),
-                                     f.colsum.f32(), f.shift.f32(), qw, qb, kw, kb, sn, cs,
-                                     static_cast<float*>(ws.data()), out.q.data(), out.k.data(),
-                                     out.v.data(), i32(s), i32(t), i32(h), i32(d), i32(k),
-                                     i32(prefix), eps),
+        check(hs_linear_ln_qkv_heads(stream_, hs_dtype(x.dtype()), x.data(), norm.weight->f32(),
+                                     norm.bias->f32(), w_qkv.data(), b_qkv ? b_qkv->f32() : nullptr,
+                                     qw, qb, kw, kb, sn, cs, static_cast<float*>(ws.data()),
+                                     out.q.data(), out.k.data(), out.v.data(), i32(s), i32(t),
+                                     i32(h), i32(d), i32(k), i32(prefix), eps),
               "linear_ln_qkv_heads");
         return out;
     }
@@ -715,20 +680,23 @@ class HipContext {
 
    private:
     static ::hs_dtype hs_dtype(Dtype dt) { return static_cast<::hs_dtype>(static_cast<int>(dt)); }
-    HipTensor folded_call(const HipTensor& x, const FoldedLinear& f, float eps, bool gelu) const {
-        const auto& sh = f.w_fold.shape();
-        HS_REQUIRE(sh.size() == 2, "w_fold must be (n, k)");
-        const size_t n = sh[0], k = sh[1];
-        HS_REQUIRE(x.last() == k && x.dtype() == f.w_fold.dtype(),
-                   "x must be (m, k) in w_fold's dtype");
-        const size_t m = x.len() / k;
-        HS_REQUIRE(f.colsum.len() == n && f.shift.len() == n, "colsum/shift length");
+    static void ln_params(const Norm& norm, size_t k) {
+        HS_REQUIRE(norm.weight && norm.bias, "layernorm needs weight and bias");
+        HS_REQUIRE(norm.weight->dtype() == Dtype::F32 && norm.weight->len() == k &&
+                       norm.bias->dtype() == Dtype::F32 && norm.bias->len() == k,
+                   "layernorm parameters must be f32 (k)");
+    }
+    HipTensor ln_call(const HipTensor& x, const Norm& norm, const HipTensor& w,
+                      const HipTensor* bias, float eps, bool gelu) const {
+        size_t m, n, k;
+        linear_shape(x, w, bias, m, n, k);
+        ln_params(norm, k);
         HipTensor ws = empty_typed({2 * m}, Dtype::F32);
         HipTensor out = empty_typed({m, n}, x.dtype());
         check((gelu ? hs_linear_ln_gelu : hs_linear_ln)(
-                  stream_, hs_dtype(x.dtype()), x.data(), f.w_fold.data(), f.colsum.f32(),
-                  f.shift.f32(), static_cast<float*>(ws.data()), out.data(),
-                  static_cast<int64_t>(m), i32(n), i32(k), eps),
+                  stream_, hs_dtype(x.dtype()), x.data(), norm.weight->f32(), norm.bias->f32(),
+                  w.data(), bias ? bias->f32() : nullptr, static_cast<float*>(ws.data()),
+                  out.data(), static_cast<int64_t>(m), i32(n), i32(k), eps),
               gelu ? "linear_ln_gelu" : "linear_ln");
         return out;
     }

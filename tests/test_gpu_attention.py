@@ -144,6 +144,41 @@ def test_attention_f16_reference_moves(ctx, case):
     check(got, O.attention(q, k, v), f"attention reference moves ({case})")
 
 
+@pytest.mark.parametrize("v_scale", [1.0, 1000.0])
+def test_attention_f16_row_sum_rounding_worst_case(ctx, v_scale):
+    """The f16 matrix-core kernel sums each lane's weights in groups of four
+    keys (the keys of one 32-key block that agree mod 8) by two levels of
+    f16 additions, then in f32. Its worst case: one weight of 1 per group
+    and three that f16 drops, one (just under half an f16 ulp of 1) at the
+    first level beside the 1 and two (together just under it) at the
+    second. Every group then loses ~1.97 * 2^-11 of its 1 + 1.97 * 2^-11,
+    so l is low by ~9.6e-4 relative, and with V constant the output is high
+    by as much (the numerator adds the same f16 weights in f32). Bound: at
+    most 2^-10 from the two rounding levels plus 2^-11 from the output's
+    f16 rounding, relative, which is also inside the f16 gate."""
+    s_, h, t, d = 1, 2, 512, 64
+    k = np.zeros((s_, h, t, d), np.float32)
+    m32 = np.arange(t) % 32
+    # scores q.k / 8 = a * 8 / 8 = a: weights exp(a) against the max 0
+    a = np.where(m32 < 8, 0.0, np.where((m32 >= 16) & (m32 < 24), -7.6328125, -8.3359375))
+    k[..., 0] = a
+    q = np.zeros((s_, h, t, d), np.float32)
+    q[..., 0] = 8.0
+    v = np.full((s_, h, t, d), v_scale, np.float32)
+    qh, kh, vh = (O.to_f16(x) for x in (q, k, v))
+    w = np.exp2(np.float64(a) * np.log2(np.e))
+    lost = w[(m32 >= 8)].reshape(-1)  # every non-dominant weight is dropped by the f16 sums
+    assert np.all(w[(m32 >= 16) & (m32 < 24)] < 2.0 ** -11), "first-level weight below half an ulp"
+    assert np.all(2 * w[(m32 >= 8) & (m32 < 16)] < 2.0 ** -11), "second-level pair below half an ulp"
+    got = back(ctx.attention(dev(qh), dev(kh), dev(vh))).astype(np.float64)
+    want = naive64(qh, kh, vh)
+    rel = np.abs(got - want) / np.abs(want)
+    # the construction reaches the bound's order: l low by ~lost / total
+    assert rel.max() > 0.5 * lost.sum() / w.sum(), "the worst case did not show"
+    assert rel.max() <= 2.0 ** -10 + 2.0 ** -11, f"row-sum rounding {rel.max():.3g} beyond its bound"
+    f16_close(got.astype(np.float32), want.astype(np.float32), "row-sum worst case")
+
+
 @pytest.mark.parametrize("case", range(24))
 def test_attention_f16_random_sweep(ctx, case):
     """Seeded random shapes and score statistics against float32 torch: T

@@ -96,11 +96,10 @@ def test_block_full_size_frame(ctx):
 
 
 @pytest.mark.parametrize("kind", ["frame", "global"])
-@pytest.mark.parametrize("fold_ln1", [False, True])
-def test_block_ln_folded(ctx, kind, fold_ln1):
-    """The block with LN2 folded into fc1 (and LN1 into the q|k|v
-    projection) against the reference's unfused sequence and against float32
-    torch, frame block at S=2 and global block at T=300."""
+def test_block_ln_prologue(ctx, kind):
+    """The block with each LayerNorm as the prologue of the product after it
+    (fuse_ln) is bit-identical to the block with the LayerNorm passes, frame
+    block at S=2 and global block at T=300."""
     g = torch.Generator(device="cpu").manual_seed(15)
     if kind == "frame":
         s, grid = 2, (5, 29)
@@ -111,11 +110,9 @@ def test_block_ln_folded(ctx, kind, fold_ln1):
         s, t, rope = 1, 300, None
     wts = BlockWeights.random(DIM, HIDDEN, 64, torch.float16, "cuda:0",
                               torch.Generator(device="cuda:0").manual_seed(15), ls_init=0.1)
-    wts.fold_layernorms(ctx)
     x = torch.randn((s * t, DIM), generator=g).half().to("cuda:0")
-    fused = back(block_forward(ctx, wts, x, s, t, rope=rope, fold_ln2=True, fold_ln1=fold_ln1))
-    seq = back(block_forward_reference(ctx, wts, x, s, t, rope=rope))
-    f16_close(fused, seq, f"block {kind} folded LN vs reference sequence")
-    ref = back(torch_block(wts, x, s, t, rope, 1e-6))
-    err = np.abs(fused - ref) / np.maximum(1.0, np.abs(ref))
-    assert err.max() <= 1e-2, f"block {kind} folded LN vs float32: max scaled error {err.max():.3g}"
+    fused = block_forward(ctx, wts, x, s, t, rope=rope, fuse_ln=True)
+    unfused = block_forward(ctx, wts, x, s, t, rope=rope, fuse_ln=False)
+    torch.cuda.synchronize()
+    assert torch.equal(fused.view(torch.int16), unfused.view(torch.int16)), \
+        f"block {kind}: {(fused != unfused).sum().item()} values differ with the LayerNorm prologue"

@@ -482,4 +482,18 @@ def test_every_op_accepts_empty_inputs(ctx):
     assert ctx.linear_gelu(e(0, 1024), w, ones(256)).shape == (0, 256)
     assert ctx.linear_ls_residual(e(0, 1024), w, ones(256), e(0, 256), ones(256)).shape == (0, 256)
     assert ctx.cache_build(e(0, 1024), e(0, 1024)).shape == (0, 2048)
+    ln = (ones(1024), ones(1024))
+    assert ctx.linear_ln(e(0, 1024), ln, w, ones(256)).shape == (0, 256)
+    assert ctx.linear_ln_gelu(e(0, 1024), ln, w, ones(256)).shape == (0, 256)
+    wqkv = torch.zeros((3072, 1024), dtype=f16, device=d)
+    outs = ctx.linear_ln_qkv_heads(e(0, 1024), ln, wqkv, ones(3072), 0, 1374, 16,
+                                   qn=(ones(64), ones(64)), kn=(ones(64), ones(64)))
+    assert all(o.numel() == 0 for o in outs)
+    # the allocation-free entry: zero rows return before its array is used
+    from headshot_amd import _lib
+    L = _lib.load()
+    rc = L.hs_linear_ln_gelu_noalloc(torch.cuda.current_stream().cuda_stream, _lib.HS_F16,
+                                     e(0, 1024).data_ptr(), ln[0].data_ptr(), ln[1].data_ptr(),
+                                     w.data_ptr(), None, e(0, 256).data_ptr(), 0, 256, 1024, 1e-6)
+    assert rc == _lib.HS_OK, L.hs_last_error().decode()
     torch.cuda.synchronize()

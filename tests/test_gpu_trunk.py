@@ -49,15 +49,14 @@ def dino():
     return torch.randn((N * GRID[0] * GRID[1], 1024), generator=g)
 
 
-def run(ctx, trunk, tokens, fused=True, fold_ln=False):
+def run(ctx, trunk, tokens, fused=True):
     taps = {}
 
     def tap(name, t):
         torch.cuda.synchronize()
         taps[name] = t.float().cpu().numpy().copy()
 
-    caches = trunk.forward(ctx, tokens.to("cuda:0"), N, *GRID, tap=tap, fused=fused,
-                           fold_ln=fold_ln)
+    caches = trunk.forward(ctx, tokens.to("cuda:0"), N, *GRID, tap=tap, fused=fused)
     assert len(caches) == len([k for k in CACHED_LAYERS if k < DEPTH])
     return taps
 
@@ -175,23 +174,6 @@ def test_trunk_f16_vs_float32(ctx, ckpt, dino):
     ref = torch_trunk(st, dino, precision_round=True)
     gate_all(ours, ref, Gate.F16_TRUNK, "f16 trunk vs float32 (reference f16 gate)")
     gate_all(ours, ref, Gate(5e-3, 1.0 - 2e-6), "f16 trunk vs float32")
-
-
-@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
-def test_trunk_layernorm_folded_vs_float32(ctx, ckpt, dino, dtype):
-    """Every block with both LayerNorms folded into the products after them:
-    against the same float32 trunk, within the gates the unfolded trunk
-    meets (f16: the reference's f16 trunk gate and rel_max 5e-3, 1 - cosine
-    2e-6; f32: the reference's shallow f32 gate)."""
-    d, tree, st = ckpt
-    tr = Trunk.load(W.Weights.open(d, tree=tree), dtype, "cuda:0", depth=DEPTH).fold_layernorms(ctx)
-    ours = run(ctx, tr, dino, fold_ln=True)
-    ref = torch_trunk(st, dino, precision_round=dtype == torch.float16)
-    if dtype == torch.float16:
-        gate_all(ours, ref, Gate.F16_TRUNK, "folded f16 trunk vs float32 (reference f16 gate)")
-        gate_all(ours, ref, Gate(5e-3, 1.0 - 2e-6), "folded f16 trunk vs float32")
-    else:
-        gate_all(ours, ref, Gate.F32_TIGHT, "folded f32 trunk vs float32 (reference f32 gate)")
 
 
 def test_trunk_f32_vs_float32(ctx, ckpt, dino):
