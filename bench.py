@@ -57,7 +57,8 @@ PREFIX = 5  # 1 camera + 4 register tokens
 N_REG = 4
 EPS = 1e-6
 N_FRAME_BLOCKS = N_GLOBAL_BLOCKS = 24
-OPS = ["assemble", "layernorm", "qknorm_rope", "bias_ls_residual", "bias_gelu"]
+OPS = ["assemble", "layernorm", "qknorm_rope", "bias_ls_residual", "bias_gelu",
+       "bias_ls_residual_layernorm"]
 
 
 def op_bytes(rows: int, esz: int, n_patch_rows: int, n_pos_rows: int) -> dict:
@@ -66,11 +67,25 @@ def op_bytes(rows: int, esz: int, n_patch_rows: int, n_pos_rows: int) -> dict:
         "layernorm": rows * DIM * esz * 2,                   # read x, write out
         "qknorm_rope": rows * DIM * esz * 2 * 2,             # q and k, one launch
         "bias_ls_residual": rows * DIM * esz * 3,            # read res, x; write out
+        "bias_ls_residual_layernorm": rows * DIM * esz * 4,  # read res, x; write out, normed
         "bias_gelu": rows * HIDDEN * esz * 2,                # read h, write act
         "assemble": (n_patch_rows * DIM * 4                  # read f32 patches
                      + n_pos_rows * DIM * 4                  # pos-embed once
                      + rows * DIM * esz),                    # write tokens
     }
+
+
+def pass_launches(n_frame: int, n_global: int, fuse: bool = False) -> dict:
+    """Launches of each op in one pass (FusedOpPass's sequence): per block
+    the QK-norm pair and GELU; fused, LayerScale + residual with the
+    LayerNorm after it twice (the first block's LN1 and the last block's LS2
+    alone), unfused, two LayerNorms and two LayerScale + residual."""
+    n = n_frame + n_global
+    if fuse:
+        return {"assemble": 1, "layernorm": 1, "qknorm_rope": n, "bias_gelu": n,
+                "bias_ls_residual_layernorm": 2 * n - 1, "bias_ls_residual": 1}
+    return {"assemble": 1, "layernorm": 2 * n, "qknorm_rope": n, "bias_gelu": n,
+            "bias_ls_residual": 2 * n}
 
 
 def parse():
@@ -81,6 +96,9 @@ def parse():
     ap.add_argument("--frames", type=int, default=32)
     ap.add_argument("--dtype", choices=["f16", "f32"], default="f16")
     ap.add_argument("--op-passes", type=int, default=3)
+    ap.add_argument("--fuse-layernorm", action="store_true",
+                    help="time the four-op block sequence (each LayerScale + residual fused with "
+                         "the LayerNorm after it) as the headline pass")
     ap.add_argument("--shared-inputs", action="store_true",
                     help="all blocks read one set of raw GEMM outputs (default: each its own)")
     ap.add_argument("--no-workloads", action="store_true",
@@ -121,21 +139,23 @@ class Pass:
     GEMM outputs of its own (48 x 720 MB at S=32)."""
 
     def __init__(self, ctx, frames: int, dtype, grid=GRID, n_frame: int = N_FRAME_BLOCKS,
-                 n_global: int = N_GLOBAL_BLOCKS, distinct: bool = True):
+                 n_global: int = N_GLOBAL_BLOCKS, distinct: bool = True, fuse: bool = False):
         import torch
 
         from headshot_amd.aggregator import FusedOpPass
 
         self.fp = fp = FusedOpPass(ctx, frames, grid=grid, n_reg=N_REG, n_frame=n_frame,
                                    n_global=n_global, dtype=dtype, eps=EPS,
-                                   distinct_inputs=distinct)
+                                   distinct_inputs=distinct, fuse=fuse)
         self.ctx, self.frames, self.dtype = ctx, frames, dtype
         self.p, self.t, self.rows = fp.p, fp.t, fp.rows
         self.seq = fp.seq
         esz = 2 if dtype == torch.float16 else 4
         self.bytes = op_bytes(self.rows, esz, frames * fp.p, fp.p)
         self.launches = fp.launches()
-        self.pass_bytes = sum(self.bytes[k] * self.launches.get(k, 0) for k in OPS)
+        assert self.launches == pass_launches(n_frame, n_global, fuse), "launch sequence"
+        self.ops = [op for op in OPS if op in self.launches]
+        self.pass_bytes = sum(self.bytes[k] * self.launches[k] for k in self.ops)
 
     def run(self):
         self.fp.run()
@@ -214,8 +234,8 @@ def per_op_times(bench: Pass, passes: int, flush=None) -> dict:
     import torch
 
     pairs = [(KernelEvent(), KernelEvent()) for _ in bench.seq]
-    sums = {op: 0.0 for op in OPS}
-    counts = {op: 0 for op in OPS}
+    sums = {op: 0.0 for op in bench.ops}
+    counts = {op: 0 for op in bench.ops}
     for _ in range(passes):
         torch.cuda.synchronize()
         torch.cuda._sleep(100_000_000)  # ~40 ms head start
@@ -231,7 +251,7 @@ def per_op_times(bench: Pass, passes: int, flush=None) -> dict:
         for (op, _), (a, b) in zip(bench.seq, pairs):
             sums[op] += a.elapsed_time(b)
             counts[op] += 1
-    return {op: sums[op] / counts[op] for op in OPS}
+    return {op: sums[op] / counts[op] for op in bench.ops}
 
 
 FLUSH_BYTES = 1 << 30  # > the 256 MB Infinity Cache + 8 x 4 MB L2
@@ -254,7 +274,7 @@ def cache_flusher(device):
 
 def op_rates(bench: Pass, mean_ms: dict) -> dict:
     per_op = {}
-    for op in OPS:
+    for op in bench.ops:
         us = mean_ms[op] * 1e3
         gbs = bench.bytes[op] / (us * 1e-6) / 1e9
         per_op[op] = {"us": round(us, 2), "GB/s": round(gbs, 1),
@@ -263,11 +283,40 @@ def op_rates(bench: Pass, mean_ms: dict) -> dict:
     return per_op
 
 
+def sequence_pass(ctx, frames: int, dtype, distinct: bool, steps: int, fuse: bool) -> dict:
+    """The same pass with the other op sequence (fuse False: LayerScale +
+    residual and LayerNorm as separate launches, six per block), replayed
+    from a HIP graph like the headline: ms, its own algorithmic bytes, GB/s."""
+    import torch
+
+    b = Pass(ctx, frames, dtype, distinct=distinct, fuse=fuse)
+    b.run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        b.run()
+    graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    gbs = b.pass_bytes / (ms * 1e-3) / 1e9
+    out = {"fused_layernorm": fuse, "launches": sum(b.launches.values()), "ms": round(ms, 3),
+           "pass_bytes": b.pass_bytes, "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
+    del graph, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def pass_from_ops(bench: Pass, per_op: dict) -> dict:
     """The pass rate that the per-op kernel times imply: pass bytes / the sum
     of each op's mean duration x its launches (with cold per-op times: every
     launch finding none of its inputs in a cache)."""
-    ms = sum(per_op[op]["us"] * bench.launches.get(op, 0) for op in OPS) / 1e3
+    ms = sum(per_op[op]["us"] * bench.launches[op] for op in bench.ops) / 1e3
     gbs = bench.pass_bytes / (ms * 1e-3) / 1e9
     return {"ms": round(ms, 3), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4)}
 
@@ -296,10 +345,7 @@ def workload_legs(ctx, op_passes: int, flush, min_launches: int = 64, replays: i
     cold (event pairs, as the headline's ``ops``)."""
     import torch
 
-    out = {}
-    for key, (frames, grid, dt, nf, ng) in WORKLOADS.items():
-        dtype = torch.float16 if dt == "f16" else torch.float32
-        b = Pass(ctx, frames, dtype, grid=grid, n_frame=nf, n_global=ng, distinct=True)
+    def replayed_ms(b):
         reps = max(1, -(-min_launches // len(b.fp.seq)))
         b.run()
         torch.cuda.synchronize()
@@ -315,7 +361,14 @@ def workload_legs(ctx, op_passes: int, flush, min_launches: int = 64, replays: i
             graph.replay()
         end.record()
         torch.cuda.synchronize()
-        ms = start.elapsed_time(end) / (replays * reps)
+        del graph
+        return start.elapsed_time(end) / (replays * reps), reps
+
+    out = {}
+    for key, (frames, grid, dt, nf, ng) in WORKLOADS.items():
+        dtype = torch.float16 if dt == "f16" else torch.float32
+        b = Pass(ctx, frames, dtype, grid=grid, n_frame=nf, n_global=ng, distinct=True)
+        ms, reps = replayed_ms(b)
         gbs = b.pass_bytes / (ms * 1e-3) / 1e9
         warm = op_rates(b, per_op_times(b, op_passes))
         cold = op_rates(b, per_op_times(b, op_passes, flush=flush))
@@ -326,7 +379,15 @@ def workload_legs(ctx, op_passes: int, flush, min_launches: int = 64, replays: i
                     "tokens_per_s": round(b.rows / (ms * 1e-3), 1),
                     "pass_cold": pass_from_ops(b, cold), "ops": warm, "ops_cold": cold,
                     "graph_repeats": reps}
-        del graph, b
+        del b
+        f = Pass(ctx, frames, dtype, grid=grid, n_frame=nf, n_global=ng, distinct=True, fuse=True)
+        ms_f, _ = replayed_ms(f)
+        gbs_f = f.pass_bytes / (ms_f * 1e-3) / 1e9
+        out[key]["fused_layernorm"] = {"ms_per_sequence": round(ms_f, 4),
+                                       "bytes_per_sequence": f.pass_bytes,
+                                       "GB/s": round(gbs_f, 1), "frac": round(gbs_f / PEAK_GBS, 4),
+                                       "tokens_per_s": round(f.rows / (ms_f * 1e-3), 1)}
+        del f
         torch.cuda.empty_cache()
     return out
 
@@ -371,8 +432,10 @@ CEILING_PROBES = {
                              "sequence of S*T), as the pass runs 24 of each"),
     "assemble": ("cast", "S*P x 1024 f32 read, f16 written, contiguous (positional table "
                          "and prefix rows not included)"),
+    "bias_ls_residual_layernorm": ("add2w2", "two rows x 1024 f16 read, two written, "
+                                             "contiguous"),
 }
-KINDS = {"copy": 0, "add2": 1, "heads": 2, "cast": 3}
+KINDS = {"copy": 0, "add2": 1, "heads": 2, "cast": 3, "widen": 4, "inplace": 5, "add2w2": 6}
 # hsc_run shape flags: bit 0 cached loads/stores (else streaming), bit 1 one
 # 16-byte vector per lane / one token's 8-head chunk per wave, chunk by chunk
 # (else four / two whole rows)
@@ -380,6 +443,68 @@ CEILING_SHAPES = {"streaming x4": 0, "cached x4": 1, "streaming x1": 2, "cached 
 
 
 ROTATE_BYTES = 768 << 20  # > the 256 MB Infinity Cache: no reuse across launches
+
+
+def probe_times(lib, probe: str, args, sets, flush, iters: int = 20):
+    """(warm us per policy, cold us) of one probe: warm, ``iters``
+    back-to-back launches rotating over the buffer ``sets`` (each set: a, b,
+    o, o2 tensors or None), each policy and launch shape; cold, a cache
+    flush then one launch per event pair, streaming stores only."""
+    import torch
+
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def ptrs(bufs):
+        return tuple(None if x is None else x.data_ptr() for x in bufs[:4])
+
+    def launch(shape, bufs):
+        rc = lib.hsc_run(KINDS[probe], shape, *bufs, *args, stream)
+        if rc != 0:
+            raise RuntimeError(f"hsc_run({probe}) returned {rc}")
+
+    warm = {}
+    for policy, shape in CEILING_SHAPES.items():
+        for bufs in sets:
+            launch(shape, ptrs(bufs))
+        torch.cuda.synchronize()
+        a, b = KernelEvent(), KernelEvent()
+        a.record()
+        for i in range(iters):
+            launch(shape, ptrs(sets[i % len(sets)]))
+        b.record()
+        torch.cuda.synchronize()
+        warm[policy] = a.elapsed_time(b) / iters * 1e3
+    cold = []
+    for shape in (s for s in CEILING_SHAPES.values() if not s & 1):  # streaming stores only
+        ev = [(KernelEvent(), KernelEvent()) for _ in range(iters)]
+        for a, b in ev:
+            flush()
+            a.record()
+            launch(shape, ptrs(sets[0]))
+            b.record()
+        torch.cuda.synchronize()
+        cold.append(sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3)
+    return warm, min(cold)
+
+
+def probe_entry(lib, probe: str, make_set, nbytes: int, args, flush, op_us: float,
+                op_cold_us: float | None = None) -> dict:
+    """A probe's warm (fastest policy) and cold rates beside an op that moves
+    the same ``nbytes``: ``make_set()`` builds one buffer set; enough sets
+    rotate to exceed ROTATE_BYTES."""
+    sets = [make_set() for _ in range(max(1, -(-ROTATE_BYTES // nbytes)))]
+    warm, cold_us = probe_times(lib, probe, args, sets, flush)
+    policy = min(warm, key=warm.get)
+    us = warm[policy]
+    out = {"probe": probe, "bytes": nbytes, "us": round(us, 2),
+           "GB/s": round(nbytes / us / 1e3, 1), "frac": round(nbytes / us / 1e3 / PEAK_GBS, 4),
+           "policy": policy, "cold_us": round(cold_us, 2),
+           "cold_frac": round(nbytes / cold_us / 1e3 / PEAK_GBS, 4),
+           "op_frac_of_probe": round(us / op_us, 4)}
+    if op_cold_us is not None:
+        out["op_cold_frac_of_probe"] = round(cold_us / op_cold_us, 4)
+    del sets
+    return out
 
 
 def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int = 20) -> dict:
@@ -410,12 +535,14 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
 
     def buffers(op, probe):
         """(a, b, o, o2, bytes moved, (n, s, t)) for one launch."""
-        if probe in ("copy", "add2"):
+        if probe in ("copy", "add2", "add2w2"):
             width = HIDDEN if op == "bias_gelu" else DIM
             a = torch.ones((rows, width), device=dev, dtype=f16)
-            b = torch.ones_like(a) if probe == "add2" else None
+            b = torch.ones_like(a) if probe != "copy" else None
+            o2 = torch.empty_like(a) if probe == "add2w2" else None
             n = a.numel() * 2 // 16
-            return a, b, torch.empty_like(a), None, n * 16 * (3 if b is not None else 2), (n, 0, 0)
+            streams = {"copy": 2, "add2": 3, "add2w2": 4}[probe]
+            return a, b, torch.empty_like(a), o2, n * 16 * streams, (n, 0, 0)
         if probe == "heads":
             a = torch.ones((rows, DIM), device=dev, dtype=f16)
             return (a, torch.ones_like(a), torch.empty_like(a), torch.empty_like(a),
@@ -424,42 +551,13 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
         return (a, None, torch.empty((frames * p, DIM), device=dev, dtype=f16), None,
                 a.numel() * 6, (a.numel(), 0, 0))
 
-    def ptrs(bufs):
-        return tuple(None if x is None else x.data_ptr() for x in bufs[:4])
-
     def timed(probe, args, sets):
-        """(warm us per policy, cold us) of one probe launch shape."""
-        def launch(shape, bufs):
-            rc = lib.hsc_run(KINDS[probe], shape, *bufs, *args, stream)
-            if rc != 0:
-                raise RuntimeError(f"hsc_run({probe}) returned {rc}")
-
-        warm = {}
-        for policy, shape in CEILING_SHAPES.items():
-            for bufs in sets:
-                launch(shape, ptrs(bufs))
-            torch.cuda.synchronize()
-            a, b = KernelEvent(), KernelEvent()
-            a.record()
-            for i in range(iters):
-                launch(shape, ptrs(sets[i % len(sets)]))
-            b.record()
-            torch.cuda.synchronize()
-            warm[policy] = a.elapsed_time(b) / iters * 1e3
-        cold = []
-        for shape in (s for s in CEILING_SHAPES.values() if not s & 1):  # streaming stores only
-            ev = [(KernelEvent(), KernelEvent()) for _ in range(iters)]
-            for a, b in ev:
-                flush()
-                a.record()
-                launch(shape, ptrs(sets[0]))
-                b.record()
-            torch.cuda.synchronize()
-            cold.append(sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3)
-        return warm, min(cold)
+        return probe_times(lib, probe, args, sets, flush, iters)
 
     out = {}
     for op, (probe, what) in CEILING_PROBES.items():
+        if op not in bench.ops:
+            continue
         first = buffers(op, probe)
         nbytes, args = first[4], first[5]
         sets = [first] + [buffers(op, probe) for _ in range(max(1, -(-ROTATE_BYTES // nbytes)) - 1)]
@@ -552,12 +650,44 @@ def attention_times(ctx, frames: int, iters: int) -> dict:
 CACHED_LAYERS = 4  # trunk layers whose outputs feed the heads (model/trunk.rs:125-135)
 
 
-def cache_times(ctx, frames: int, iters: int) -> dict:
+def cold_us(fn, flush, iters: int) -> float:
+    """Mean kernel time (us) of ``fn``'s launch behind a cache flush, one
+    KernelEvent pair per launch."""
+    import torch
+
+    ev = [(KernelEvent(), KernelEvent()) for _ in range(iters)]
+    for a, b in ev:
+        flush()
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3
+
+
+def warm_us(fn, iters: int) -> float:
+    """Mean kernel time (us) of ``iters`` back-to-back launches of ``fn``."""
+    import torch
+
+    fn()
+    torch.cuda.synchronize()
+    a, b = KernelEvent(), KernelEvent()
+    a.record()
+    for _ in range(iters):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / iters * 1e3
+
+
+def cache_times(ctx, frames: int, iters: int, flush) -> dict:
     """Cache::build at this S (model/cache.rs:21-52): the frame- and
     inter-block outputs (S*1374, 1024) f16 each, concatenated and cast to f32
     in one pass (hs_cache_build); the reference's two-dispatch sequence
     (concat_channels, then cast_to_f32) through the same library beside it.
-    Algorithmic bytes: rows * 2048 * (2 read + 4 written)."""
+    Algorithmic bytes: rows * 2048 * (2 read + 4 written). Beside it the
+    ``widen`` probe (f16 read, f32 written, the same bytes, no
+    concatenation), warm and cold."""
     import torch
 
     rows = frames * (GRID[0] * GRID[1] + PREFIX)
@@ -567,30 +697,83 @@ def cache_times(ctx, frames: int, iters: int) -> dict:
     out = torch.empty((rows, 2 * DIM), dtype=torch.float32, device=ctx.device)
     nbytes = rows * 2 * DIM * (2 + 4)
 
-    def timed(fn):
-        fn()
-        torch.cuda.synchronize()
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(iters):
-            fn()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) / iters
-
     ctx.cache_build(fo, io, out=out)
     fused = ctx.last_launch
-    ms = timed(fused)
+    us = warm_us(fused, iters)
+    us_cold = cold_us(fused, flush, iters)
     cat = ctx.concat_channels(fo, io)
     c1 = ctx.last_launch
     cast_out = ctx.cast_to_f32(cat)  # noqa: F841 (the replayed launch writes it)
     c2 = ctx.last_launch
-    ms_seq = timed(lambda: (c1(), c2()))
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    return {"rows": rows, "channels": 2 * DIM, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
-            "frac": round(gbs / PEAK_GBS, 4), "bytes": nbytes,
-            "reference_sequence_us": round(ms_seq * 1e3, 2),
-            "calls_per_pass": CACHED_LAYERS}
+    us_seq = warm_us(lambda: (c1(), c2()), iters)
+    gbs = nbytes / us / 1e3
+    res = {"rows": rows, "channels": 2 * DIM, "us": round(us, 2), "GB/s": round(gbs, 1),
+           "frac": round(gbs / PEAK_GBS, 4), "cold_us": round(us_cold, 2),
+           "cold_frac": round(nbytes / us_cold / 1e3 / PEAK_GBS, 4), "bytes": nbytes,
+           "reference_sequence_us": round(us_seq, 2), "calls_per_pass": CACHED_LAYERS}
+    if os.path.exists(CEILING_LIB):
+        n16 = rows * 2 * DIM * 2 // 16  # f16 input vectors
+
+        def make_set():
+            return (torch.ones(rows * 2 * DIM, device=ctx.device, dtype=torch.float16), None,
+                    torch.empty(rows * 2 * DIM, device=ctx.device, dtype=torch.float32), None)
+
+        res["ceiling"] = probe_entry(load_ceiling(), "widen", make_set, nbytes, (n16, 0, 0), flush,
+                                     us, us_cold)
+    return res
+
+
+def surface_times(ctx, frames: int, iters: int, flush) -> dict:
+    """The reference's single ops that the fused ops replace in the pass,
+    timed alone at this S (f16, head-major (S, 16, T, 64) where the op is
+    head-major): rope_apply in place (engine/ops.rs:202-223), attn_merge
+    (:255-267), tiled_add of the positional table (:374-389) and
+    cast_to_f16 (tensor.rs:148-160). Warm (back-to-back launches) and cold
+    (behind a cache flush); rope_apply beside the ``inplace`` probe (one
+    buffer read and written back)."""
+    import torch
+
+    from headshot_amd import rope as _rope
+
+    t = GRID[0] * GRID[1] + PREFIX
+    p = GRID[0] * GRID[1]
+    rows = frames * t
+    d = ctx.device
+    g = torch.Generator(device="cpu").manual_seed(12)
+    sin, cos = (torch.from_numpy(a).to(d) for a in _rope.tables(_rope.periods(), *GRID))
+    out = {}
+
+    def entry(fn, nbytes):
+        us, us_c = warm_us(fn, iters), cold_us(fn, flush, iters)
+        return {"us": round(us, 2), "GB/s": round(nbytes / us / 1e3, 1),
+                "frac": round(nbytes / us / 1e3 / PEAK_GBS, 4), "cold_us": round(us_c, 2),
+                "cold_frac": round(nbytes / us_c / 1e3 / PEAK_GBS, 4), "bytes": nbytes}
+
+    q = torch.randn((frames, HEADS, t, HEAD_DIM), generator=g).half().to(d)
+    ctx.rope_apply(q, sin, cos, PREFIX)
+    rope_call = ctx.last_launch
+    nb = q.numel() * 2 * 2
+    out["rope_apply"] = entry(rope_call, nb)
+    if os.path.exists(CEILING_LIB):
+        def make_set():
+            return (None, None, torch.ones(q.numel(), device=d, dtype=torch.float16), None)
+
+        out["rope_apply"]["ceiling"] = probe_entry(
+            load_ceiling(), "inplace", make_set, nb, (q.numel() * 2 // 16, 0, 0), flush,
+            out["rope_apply"]["us"], out["rope_apply"]["cold_us"])
+    merged = ctx.attn_merge(q)
+    out["attn_merge"] = entry(ctx.last_launch, q.numel() * 2 * 2)
+    del merged
+    x = torch.randn((rows, DIM), generator=g).half().to(d)
+    pos = torch.randn((p, DIM), generator=g).to(d) * 0.02
+    x32 = torch.randn((frames * p, DIM), generator=g).to(d)
+    tiled = ctx.tiled_add(x32, pos)
+    out["tiled_add"] = entry(ctx.last_launch, x32.numel() * 4 * 2 + pos.numel() * 4)
+    del tiled
+    h = ctx.cast_to_f16(x32)
+    out["cast_to_f16"] = entry(ctx.last_launch, x32.numel() * (4 + 2))
+    del h, x, q
+    return out
 
 
 def alternating_best(fns: dict, timed, rounds: int = 3) -> dict:
@@ -762,8 +945,8 @@ def block_times(ctx, frames: int, iters: int) -> dict:
     sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(_rope.periods(), *GRID))
     out = {}
 
-    def ln_passes(*a, **kw):
-        return block_forward(*a, fuse_ln=False, **kw)
+    def ln_prologue(*a, **kw):
+        return block_forward(*a, fuse_ln=True, **kw)
 
     for kind, (s, tt, rope) in {"frame": (frames, t, (sin, cos, PREFIX)),
                                 "global": (1, frames * t, None)}.items():
@@ -780,16 +963,16 @@ def block_times(ctx, frames: int, iters: int) -> dict:
 
         fns = {name: (lambda f=f: f(ctx, wts, x, s, tt, rope=rope, eps=EPS))
                for name, f in (("fused", block_forward), ("reference_sequence", block_forward_reference),
-                               ("fused_layernorm_passes", ln_passes))}
+                               ("fused_layernorm_prologue", ln_prologue))}
         out[kind] = {name + "_ms": round(ms, 3) for name, ms in alternating_best(fns, timed).items()}
     out["aggregator_ms"] = round(N_FRAME_BLOCKS * out["frame"]["fused_ms"]
                                  + N_GLOBAL_BLOCKS * out["global"]["fused_ms"], 1)
     out["aggregator_reference_sequence_ms"] = round(
         N_FRAME_BLOCKS * out["frame"]["reference_sequence_ms"]
         + N_GLOBAL_BLOCKS * out["global"]["reference_sequence_ms"], 1)
-    out["aggregator_layernorm_passes_ms"] = round(
-        N_FRAME_BLOCKS * out["frame"]["fused_layernorm_passes_ms"]
-        + N_GLOBAL_BLOCKS * out["global"]["fused_layernorm_passes_ms"], 1)
+    out["aggregator_layernorm_prologue_ms"] = round(
+        N_FRAME_BLOCKS * out["frame"]["fused_layernorm_prologue_ms"]
+        + N_GLOBAL_BLOCKS * out["global"]["fused_layernorm_prologue_ms"], 1)
     return out
 
 
@@ -1086,7 +1269,7 @@ def cpu_model() -> str:
 KERNEL_OPS = {"ln_vec_kernel": "layernorm", "ln_generic_kernel": "layernorm",
               "qkn_row_kernel": "qknorm_rope", "qkn_generic_kernel": "qknorm_rope",
               "bias_ls_kernel": "bias_ls_residual", "bias_gelu_kernel": "bias_gelu",
-              "assemble_kernel": "assemble"}
+              "assemble_kernel": "assemble", "ls_ln_kernel": "bias_ls_residual_layernorm"}
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "aggregator_pass_s32_f16_traffic.json")
 
 
@@ -1198,8 +1381,7 @@ def summarize(args) -> None:
     p = GRID[0] * GRID[1]
     rows = args.frames * (p + PREFIX)
     nbytes = op_bytes(rows, esz, args.frames * p, p)
-    launches = {"assemble": 1, "layernorm": 96, "qknorm_rope": 48, "bias_ls_residual": 96,
-                "bias_gelu": 48}
+    launches = pass_launches(N_FRAME_BLOCKS, N_GLOBAL_BLOCKS, args.fuse_layernorm)
     legs = args.legs_trace or args.summarize
     dur = defaultdict(list)
     for r in csv.DictReader(open(args.summarize)):
@@ -1210,7 +1392,7 @@ def summarize(args) -> None:
            "| op | kernel calls | mean us | median us | algorithmic MB/launch | GB/s (mean) "
            "| of 8 TB/s |", "|---|---|---|---|---|---|---|"]
     pass_us = 0.0
-    for op in OPS:
+    for op in launches:
         if not dur[op]:
             continue
         m, med = st.mean(dur[op]), st.median(dur[op])
@@ -1219,7 +1401,7 @@ def summarize(args) -> None:
         out.append(f"| {op} | {len(dur[op])} | {m:.2f} | {med:.2f} | {nbytes[op] / 1e6:.1f} | "
                    f"{gbs:.0f} | {gbs / PEAK_GBS:.1%} |")
     out += ["", f"Sum of mean kernel times x launches per pass: {pass_us / 1e3:.3f} ms "
-                f"({sum(nbytes[o] * launches[o] for o in OPS) / (pass_us * 1e-6) / 1e9:.0f} GB/s "
+                f"({sum(nbytes[o] * launches[o] for o in launches) / (pass_us * 1e-6) / 1e9:.0f} GB/s "
                 f"algorithmic)."]
     # Attention (the benchmark's attention leg): the flash kernel, told apart by
     # grid size: one workgroup of 8 waves (512 work-items) per 256 queries of
@@ -1375,7 +1557,7 @@ def main():
 
     dtype = torch.float16 if args.dtype == "f16" else torch.float32
     ctx = HipContext("cuda:0")
-    bench = Pass(ctx, args.frames, dtype, distinct=not args.shared_inputs)
+    bench = Pass(ctx, args.frames, dtype, distinct=not args.shared_inputs, fuse=args.fuse_layernorm)
     torch.cuda.synchronize()
 
     # HBM counter calibration: one plain copy of known size (outside timing).
@@ -1431,8 +1613,8 @@ def main():
         if not args.no_workloads:
             workloads = workload_legs(ctx, args.op_passes, flush)
         del flush
-        ops_ms = round(sum(per_op[op]["us"] * bench.launches[op] for op in OPS) / 1e3, 3)
-        dominant = max(OPS, key=lambda op: per_op[op]["us"] * bench.launches[op])
+        ops_ms = round(sum(per_op[op]["us"] * bench.launches[op] for op in bench.ops) / 1e3, 3)
+        dominant = max(bench.ops, key=lambda op: per_op[op]["us"] * bench.launches[op])
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": per_op[dominant]["GB/s"],
                     "peak": PEAK_GBS, "unit": "GB/s", "frac": per_op[dominant]["frac"],
                     "traffic": None}
@@ -1441,6 +1623,15 @@ def main():
             roofline["traffic"] = traffic["bytes_per_launch"]
             roofline["traffic_source"] = traffic["source"]
     value = bench.pass_bytes / (ms * 1e-3) / 1e9
+    sequences = None
+    if args.op_passes > 0:
+        this = {"fused_layernorm": args.fuse_layernorm, "launches": sum(bench.launches.values()),
+                "ms": round(ms, 3), "pass_bytes": bench.pass_bytes,
+                "GB/s": round(value, 1), "frac": round(value / PEAK_GBS, 4)}
+        other = sequence_pass(ctx, args.frames, dtype, not args.shared_inputs, args.steps,
+                              fuse=not args.fuse_layernorm)
+        sequences = {"six_op": other if args.fuse_layernorm else this,
+                     "fused_layernorm": this if args.fuse_layernorm else other}
 
     line = {
         "metric": METRIC,
@@ -1459,6 +1650,9 @@ def main():
         "config": {"workload": f"aggregator fused-op pass: assembly + {N_FRAME_BLOCKS} frame + "
                                f"{N_GLOBAL_BLOCKS} global blocks",
                    "block_inputs": "shared" if args.shared_inputs else "per block",
+                   "block_sequence": ("4 ops (LayerScale + residual fused with the LayerNorm after it)"
+                                      if args.fuse_layernorm else
+                                      "6 ops (LN1, QK-norm pair, LS1, LN2, GELU, LS2)"),
                    "frames": args.frames, "tokens_per_frame": bench.t, "dim": DIM,
                    "heads": HEADS, "head_dim": HEAD_DIM, "hidden": HIDDEN, "prefix": PREFIX,
                    "grid": f"{GRID[0]}x{GRID[1]}", "eps": EPS, "launch": launch},
@@ -1467,6 +1661,7 @@ def main():
         "tokens_per_s": round(bench.rows / (ms * 1e-3), 1),
         "ops_ms_per_step": ops_ms,
         "pass_cold": pass_cold,
+        "sequences": sequences,
         "ops": per_op,
         "ops_cold": per_op_cold,
         "ceilings": ceilings,
@@ -1475,7 +1670,10 @@ def main():
     }
     if args.attention_iters > 0:
         line["attention"] = attention_times(ctx, args.frames, args.attention_iters)
-        line["cache_build"] = cache_times(ctx, args.frames, args.attention_iters)
+        flush = cache_flusher(ctx.device)
+        line["cache_build"] = cache_times(ctx, args.frames, args.attention_iters, flush)
+        line["surface"] = surface_times(ctx, args.frames, args.attention_iters, flush)
+        del flush
         line["linear"] = gemm_times(ctx, args.frames, args.attention_iters)
         line["block"] = block_times(ctx, args.frames, max(1, args.attention_iters // 2))
         trunk_iters = args.trunk_iters if args.trunk_iters >= 0 else max(1, args.attention_iters // 5)

@@ -12,6 +12,9 @@
 //          by chunk): the fused QK-norm + RoPE pair kernel's two orders
 //          (qknorm_rope)
 //   cast   f32 rows in, f16 rows out, contiguous   (assembly's byte mix)
+//   widen  f16 in, f32 out: 1 read : 2 written     (the cache build's mix)
+//   inplace  1 read : 1 write of the same buffer   (rope_apply in place)
+//   add2w2 2 reads : 2 writes, contiguous          (bias_ls_residual_layernorm)
 //
 // Each kernel runs with non-temporal (streaming) or ordinary cached loads and
 // stores, the two policies the library's kernels use, and in two launch
@@ -142,6 +145,65 @@ __global__ __launch_bounds__(kBlock) void cast_kernel(const float* __restrict__ 
     }
 }
 
+// n f16 -> f32, eight elements (16 bytes in, 32 out) per lane per step.
+template <bool NT, int U>
+__global__ __launch_bounds__(kBlock) void widen_kernel(const u32x4* __restrict__ a,
+                                                       u32x4* __restrict__ o, int64_t n) {
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * U +
+                         (threadIdx.x & 63);
+    u32x4 r[U];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (base + u * 64 < n) r[u] = ld<NT>(a + base + u * 64);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        if (base + u * 64 >= n) continue;
+        u32x4 lo, hi;
+#pragma unroll
+        for (int w = 0; w < 2; w++) {
+            const hs::f16x2 p = hs::u2h2(r[u][w]), q = hs::u2h2(r[u][w + 2]);
+            lo[2 * w] = hs::f2u(static_cast<float>(p.x)), lo[2 * w + 1] = hs::f2u(static_cast<float>(p.y));
+            hi[2 * w] = hs::f2u(static_cast<float>(q.x)), hi[2 * w + 1] = hs::f2u(static_cast<float>(q.y));
+        }
+        st<NT>(o + 2 * (base + u * 64), lo);
+        st<NT>(o + 2 * (base + u * 64) + 1, hi);
+    }
+}
+
+// o = a + b and o2 = a - b (as 32-bit lanes), n 16-byte vectors each.
+template <bool NT, int U>
+__global__ __launch_bounds__(kBlock) void add2w2_kernel(const u32x4* __restrict__ a,
+                                                        const u32x4* __restrict__ b,
+                                                        u32x4* __restrict__ o,
+                                                        u32x4* __restrict__ o2, int64_t n) {
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * U +
+                         (threadIdx.x & 63);
+    u32x4 ra[U], rb[U];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (base + u * 64 < n) ra[u] = ld<NT>(a + base + u * 64), rb[u] = ld<NT>(b + base + u * 64);
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (base + u * 64 < n) {
+            st<NT>(o + base + u * 64, ra[u] + rb[u]);
+            st<NT>(o2 + base + u * 64, ra[u] - rb[u]);
+        }
+}
+
+// n 16-byte vectors read and written back in place (each lane its own).
+template <bool NT, int U>
+__global__ __launch_bounds__(kBlock) void inplace_kernel(u32x4* a, int64_t n) {
+    const int64_t base = (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * U +
+                         (threadIdx.x & 63);
+    u32x4 r[U];
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (base + u * 64 < n) r[u] = ld<NT>(a + base + u * 64);
+#pragma unroll
+    for (int u = 0; u < U; u++)
+        if (base + u * 64 < n) st<NT>(a + base + u * 64, r[u] + u32x4{1, 1, 1, 1});
+}
+
 int64_t blocks_for(int64_t lanes_work) { return (lanes_work + kBlock - 1) / kBlock; }
 
 // U: 16-byte vectors per lane (copy, add2, cast) or tokens per wave (heads).
@@ -187,6 +249,28 @@ int run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n, in
                 static_cast<const float*>(a), static_cast<f16*>(o), n);
             break;
         }
+        case 6: {
+            const int64_t blocks = blocks_for((n + U - 1) / U);
+            if (blocks == 0) return 0;
+            if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
+            add2w2_kernel<NT, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                static_cast<const u32x4*>(a), static_cast<const u32x4*>(b), static_cast<u32x4*>(o),
+                static_cast<u32x4*>(o2), n);
+            break;
+        }
+        case 4:
+        case 5: {
+            const int64_t blocks = blocks_for((n + U - 1) / U);
+            if (blocks == 0) return 0;
+            if (blocks * kBlock >= (int64_t{1} << 32)) return -1;  // 32-bit grid size
+            if (kind == 4)
+                widen_kernel<NT, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                    static_cast<const u32x4*>(a), static_cast<u32x4*>(o), n);
+            else
+                inplace_kernel<NT, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, stream>>>(
+                    static_cast<u32x4*>(o), n);
+            break;
+        }
         default:
             return -1;
     }
@@ -199,7 +283,9 @@ extern "C" {
 
 // kind 0 copy / 1 add2: n 16-byte vectors (a, b -> o). kind 2 heads: s
 // frames of t tokens, a and b -> o and o2. kind 3 cast: n f32 elements
-// (n % 4 == 0). shape: bit 0 set = cached loads and stores (clear:
+// (n % 4 == 0). kind 4 widen: n 16-byte f16 vectors of a -> 2n 16-byte f32
+// vectors of o. kind 5 inplace: n 16-byte vectors of o, read and rewritten.
+// kind 6 add2w2: n 16-byte vectors, a and b -> o = a + b, o2 = a - b. shape: bit 0 set = cached loads and stores (clear:
 // non-temporal), bit 1 set = one 16-byte vector per lane / one token's
 // 8-head chunk per wave (clear: four / two whole rows). Buffers are 16-byte aligned and sized by the
 // caller. Returns 0, or -1 for an argument the kernels do not take, or the

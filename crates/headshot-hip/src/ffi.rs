@@ -70,6 +70,11 @@ extern "C" {
     pub fn hs_bias_ls_residual(stream: HsStream, dt: HsDtype, res: *const c_void,
                                x: *const c_void, bias: *const f32, gamma: *const f32,
                                out: *mut c_void, rows: i64, dim: i32) -> HsStatus;
+    pub fn hs_bias_ls_residual_layernorm(stream: HsStream, dt: HsDtype, res: *const c_void,
+                                         x: *const c_void, bias: *const f32, gamma: *const f32,
+                                         ln_w: *const f32, ln_b: *const f32, out: *mut c_void,
+                                         normed: *mut c_void, rows: i64, dim: i32, eps: f32)
+                                         -> HsStatus;
     pub fn hs_assemble_tokens(stream: HsStream, out_dt: HsDtype, patches: *const c_void,
                               patch_dt: HsDtype, patch_bias: *const f32, pos: *const f32,
                               cam: *const c_void, reg: *const c_void, out: *mut c_void, s: i32,

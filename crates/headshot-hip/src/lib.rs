@@ -494,6 +494,28 @@ impl HipContext {
         out
     }
 
+    /// `bias_ls_residual` then `layernorm` of its output in one pass
+    /// (model/block.rs:150-153: x1 into LN2; a block's output into the next
+    /// block's LN1). Returns (out, normed), bit-identical to the two calls.
+    pub fn bias_ls_residual_layernorm(&self, res: &HipTensor, x: &HipTensor, gamma: &HipTensor,
+                                      bias: Option<&HipTensor>, ln: (&HipTensor, &HipTensor),
+                                      eps: f32) -> (HipTensor, HipTensor) {
+        assert_eq!(res.len(), x.len(), "bias_ls_residual length");
+        assert_eq!(res.dtype, x.dtype, "bias_ls_residual dtype");
+        let (rows, dim) = x.dims();
+        let out = self.empty_typed(&res.shape, x.dtype);
+        let normed = self.empty_typed(&res.shape, x.dtype);
+        check(unsafe {
+            ffi::hs_bias_ls_residual_layernorm(self.stream, x.dtype.raw(), res.cptr(), x.cptr(),
+                                               opt_f32(bias, dim, "bias"),
+                                               opt_f32(Some(gamma), dim, "gamma"),
+                                               opt_f32(Some(ln.0), dim, "norm weight"),
+                                               opt_f32(Some(ln.1), dim, "norm bias"), out.mptr(),
+                                               normed.mptr(), rows as i64, i32_of(dim, "dim"), eps)
+        }, "bias_ls_residual_layernorm");
+        (out, normed)
+    }
+
     /// Token assembly (model/trunk.rs:68-85, model/dino.rs:76-93): per frame
     /// `[cam[v], reg[v*R..v*R+R], patches + bias + pos]`, v = 1 for frames
     /// after the first when `n_var` is 2.

@@ -43,6 +43,8 @@ SIGNATURES = {
                                  _I32, _I32, _I32, _I32, _I32, _F]),
     "hs_bias_gelu": (_S, [_P, _I32, _P, _P, _P, _I64, _I32]),
     "hs_bias_ls_residual": (_S, [_P, _I32, _P, _P, _P, _P, _P, _I64, _I32]),
+    "hs_bias_ls_residual_layernorm": (_S, [_P, _I32, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I32,
+                                           _F]),
     "hs_assemble_tokens": (_S, [_P, _I32, _P, _I32, _P, _P, _P, _P, _P,
                                 _I32, _I32, _I32, _I32, _I32]),
     "hs_linear": (_S, [_P, _I32, _P, _P, _P, _P, _I64, _I32, _I32]),

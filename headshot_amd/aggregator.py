@@ -79,27 +79,45 @@ class BlockIO:
 
 
 def run_block_ops(ctx: HipContext, p: BlockParams, io: BlockIO, s: int, t: int, heads: int,
-                  head_dim: int, rope=None, eps: float = 1e-5, record=None) -> None:
+                  head_dim: int, rope=None, eps: float = 1e-5, record=None, fuse: bool = False,
+                  ln1_done: bool = False, next_ln1=None) -> None:
     """One block's per-layer ops (model/block.rs:128-155 minus GEMMs and
     attention). ``rope`` = (sin, cos, prefix) for frame blocks, None for
     global blocks (which the trunk runs as one sequence, s=1, t=S*T).
-    ``record(op_name)`` is called after each launch (for launch recording)."""
+    ``record(op_name)`` is called after each launch (for launch recording).
+
+    With ``fuse`` each LayerScale + residual and the LayerNorm of its output
+    run as one launch (``bias_ls_residual_layernorm``, bit-identical to the
+    two): LS1 with LN2, and, when ``next_ln1`` (the next block's LN1 weight
+    and bias) is given, LS2 with the next block's LN1 into ``io.normed``;
+    ``ln1_done`` skips this block's LN1, done so by the block before."""
     rec = record or (lambda op: None)
-    ctx.layernorm(io.x, *p.ln1, eps=eps, out=io.normed)
-    rec("layernorm")
+    if not ln1_done:
+        ctx.layernorm(io.x, *p.ln1, eps=eps, out=io.normed)
+        rec("layernorm")
     # always: with neither QK-norm nor RoPE this is the plain split_heads
     # the reference runs unconditionally (model/block.rs:130-133)
     ctx.qknorm_rope_pair(io.q_raw, io.k_raw, s, t, heads, head_dim, qn=p.qn, kn=p.kn,
                          rope=rope, eps=eps, out_q=io.q_head, out_k=io.k_head)
     rec("qknorm_rope")
-    ctx.bias_ls_residual(io.x, io.proj_raw, p.ls1, p.proj_b, out=io.x1)
-    rec("bias_ls_residual")
-    ctx.layernorm(io.x1, *p.ln2, eps=eps, out=io.normed2)
-    rec("layernorm")
+    if fuse:
+        ctx.bias_ls_residual_layernorm(io.x, io.proj_raw, p.ls1, p.proj_b, p.ln2, eps=eps,
+                                       out=io.x1, normed=io.normed2)
+        rec("bias_ls_residual_layernorm")
+    else:
+        ctx.bias_ls_residual(io.x, io.proj_raw, p.ls1, p.proj_b, out=io.x1)
+        rec("bias_ls_residual")
+        ctx.layernorm(io.x1, *p.ln2, eps=eps, out=io.normed2)
+        rec("layernorm")
     ctx.bias_gelu(io.fc1_raw, p.fc1_b, out=io.act)
     rec("bias_gelu")
-    ctx.bias_ls_residual(io.x1, io.fc2_raw, p.ls2, p.fc2_b, out=io.x_out)
-    rec("bias_ls_residual")
+    if fuse and next_ln1 is not None:
+        ctx.bias_ls_residual_layernorm(io.x1, io.fc2_raw, p.ls2, p.fc2_b, next_ln1, eps=eps,
+                                       out=io.x_out, normed=io.normed)
+        rec("bias_ls_residual_layernorm")
+    else:
+        ctx.bias_ls_residual(io.x1, io.fc2_raw, p.ls2, p.fc2_b, out=io.x_out)
+        rec("bias_ls_residual")
 
 
 class FusedOpPass:
@@ -110,13 +128,17 @@ class FusedOpPass:
     outputs, random-init parameters (``BlockParams.random``). With
     ``distinct_inputs`` every block reads raw GEMM outputs of its own (as
     in the trunk, where each block's products are new data); otherwise all
-    blocks share one set."""
+    blocks share one set. With ``fuse`` (``run_block_ops``) every
+    LayerScale + residual is one launch with the LayerNorm after it: LS1
+    with LN2, LS2 with the next block's LN1 (the first block's LN1 and the
+    last block's LS2 stay single ops)."""
 
     def __init__(self, ctx: HipContext, frames: int, grid=(37, 37), n_reg: int = 4,
                  n_frame: int = 24, n_global: int = 24, dtype=torch.float16, eps: float = 1e-6,
                  dim: int = DIM, heads: int = HEADS, hidden: int = HIDDEN, seed: int = 42,
-                 distinct_inputs: bool = False):
+                 distinct_inputs: bool = False, fuse: bool = False):
         self.ctx, self.frames, self.dtype, self.eps = ctx, frames, dtype, eps
+        self.fuse = fuse
         self.dim, self.heads, self.hidden = dim, heads, hidden
         self.head_dim = dim // heads
         dev = ctx.device
@@ -179,7 +201,8 @@ class FusedOpPass:
                           out=self.x[0])
         rec("assemble")
         x = self.x[0]
-        for kind, p, raw in zip(self.kinds, self.blocks, self.raws):
+        n = len(self.blocks)
+        for i, (kind, p, raw) in enumerate(zip(self.kinds, self.blocks, self.raws)):
             io.q_raw, io.k_raw, io.proj_raw, io.fc1_raw, io.fc2_raw = raw
             io.x = x
             io.x_out = self.x[1] if x is self.x[0] else self.x[0]
@@ -187,8 +210,9 @@ class FusedOpPass:
                 s, t, rp = self.frames, self.t, (self.sin, self.cos, self.prefix)
             else:
                 s, t, rp = 1, self.rows, None
+            nxt = self.blocks[i + 1].ln1 if self.fuse and i + 1 < n else None
             run_block_ops(c, p, io, s, t, self.heads, self.head_dim, rope=rp, eps=self.eps,
-                          record=rec)
+                          record=rec, fuse=self.fuse, ln1_done=self.fuse and i > 0, next_ln1=nxt)
             x = io.x_out
         self.out = x
         return seq

@@ -551,6 +551,30 @@ class HipContext:
                      _dev(x, "x"), b, g, _dev(out, "out"), rows, dim)
         return out
 
+    def bias_ls_residual_layernorm(self, res, x, gamma, bias, ln, eps: float = 1e-5, out=None,
+                                   normed=None):
+        """``bias_ls_residual`` then ``layernorm`` of its output in one pass
+        (the pre-norm block's residual_ls -> layernorm pairs,
+        model/block.rs:150-153, and a block's output into the next block's
+        LN1): returns (out, normed), bit-identical to the two calls. ``ln``
+        = (weight, bias) of the LayerNorm."""
+        assert res.numel() == x.numel() and res.dtype == x.dtype, "res/x shape or dtype"
+        dim = x.shape[-1]
+        rows = x.numel() // dim if dim else 0
+        g = _param(gamma, dim, "gamma")
+        b = _opt(bias, dim, "bias")
+        lw, lb = _param(ln[0], dim, "norm weight"), _param(ln[1], dim, "norm bias")
+        if out is None:
+            out = self.empty_typed(res.shape, x.dtype)
+        if normed is None:
+            normed = self.empty_typed(res.shape, x.dtype)
+        for t in (out, normed):
+            assert t.dtype == x.dtype and t.numel() == x.numel(), "out/normed shape/dtype"
+        self._launch("bias_ls_residual_layernorm", self.lib.hs_bias_ls_residual_layernorm, _dt(x),
+                     _dev(res, "res"), _dev(x, "x"), b, g, lw, lb, _dev(out, "out"),
+                     _dev(normed, "normed"), rows, dim, eps)
+        return out, normed
+
     def assemble_tokens(self, patches, s: int, p: int, cam, reg, patch_bias=None, pos=None,
                         out_dtype: torch.dtype = F16, n_var: int = 2, out=None) -> torch.Tensor:
         """Token assembly (model/trunk.rs:68-85): per frame

@@ -22,6 +22,12 @@ namespace hs {
 namespace {
 
 constexpr int kBlock = 256;
+#ifndef HS_CACHE_NTL
+#define HS_CACHE_NTL 1  // non-temporal loads of the cache build's inputs
+#endif
+#ifndef HS_CACHE_NTS
+#define HS_CACHE_NTS 1  // non-temporal stores of its f32 output
+#endif
 #ifndef HS_CACHE_BPC
 #define HS_CACHE_BPC 8  // resident workgroups per CU
 #endif
@@ -44,7 +50,7 @@ __device__ __forceinline__ void copy_chunk(const TI* src, TO* dst) {
             st_stream(dst, ld_stream(src));
         }
     } else {
-        const u32x4 v = ld_stream(src);
+        const u32x4 v = ld_stream<HS_CACHE_NTL != 0>(src);
         u32x4 lo, hi;
 #pragma unroll
         for (int w = 0; w < 2; w++) {
@@ -52,32 +58,35 @@ __device__ __forceinline__ void copy_chunk(const TI* src, TO* dst) {
             lo[2 * w] = f2u(static_cast<float>(p.x)), lo[2 * w + 1] = f2u(static_cast<float>(p.y));
             hi[2 * w] = f2u(static_cast<float>(q.x)), hi[2 * w + 1] = f2u(static_cast<float>(q.y));
         }
-        st_stream(dst, lo);
-        st_stream(dst + 4, hi);
+        st_stream<HS_CACHE_NTS != 0>(dst, lo);
+        st_stream<HS_CACHE_NTS != 0>(dst + 4, hi);
     }
 }
 
-// Workgroups stride over rows (two rows per iteration, so each thread has
-// two loads in flight); threads stride over the row's 8-element chunks,
-// the first cc1 from a and the next cc2 from b (cc* = channels / 8). No
-// per-element index division.
-template <typename TI, typename TO>
+#ifndef HS_CACHE_ROWS
+#define HS_CACHE_ROWS 2  // rows per workgroup and iteration
+#endif
+
+// Workgroups stride over rows, R rows per iteration (rows b, b + step, ...,
+// b + (R - 1) step for workgroup b, so each thread has R loads in flight);
+// threads stride over the row's 8-element chunks, the first cc1 from a and
+// the next cc2 from b (cc* = channels / 8). No per-element index division.
+template <typename TI, typename TO, int R>
 __global__ __launch_bounds__(kBlock) void concat_vec_kernel(const TI* __restrict__ a,
                                                             const TI* __restrict__ b,
                                                             TO* __restrict__ out, int64_t rows,
                                                             int cc1, int cc2) {
     const int cc = cc1 + cc2;
     const int64_t step = static_cast<int64_t>(gridDim.x);
-    for (int64_t r = blockIdx.x; r < rows; r += 2 * step) {
-        const int64_t r2 = r + step;
-        const bool two = r2 < rows;
+    for (int64_t r0 = blockIdx.x; r0 < rows; r0 += R * step) {
         for (int k = threadIdx.x; k < cc; k += kBlock) {
             const bool left = k < cc1;
-            const TI* s0 = left ? a + (r * cc1 + k) * 8 : b + (r * cc2 + (k - cc1)) * 8;
-            copy_chunk(s0, out + (r * cc + k) * 8);
-            if (two) {
-                const TI* s1 = left ? a + (r2 * cc1 + k) * 8 : b + (r2 * cc2 + (k - cc1)) * 8;
-                copy_chunk(s1, out + (r2 * cc + k) * 8);
+#pragma unroll
+            for (int i = 0; i < R; i++) {
+                const int64_t r = r0 + i * step;
+                if (r >= rows) break;
+                const TI* src = left ? a + (r * cc1 + k) * 8 : b + (r * cc2 + (k - cc1)) * 8;
+                copy_chunk(src, out + (r * cc + k) * 8);
             }
         }
     }
@@ -127,9 +136,10 @@ hs_status launch_concat(hipStream_t st, const void* a, const void* b, void* out,
         // 1024 f16 -> f32 this measured 109 us (62% of peak) against 111-127 us
         // for persistent grids of 8-128 workgroups per CU and 127 us for one
         // row per workgroup.
-        const int64_t want = ceil_div(rows, int64_t{2}), cap = int64_t{1} << 22;
+        constexpr int R = HS_CACHE_ROWS;
+        const int64_t want = ceil_div(rows, int64_t{R}), cap = int64_t{1} << 22;
         const int64_t blocks = want < cap ? want : cap;
-        concat_vec_kernel<TI, TO><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+        concat_vec_kernel<TI, TO, R><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
             A, B, O, rows, c1 / 8, c2 / 8);
     } else {
         const int64_t total = rows * (c1 + c2);

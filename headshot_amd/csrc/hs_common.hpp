@@ -162,6 +162,13 @@ __device__ __forceinline__ float storage_round(float v, f16) {
 }
 __device__ __forceinline__ float storage_round(float v, float) { return v; }
 
+// One LayerScale + residual output value before its storage rounding
+// (residual_ls.wesl:28, res + gamma * x): the multiply-add as fmaf, the f32
+// result materialised, so every kernel that applies it rounds the same way.
+__device__ __forceinline__ float ls_affine(float res, float gamma, float x) {
+    return as_f32(fmaf(gamma, x, res));
+}
+
 // One LayerNorm output value before its storage rounding: (x - mean) * inv *
 // w + b, the multiply-add spelled as fmaf and the f32 result materialised.
 // Every kernel that normalises a row (the LayerNorm kernels and the linear

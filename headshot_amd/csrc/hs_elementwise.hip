@@ -141,6 +141,44 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
     }
 }
 
+#ifndef HS_GELU_TILE
+#define HS_GELU_TILE 0  // rows per lane of a one-shot tiled grid (0: column-stationary loop)
+#endif
+
+// One-shot tiled grid: workgroup b takes rows [R t, R t + R) of column block
+// cb (kBlock * V columns), t = b / cblocks, cb = b % cblocks; each lane loads
+// its R vectors (one per row, the same columns) and its columns' bias once.
+template <typename T, int R>
+__global__ __launch_bounds__(kBlock) void bias_gelu_tile_kernel(const T* x,
+                                                                const float* __restrict__ bias,
+                                                                T* out, int64_t rows, int cols,
+                                                                int cblocks) {
+    constexpr int V = Vec<T>::N;
+    const int64_t tile = blockIdx.x / cblocks;
+    const int cb = static_cast<int>(blockIdx.x - tile * cblocks);
+    const int c0 = (cb * kBlock + static_cast<int>(threadIdx.x)) * V;
+    const int64_t r0 = tile * R;
+    u32x4 raw[R];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+        if (r0 + r < rows) raw[r] = ld_stream<HS_GELU_NTL>(x + (r0 + r) * cols + c0);
+    float bv[V];
+#pragma unroll
+    for (int k = 0; k < V; k += 4) {
+        const float4 b4 = bias ? ld_f32x4(bias + c0 + k) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        bv[k] = b4.x, bv[k + 1] = b4.y, bv[k + 2] = b4.z, bv[k + 3] = b4.w;
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        if (r0 + r >= rows) break;
+        float f[V];
+        unpack(raw[r], f, T{});
+#pragma unroll
+        for (int k = 0; k < V; k++) f[k] = gelu_f(f[k] + bv[k]);
+        st_stream<HS_GELU_NTS>(out + (r0 + r) * cols + c0, pack(f, T{}));
+    }
+}
+
 template <typename T, bool BIAS, int U>
 __global__ __launch_bounds__(kBlock) void bias_ls_kernel(const T* res, const T* x,
                                                          const float* __restrict__ bias,
@@ -179,7 +217,7 @@ __global__ __launch_bounds__(kBlock) void bias_ls_kernel(const T* res, const T* 
             for (int k = 0; k < V; k++) {
                 float v = fx[k];
                 if constexpr (BIAS) v = storage_round(v + bv[k], T{});
-                fr[k] = fr[k] + gv[k] * v;  // residual_ls.wesl:28
+                fr[k] = ls_affine(fr[k], gv[k], v);  // residual_ls.wesl:28
             }
             st_stream(out + base + u * stride, pack(fr, T{}));
         }
@@ -208,7 +246,7 @@ __global__ __launch_bounds__(kBlock) void bias_ls_scalar_kernel(const T* res, co
         const int c = static_cast<int>(i % cols);
         float v = load_elem(x + i);
         if (bias) v = storage_round(v + bias[c], T{});
-        store_elem(out + i, load_elem(res + i) + gamma[c] * v);
+        store_elem(out + i, ls_affine(load_elem(res + i), gamma[c], v));
     }
 }
 
@@ -286,6 +324,18 @@ hs_status launch_gelu(hipStream_t st, const void* x, const float* bias, void* ou
     constexpr int U = HS_GELU_U;
     const int64_t total = rows * cols;
     const bool vec_ok = cols % V == 0 && aligned16(x) && aligned16(out) && (!bias || aligned16(bias));
+    if constexpr (HS_GELU_TILE > 0) {
+        constexpr int R = HS_GELU_TILE;
+        if (vec_ok && cols % (kBlock * V) == 0) {
+            const int cblocks = cols / (kBlock * V);
+            const int64_t blocks = ceil_div(rows, R) * cblocks;
+            if (blocks < (int64_t{1} << 31)) {
+                bias_gelu_tile_kernel<T, R><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
+                    static_cast<const T*>(x), bias, static_cast<T*>(out), rows, cols, cblocks);
+                return check_launch("bias_gelu");
+            }
+        }
+    }
     const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U, HS_GELU_BPC) : 0;
     if (blocks > 0) {
         if (bias)

@@ -44,6 +44,32 @@ constexpr int kBlock = 256;  // 4 waves per workgroup
 constexpr int kWavesPerBlock = kBlock / 64;
 constexpr int kBlocksPerCu = 4;  // generic path
 
+// A row's mean and rsqrt(var + eps) over the f32 values f (lane's values
+// at columns c * 64 V + lane * V + k), two-pass, reduced across the wave.
+// Shared by every kernel that normalises whole rows per wave, so they agree
+// bit for bit on the same row.
+template <int CHUNKS, int V>
+__device__ __forceinline__ void row_moments(const float (&f)[CHUNKS][V], float eps, float& mean,
+                                            float& inv) {
+    constexpr int DIM = 64 * V * CHUNKS;
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++)
+#pragma unroll
+        for (int k = 0; k < V; k++) s += f[c][k];
+    mean = wave_sum(s) / static_cast<float>(DIM);
+    float q = 0.0f;
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++)
+#pragma unroll
+        for (int k = 0; k < V; k++) {
+            const float d = f[c][k] - mean;
+            q += d * d;
+        }
+    const float var = wave_sum(q) / static_cast<float>(DIM);
+    inv = rsqrtf(var + eps);
+}
+
 // STATS: write each row's (mean, rsqrt(var + eps)) to stats[2 r], [2 r + 1]
 // instead of the normalised row (the statistics the row would be normalised
 // with, from the same code).
@@ -83,24 +109,10 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
         for (int u = 0; u < U; u++) {
             if (r0 + u >= rows) break;
             float f[CHUNKS][V];
-            float s = 0.0f;
 #pragma unroll
-            for (int c = 0; c < CHUNKS; c++) {
-                unpack(raw[u][c], f[c], T{});
-#pragma unroll
-                for (int k = 0; k < V; k++) s += f[c][k];
-            }
-            const float mean = wave_sum(s) / static_cast<float>(DIM);
-            float q = 0.0f;
-#pragma unroll
-            for (int c = 0; c < CHUNKS; c++)
-#pragma unroll
-                for (int k = 0; k < V; k++) {
-                    const float d = f[c][k] - mean;
-                    q += d * d;
-                }
-            const float var = wave_sum(q) / static_cast<float>(DIM);
-            const float inv = rsqrtf(var + eps);
+            for (int c = 0; c < CHUNKS; c++) unpack(raw[u][c], f[c], T{});
+            float mean, inv;
+            row_moments(f, eps, mean, inv);
             if constexpr (STATS) {
                 if (lane == 0) {
                     f32x2 m2;
@@ -116,6 +128,92 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
 #pragma unroll
                 for (int k = 0; k < V; k++) y[k] = ln_affine(f[c][k], mean, inv, wr[c][k], br[c][k]);
                 st_stream(orow + c * 64 * V, pack(y, T{}));
+            }
+        }
+    }
+}
+
+// LayerScale + residual, then the LayerNorm of its output
+// (hs_bias_ls_residual_layernorm): the pre-norm block stores x1 = res +
+// gamma * dt(x + bias) and the next op normalises x1 (model/block.rs:150-153,
+// and a block's output into the next block's LN1, :128). A wave takes U rows
+// in the lane layout of ln_vec_kernel; each row's x1 is formed in registers
+// exactly as bias_ls_kernel forms it, stored, and normalised from its stored
+// (rounded) values by the same moments and affine as ln_vec_kernel, so out
+// and normed are bit-identical to hs_bias_ls_residual then hs_layernorm.
+// Each row is read once (res and x) and written twice (out and normed).
+template <typename T, int CHUNKS, int U, bool BIAS>
+__global__ __launch_bounds__(kBlock) void ls_ln_kernel(const T* res, const T* x,
+                                                       const float* __restrict__ bias,
+                                                       const float* __restrict__ gamma,
+                                                       const float* __restrict__ w,
+                                                       const float* __restrict__ b, T* out,
+                                                       T* normed, int64_t rows, float eps) {
+    constexpr int V = Vec<T>::N;
+    constexpr int DIM = 64 * V * CHUNKS;
+    const int lane = lane_id();
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
+    const int64_t nwaves = static_cast<int64_t>(gridDim.x) * kWavesPerBlock;
+
+    float gr[CHUNKS][V], bsr[CHUNKS][V], wr[CHUNKS][V], br[CHUNKS][V];
+#pragma unroll
+    for (int c = 0; c < CHUNKS; c++) {
+        const int col = c * 64 * V + lane * V;
+#pragma unroll
+        for (int k = 0; k < V; k += 4) {
+            const float4 g4 = ld_f32x4(gamma + col + k), w4 = ld_f32x4(w + col + k);
+            const float4 b4 = ld_f32x4(b + col + k);
+            gr[c][k] = g4.x, gr[c][k + 1] = g4.y, gr[c][k + 2] = g4.z, gr[c][k + 3] = g4.w;
+            wr[c][k] = w4.x, wr[c][k + 1] = w4.y, wr[c][k + 2] = w4.z, wr[c][k + 3] = w4.w;
+            br[c][k] = b4.x, br[c][k + 1] = b4.y, br[c][k + 2] = b4.z, br[c][k + 3] = b4.w;
+            if constexpr (BIAS) {
+                const float4 s4 = ld_f32x4(bias + col + k);
+                bsr[c][k] = s4.x, bsr[c][k + 1] = s4.y, bsr[c][k + 2] = s4.z, bsr[c][k + 3] = s4.w;
+            }
+        }
+    }
+
+    for (int64_t r0 = wave * U; r0 < rows; r0 += nwaves * U) {
+        u32x4 rr[U][CHUNKS], xr[U][CHUNKS];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (r0 + u < rows) {
+                const int64_t off = (r0 + u) * DIM + lane * V;
+#pragma unroll
+                for (int c = 0; c < CHUNKS; c++) {
+                    rr[u][c] = ld_stream(res + off + c * 64 * V);
+                    xr[u][c] = ld_stream(x + off + c * 64 * V);
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (r0 + u >= rows) break;
+            const int64_t off = (r0 + u) * DIM + lane * V;
+            float f[CHUNKS][V];
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) {
+                float fr[V], fx[V];
+                unpack(rr[u][c], fr, T{});
+                unpack(xr[u][c], fx, T{});
+#pragma unroll
+                for (int k = 0; k < V; k++) {
+                    float v = fx[k];
+                    if constexpr (BIAS) v = storage_round(v + bsr[c][k], T{});
+                    fr[k] = ls_affine(fr[k], gr[c][k], v);
+                }
+                const u32x4 o = pack(fr, T{});
+                st_stream(out + off + c * 64 * V, o);
+                unpack(o, f[c], T{});  // the stored value, as hs_layernorm reads it
+            }
+            float mean, inv;
+            row_moments(f, eps, mean, inv);
+#pragma unroll
+            for (int c = 0; c < CHUNKS; c++) {
+                float y[V];
+#pragma unroll
+                for (int k = 0; k < V; k++) y[k] = ln_affine(f[c][k], mean, inv, wr[c][k], br[c][k]);
+                st_stream(normed + off + c * 64 * V, pack(y, T{}));
             }
         }
     }
@@ -279,6 +377,48 @@ hs_status launch(hipStream_t st, const void* x, const float* w, const float* b, 
     return check_launch("layernorm");
 }
 
+// The fused LayerScale + residual + LayerNorm launch for row widths of 1,
+// 2 or 4 chunks of 64 16-byte vectors with aligned buffers; false if the
+// shape needs the two single ops.
+#ifndef HS_LSLN_U
+#define HS_LSLN_U 2  // rows per wave and iteration of the fused LayerScale + LayerNorm kernel
+#endif
+#ifndef HS_LSLN_BPC
+#define HS_LSLN_BPC 0  // its workgroups per CU (a persistent grid); 0: one wave per U rows
+#endif
+
+template <typename T>
+bool launch_ls_ln(hipStream_t st, const void* res, const void* x, const float* bias,
+                  const float* gamma, const float* w, const float* b, void* out, void* normed,
+                  int64_t rows, int dim, float eps) {
+    constexpr int V = Vec<T>::N;
+    constexpr int U = HS_LSLN_U;
+    if (!(aligned16(res) && aligned16(x) && aligned16(gamma) && aligned16(w) && aligned16(b) &&
+          aligned16(out) && aligned16(normed) && (!bias || aligned16(bias)) && dim % (64 * V) == 0))
+        return false;
+    const int chunks = dim / (64 * V);
+    if (chunks != 1 && chunks != 2 && chunks != 4) return false;
+    const int64_t want = ceil_div(ceil_div(rows, U), kWavesPerBlock);
+    const int64_t cap = HS_LSLN_BPC > 0 ? static_cast<int64_t>(num_cus()) * HS_LSLN_BPC : int64_t{1} << 22;
+    const dim3 grid(static_cast<uint32_t>(want < cap ? want : cap));
+    const T* R = static_cast<const T*>(res);
+    const T* X = static_cast<const T*>(x);
+    T* O = static_cast<T*>(out);
+    T* N = static_cast<T*>(normed);
+#define HS_LS_LN(C)                                                                               \
+    (bias ? (ls_ln_kernel<T, C, U, true><<<grid, dim3(kBlock), 0, st>>>(R, X, bias, gamma, w, b, O, \
+                                                                         N, rows, eps), 0)       \
+          : (ls_ln_kernel<T, C, U, false><<<grid, dim3(kBlock), 0, st>>>(R, X, bias, gamma, w, b, \
+                                                                          O, N, rows, eps), 0))
+    switch (chunks) {
+        case 1: HS_LS_LN(1); break;
+        case 2: HS_LS_LN(2); break;
+        default: HS_LS_LN(4); break;
+    }
+#undef HS_LS_LN
+    return true;
+}
+
 // Row statistics only: the kernel (and so the arithmetic) that the
 // normalising launch above picks for the same x when the other buffers are
 // 16-byte aligned too.
@@ -337,4 +477,35 @@ extern "C" hs_status hs_layernorm_stats(hs_stream_t stream, hs_dtype dt, const v
     hipStream_t st = static_cast<hipStream_t>(stream);
     return dt == HS_F16 ? launch_stats<f16>(st, x, stats, rows, dim, eps)
                         : launch_stats<float>(st, x, stats, rows, dim, eps);
+}
+
+extern "C" hs_status hs_bias_ls_residual_layernorm(hs_stream_t stream, hs_dtype dt, const void* res,
+                                                   const void* x, const float* bias,
+                                                   const float* gamma, const float* ln_w,
+                                                   const float* ln_b, void* out, void* normed,
+                                                   int64_t rows, int32_t dim, float eps) {
+    using namespace hs;
+    const char* op = "bias_ls_residual_layernorm";
+    if (!valid_dtype(dt)) return fail(HS_EINVAL, "%s: unknown dtype %d", op, (int)dt);
+    if (rows < 0 || dim <= 0) return fail(HS_EINVAL, "%s: rows %lld / dim %d", op, (long long)rows, dim);
+    if (rows == 0) return HS_OK;
+    if (!res || !x || !gamma || !ln_w || !ln_b || !out || !normed)
+        return fail(HS_EINVAL, "%s: null buffer", op);
+    const int64_t bytes = rows * dim * dtype_size(dt);
+    if ((out != res && overlaps(out, bytes, res, bytes)) || (out != x && overlaps(out, bytes, x, bytes)))
+        return fail(HS_EINVAL, "%s: out partially overlaps res or x", op);
+    if (overlaps(normed, bytes, res, bytes) || overlaps(normed, bytes, x, bytes) ||
+        overlaps(normed, bytes, out, bytes))
+        return fail(HS_EINVAL, "%s: normed overlaps res, x or out", op);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const bool fused = dt == HS_F16 ? launch_ls_ln<f16>(st, res, x, bias, gamma, ln_w, ln_b, out,
+                                                       normed, rows, dim, eps)
+                                    : launch_ls_ln<float>(st, res, x, bias, gamma, ln_w, ln_b, out,
+                                                          normed, rows, dim, eps);
+    if (fused) return check_launch(op);
+    // other widths and alignments: the two single ops, which the fused
+    // kernel reproduces bit for bit
+    const hs_status rc = hs_bias_ls_residual(stream, dt, res, x, bias, gamma, out, rows, dim);
+    if (rc != HS_OK) return rc;
+    return hs_layernorm(stream, dt, out, ln_w, ln_b, normed, rows, dim, eps);
 }

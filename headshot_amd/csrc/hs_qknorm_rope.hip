@@ -59,6 +59,11 @@ namespace {
 #ifndef HS_QK_BPC
 #define HS_QK_BPC 8  // resident workgroups per CU (generic path)
 #endif
+#ifndef HS_ROPE_HB
+// heads loaded together by the in-place rope_apply kernel: 16 (a frame
+// block's all) took S=32 from 33.7 to 32.8 us against 8; 4 and 2 were slower
+#define HS_ROPE_HB 16
+#endif
 // Sequence length from which a wave takes one load chunk of each row
 // instead of the whole row (see above).
 constexpr int kSplitSeq = 8192;
@@ -576,7 +581,7 @@ hs_status hs_rope_apply(hs_stream_t stream, hs_dtype dt, void* x, const float* s
     const int64_t blocks = ceil_div(units, int64_t{kWavesPerBlock});
     if (d == 64 && aligned16(x) && aligned16(sin_tab) && aligned16(cos_tab) &&
         blocks * kBlock < (int64_t{1} << 32)) {
-        constexpr int HB = 8;
+        constexpr int HB = HS_ROPE_HB;
         if (dt == HS_F16)
             rope_vec_kernel<f16, HB><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
                 static_cast<f16*>(x), sin_tab, cos_tab, s, h, t, prefix);

@@ -155,6 +155,20 @@ hs_status hs_bias_ls_residual(hs_stream_t stream, hs_dtype dt, const void* res, 
                               const float* bias, const float* gamma, void* out, int64_t rows,
                               int32_t dim);
 
+/* hs_bias_ls_residual, then GpuContext::layernorm (engine/ops.rs:130-153)
+ * of its output, in one pass: the pre-norm block's residual_ls -> layernorm
+ * pairs (model/block.rs:150-153, x1 into LN2; a block's output into the next
+ * block's LN1, :128). out[r, c] = res[r, c] + gamma[c] * dt(x[r, c] +
+ * bias[c]) stored in dt, as hs_bias_ls_residual; normed = layernorm(out,
+ * ln_w, ln_b, eps) computed from out's stored values, as hs_layernorm. Both
+ * are bit-identical to the two calls. bias may be NULL; ln_w, ln_b, gamma
+ * (dim) f32. out may equal res or x; normed must not overlap res, x or
+ * out. */
+hs_status hs_bias_ls_residual_layernorm(hs_stream_t stream, hs_dtype dt, const void* res,
+                                        const void* x, const float* bias, const float* gamma,
+                                        const float* ln_w, const float* ln_b, void* out,
+                                        void* normed, int64_t rows, int32_t dim, float eps);
+
 /* Patch-token assembly (model/trunk.rs:68-85 with engine/ops.rs:337-348,
  * model/dino.rs:76-93; pos-embed add as shaders/tiled_add.wesl:23). Output
  * (S*T, D) in out_dt with T = 1 + R + P; for frame f and v = (f != 0 && n_var

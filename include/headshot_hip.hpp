@@ -657,6 +657,31 @@ class HipContext {
         return out;
     }
 
+    // bias_ls_residual then layernorm of its output in one pass
+    // (model/block.rs:150-153: x1 into LN2; a block's output into the next
+    // block's LN1): bit-identical to the two calls.
+    struct ResidualNormed {
+        HipTensor out, normed;
+    };
+    ResidualNormed bias_ls_residual_layernorm(const HipTensor& res, const HipTensor& x,
+                                              const HipTensor& gamma, const HipTensor* bias,
+                                              const Norm& norm, float eps = 1e-5f) const {
+        HS_REQUIRE(res.len() == x.len() && res.dtype() == x.dtype(), "res/x");
+        const size_t dim = x.last();
+        HS_REQUIRE(gamma.len() == dim && gamma.dtype() == Dtype::F32, "gamma");
+        if (bias) HS_REQUIRE(bias->len() == dim && bias->dtype() == Dtype::F32, "bias");
+        ln_params(norm, dim);
+        ResidualNormed r{empty_typed(res.shape(), x.dtype()), empty_typed(res.shape(), x.dtype())};
+        check(hs_bias_ls_residual_layernorm(stream_, hs_dtype(x.dtype()), res.data(), x.data(),
+                                            bias ? bias->f32() : nullptr, gamma.f32(),
+                                            norm.weight->f32(), norm.bias->f32(), r.out.data(),
+                                            r.normed.data(),
+                                            dim ? static_cast<int64_t>(x.len() / dim) : 0, i32(dim),
+                                            eps),
+              "bias_ls_residual_layernorm");
+        return r;
+    }
+
     // model/trunk.rs:68-85: per frame [cam[v], reg[v*R..], patches + bias + pos]
     HipTensor assemble_tokens(const HipTensor& patches, size_t s, size_t p, const HipTensor& cam,
                               const HipTensor* reg, const HipTensor* patch_bias,

@@ -258,6 +258,18 @@ void fused_ops_equal_reference_sequence(HipContext& ctx) {
                  "bias_ls_residual");
     assert_close(ctx.download(ctx.bias_gelu(ctx.tensor_from_slice({rows, c}, xb), &gbias)),
                  ctx.download(ctx.gelu(ctx.tensor_from_slice({rows, c}, xpb))), 1e-6f, "bias_gelu");
+    // bias + LayerScale + residual, then layernorm of its output, in one pass ==
+    // bias_ls_residual then layernorm, bit for bit
+    auto lw = ctx.tensor_from_slice({c}, rng.vec(c)), lb = ctx.tensor_from_slice({c}, rng.vec(c));
+    hs::Norm ln{&lw, &lb};
+    for (Dtype dt : {Dtype::F32, Dtype::F16}) {
+        auto r16 = ctx.tensor_from_f32({rows, c}, res, dt), x16 = ctx.tensor_from_f32({rows, c}, xb, dt);
+        auto fused = ctx.bias_ls_residual_layernorm(r16, x16, ggam, &gbias, ln, 1e-6f);
+        auto x1 = ctx.bias_ls_residual(r16, x16, ggam, &gbias);
+        exact(ctx.download(fused.out), ctx.download(x1), "bias_ls_residual_layernorm out");
+        exact(ctx.download(fused.normed), ctx.download(ctx.layernorm(x1, lw, lb, 1e-6f)),
+              "bias_ls_residual_layernorm normed");
+    }
 }
 
 // model/trunk.rs:68-85: cast_to_f16 + copy_rows per frame == assemble_tokens.

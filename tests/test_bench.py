@@ -65,7 +65,22 @@ def test_host_threads_uses_the_visible_cores_within_the_share(monkeypatch):
 
 def test_ceiling_probes_cover_every_op():
     assert set(bench.CEILING_PROBES) == set(bench.OPS)
-    assert {probe for probe, _ in bench.CEILING_PROBES.values()} == set(bench.KINDS)
+    # every probe kernel serves an op of the pass, or the cache build (widen)
+    # or the in-place rope_apply (inplace) legs
+    used = {probe for probe, _ in bench.CEILING_PROBES.values()} | {"widen", "inplace"}
+    assert used == set(bench.KINDS)
+
+
+def test_pass_launches_count_each_op_of_the_sequence():
+    fused = bench.pass_launches(24, 24, fuse=True)
+    unfused = bench.pass_launches(24, 24)
+    assert sum(fused.values()) == 1 + 4 * 48 + 1, fused  # 4 per block, + assembly, + LN1
+    assert sum(unfused.values()) == 1 + 6 * 48, unfused
+    # each fused LayerScale + LayerNorm pair skips the LayerNorm's re-read of
+    # the row the LayerScale wrote: 1024 f16 = 2048 B per token
+    b = bench.op_bytes(100, 2, 0, 0)
+    per = lambda l: sum(b[k] * v for k, v in l.items() if k != "assemble")  # noqa: E731
+    assert per(unfused) - per(fused) == 95 * 100 * 1024 * 2
 
 
 def test_ceiling_library_exports_its_entry_point():

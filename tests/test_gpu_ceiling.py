@@ -70,6 +70,23 @@ def test_cast(lib, n, temporal):
     assert torch.equal(o, x.half())
 
 
+@pytest.mark.parametrize("temporal", POLICIES)
+@pytest.mark.parametrize("n", [8, 1024 * 37, 1374 * 2048])
+def test_widen_and_inplace(lib, n, temporal):
+    g = torch.Generator(device="cuda").manual_seed(n)
+    x = (torch.randn(n, device="cuda", generator=g) * 100).half()
+    o = torch.empty(n, device="cuda", dtype=torch.float32)
+    _run(lib, "widen", temporal, x, None, o, None, n // 8, 0, 0)
+    assert torch.equal(o, x.float())
+    a = torch.randint(-2**31, 2**31 - 1, (n // 4, 4), device="cuda", dtype=torch.int32, generator=g)
+    want = (a.to(torch.int64) + 1) & 0xFFFFFFFF
+    want = torch.where(want >= 2**31, want - 2**32, want).to(torch.int32)
+    rc = lib.hsc_run(bench.KINDS["inplace"], temporal, None, None, a.data_ptr(), None, n // 4, 0,
+                     0, torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert rc == 0 and torch.equal(a, want)
+
+
 def test_kernel_event_times_what_torch_events_time():
     """bench.KernelEvent (no system-scope release at record) measures the
     same interval as torch's default events around a fixed-length GPU

@@ -287,6 +287,24 @@ def test_rope_preserves_pair_norms_full_size(ctx):
     assert torch.equal(a[:, :, :5], b[:, :, :5]), "prefix tokens must pass through"
 
 
+@pytest.mark.parametrize("frames,grid,dtype", [(2, (37, 37), torch.float16),
+                                               (2, (21, 37), torch.float32)])
+def test_fused_pass_equals_six_op_pass(ctx, frames, grid, dtype):
+    """The pass with every LayerScale + residual fused with the LayerNorm
+    after it (LS1 with LN2, LS2 with the next block's LN1) against the same
+    pass with the six single ops per block, same seed: bit-identical block
+    outputs and LayerNorm outputs."""
+    a = FusedOpPass(ctx, frames, grid=grid, n_frame=3, n_global=3, dtype=dtype, fuse=True)
+    b = FusedOpPass(ctx, frames, grid=grid, n_frame=3, n_global=3, dtype=dtype, fuse=False)
+    assert len(a.seq) == 1 + 4 * 6 + 1 and len(b.seq) == 1 + 6 * 6
+    a.run()
+    b.run()
+    torch.cuda.synchronize()
+    for k in ("normed", "normed2", "act", "x1", "q_head", "k_head"):
+        assert_bit_exact(host(getattr(a.io, k)), host(getattr(b.io, k)), f"fused pass {k}")
+    assert_bit_exact(host(a.out), host(b.out), "fused pass output")
+
+
 def test_graph_replay_matches_eager(ctx):
     """The pass captured in a HIP graph, replayed three times with eager work
     and synchronisation between replays; every replay equals eager launches."""

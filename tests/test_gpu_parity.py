@@ -320,6 +320,52 @@ def test_residual_ls_surface_in_place(ctx, dtype):
     check(back(t), O.residual_ls(res, x, g), "residual_ls in place on res")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,dim", [(37, 1024), (1, 1024), (1374, 1024), (9, 512), (5, 2048),
+                                      (7, 256), (5, 300), (3, 64)])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_bias_ls_residual_layernorm(ctx, dtype, rows, dim, with_bias):
+    """LayerScale + residual, then the LayerNorm of its output, in one pass:
+    bit-exact against hs_bias_ls_residual then hs_layernorm (the one-row
+    kernel for 1, 2 or 4 chunks of 64 vectors, the two single ops for other
+    widths), and within the bars of the oracle's two dispatches."""
+    res = host(O.normal(71, (rows, dim)), dtype)
+    x = host(O.normal(72, (rows, dim)), dtype)
+    b = O.normal(73, (dim,), 0.0, 0.02) if with_bias else None
+    g = O.normal(74, (dim,))  # gamma ~ N(0, 1): the residual branch is visible
+    lw, lb = O.normal(75, (dim,), 1.0, 0.02), O.normal(76, (dim,), 0.0, 0.02)
+    bd = None if b is None else dev(b)
+    out, normed = ctx.bias_ls_residual_layernorm(dev(res), dev(x), dev(g), bd, (dev(lw), dev(lb)),
+                                                 eps=1e-6)
+    x1 = ctx.bias_ls_residual(dev(res), dev(x), dev(g), bd)
+    n2 = ctx.layernorm(x1, dev(lw), dev(lb), eps=1e-6)
+    what = f"bias_ls_residual_layernorm {dtype} {rows}x{dim}"
+    assert_bit_exact(back(out), back(x1), what + " out")
+    assert_bit_exact(back(normed), back(n2), what + " normed")
+    want_x1 = O.bias_ls_residual(res, x, b, g)
+    check(back(out), want_x1, what + " out vs oracle")
+    # the LayerNorm stage on the stored out, then the whole chain (where a
+    # 1-ulp difference in out can move a normalised value by more)
+    check(back(normed), O.layernorm(back(out), lw, lb, 1e-6), what + " normed vs oracle")
+    check(back(normed), O.layernorm(want_x1, lw, lb, 1e-6), what + " chain vs oracle", stages=2)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_bias_ls_residual_layernorm_in_place(ctx, dtype):
+    """out may be res (the residual stream updated in place)."""
+    res = host(O.normal(77, (300, 1024)), dtype)
+    x = host(O.normal(78, (300, 1024)), dtype)
+    g = O.normal(79, (1024,))
+    lw, lb = O.normal(80, (1024,), 1.0, 0.02), O.normal(81, (1024,), 0.0, 0.02)
+    t = dev(res)
+    _, normed = ctx.bias_ls_residual_layernorm(t, dev(x), dev(g), None, (dev(lw), dev(lb)),
+                                               eps=1e-6, out=t)
+    x1 = ctx.bias_ls_residual(dev(res), dev(x), dev(g), None)
+    assert_bit_exact(back(t), back(x1), "in place out")
+    assert_bit_exact(back(normed), back(ctx.layernorm(x1, dev(lw), dev(lb), eps=1e-6)),
+                     "in place normed")
+
+
 def test_cast_to_f16(ctx):
     for n in (1 << 16, 1001, 7):
         x = O.normal(71, (n,)) * np.float32(300.0)
@@ -483,6 +529,8 @@ def test_every_op_accepts_empty_inputs(ctx):
     assert ctx.linear_ls_residual(e(0, 1024), w, ones(256), e(0, 256), ones(256)).shape == (0, 256)
     assert ctx.cache_build(e(0, 1024), e(0, 1024)).shape == (0, 2048)
     ln = (ones(1024), ones(1024))
+    o, nrm = ctx.bias_ls_residual_layernorm(e(0, 1024), e(0, 1024), ones(1024), ones(1024), ln)
+    assert o.shape == (0, 1024) and nrm.shape == (0, 1024)
     assert ctx.linear_ln(e(0, 1024), ln, w, ones(256)).shape == (0, 256)
     assert ctx.linear_ln_gelu(e(0, 1024), ln, w, ones(256)).shape == (0, 256)
     wqkv = torch.zeros((3072, 1024), dtype=f16, device=d)
