@@ -1661,6 +1661,7 @@ def main():
         "tokens_per_s": round(bench.rows / (ms * 1e-3), 1),
         "ops_ms_per_step": ops_ms,
         "pass_cold": pass_cold,
+        "ms_per_pass_fused_layernorm": (sequences or {}).get("fused_layernorm", {}).get("ms"),
         "sequences": sequences,
         "ops": per_op,
         "ops_cold": per_op_cold,

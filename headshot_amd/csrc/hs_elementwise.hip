@@ -43,6 +43,9 @@ namespace {
 #ifndef HS_LS_BPC
 #define HS_LS_BPC 32
 #endif
+#ifndef HS_LS_NTS
+#define HS_LS_NTS (HS_NT != 0)  // non-temporal stores of the LayerScale + residual output
+#endif
 #ifndef HS_EW_BPC
 #define HS_EW_BPC 4  // cast and tiled add
 #endif
@@ -219,7 +222,7 @@ __global__ __launch_bounds__(kBlock) void bias_ls_kernel(const T* res, const T* 
                 if constexpr (BIAS) v = storage_round(v + bv[k], T{});
                 fr[k] = ls_affine(fr[k], gv[k], v);  // residual_ls.wesl:28
             }
-            st_stream(out + base + u * stride, pack(fr, T{}));
+            st_stream<HS_LS_NTS>(out + base + u * stride, pack(fr, T{}));
         }
     }
 }

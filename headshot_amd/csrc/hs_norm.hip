@@ -133,6 +133,32 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
     }
 }
 
+#ifndef HS_LSLN_U
+#define HS_LSLN_U 2  // rows per wave and iteration of the fused LayerScale + LayerNorm kernel
+#endif
+// Its cache policy per stream (1: non-temporal): res and x loads, out and
+// normed stores. In the pass, out (the residual stream) is read again two
+// ops later (by LS2, or by the next block's LS1) and res was written so by
+// the op before: cached res loads and out stores keep them in the Infinity
+// Cache for that reader (S=32 pass 14.51 against 14.83 ms with all four
+// streaming, 15.22 ms all cached; the six-op pass took 15.22 ms on the same
+// box).
+#ifndef HS_LSLN_NT_RES
+#define HS_LSLN_NT_RES 0
+#endif
+#ifndef HS_LSLN_NT_X
+#define HS_LSLN_NT_X 1
+#endif
+#ifndef HS_LSLN_NT_OUT
+#define HS_LSLN_NT_OUT 0
+#endif
+#ifndef HS_LSLN_NT_NORMED
+#define HS_LSLN_NT_NORMED 1
+#endif
+#ifndef HS_LSLN_BPC
+#define HS_LSLN_BPC 0  // its workgroups per CU (a persistent grid); 0: one wave per U rows
+#endif
+
 // LayerScale + residual, then the LayerNorm of its output
 // (hs_bias_ls_residual_layernorm): the pre-norm block stores x1 = res +
 // gamma * dt(x + bias) and the next op normalises x1 (model/block.rs:150-153,
@@ -181,8 +207,8 @@ __global__ __launch_bounds__(kBlock) void ls_ln_kernel(const T* res, const T* x,
                 const int64_t off = (r0 + u) * DIM + lane * V;
 #pragma unroll
                 for (int c = 0; c < CHUNKS; c++) {
-                    rr[u][c] = ld_stream(res + off + c * 64 * V);
-                    xr[u][c] = ld_stream(x + off + c * 64 * V);
+                    rr[u][c] = ld_stream<HS_LSLN_NT_RES != 0>(res + off + c * 64 * V);
+                    xr[u][c] = ld_stream<HS_LSLN_NT_X != 0>(x + off + c * 64 * V);
                 }
             }
         }
@@ -203,7 +229,7 @@ __global__ __launch_bounds__(kBlock) void ls_ln_kernel(const T* res, const T* x,
                     fr[k] = ls_affine(fr[k], gr[c][k], v);
                 }
                 const u32x4 o = pack(fr, T{});
-                st_stream(out + off + c * 64 * V, o);
+                st_stream<HS_LSLN_NT_OUT != 0>(out + off + c * 64 * V, o);
                 unpack(o, f[c], T{});  // the stored value, as hs_layernorm reads it
             }
             float mean, inv;
@@ -213,7 +239,7 @@ __global__ __launch_bounds__(kBlock) void ls_ln_kernel(const T* res, const T* x,
                 float y[V];
 #pragma unroll
                 for (int k = 0; k < V; k++) y[k] = ln_affine(f[c][k], mean, inv, wr[c][k], br[c][k]);
-                st_stream(normed + off + c * 64 * V, pack(y, T{}));
+                st_stream<HS_LSLN_NT_NORMED != 0>(normed + off + c * 64 * V, pack(y, T{}));
             }
         }
     }
@@ -380,12 +406,6 @@ hs_status launch(hipStream_t st, const void* x, const float* w, const float* b, 
 // The fused LayerScale + residual + LayerNorm launch for row widths of 1,
 // 2 or 4 chunks of 64 16-byte vectors with aligned buffers; false if the
 // shape needs the two single ops.
-#ifndef HS_LSLN_U
-#define HS_LSLN_U 2  // rows per wave and iteration of the fused LayerScale + LayerNorm kernel
-#endif
-#ifndef HS_LSLN_BPC
-#define HS_LSLN_BPC 0  // its workgroups per CU (a persistent grid); 0: one wave per U rows
-#endif
 
 template <typename T>
 bool launch_ls_ln(hipStream_t st, const void* res, const void* x, const float* bias,
