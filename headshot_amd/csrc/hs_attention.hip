@@ -504,6 +504,50 @@ __global__ __launch_bounds__(256) void merge_vec_kernel(const T* __restrict__ x,
     }
 }
 
+// One wave per kMergeTok consecutive tokens: a token's output row is H*D
+// contiguous elements, NV 16-byte vectors per lane (lane l holds vectors l,
+// l + 64, ...: head j / dv, chunk j % dv of vector j). The token's frame
+// and position are wave-uniform; the per-lane head and chunk offsets are
+// computed once. All kMergeTok * NV loads are in flight before the first
+// store, and every store instruction writes 1 KiB contiguous.
+constexpr int kMergeTok = 2;
+
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void merge_tok_kernel(const T* __restrict__ x, T* __restrict__ out,
+                                                        int rows, int heads, int t, int d) {
+    constexpr int V = Vec<T>::N;
+    const int lane = lane_id();
+    const int dv = d / V;
+    const int hv = heads * dv;  // = 64 * NV
+    const int r0 = (static_cast<int>(blockIdx.x) * 4 + wave_in_block()) * kMergeTok;
+    if (r0 >= rows) return;  // wave-uniform; no barriers
+    int64_t off[NV];  // per-lane element offset within a frame for token 0
+#pragma unroll
+    for (int n = 0; n < NV; n++) {
+        const int j = lane + 64 * n;
+        const int h = j / dv;
+        off[n] = static_cast<int64_t>(h) * t * d + static_cast<int64_t>(j - h * dv) * V;
+    }
+    u32x4 v[kMergeTok][NV];
+#pragma unroll
+    for (int k = 0; k < kMergeTok; k++) {
+        const int r = r0 + k;
+        if (r >= rows) break;
+        const int s = r / t, ti = r - s * t;
+        const T* src = x + (static_cast<int64_t>(s) * heads * t + ti) * d;
+#pragma unroll
+        for (int n = 0; n < NV; n++) v[k][n] = ld_stream(src + off[n]);
+    }
+#pragma unroll
+    for (int k = 0; k < kMergeTok; k++) {
+        const int r = r0 + k;
+        if (r >= rows) break;
+        T* dst = out + static_cast<int64_t>(r) * hv * V;
+#pragma unroll
+        for (int n = 0; n < NV; n++) st_stream(dst + (lane + 64 * n) * V, v[k][n]);
+    }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void merge_scalar_kernel(const T* __restrict__ x, T* __restrict__ out,
                                                            int64_t total, int heads, int t, int d) {
@@ -633,6 +677,30 @@ extern "C" hs_status hs_attn_merge(hs_stream_t stream, hs_dtype dt, const void* 
     if (overlaps(out, bytes, x, bytes)) return fail(HS_EINVAL, "attn_merge: out overlaps x");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int per = dt == HS_F16 ? 8 : 4;
+    const int64_t rows = static_cast<int64_t>(s) * t;
+    const int64_t hv = d % per == 0 ? static_cast<int64_t>(h) * (d / per) : 0;
+    if (aligned16(x) && aligned16(out) && rows < (int64_t{1} << 30) &&
+        (hv == 64 || hv == 128 || hv == 256)) {
+        const int64_t waves = ceil_div(rows, int64_t{kMergeTok});
+        const dim3 grid(static_cast<uint32_t>(ceil_div(waves, int64_t{4})));
+        const int r = static_cast<int>(rows);
+#define HS_MERGE_LAUNCH(NV)                                                                        \
+    if (dt == HS_F16)                                                                              \
+        merge_tok_kernel<f16, NV><<<grid, dim3(256), 0, st>>>(static_cast<const f16*>(x),          \
+                                                             static_cast<f16*>(out), r, h, t, d);  \
+    else                                                                                           \
+        merge_tok_kernel<float, NV><<<grid, dim3(256), 0, st>>>(static_cast<const float*>(x),      \
+                                                               static_cast<float*>(out), r, h, t, d)
+        if (hv == 64) {
+            HS_MERGE_LAUNCH(1);
+        } else if (hv == 128) {
+            HS_MERGE_LAUNCH(2);
+        } else {
+            HS_MERGE_LAUNCH(4);
+        }
+#undef HS_MERGE_LAUNCH
+        return check_launch("attn_merge");
+    }
     if (d % per == 0 && aligned16(x) && aligned16(out)) {
         const int64_t nvec = total / per;
         const dim3 grid(static_cast<uint32_t>(grid_blocks(nvec)));

@@ -14,8 +14,9 @@
 // sequence and later write them back, 2*N copy_rows calls in the reference.
 // hs_copy_row_blocks moves all N blocks of rows in one launch.
 //
-// All kernels stream 16-byte vectors with non-temporal accesses; other
-// shapes and alignments take scalar loops.
+// All kernels move 16-byte vectors (the cache build reads through the
+// caches and streams its output; the copies stream both); other shapes and
+// alignments take scalar loops.
 #include "hs_common.hpp"
 
 namespace hs {
@@ -23,7 +24,7 @@ namespace {
 
 constexpr int kBlock = 256;
 #ifndef HS_CACHE_NTL
-#define HS_CACHE_NTL 1  // non-temporal loads of the cache build's inputs
+#define HS_CACHE_NTL 0  // non-temporal loads of the cache build's inputs
 #endif
 #ifndef HS_CACHE_NTS
 #define HS_CACHE_NTS 1  // non-temporal stores of its f32 output
@@ -64,7 +65,10 @@ __device__ __forceinline__ void copy_chunk(const TI* src, TO* dst) {
 }
 
 #ifndef HS_CACHE_ROWS
-#define HS_CACHE_ROWS 2  // rows per workgroup and iteration
+#define HS_CACHE_ROWS 1  // rows per workgroup and iteration
+#endif
+#ifndef HS_CACHE_DESC
+#define HS_CACHE_DESC 1  // 1: workgroups take the rows from the last to the first
 #endif
 
 // Workgroups stride over rows, R rows per iteration (rows b, b + step, ...,
@@ -83,8 +87,9 @@ __global__ __launch_bounds__(kBlock) void concat_vec_kernel(const TI* __restrict
             const bool left = k < cc1;
 #pragma unroll
             for (int i = 0; i < R; i++) {
-                const int64_t r = r0 + i * step;
-                if (r >= rows) break;
+                const int64_t ri = r0 + i * step;
+                if (ri >= rows) break;
+                const int64_t r = HS_CACHE_DESC ? rows - 1 - ri : ri;
                 const TI* src = left ? a + (r * cc1 + k) * 8 : b + (r * cc2 + (k - cc1)) * 8;
                 copy_chunk(src, out + (r * cc + k) * 8);
             }
@@ -132,10 +137,17 @@ hs_status launch_concat(hipStream_t st, const void* a, const void* b, void* out,
     auto* O = static_cast<TO*>(out);
     const bool vec = c1 % 8 == 0 && c2 % 8 == 0 && aligned16(a) && aligned16(b) && aligned16(out);
     if (vec) {
-        // Two rows per workgroup, all in one round: at 43,968 rows of 1024 +
-        // 1024 f16 -> f32 this measured 109 us (62% of peak) against 111-127 us
-        // for persistent grids of 8-128 workgroups per CU and 127 us for one
-        // row per workgroup.
+        // One row per workgroup, all in one round, the last row first, the
+        // inputs read through the caches and the f32 output streamed. At
+        // 43,968 rows of 1024 + 1024 f16 -> f32 (540 MB) this measured 94.5
+        // us back to back (71% of peak, at its f16 -> f32 widening probe)
+        // and 82.9 us behind a cache flush (81%), against 106.6 / 108.6 us
+        // for two rows per workgroup with streaming loads, 111-127 us for
+        // persistent grids. In the trunk the block output it reads is read
+        // next by the following block's LayerNorm, from the first row on:
+        // walking the rows backwards leaves the first rows the most recently
+        // cached (LayerScale write, this build, LayerNorm: 175.6 against
+        // 179-183 us for the ascending orders with streaming loads).
         constexpr int R = HS_CACHE_ROWS;
         const int64_t want = ceil_div(rows, int64_t{R}), cap = int64_t{1} << 22;
         const int64_t blocks = want < cap ? want : cap;

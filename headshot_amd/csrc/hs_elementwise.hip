@@ -253,20 +253,33 @@ __global__ __launch_bounds__(kBlock) void bias_ls_scalar_kernel(const T* res, co
     }
 }
 
+// f32 -> f16 in a one-shot grid: each wave takes kCastU * 64 consecutive
+// 4-float vectors, lane l the vectors l, l + 64, ..., so every load
+// instruction reads 1 KiB and every store writes 512 contiguous bytes, all
+// kCastU loads in flight before the first store. Elements past the last
+// whole vector (total % 4) are cast by the first lanes of workgroup 0.
+constexpr int kCastU = 4;
+
 __global__ __launch_bounds__(kBlock) void cast_f32_f16_kernel(const float* x, f16* out, int64_t total) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * 8;
-    const int64_t nvec = total / 8 * 8;
-    for (int64_t i = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * 8; i < nvec;
-         i += stride) {
-        float f[8], g[4];
-        unpack(ld_stream(x + i), g, float{});
-        f[0] = g[0], f[1] = g[1], f[2] = g[2], f[3] = g[3];
-        unpack(ld_stream(x + i + 4), g, float{});
-        f[4] = g[0], f[5] = g[1], f[6] = g[2], f[7] = g[3];
-        st_stream(out + i, pack(f, f16{}));
+    const int64_t n4 = total / 4;
+    const int64_t base =
+        (static_cast<int64_t>(blockIdx.x) * kBlock + (threadIdx.x & ~63)) * kCastU + (threadIdx.x & 63);
+    u32x4 r[kCastU];
+#pragma unroll
+    for (int u = 0; u < kCastU; u++)
+        if (base + u * 64 < n4) r[u] = ld_stream(x + (base + u * 64) * 4);
+#pragma unroll
+    for (int u = 0; u < kCastU; u++) {
+        if (base + u * 64 >= n4) break;
+        float f[4];
+        unpack(r[u], f, float{});
+        u32x2 v;
+        v[0] = h22u(f16x2{static_cast<f16>(f[0]), static_cast<f16>(f[1])});
+        v[1] = h22u(f16x2{static_cast<f16>(f[2]), static_cast<f16>(f[3])});
+        st_stream_as(reinterpret_cast<u32x2*>(out + (base + u * 64) * 4), v);
     }
-    if (blockIdx.x == 0 && threadIdx.x < total - nvec)
-        out[nvec + threadIdx.x] = static_cast<f16>(x[nvec + threadIdx.x]);
+    if (blockIdx.x == 0 && threadIdx.x < total - n4 * 4)
+        out[n4 * 4 + threadIdx.x] = static_cast<f16>(x[n4 * 4 + threadIdx.x]);
 }
 
 __global__ __launch_bounds__(kBlock) void cast_f32_f16_scalar_kernel(const float* x, f16* out,
@@ -283,35 +296,39 @@ __global__ __launch_bounds__(kBlock) void tiled_add_kernel(const float* x, const
         out[i] = x[i] + table[i % block];
 }
 
-// Table-stationary tiled add: thread j owns table vector j (4 floats, kept
-// in registers) and walks its total / block repetitions, two 16-byte loads
-// in flight, so the table is read once and no index needs a modulo. Used
-// when the table is a whole number of 16-byte vectors and large enough to
-// fill the GPU (a pos-embed table: P x 1024 floats); other shapes take the
-// flat kernel.
+// Tiled add over a large table in a one-shot 2D grid: workgroup (bx, by)
+// takes table vectors [256 bx, 256 bx + 256) (4 floats each, read once per
+// thread from the cache) and repetitions [kTileReps by, kTileReps by +
+// kTileReps) of them; a thread's kTileReps loads are in flight before its
+// first store, and lanes read and write consecutive vectors. No index needs
+// a division. Used when the table is a whole number of 16-byte vectors and
+// large enough to fill the GPU (a pos-embed table: P x 1024 floats); other
+// shapes take the flat kernel.
+constexpr int kTileReps = 4;
+
 __global__ __launch_bounds__(kBlock) void tiled_add_vec_kernel(const float* x,
                                                                const float* __restrict__ table,
                                                                float* out, int64_t reps,
                                                                int64_t block4) {
     const int64_t j = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
     if (j >= block4) return;  // no barriers below
+    const int64_t r0 = static_cast<int64_t>(blockIdx.y) * kTileReps;
     const float4 t = ld_f32x4(table + 4 * j);
     const int64_t stride = block4 * 4;
-    const float* xp = x + 4 * j;
-    float* op = out + 4 * j;
-    auto add = [&](u32x4 v) {
+    const float* xp = x + r0 * stride + 4 * j;
+    float* op = out + r0 * stride + 4 * j;
+    u32x4 v[kTileReps];
+#pragma unroll
+    for (int r = 0; r < kTileReps; r++)
+        if (r0 + r < reps) v[r] = ld_stream(xp + r * stride);
+#pragma unroll
+    for (int r = 0; r < kTileReps; r++) {
+        if (r0 + r >= reps) break;
         u32x4 o;
-        o[0] = f2u(u2f(v[0]) + t.x), o[1] = f2u(u2f(v[1]) + t.y);
-        o[2] = f2u(u2f(v[2]) + t.z), o[3] = f2u(u2f(v[3]) + t.w);
-        return o;
-    };
-    int64_t r = 0;
-    for (; r + 2 <= reps; r += 2) {
-        const u32x4 a = ld_stream(xp + r * stride), b = ld_stream(xp + (r + 1) * stride);
-        st_stream(op + r * stride, add(a));
-        st_stream(op + (r + 1) * stride, add(b));
+        o[0] = f2u(u2f(v[r][0]) + t.x), o[1] = f2u(u2f(v[r][1]) + t.y);
+        o[2] = f2u(u2f(v[r][2]) + t.z), o[3] = f2u(u2f(v[r][3]) + t.w);
+        st_stream(op + r * stride, o);
     }
-    if (r < reps) st_stream(op + r * stride, add(ld_stream(xp + r * stride)));
 }
 
 int64_t flat_blocks(int64_t items) {
@@ -449,8 +466,11 @@ hs_status hs_cast_f32_to_f16(hs_stream_t stream, const float* x, void* out, int6
     if (overlaps(x, total * 4, out, total * 2))
         return fail(HS_EINVAL, "cast_f32_to_f16: out overlaps x");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (aligned16(x) && aligned16(out))
-        cast_f32_f16_kernel<<<dim3(static_cast<uint32_t>(flat_blocks(ceil_div(total, 8)))), dim3(kBlock), 0, st>>>(
+    int64_t blocks = ceil_div(ceil_div(total / 4, int64_t{kCastU}), int64_t{kBlock});
+    if (blocks < 1) blocks = 1;  // total < 4: workgroup 0 casts the tail
+    // the dispatch packet counts work-items in 32 bits
+    if (aligned16(x) && aligned16(out) && blocks * kBlock < (int64_t{1} << 32))
+        cast_f32_f16_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
             x, static_cast<f16*>(out), total);
     else
         cast_f32_f16_scalar_kernel<<<dim3(static_cast<uint32_t>(flat_blocks(total))), dim3(kBlock), 0, st>>>(
@@ -469,11 +489,13 @@ hs_status hs_tiled_add(hs_stream_t stream, const float* x, const float* table, f
     if (!x || !table || !out) return fail(HS_EINVAL, "tiled_add: null buffer");
     if (bad_alias(x, out, total * 4)) return fail(HS_EINVAL, "tiled_add: out partially overlaps x");
     hipStream_t st = static_cast<hipStream_t>(stream);
-    if (block % 4 == 0 && block / 4 >= 65536 && block / 4 < (int64_t{1} << 31) && aligned16(x) &&
-        aligned16(table) && aligned16(out)) {
+    const int64_t rgroups = ceil_div(total / block, int64_t{kTileReps});
+    if (block % 4 == 0 && block / 4 >= 65536 && block / 4 < (int64_t{1} << 31) && rgroups < 65536 &&
+        aligned16(x) && aligned16(table) && aligned16(out)) {
         const int64_t block4 = block / 4;
-        tiled_add_vec_kernel<<<dim3(static_cast<uint32_t>(ceil_div(block4, kBlock))), dim3(kBlock), 0,
-                               st>>>(x, table, out, total / block, block4);
+        const dim3 grid(static_cast<uint32_t>(ceil_div(block4, int64_t{kBlock})),
+                        static_cast<uint32_t>(rgroups));
+        tiled_add_vec_kernel<<<grid, dim3(kBlock), 0, st>>>(x, table, out, total / block, block4);
         return check_launch("tiled_add");
     }
     tiled_add_kernel<<<dim3(static_cast<uint32_t>(flat_blocks(total))), dim3(kBlock), 0, st>>>(

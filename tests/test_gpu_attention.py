@@ -246,8 +246,11 @@ def test_attention_unsupported_shapes(ctx):
 # ------------------------------------------------------------------ merge
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("s,h,t,d", [(2, 4, 5, 8), (2, 16, 37, 64), (1, 3, 11, 6), (3, 2, 7, 128)])
+@pytest.mark.parametrize("s,h,t,d", [(2, 4, 5, 8), (2, 16, 37, 64), (1, 3, 11, 6), (3, 2, 7, 128),
+                                     (1, 8, 13, 64), (3, 16, 131, 64)])
 def test_attn_merge_exact(ctx, dtype, s, h, t, d):
+    """Covers the token-per-wave kernel at 64, 128 and 256 vectors per token
+    (odd token counts leave a half-filled wave) and the flat kernel."""
     rng = np.random.default_rng(s * 1000 + t)
     x = host(rng.standard_normal((s, h, t, d)), dtype)
     got = back(ctx.attn_merge(dev(x)))

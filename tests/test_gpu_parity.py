@@ -367,7 +367,7 @@ def test_bias_ls_residual_layernorm_in_place(ctx, dtype):
 
 
 def test_cast_to_f16(ctx):
-    for n in (1 << 16, 1001, 7):
+    for n in (1 << 16, 1001, 7, 3, 12293, (1 << 22) + 5):
         x = O.normal(71, (n,)) * np.float32(300.0)
         assert_bit_exact(back(ctx.cast_to_f16(dev(x))), O.cast_to_f16(x), f"cast n={n}")
     edge = np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, -7e4, 6.0e-8, 2.98e-8, 1e-10,
@@ -379,9 +379,10 @@ def test_cast_to_f16(ctx):
 
 def test_tiled_add_table_stationary(ctx):
     """A table of >= 64K 16-byte vectors takes the vector kernel: odd and even
-    repetition counts, and in place."""
+    repetition counts, several groups of four repetitions with a partial
+    last one, and in place."""
     table = O.normal(84, (65536 * 4 + 8,))
-    for reps in (1, 3, 4):
+    for reps in (1, 3, 4, 9):
         x = O.normal(85 + reps, (reps, table.size))
         assert_bit_exact(back(ctx.tiled_add(dev(x), dev(table))), O.tiled_add(x, table),
                          f"tiled_add x{reps}")
