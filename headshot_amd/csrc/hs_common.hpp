@@ -144,6 +144,34 @@ __device__ __forceinline__ u32x4 pack(const float (&f)[4], float) {
     return v;
 }
 
+// Exact-erf GELU, gelu.wesl:18-38: 0.5*v*(1 + erf(v/sqrt(2))) with erf by
+// Abramowitz & Stegun 7.1.26, erf(z) = sign(z)*(1 - P(t)*t*exp(-z^2)),
+// t = 1/(1 + p*|z|). Evaluated in f32 from h = v/2 (exact), with the
+// scale folded into the constants (z = v/sqrt(2) is never formed) and the
+// sign folded into the final multiply-add, since 0.5*v*sign(v) = |h|:
+//   gelu(v) = h + |h| * (1 - P(t)*t*2^(-(h*2k)^2)),
+//   t = 1/(1 + (2p/sqrt(2))*|h|),  k = sqrt(log2(e)/2).
+// 2p/sqrt(2) * |h| and 2k * h equal p/sqrt(2) * |v| and k * v exactly (the
+// factor 2 is exact), so starting from h changes no rounding. 12 VALU
+// operations per element from h, including one v_rcp_f32 and one
+// v_exp_f32 (both ~1 ulp); the folded constants move the result by a few
+// f32 ulps against the shader's operand order, far inside the parity bars.
+constexpr float kGeluAsP = 0.3275911f * 0.70710678118654752f;  // p / sqrt(2)
+constexpr float kGeluExpK = 0.84932180028801904f;               // sqrt(log2(e) / 2)
+
+__device__ __forceinline__ float gelu_half(float h) {
+    const float t = __builtin_amdgcn_rcpf(fmaf(2.0f * kGeluAsP, fabsf(h), 1.0f));
+    float p = fmaf(1.061405429f, t, -1.453152027f);
+    p = fmaf(p, t, 1.421413741f);
+    p = fmaf(p, t, -0.284496736f);
+    p = fmaf(p, t, 0.254829592f);
+    p = p * t;
+    const float w = h * (2.0f * kGeluExpK);
+    const float e = __builtin_amdgcn_exp2f(-(w * w));  // exp(-v^2/2)
+    return fmaf(fabsf(h), fmaf(-p, e, 1.0f), h);
+}
+__device__ __forceinline__ float gelu_f(float v) { return gelu_half(0.5f * v); }
+
 // v as a materialised f32 value. The reference computes in f32 and then
 // stores its storage type: two roundings. Left alone, the compiler may fold
 // a multiply-add and the following f16 conversion into one v_fma_mix_f16

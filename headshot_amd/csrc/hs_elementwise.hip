@@ -53,32 +53,6 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int kBlocksPerCu = HS_EW_BPC;
 
-// Exact-erf GELU, gelu.wesl:18-38: 0.5*v*(1 + erf(v/sqrt(2))) with erf by
-// Abramowitz & Stegun 7.1.26, erf(z) = sign(z)*(1 - P(t)*t*exp(-z^2)),
-// t = 1/(1 + p*|z|). Evaluated in f32 with the scale folded into the
-// constants (z = v/sqrt(2) is never formed) and the sign folded into the
-// final multiply-add, since 0.5*v*sign(v) = |0.5*v|:
-//   gelu(v) = h + |h| * (1 - P(t)*t*2^(-(v*k)^2)),   h = v/2,
-//   t = 1/(1 + (p/sqrt(2))*|v|),  k = sqrt(log2(e)/2).
-// That is 13 VALU operations per element including one v_rcp_f32 and one
-// v_exp_f32 (both ~1 ulp); the folded constants move the result by a few
-// f32 ulps against the shader's operand order, far inside the parity bars.
-constexpr float kAsP = 0.3275911f * 0.70710678118654752f;  // p / sqrt(2)
-constexpr float kExpK = 0.84932180028801904f;               // sqrt(log2(e) / 2)
-
-__device__ __forceinline__ float gelu_f(float v) {
-    const float h = 0.5f * v;
-    const float t = __builtin_amdgcn_rcpf(fmaf(kAsP, fabsf(v), 1.0f));
-    float p = fmaf(1.061405429f, t, -1.453152027f);
-    p = fmaf(p, t, 1.421413741f);
-    p = fmaf(p, t, -0.284496736f);
-    p = fmaf(p, t, 0.254829592f);
-    p = p * t;
-    const float w = v * kExpK;
-    const float e = __builtin_amdgcn_exp2f(-(w * w));  // exp(-v^2/2)
-    return fmaf(fabsf(h), fmaf(-p, e, 1.0f), h);
-}
-
 // Grid size (in blocks) for a column-stationary launch: the stride
 // blocks*kBlock*V must be a multiple of cols. Returns 0 if no such grid of
 // useful size exists.
@@ -105,6 +79,14 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
     constexpr int V = Vec<T>::N;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * kBlock * V;
     const int64_t e0 = (static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x) * V;
+    // The fc1 bias joins in f32; the reference's GEMM epilogue would have
+    // stored x + bias as f16 first (one extra rounding this fused op leaves
+    // out). For f16 input the bias is kept halved: h = x * 0.5 + b / 2 is one
+    // mixed-precision FMA straight from the f16 half (no conversion, no
+    // separate add) and equals 0.5f * (float(x) + b) bit for bit (halving is
+    // exact, and x + b is never subnormal: a nonzero f16 x is at least 2^-24,
+    // so an f32 b cancels it to 0 or to at least 2^-47).
+    constexpr bool kHalfBias = BIAS && sizeof(T) == 2;
     float bv[V];
     if constexpr (BIAS) {
         const int c0 = static_cast<int>(e0 % cols);
@@ -112,6 +94,10 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
         for (int k = 0; k < V; k += 4) {
             float4 b4 = ld_f32x4(bias + c0 + k);
             bv[k] = b4.x, bv[k + 1] = b4.y, bv[k + 2] = b4.z, bv[k + 3] = b4.w;
+        }
+        if constexpr (kHalfBias) {
+#pragma unroll
+            for (int k = 0; k < V; k++) bv[k] *= 0.5f;
         }
     }
     auto load = [&](u32x4 (&raw)[U], int64_t base) {
@@ -127,12 +113,12 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
             unpack(raw[u], f, T{});
 #pragma unroll
             for (int k = 0; k < V; k++) {
-                // The fc1 bias joins in f32; the reference's GEMM epilogue
-                // would have stored x + bias as f16 first (one extra
-                // rounding this fused op leaves out).
-                float v = f[k];
-                if constexpr (BIAS) v = v + bv[k];
-                f[k] = gelu_f(v);
+                if constexpr (kHalfBias)
+                    f[k] = gelu_half(fmaf(f[k], 0.5f, bv[k]));
+                else if constexpr (BIAS)
+                    f[k] = gelu_f(f[k] + bv[k]);
+                else
+                    f[k] = gelu_f(f[k]);
             }
             st_stream<HS_GELU_NTS>(out + base + u * stride, pack(f, T{}));
         }

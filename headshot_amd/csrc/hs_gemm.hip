@@ -69,23 +69,6 @@ struct LnArgs {
     const float* ln_b;
 };
 
-// Exact-erf GELU in the A&S 7.1.26 form used by the elementwise GELU kernel
-// (gelu.wesl:18-38 with the 1/sqrt(2) folded into the constants).
-__device__ __forceinline__ float gelu_erf(float v) {
-    constexpr float kAsP = 0.3275911f * 0.70710678118654752f;
-    constexpr float kExpK = 0.84932180028801904f;
-    const float h = 0.5f * v;
-    const float t = __builtin_amdgcn_rcpf(fmaf(kAsP, fabsf(v), 1.0f));
-    float p = fmaf(1.061405429f, t, -1.453152027f);
-    p = fmaf(p, t, 1.421413741f);
-    p = fmaf(p, t, -0.284496736f);
-    p = fmaf(p, t, 0.254829592f);
-    p = p * t;
-    const float w = v * kExpK;
-    const float e = __builtin_amdgcn_exp2f(-(w * w));
-    return fmaf(fabsf(h), fmaf(-p, e, 1.0f), h);
-}
-
 // ---------------------------------------------------------------------------
 // matrix-core path
 
@@ -601,7 +584,7 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
                 v[2] = acc[a][b][4 * r4 + 2] + bv.z, v[3] = acc[a][b][4 * r4 + 3] + bv.w;
                 if constexpr (EPI == EPI_GELU) {
 #pragma unroll
-                    for (int e = 0; e < 4; e++) v[e] = gelu_erf(v[e]);
+                    for (int e = 0; e < 4; e++) v[e] = gelu_f(v[e]);
                 }
                 u32x2 o;
                 o[0] = pk_f16(v[0], v[1]), o[1] = pk_f16(v[2], v[3]);
@@ -698,7 +681,7 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(
             const int64_t n = n0 + tc * 4 + j;
             if (n >= N) continue;
             float v = acc[i][j] + (bias ? bias[n] : 0.0f);
-            if constexpr (EPI == EPI_GELU) v = gelu_erf(v);
+            if constexpr (EPI == EPI_GELU) v = gelu_f(v);
             if constexpr (EPI == EPI_LS)
                 v = static_cast<float>(res[m * N + n]) + gamma[n] * storage_round(v, T{});
             out[m * N + n] = static_cast<T>(v);
