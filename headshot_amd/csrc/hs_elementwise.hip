@@ -290,7 +290,10 @@ __global__ __launch_bounds__(kBlock) void tiled_add_kernel(const float* x, const
 // a division. Used when the table is a whole number of 16-byte vectors and
 // large enough to fill the GPU (a pos-embed table: P x 1024 floats); other
 // shapes take the flat kernel.
-constexpr int kTileReps = 4;
+#ifndef HS_TILE_REPS
+#define HS_TILE_REPS 4
+#endif
+constexpr int kTileReps = HS_TILE_REPS;
 
 __global__ __launch_bounds__(kBlock) void tiled_add_vec_kernel(const float* x,
                                                                const float* __restrict__ table,

@@ -42,7 +42,8 @@
 //
 // rope_apply on head-major tensors with head_dim 64 runs the same lane
 // layout in place (rope_vec_kernel: a wave takes a few tokens of one frame
-// across all heads, so each token's table row is read once).
+// across a group of heads, so each token's table row is read once per
+// group).
 //
 // Generic path (any head_dim, either input layout): one wave per head vector,
 // lanes strided over the vector; used for shapes the fast paths do not
@@ -60,9 +61,10 @@ namespace {
 #define HS_QK_BPC 8  // resident workgroups per CU (generic path)
 #endif
 #ifndef HS_ROPE_HB
-// heads loaded together by the in-place rope_apply kernel: 16 (a frame
-// block's all) took S=32 from 33.7 to 32.8 us against 8; 4 and 2 were slower
-#define HS_ROPE_HB 16
+// heads per wave of the in-place rope_apply kernel, all loaded together:
+// at S=32 (16 heads) 8 took 30.5 us warm / 33.2 cold against 31.9 / 35.1
+// for 16 (one wave per token tile), 31.6 / 33.2 for 4 and 34.2 / 36.1 for 2
+#define HS_ROPE_HB 8
 #endif
 // Sequence length from which a wave takes one load chunk of each row
 // instead of the whole row (see above).
@@ -255,10 +257,11 @@ __global__ __launch_bounds__(kBlock) void qkn_row_kernel(
 // In-place rotate-half RoPE on head-major (S, H, T, 64) vectors (the
 // rope_apply surface op), in the row kernel's lane layout: a vector in a
 // group of G lanes, each channel's RoPE partner in the mirror lane. A wave
-// takes TG = 64 / G consecutive tokens of one frame and walks all heads, HB
-// at a time: each load instruction covers one head's TG vectors (contiguous
-// in head-major order), and each lane reads its token's sin/cos row once
-// for all heads. Prefix tokens are neither read nor written.
+// takes TG = 64 / G consecutive tokens of one frame in a group of HB heads,
+// all HB loads in flight together: each load instruction covers one head's
+// TG vectors (contiguous in head-major order), and each lane reads its
+// token's sin/cos row once for the group. Prefix tokens are neither read
+// nor written.
 template <typename T, int HB>
 __global__ __launch_bounds__(kBlock) void rope_vec_kernel(T* x, const float* __restrict__ sin_tab,
                                                           const float* __restrict__ cos_tab,
@@ -271,10 +274,16 @@ __global__ __launch_bounds__(kBlock) void rope_vec_kernel(T* x, const float* __r
     const int ch = upper ? 32 + (G - 1 - piece) * V : piece * V;
     const float none[V] = {};
     const int tiles = static_cast<int>(ceil_div(seq, TG));
+    // unit = (frame, head group of HB, token tile), token tiles fastest
+    const int groups = static_cast<int>(ceil_div(heads, HB));
+    const int64_t per_frame = static_cast<int64_t>(groups) * tiles;
     const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWavesPerBlock + wave_in_block();
-    if (unit >= static_cast<int64_t>(nseq) * tiles) return;  // wave-uniform; no barriers
-    const int s = static_cast<int>(unit / tiles);
-    const int t = static_cast<int>(unit - static_cast<int64_t>(s) * tiles) * TG + lane / G;
+    if (unit >= static_cast<int64_t>(nseq) * per_frame) return;  // wave-uniform; no barriers
+    const int s = static_cast<int>(unit / per_frame);
+    const int rem = static_cast<int>(unit - static_cast<int64_t>(s) * per_frame);
+    const int grp = rem / tiles;
+    const int t = (rem - grp * tiles) * TG + lane / G;
+    const int hend = grp * HB + HB < heads ? grp * HB + HB : heads;
     // a group's lanes share their token, so `live` is uniform across the
     // group that the mirror permute reads
     const bool live = t < seq && t >= prefix;
@@ -293,17 +302,18 @@ __global__ __launch_bounds__(kBlock) void rope_vec_kernel(T* x, const float* __r
     }
     T* base = x + (static_cast<int64_t>(s) * heads * seq + t) * D + ch;
     const int64_t hstride = static_cast<int64_t>(seq) * D;
-    for (int h0 = 0; h0 < heads; h0 += HB) {
+    {
+        const int h0 = grp * HB;
         u32x4 raw[HB];
 #pragma unroll
         for (int j = 0; j < HB; j++) {
             raw[j] = u32x4{0, 0, 0, 0};
-            if (live && h0 + j < heads) raw[j] = ld_stream(base + (h0 + j) * hstride);
+            if (live && h0 + j < hend) raw[j] = ld_stream(base + (h0 + j) * hstride);
         }
-        if (!live) continue;
+        if (!live) return;
 #pragma unroll
         for (int j = 0; j < HB; j++) {
-            if (h0 + j >= heads) break;  // wave-uniform
+            if (h0 + j >= hend) break;  // wave-uniform
             float f[V];
             unpack(raw[j], f, T{});
             qk_norm_rope_vec<T, G, false>(f, none, none, 0.0f, true, cs, sn);
@@ -577,11 +587,11 @@ hs_status hs_rope_apply(hs_stream_t stream, hs_dtype dt, void* x, const float* s
     if (!x || !sin_tab || !cos_tab) return fail(HS_EINVAL, "rope_apply: null buffer");
     hipStream_t st = static_cast<hipStream_t>(stream);
     const int tg = dt == HS_F16 ? 8 : 4;  // tokens per load instruction
-    const int64_t units = static_cast<int64_t>(s) * ceil_div(t, tg);
+    constexpr int HB = HS_ROPE_HB;
+    const int64_t units = static_cast<int64_t>(s) * ceil_div(h, HB) * ceil_div(t, tg);
     const int64_t blocks = ceil_div(units, int64_t{kWavesPerBlock});
     if (d == 64 && aligned16(x) && aligned16(sin_tab) && aligned16(cos_tab) &&
         blocks * kBlock < (int64_t{1} << 32)) {
-        constexpr int HB = HS_ROPE_HB;
         if (dt == HS_F16)
             rope_vec_kernel<f16, HB><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
                 static_cast<f16*>(x), sin_tab, cos_tab, s, h, t, prefix);
