@@ -19,17 +19,24 @@ namespace {
 
 // Launch shape (overridable at build time for tuning sweeps).
 // U: 16-byte vectors per input stream per thread per iteration; BPC:
-// workgroups launched per CU. Chosen by timing the whole aggregator pass,
-// not the op alone. Both ops run fastest with one vector per stream per
-// thread and many workgroups (GELU 64 per CU, ~5 vectors per thread at
-// S=32; LayerScale 32 per CU, ~3); GELU must keep non-temporal
-// stores, because with plain stores its output occupies the cache and the
-// LayerNorm after it slows by a third.
+// workgroups launched per CU; ITERS (GELU): a grid sized so that each
+// thread visits that many rows instead. Chosen by timing the whole
+// aggregator pass, not the op alone. Both ops run fastest with one vector
+// per stream per thread and many workgroups: GELU with two visits per
+// thread (S=32: 117.3 us against 120.8 for 64 workgroups per CU, ~5
+// visits, and 118.0-119.7 for 96-176 workgroups per CU or three or four
+// visits; 130 for 256 per CU, 157 for one visit in a one-shot grid),
+// LayerScale with 32 workgroups per CU (~3 visits). GELU must keep
+// non-temporal stores, because with plain stores its output occupies the
+// cache and the LayerNorm after it slows by a third.
 #ifndef HS_GELU_U
 #define HS_GELU_U 1
 #endif
 #ifndef HS_GELU_BPC
 #define HS_GELU_BPC 64
+#endif
+#ifndef HS_GELU_ITERS
+#define HS_GELU_ITERS 2
 #endif
 #ifndef HS_GELU_NTL
 #define HS_GELU_NTL (HS_NT != 0)  // non-temporal loads of the fc1 output
@@ -42,6 +49,9 @@ namespace {
 #endif
 #ifndef HS_LS_BPC
 #define HS_LS_BPC 32
+#endif
+#ifndef HS_LS_ITERS
+#define HS_LS_ITERS 0
 #endif
 #ifndef HS_LS_NTS
 #define HS_LS_NTS (HS_NT != 0)  // non-temporal stores of the LayerScale + residual output
@@ -151,11 +161,16 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_tile_kernel(const T* x,
 #pragma unroll
     for (int r = 0; r < R; r++)
         if (r0 + r < rows) raw[r] = ld_stream<HS_GELU_NTL>(x + (r0 + r) * cols + c0);
+    constexpr bool kHalfBias = sizeof(T) == 2;  // as in bias_gelu_kernel
     float bv[V];
 #pragma unroll
     for (int k = 0; k < V; k += 4) {
         const float4 b4 = bias ? ld_f32x4(bias + c0 + k) : float4{0.0f, 0.0f, 0.0f, 0.0f};
         bv[k] = b4.x, bv[k + 1] = b4.y, bv[k + 2] = b4.z, bv[k + 3] = b4.w;
+    }
+    if constexpr (kHalfBias) {
+#pragma unroll
+        for (int k = 0; k < V; k++) bv[k] *= 0.5f;
     }
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -163,7 +178,8 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_tile_kernel(const T* x,
         float f[V];
         unpack(raw[r], f, T{});
 #pragma unroll
-        for (int k = 0; k < V; k++) f[k] = gelu_f(f[k] + bv[k]);
+        for (int k = 0; k < V; k++)
+            f[k] = kHalfBias ? gelu_half(fmaf(f[k], 0.5f, bv[k])) : gelu_f(f[k] + bv[k]);
         st_stream<HS_GELU_NTS>(out + (r0 + r) * cols + c0, pack(f, T{}));
     }
 }
@@ -345,7 +361,13 @@ hs_status launch_gelu(hipStream_t st, const void* x, const float* bias, void* ou
             }
         }
     }
-    const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U, HS_GELU_BPC) : 0;
+    // HS_GELU_ITERS > 0: a grid in which each thread visits that many rows
+    // (the last visit partial), whatever the tensor's size; else a grid of
+    // HS_GELU_BPC workgroups per CU.
+    const int64_t blocks =
+        !vec_ok ? 0
+        : HS_GELU_ITERS > 0 ? column_stationary_blocks(total, cols, V, U * HS_GELU_ITERS, 1 << 16)
+                            : column_stationary_blocks(total, cols, V, U, HS_GELU_BPC);
     if (blocks > 0) {
         if (bias)
             bias_gelu_kernel<T, true, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
@@ -368,7 +390,10 @@ hs_status launch_ls(hipStream_t st, const void* res, const void* x, const float*
     const int64_t total = rows * cols;
     const bool vec_ok = cols % V == 0 && aligned16(res) && aligned16(x) && aligned16(out) &&
                         aligned16(gamma) && (!bias || aligned16(bias));
-    const int64_t blocks = vec_ok ? column_stationary_blocks(total, cols, V, U, HS_LS_BPC) : 0;
+    const int64_t blocks =
+        !vec_ok ? 0
+        : HS_LS_ITERS > 0 ? column_stationary_blocks(total, cols, V, U * HS_LS_ITERS, 1 << 16)
+                          : column_stationary_blocks(total, cols, V, U, HS_LS_BPC);
     if (blocks > 0) {
         if (bias)
             bias_ls_kernel<T, true, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
