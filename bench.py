@@ -467,13 +467,14 @@ def probe_times(lib, probe: str, args, sets, flush, iters: int = 20):
         for bufs in sets:
             launch(shape, ptrs(bufs))
         torch.cuda.synchronize()
-        a, b = KernelEvent(), KernelEvent()
-        a.record()
-        for i in range(iters):
+        ev = [(KernelEvent(), KernelEvent()) for _ in range(iters)]
+        torch.cuda._sleep(20_000_000)  # the host enqueues ahead
+        for i, (a, b) in enumerate(ev):
+            a.record()
             launch(shape, ptrs(sets[i % len(sets)]))
-        b.record()
+            b.record()
         torch.cuda.synchronize()
-        warm[policy] = a.elapsed_time(b) / iters * 1e3
+        warm[policy] = sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3
     cold = []
     for shape in (s for s in CEILING_SHAPES.values() if not s & 1):  # streaming stores only
         ev = [(KernelEvent(), KernelEvent()) for _ in range(iters)]
@@ -511,11 +512,11 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
     """Each op beside a data-movement probe with its byte mix and access
     pattern (bench_ceiling.hip).
 
-    Warm: ``iters`` back-to-back launches that rotate over as many buffer
-    sets as make ROTATE_BYTES, so no launch finds its inputs in a cache and
-    each pays for its own write-back (streaming and cached loads/stores, each
-    with four and with one 16-byte vector per lane; the fastest is the
-    ceiling). Compared with the op's rate inside the pass. Cold: the per-op
+    Warm: ``iters`` back-to-back launches, an event pair around each as
+    for the ops, that rotate over as many buffer sets as make ROTATE_BYTES,
+    so no launch finds its inputs in a cache and each pays for its own
+    write-back (streaming and cached loads/stores, each with four and with
+    one 16-byte vector per lane; the fastest is the ceiling). Compared with the op's rate inside the pass. Cold: the per-op
     cold method (cache flush, then a HIP event pair around one launch) with
     streaming stores only, the faster launch shape: cached stores leave their
     write-back for after the end event, so their cold time undercounts.
@@ -666,18 +667,22 @@ def cold_us(fn, flush, iters: int) -> float:
 
 
 def warm_us(fn, iters: int) -> float:
-    """Mean kernel time (us) of ``iters`` back-to-back launches of ``fn``."""
+    """Mean kernel time (us) of ``iters`` back-to-back launches of ``fn``,
+    one KernelEvent pair around each (as the per-op pass timing), so the
+    gaps between launches are not counted; the host enqueues ahead behind a
+    GPU busy-wait."""
     import torch
 
     fn()
     torch.cuda.synchronize()
-    a, b = KernelEvent(), KernelEvent()
-    a.record()
-    for _ in range(iters):
+    ev = [(KernelEvent(), KernelEvent()) for _ in range(iters)]
+    torch.cuda._sleep(20_000_000)  # ~8 ms head start
+    for a, b in ev:
+        a.record()
         fn()
-    b.record()
+        b.record()
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / iters * 1e3
+    return sum(a.elapsed_time(b) for a, b in ev) / iters * 1e3
 
 
 def cache_times(ctx, frames: int, iters: int, flush) -> dict:
@@ -1674,8 +1679,10 @@ def main():
     if args.attention_iters > 0:
         line["attention"] = attention_times(ctx, args.frames, args.attention_iters)
         flush = cache_flusher(ctx.device)
-        line["cache_build"] = cache_times(ctx, args.frames, args.attention_iters, flush)
-        line["surface"] = surface_times(ctx, args.frames, args.attention_iters, flush)
+        # the HBM legs run ~0.1 ms a launch: at least 20 timed launches each
+        hbm_iters = max(20, args.attention_iters)
+        line["cache_build"] = cache_times(ctx, args.frames, hbm_iters, flush)
+        line["surface"] = surface_times(ctx, args.frames, hbm_iters, flush)
         del flush
         line["linear"] = gemm_times(ctx, args.frames, args.attention_iters)
         line["block"] = block_times(ctx, args.frames, max(1, args.attention_iters // 2))
