@@ -130,6 +130,12 @@ def parse():
     ap.add_argument("--summarize-counters", metavar="CSV", nargs="+",
                     help="print derived shader-counter ratios (matrix-core and LDS use) per "
                          "kernel from rocprofv3 --pmc counter_collection CSVs of this benchmark")
+    ap.add_argument("--counter-pair", action="store_true",
+                    help="launch bias + GELU at this S (rows x 4096 f16) and its copy probe 8 "
+                         "times each over rotating buffers, then exit (for rocprofv3 --pmc)")
+    ap.add_argument("--summarize-pair", metavar="CSV", nargs="+",
+                    help="print each counter's mean per dispatch for bias + GELU and its copy "
+                         "probe, and their ratio, from --counter-pair counter_collection CSVs")
     return ap.parse_args()
 
 
@@ -1545,6 +1551,82 @@ def summarize(args) -> None:
     print("\n".join(out))
 
 
+COUNTER_PAIR = {"bias_gelu_kernel": "bias + GELU", "copy_kernel": "copy probe"}
+
+
+def counter_pair(frames: int) -> None:
+    """bias + GELU on (frames * 1374, 4096) f16 with its fc1 bias, then the
+    copy probe (one 16-byte vector per lane, streaming: the fastest shape)
+    on the same bytes, each launched 8 times over 3 rotating buffer sets
+    (more than the Infinity Cache holds): the workload of the op-against-
+    probe counter comparison (rocprofv3 --pmc, one counter set per run)."""
+    import torch
+
+    from headshot_amd.context import HipContext
+
+    ctx = HipContext("cuda:0")
+    lib = load_ceiling()
+    rows = frames * (GRID[0] * GRID[1] + PREFIX)
+    g = torch.Generator(device="cpu").manual_seed(13)
+    sets = [(torch.randn((rows, HIDDEN), generator=g).half().to(ctx.device),
+             torch.empty((rows, HIDDEN), device=ctx.device, dtype=torch.float16))
+            for _ in range(3)]
+    bias = (torch.randn(HIDDEN, generator=g) * 0.02).to(ctx.device)
+    stream = torch.cuda.current_stream().cuda_stream
+    n16 = rows * HIDDEN * 2 // 16
+    for i in range(8):
+        x, o = sets[i % 3]
+        ctx.bias_gelu(x, bias, out=o)
+    torch.cuda.synchronize()
+    for i in range(8):
+        x, o = sets[i % 3]
+        rc = lib.hsc_run(KINDS["copy"], CEILING_SHAPES["streaming x1"], x.data_ptr(), None,
+                         o.data_ptr(), None, n16, 0, 0, stream)
+        if rc != 0:
+            raise RuntimeError(f"hsc_run(copy) returned {rc}")
+    torch.cuda.synchronize()
+    print(json.dumps({"counter_pair": "done", "rows": rows, "cols": HIDDEN}), flush=True)
+
+
+def summarize_pair(paths) -> None:
+    """Mean per dispatch of every counter in the --counter-pair CSVs for the
+    op and the probe, their ratio, and the kernel-trace duration; derived:
+    memory instructions in flight per busy cycle (SQ_INST_LEVEL_VMEM /
+    SQ_BUSY_CYCLES) and wave cycles per wave."""
+    import csv
+    import statistics as st
+    from collections import defaultdict
+
+    vals = defaultdict(lambda: defaultdict(list))
+    dur = defaultdict(list)
+    for path in paths:
+        for r in csv.DictReader(open(path)):
+            who = next((v for k, v in COUNTER_PAIR.items() if k in r["Kernel_Name"]), None)
+            if who is None:
+                continue
+            vals[who][r["Counter_Name"]].append(float(r["Counter_Value"]))
+            dur[who].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
+    op, probe = COUNTER_PAIR.values()
+    if not vals[op] or not vals[probe]:
+        print("no bias_gelu_kernel / copy_kernel dispatches in these CSVs")
+        return
+    a = {k: st.mean(v) for k, v in vals[op].items()}
+    b = {k: st.mean(v) for k, v in vals[probe].items()}
+    out = [f"| counter | {op} | {probe} | {op} / {probe} |", "|---|---|---|---|",
+           f"| duration under the profiler (us) | {st.mean(dur[op]):.1f} | {st.mean(dur[probe]):.1f} "
+           f"| {st.mean(dur[op]) / st.mean(dur[probe]):.3f} |"]
+    for k in sorted(set(a) & set(b)):
+        ratio = f"{a[k] / b[k]:.3f}" if b[k] else "-"
+        out.append(f"| {k} | {a[k]:.4g} | {b[k]:.4g} | {ratio} |")
+    derived = [("SQ_INST_LEVEL_VMEM / SQ_BUSY_CYCLES", "SQ_INST_LEVEL_VMEM", "SQ_BUSY_CYCLES"),
+               ("SQ_WAVE_CYCLES / SQ_WAVES", "SQ_WAVE_CYCLES", "SQ_WAVES")]
+    for name, num, den in derived:
+        if all(x in a and x in b for x in (num, den)) and a[den] and b[den]:
+            ra, rb = a[num] / a[den], b[num] / b[den]
+            out.append(f"| {name} | {ra:.4g} | {rb:.4g} | {ra / rb:.3f} |")
+    print("\n".join(out))
+
+
 def main():
     args = parse()
     if args.summarize:
@@ -1552,6 +1634,12 @@ def main():
         return
     if args.summarize_counters:
         summarize_counters(args.summarize_counters)
+        return
+    if args.summarize_pair:
+        summarize_pair(args.summarize_pair)
+        return
+    if args.counter_pair:
+        counter_pair(args.frames)
         return
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU: the fused per-layer ops are "

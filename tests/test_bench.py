@@ -115,3 +115,26 @@ def test_summarize_counters_stall_table(tmp_path, capsys):
     out = capsys.readouterr().out
     # 1000 cycles per XCD, 1024 SIMDs: 4 x 512000 quad-cycles = 2 waves per SIMD
     assert "| flash_f16_kernel | 4096 | 2.00 | 25.0% | 40.0% | 5.0% |" in out
+
+
+def test_summarize_pair_ratios(tmp_path, capsys):
+    """The op-against-probe counter table: per-dispatch means, the ratio,
+    durations from the timestamps, and the derived in-flight and per-wave
+    figures; other kernels in the CSV are ignored."""
+    head = "Kernel_Name,Grid_Size,Counter_Name,Counter_Value,Start_Timestamp,End_Timestamp\n"
+    gelu = "void hs::(anonymous namespace)::bias_gelu_kernel<_Float16, true, 1>(x)"
+    copy = "void (anonymous namespace)::copy_kernel<true, 1>(x)"
+    other = "void hs::(anonymous namespace)::ln_vec_kernel<_Float16, 2, 2>(x)"
+    lines = []
+    for name, scale, ns in ((gelu, 2.0, 120000), (copy, 1.0, 110000), (other, 9.0, 5000)):
+        for k, v in (("SQ_WAVES", 10), ("SQ_WAVE_CYCLES", 100), ("SQ_BUSY_CYCLES", 5),
+                     ("SQ_INST_LEVEL_VMEM", 20)):
+            lines += [f'"{name}",4096,{k},{v * scale},0,{ns}\n'] * 2
+    path = tmp_path / "p.csv"
+    path.write_text(head + "".join(lines))
+    bench.summarize_pair([str(path)])
+    out = capsys.readouterr().out
+    assert "| duration under the profiler (us) | 120.0 | 110.0 | 1.091 |" in out
+    assert "| SQ_INST_LEVEL_VMEM | 40 | 20 | 2.000 |" in out
+    assert "| SQ_INST_LEVEL_VMEM / SQ_BUSY_CYCLES | 4 | 4 | 1.000 |" in out
+    assert "| SQ_WAVE_CYCLES / SQ_WAVES | 10 | 10 | 1.000 |" in out
