@@ -266,9 +266,12 @@ def test_rope_apply(ctx, dtype, case):
 # ------------------------------------------------------------- elementwise
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,cols", [(37, 4096), (5, 1000), (3, 30), (64, 1024), (1, 8)])
+@pytest.mark.parametrize("rows,cols", [(37, 4096), (5, 1000), (3, 30), (64, 1024), (1, 8),
+                                       (300, 3072), (1374, 4096), (97, 1000)])
 @pytest.mark.parametrize("with_bias", [True, False])
 def test_bias_gelu(ctx, dtype, rows, cols, with_bias):
+    """Shapes from one to several row visits per thread, grids rounded to
+    the column period (3072 and 1000 columns), the scalar path (30)."""
     x = host(O.normal(51, (rows, cols)) * np.float32(2.0), dtype)
     b = O.normal(52, (cols,), 0.0, 0.02) if with_bias else None
     got = back(ctx.bias_gelu(dev(x), None if b is None else dev(b)))
