@@ -442,10 +442,11 @@ CEILING_PROBES = {
                                              "contiguous"),
 }
 KINDS = {"copy": 0, "add2": 1, "heads": 2, "cast": 3, "widen": 4, "inplace": 5, "add2w2": 6}
-# hsc_run shape flags: bit 0 cached loads/stores (else streaming), bit 1 one
-# 16-byte vector per lane / one token's 8-head chunk per wave, chunk by chunk
-# (else four / two whole rows)
-CEILING_SHAPES = {"streaming x4": 0, "cached x4": 1, "streaming x1": 2, "cached x1": 3}
+# hsc_run shapes: bit 0 cached loads/stores (else streaming); 0-1 four 16-byte
+# vectors per lane (heads: two whole rows per wave), 2-3 one (heads: one
+# token's 8-head chunk per wave, chunk by chunk), 4-5 two, 6-7 eight
+CEILING_SHAPES = {"streaming x4": 0, "cached x4": 1, "streaming x1": 2, "cached x1": 3,
+                  "streaming x2": 4, "cached x2": 5, "streaming x8": 6, "cached x8": 7}
 
 
 ROTATE_BYTES = 768 << 20  # > the 256 MB Infinity Cache: no reuse across launches
@@ -521,8 +522,8 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
     Warm: ``iters`` back-to-back launches, an event pair around each as
     for the ops, that rotate over as many buffer sets as make ROTATE_BYTES,
     so no launch finds its inputs in a cache and each pays for its own
-    write-back (streaming and cached loads/stores, each with four and with
-    one 16-byte vector per lane; the fastest is the ceiling). Compared with the op's rate inside the pass. Cold: the per-op
+    write-back (streaming and cached loads/stores, each with one, two, four
+    and eight 16-byte vectors per lane; the fastest is the ceiling). Compared with the op's rate inside the pass. Cold: the per-op
     cold method (cache flush, then a HIP event pair around one launch) with
     streaming stores only, the faster launch shape: cached stores leave their
     write-back for after the end event, so their cold time undercounts.

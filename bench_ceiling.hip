@@ -285,19 +285,25 @@ extern "C" {
 // frames of t tokens, a and b -> o and o2. kind 3 cast: n f32 elements
 // (n % 4 == 0). kind 4 widen: n 16-byte f16 vectors of a -> 2n 16-byte f32
 // vectors of o. kind 5 inplace: n 16-byte vectors of o, read and rewritten.
-// kind 6 add2w2: n 16-byte vectors, a and b -> o = a + b, o2 = a - b. shape: bit 0 set = cached loads and stores (clear:
-// non-temporal), bit 1 set = one 16-byte vector per lane / one token's
-// 8-head chunk per wave (clear: four / two whole rows). Buffers are 16-byte aligned and sized by the
-// caller. Returns 0, or -1 for an argument the kernels do not take, or the
-// HIP error code of the launch.
+// kind 6 add2w2: n 16-byte vectors, a and b -> o = a + b, o2 = a - b.
+// shape 0-7: bit 0 set = cached loads and stores (clear: non-temporal);
+// shapes 0-1 four 16-byte vectors per lane (heads: two whole rows per
+// wave), 2-3 one (heads: one token's 8-head chunk per wave, chunk by
+// chunk), 4-5 two, 6-7 eight (heads: as 0-1). Buffers are 16-byte aligned
+// and sized by the caller. Returns 0, or -1 for an argument the kernels do
+// not take, or the HIP error code of the launch.
 int hsc_run(int kind, int shape, const void* a, const void* b, void* o, void* o2, int64_t n,
             int32_t s, int32_t t, hipStream_t stream) {
-    if (n < 0 || s < 0 || t < 0 || shape < 0 || shape > 3) return -1;
+    if (n < 0 || s < 0 || t < 0 || shape < 0 || shape > 7) return -1;
     switch (shape) {
         case 0: return run<true, 4>(kind, a, b, o, o2, n, s, t, stream);
         case 1: return run<false, 4>(kind, a, b, o, o2, n, s, t, stream);
         case 2: return run<true, 1>(kind, a, b, o, o2, n, s, t, stream);
-        default: return run<false, 1>(kind, a, b, o, o2, n, s, t, stream);
+        case 3: return run<false, 1>(kind, a, b, o, o2, n, s, t, stream);
+        case 4: return run<true, 2>(kind, a, b, o, o2, n, s, t, stream);
+        case 5: return run<false, 2>(kind, a, b, o, o2, n, s, t, stream);
+        case 6: return run<true, 8>(kind, a, b, o, o2, n, s, t, stream);
+        default: return run<false, 8>(kind, a, b, o, o2, n, s, t, stream);
     }
 }
 

@@ -93,7 +93,7 @@ def test_ceiling_library_exports_its_entry_point():
     # argument checks run on the host, before any launch
     run = bench.load_ceiling().hsc_run
     assert run(7, 0, None, None, None, None, 0, 0, 0, None) == -1    # unknown kind
-    assert run(0, 4, None, None, None, None, 0, 0, 0, None) == -1    # unknown shape
+    assert run(0, 8, None, None, None, None, 0, 0, 0, None) == -1    # unknown shape
     assert run(0, -1, None, None, None, None, 0, 0, 0, None) == -1   # unknown shape
     assert run(3, 1, None, None, None, None, 6, 0, 0, None) == -1    # cast needs n % 4 == 0
     assert run(0, 0, None, None, None, None, -1, 0, 0, None) == -1   # negative size

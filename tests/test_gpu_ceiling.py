@@ -1,6 +1,6 @@
 """bench.py's data-movement probes (bench_ceiling.hip) move what they claim:
 each is checked exactly against torch on a small shape under both load/store
-policies and both launch shapes, so a ceiling the bench reports is the rate
+policies and every launch shape, so a ceiling the bench reports is the rate
 of a kernel that did the op's data movement."""
 import os
 
@@ -10,9 +10,10 @@ import torch
 import bench
 
 pytestmark = pytest.mark.gpu
-# shape flags: bit 0 cached (else streaming), bit 1 one vector per lane /
-# one token's 8-head chunk per wave (else four / two whole rows)
-POLICIES = [0, 1, 2, 3]
+# shapes: bit 0 cached (else streaming); 0-1 four vectors per lane (heads:
+# two whole rows per wave), 2-3 one (heads: one token's 8-head chunk per
+# wave), 4-5 two, 6-7 eight
+POLICIES = list(range(8))
 
 
 @pytest.fixture(scope="module")
