@@ -7,9 +7,10 @@
 // tiled_add.wesl semantics, out[i] = x[i] + table[i % block]) into the cast,
 // so each patch element is read once in its input dtype and written once.
 //
-// Each lane moves LV = 4 consecutive channels per step, CHUNKS steps per
-// row (8 channels per lane, one 16-byte f16 store each, measured slower:
-// 66% of peak against 72.7% at S=32). Rows are independent; the
+// Each lane moves LV = 4 consecutive channels per step, one 1 KiB chunk
+// of the row per wave instruction (8 channels per lane, one 16-byte f16
+// store each, measured slower: 66% of peak against 72.7% at S=32); the
+// row's chunks are split over HS_AS_SPLIT waves. Rows are independent; the
 // camera/register gather is row-granular, so no LDS staging is needed.
 #include "hs_common.hpp"
 
@@ -116,8 +117,9 @@ __device__ __forceinline__ float patch_value(float x, float b, float p, bool has
 // PP = ceil(P / kXcds), so each XCD's L2 holds only its 1/kXcds share of the
 // positional table. Within an XCD the workgroups walk the frames in groups of
 // F = kFramesPerWave: workgroup b (local index l = b / kXcds) takes frame
-// group l / C and positions x PP + 4 (l % C) + [0, 4), C = ceil(PP / 4), one
-// position per wave, for the F frames of its group. A wave keeps its
+// group l / C and positions x PP + n (l % C) + [0, n), n = 4 / SPLIT
+// positions per workgroup, C = ceil(PP / n), SPLIT waves per position (each
+// its share of the row's chunks), for the F frames of its group. A wave keeps its
 // position's table row and the bias in registers across its F frames, the
 // four waves of a workgroup read four consecutive patch rows of each frame,
 // and the whole chip sweeps the frames in order, so the reads in flight at
@@ -126,22 +128,32 @@ __device__ __forceinline__ float patch_value(float x, float b, float p, bool has
 // Camera/register rows follow, 4 per workgroup.
 constexpr int kXcds = 8;
 
+#ifndef HS_AS_SPLIT
+// waves per patch row, each taking 1/SPLIT of the row's 1 KiB chunks: at
+// S=32 (D=1024, four chunks) 4 took 44.9-45.8 us warm / 46.2-46.4 cold
+// against 46.5 / 47.1-47.6 for 1 (a whole row per wave) and 45.3-46.2 /
+// 46.3-46.5 for 2
+#define HS_AS_SPLIT 4
+#endif
+
 struct AssembleGrid {
     int64_t patch_blocks;  // kXcds * ceil(S / F) * C
     int64_t special_blocks;
     int chunks;            // C: workgroups per frame group per XCD
     int pp;                // PP: positions per XCD
-    __host__ __device__ static AssembleGrid make(int s, int np, int nr) {
+    // SPL waves share a patch row: a workgroup covers kWavesPerBlock / SPL
+    // positions
+    __host__ __device__ static AssembleGrid make(int s, int np, int nr, int spl) {
         AssembleGrid g;
         g.pp = static_cast<int>(ceil_div(np, kXcds));
-        g.chunks = static_cast<int>(ceil_div(g.pp, kWavesPerBlock));
+        g.chunks = static_cast<int>(ceil_div(g.pp, kWavesPerBlock / spl));
         g.patch_blocks = static_cast<int64_t>(kXcds) * ceil_div(s, kFramesPerWave) * g.chunks;
         g.special_blocks = ceil_div(static_cast<int64_t>(s) * (1 + nr), kWavesPerBlock);
         return g;
     }
 };
 
-template <typename TO, typename TP, int CHUNKS, int LV>
+template <typename TO, typename TP, int CHUNKS, int LV, int SPL>
 __global__ __launch_bounds__(kBlock) void assemble_kernel(
     const TP* __restrict__ patches, const float* __restrict__ pbias, const float* __restrict__ pos,
     const TO* __restrict__ cam, const TO* __restrict__ reg, TO* __restrict__ out, int nframes,
@@ -150,38 +162,41 @@ __global__ __launch_bounds__(kBlock) void assemble_kernel(
     constexpr int D = CW * CHUNKS;
     const int lane = lane_id();
     const int w = wave_in_block();
-    const AssembleGrid grid = AssembleGrid::make(nframes, np, nr);
+    const AssembleGrid grid = AssembleGrid::make(nframes, np, nr, SPL);
     const int64_t b = blockIdx.x;
     if (b < grid.patch_blocks) {
         constexpr int F = kFramesPerWave;
+        constexpr int CH = CHUNKS / SPL;  // chunks of the row this wave takes
+        static_assert(CHUNKS % SPL == 0, "whole chunks per wave");
         const int x = static_cast<int>(b % kXcds);
         const int64_t l = b / kXcds;
         const int fg = static_cast<int>(l / grid.chunks);
         const int g = static_cast<int>(l - static_cast<int64_t>(fg) * grid.chunks);
-        const int64_t p = static_cast<int64_t>(x) * grid.pp + g * kWavesPerBlock + w;
+        const int64_t p = static_cast<int64_t>(x) * grid.pp + g * (kWavesPerBlock / SPL) + w / SPL;
+        const int c_lo = (w % SPL) * CH;  // first chunk of this wave's share
         const int f0 = fg * F;
         // wave-uniform; the kernel has no barriers
         if (p >= static_cast<int64_t>(x + 1) * grid.pp || p >= np || f0 >= nframes) return;
         const int f1 = f0 + F < nframes ? f0 + F : nframes;
         const bool has_b = pbias != nullptr, has_p = pos != nullptr;
-        float pe[CHUNKS][LV], bv[CHUNKS][LV];
+        float pe[CH][LV], bv[CH][LV];
 #pragma unroll
-        for (int c = 0; c < CHUNKS; c++) {
+        for (int c = 0; c < CH; c++) {
 #pragma unroll
             for (int k = 0; k < LV; k++) pe[c][k] = bv[c][k] = 0.0f;
-            if (has_p) loadv(pos + p * D + c * CW + lane * LV, pe[c]);
-            if (has_b) loadv(pbias + c * CW + lane * LV, bv[c]);
+            if (has_p) loadv(pos + p * D + (c_lo + c) * CW + lane * LV, pe[c]);
+            if (has_b) loadv(pbias + (c_lo + c) * CW + lane * LV, bv[c]);
         }
-        const TP* src = patches + (static_cast<int64_t>(f0) * np + p) * D + lane * LV;
-        TO* orow = out + (static_cast<int64_t>(f0) * seq + 1 + nr + p) * D + lane * LV;
+        const TP* src = patches + (static_cast<int64_t>(f0) * np + p) * D + c_lo * CW + lane * LV;
+        TO* orow = out + (static_cast<int64_t>(f0) * seq + 1 + nr + p) * D + c_lo * CW + lane * LV;
         const int64_t src_step = static_cast<int64_t>(np) * D, out_step = static_cast<int64_t>(seq) * D;
-        auto load = [&](float (&x)[CHUNKS][LV], int f) {
+        auto load = [&](float (&x)[CH][LV], int f) {
 #pragma unroll
-            for (int c = 0; c < CHUNKS; c++) loadv_stream(src + (f - f0) * src_step + c * CW, x[c]);
+            for (int c = 0; c < CH; c++) loadv_stream(src + (f - f0) * src_step + c * CW, x[c]);
         };
-        auto emit = [&](float (&x)[CHUNKS][LV], int f) {
+        auto emit = [&](float (&x)[CH][LV], int f) {
 #pragma unroll
-            for (int c = 0; c < CHUNKS; c++) {
+            for (int c = 0; c < CH; c++) {
 #pragma unroll
                 for (int k = 0; k < LV; k++)
                     x[c][k] = patch_value<TP>(x[c][k], bv[c][k], pe[c][k], has_b, has_p);
@@ -190,7 +205,7 @@ __global__ __launch_bounds__(kBlock) void assemble_kernel(
         };
         // two-buffer pipeline over the wave's frames: the next frame's row
         // is in flight while the current one is summed and stored
-        float xa[CHUNKS][LV], xb[CHUNKS][LV];
+        float xa[CH][LV], xb[CH][LV];
         load(xa, f0);
 #pragma unroll 1
         for (int f = f0; f < f1; f += 2) {
@@ -261,7 +276,7 @@ hs_status launch(hipStream_t st, const void* patches, const float* pbias, const 
     const int seq = 1 + nr + np;
     const int64_t out_rows = static_cast<int64_t>(s) * seq;
     const dim3 grid(static_cast<uint32_t>(persistent_blocks(out_rows)));
-    const AssembleGrid ag = AssembleGrid::make(s, np, nr);
+    const AssembleGrid ag = AssembleGrid::make(s, np, nr, d / 256 >= HS_AS_SPLIT ? HS_AS_SPLIT : 1);
     const auto* P = static_cast<const TP*>(patches);
     const auto* C = static_cast<const TO*>(cam);
     const auto* R = static_cast<const TO*>(reg);
@@ -275,15 +290,16 @@ hs_status launch(hipStream_t st, const void* patches, const float* pbias, const 
                         (!pos || aligned16(pos));
     const dim3 vgrid(static_cast<uint32_t>(vblocks));
     if (vec_ok) {
-#define HS_AS_LAUNCH(CH, LV)                                                                      \
-    assemble_kernel<TO, TP, CH, LV><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, seq, \
-                                                                   np, nr, n_var);                \
+#define HS_AS_LAUNCH(CH, LV, SPL)                                                                  \
+    assemble_kernel<TO, TP, CH, LV, SPL><<<vgrid, dim3(kBlock), 0, st>>>(P, pbias, pos, C, R, O, s, \
+                                                                        seq, np, nr, n_var);      \
     return check_launch("assemble_tokens")
+        constexpr int kS = HS_AS_SPLIT;
         switch (d / 256) {
-            case 1: HS_AS_LAUNCH(1, 4);
-            case 2: HS_AS_LAUNCH(2, 4);
-            case 4: HS_AS_LAUNCH(4, 4);
-            case 8: HS_AS_LAUNCH(8, 4);
+            case 1: HS_AS_LAUNCH(1, 4, 1);
+            case 2: HS_AS_LAUNCH(2, 4, (2 >= kS ? kS : 1));
+            case 4: HS_AS_LAUNCH(4, 4, (4 >= kS ? kS : 1));
+            case 8: HS_AS_LAUNCH(8, 4, (8 >= kS ? kS : 1));
             default: break;
         }
 #undef HS_AS_LAUNCH

@@ -258,9 +258,13 @@ __global__ __launch_bounds__(kBlock) void bias_ls_scalar_kernel(const T* res, co
 // f32 -> f16 in a one-shot grid: each wave takes kCastU * 64 consecutive
 // 4-float vectors, lane l the vectors l, l + 64, ..., so every load
 // instruction reads 1 KiB and every store writes 512 contiguous bytes, all
-// kCastU loads in flight before the first store. Elements past the last
+// kCastU loads in flight before the first store (two per lane: the cast
+// probe's fastest shape). Elements past the last
 // whole vector (total % 4) are cast by the first lanes of workgroup 0.
-constexpr int kCastU = 4;
+#ifndef HS_CAST_U
+#define HS_CAST_U 2  // S=32 (45 M floats): 42.4 us against 45.0 for 4, 46.1 for 1, 79.5 for 8
+#endif
+constexpr int kCastU = HS_CAST_U;
 
 __global__ __launch_bounds__(kBlock) void cast_f32_f16_kernel(const float* x, f16* out, int64_t total) {
     const int64_t n4 = total / 4;
