@@ -305,10 +305,12 @@ def test_fused_pass_equals_six_op_pass(ctx, frames, grid, dtype):
     assert_bit_exact(host(a.out), host(b.out), "fused pass output")
 
 
-def test_graph_replay_matches_eager(ctx):
-    """The pass captured in a HIP graph, replayed three times with eager work
-    and synchronisation between replays; every replay equals eager launches."""
-    fp = FusedOpPass(ctx, frames=2, grid=(4, 4), n_frame=2, n_global=2)
+@pytest.mark.parametrize("fuse", [False, True])
+def test_graph_replay_matches_eager(ctx, fuse):
+    """The pass (six ops per block, or four with LayerScale + LayerNorm
+    fused) captured in a HIP graph, replayed three times with eager work and
+    synchronisation between replays; every replay equals eager launches."""
+    fp = FusedOpPass(ctx, frames=2, grid=(4, 4), n_frame=2, n_global=2, fuse=fuse)
     fp.run()
     torch.cuda.synchronize()
     eager = {k: host(getattr(fp.io, k)).copy() for k in ("q_head", "k_head", "act", "normed2")}
