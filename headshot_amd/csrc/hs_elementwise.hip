@@ -140,50 +140,6 @@ __global__ __launch_bounds__(kBlock) void bias_gelu_kernel(const T* x, const flo
     }
 }
 
-#ifndef HS_GELU_TILE
-#define HS_GELU_TILE 0  // rows per lane of a one-shot tiled grid (0: column-stationary loop)
-#endif
-
-// One-shot tiled grid: workgroup b takes rows [R t, R t + R) of column block
-// cb (kBlock * V columns), t = b / cblocks, cb = b % cblocks; each lane loads
-// its R vectors (one per row, the same columns) and its columns' bias once.
-template <typename T, int R>
-__global__ __launch_bounds__(kBlock) void bias_gelu_tile_kernel(const T* x,
-                                                                const float* __restrict__ bias,
-                                                                T* out, int64_t rows, int cols,
-                                                                int cblocks) {
-    constexpr int V = Vec<T>::N;
-    const int64_t tile = blockIdx.x / cblocks;
-    const int cb = static_cast<int>(blockIdx.x - tile * cblocks);
-    const int c0 = (cb * kBlock + static_cast<int>(threadIdx.x)) * V;
-    const int64_t r0 = tile * R;
-    u32x4 raw[R];
-#pragma unroll
-    for (int r = 0; r < R; r++)
-        if (r0 + r < rows) raw[r] = ld_stream<HS_GELU_NTL>(x + (r0 + r) * cols + c0);
-    constexpr bool kHalfBias = sizeof(T) == 2;  // as in bias_gelu_kernel
-    float bv[V];
-#pragma unroll
-    for (int k = 0; k < V; k += 4) {
-        const float4 b4 = bias ? ld_f32x4(bias + c0 + k) : float4{0.0f, 0.0f, 0.0f, 0.0f};
-        bv[k] = b4.x, bv[k + 1] = b4.y, bv[k + 2] = b4.z, bv[k + 3] = b4.w;
-    }
-    if constexpr (kHalfBias) {
-#pragma unroll
-        for (int k = 0; k < V; k++) bv[k] *= 0.5f;
-    }
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        if (r0 + r >= rows) break;
-        float f[V];
-        unpack(raw[r], f, T{});
-#pragma unroll
-        for (int k = 0; k < V; k++)
-            f[k] = kHalfBias ? gelu_half(fmaf(f[k], 0.5f, bv[k])) : gelu_f(f[k] + bv[k]);
-        st_stream<HS_GELU_NTS>(out + (r0 + r) * cols + c0, pack(f, T{}));
-    }
-}
-
 template <typename T, bool BIAS, int U>
 __global__ __launch_bounds__(kBlock) void bias_ls_kernel(const T* res, const T* x,
                                                          const float* __restrict__ bias,
@@ -353,18 +309,6 @@ hs_status launch_gelu(hipStream_t st, const void* x, const float* bias, void* ou
     constexpr int U = HS_GELU_U;
     const int64_t total = rows * cols;
     const bool vec_ok = cols % V == 0 && aligned16(x) && aligned16(out) && (!bias || aligned16(bias));
-    if constexpr (HS_GELU_TILE > 0) {
-        constexpr int R = HS_GELU_TILE;
-        if (vec_ok && cols % (kBlock * V) == 0) {
-            const int cblocks = cols / (kBlock * V);
-            const int64_t blocks = ceil_div(rows, R) * cblocks;
-            if (blocks < (int64_t{1} << 31)) {
-                bias_gelu_tile_kernel<T, R><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(
-                    static_cast<const T*>(x), bias, static_cast<T*>(out), rows, cols, cblocks);
-                return check_launch("bias_gelu");
-            }
-        }
-    }
     // HS_GELU_ITERS > 0: a grid in which each thread visits that many rows
     // (the last visit partial), whatever the tensor's size; else a grid of
     // HS_GELU_BPC workgroups per CU.
