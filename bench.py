@@ -1116,8 +1116,8 @@ def config0_block(ctx, seed: int = 0):
 
 
 def cpu_baseline(ctx, target_s: float):
-    """The planned CPU baseline: config 0 (one frame block's fused-op
-    sequence, f32, S=2 x 1374 x 1024) through the oracle (the reference's f32
+    """The CPU baseline: one frame block's fused-op sequence, f32, S=2 x
+    1374 x 1024, through the oracle (the reference's f32
     WGSL kernels restated in C, run in the reference's unfused dispatch
     order: layernorm, split_heads + layernorm + rope_apply for q and k,
     residual_ls, layernorm, gelu, residual_ls), OpenMP over rows on the host
@@ -1192,7 +1192,7 @@ def cpu_baseline(ctx, target_s: float):
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"config 0: one frame block's fused-op sequence, f32, S={frames} x {t} x "
+        "sample": (f"one frame block's fused-op sequence, f32, S={frames} x {t} x "
                    f"{DIM}, 37x37 RoPE, prefix {prefix}, through oracle/hs_oracle.c (C "
                    f"restatement of the reference's f32 WGSL kernels, unfused reference "
                    f"dispatch order), {threads} OpenMP threads of {visible} visible cores; "

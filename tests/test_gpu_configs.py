@@ -171,8 +171,8 @@ def test_assembly_full_size(ctx, frames, p):
 def test_assembly_dino_layout_full_size(ctx):
     """The DINO stage's assembly (model/dino.rs:76-93): per frame [cls,
     storage x 4, patches + patch-embed bias], one token variant for every
-    frame (n_var 1), f32 in and out, at D=1024 on config 4's 16 frames of
-    21 x 37 = 777 patches; bit-exact."""
+    frame (n_var 1), f32 in and out, at D=1024 on 16 frames of the
+    non-square 21 x 37 = 777-patch grid; bit-exact."""
     frames, p, r = 16, 777, 4
     g = torch.Generator(device="cuda:0")
     g.manual_seed(21)

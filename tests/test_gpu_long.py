@@ -1,5 +1,5 @@
-"""The largest benchmark configuration, config 3 (S=200 frames flattened to
-one global sequence of 274,800 tokens, f16, no RoPE), through the attention,
+"""The largest workload: S=200 frames flattened to one global sequence of
+274,800 tokens, f16, no RoPE, through the attention,
 linear-layer and cache-build kernels at its real shapes.
 
 Bars as for the smaller sizes: f16 outputs within 2e-3 * max(1, |e|) of a
