@@ -1092,8 +1092,8 @@ def host_threads() -> tuple:
     return used, visible
 
 
-def config0_block(ctx, seed: int = 0):
-    """Config 0's workload: one frame block's fused-op sequence at S=2 frames
+def s2_f32_frame_block(ctx, seed: int = 0):
+    """One frame block's fused-op sequence at S=2 frames
     x 1374 tokens x 1024, f32, 37 x 37 RoPE grid, prefix 5, eps 1e-6, with
     random-init parameters (LN gamma N(1,.02), beta/biases N(0,.02),
     LayerScale 1e-5) and N(0,1) activations and GEMM outputs."""
@@ -1132,7 +1132,7 @@ def cpu_baseline(ctx, target_s: float):
 
     threads, visible = host_threads()
     O.set_num_threads(threads)
-    io, p, (sin, cos, prefix), frames, t = config0_block(ctx)
+    io, p, (sin, cos, prefix), frames, t = s2_f32_frame_block(ctx)
     rows = frames * t
     nbytes = rows * 45056 * 2  # per-token algorithmic bytes of a block, f32 storage
     h = lambda x: x.detach().cpu().numpy()  # noqa: E731

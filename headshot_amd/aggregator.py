@@ -38,7 +38,7 @@ class BlockParams:
     @staticmethod
     def random(dim: int, hidden: int, head_dim: int, device, generator, qk_norm: bool = True,
                ls_init: float | None = 1e-5) -> "BlockParams":
-        """Random init of the reference configs: LN gamma ~N(1,.02), beta and
+        """Random init as the benchmark workloads draw it: LN gamma ~N(1,.02), beta and
         biases ~N(0,.02), LayerScale = ls_init (or ~N(0,1) when None)."""
         def n(shape, mean=0.0, std=1.0):
             return torch.randn(shape, generator=generator, device=device) * std + mean
