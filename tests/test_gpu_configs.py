@@ -81,11 +81,11 @@ def tables(grid):
 
 @pytest.mark.parametrize("cfg", [
     # name, frames, grid, dtype, kinds
-    ("config0 f32 S=2", 2, (37, 37), torch.float32, ("frame", "global")),
-    ("config1 f16 S=8", 8, (37, 37), torch.float16, ("frame",)),
-    ("config2 f16 S=32", 32, (37, 37), torch.float16, ("frame", "global")),
-    ("config4 f32 S=16 21x37", 16, (21, 37), torch.float32, ("frame", "global")),
-    ("config4 f16 S=16 21x37", 16, (21, 37), torch.float16, ("frame", "global")),
+    ("f32 S=2 37x37", 2, (37, 37), torch.float32, ("frame", "global")),
+    ("f16 S=8 37x37", 8, (37, 37), torch.float16, ("frame",)),
+    ("f16 S=32 37x37", 32, (37, 37), torch.float16, ("frame", "global")),
+    ("f32 S=16 21x37", 16, (21, 37), torch.float32, ("frame", "global")),
+    ("f16 S=16 21x37", 16, (21, 37), torch.float16, ("frame", "global")),
 ])
 def test_block_ops_full_size(ctx, cfg):
     name, frames, grid, dtype, kinds = cfg
@@ -132,7 +132,7 @@ def test_trunk_prefix_17(ctx):
 
 
 def test_non_square_tables_bit_exact_and_used(ctx):
-    """Config 4's 21x37 grid: the tables equal the golden fixture and the
+    """The non-square 21x37 grid: the tables equal the golden fixture and the
     kernel's rotation uses row t - prefix of them."""
     g = json.load(open(os.path.join(HERE, "golden", "rope_tables.json")))["grids"]["21x37"]
     sin, cos = rope.tables(rope.periods(), 21, 37)
@@ -151,7 +151,7 @@ def test_non_square_tables_bit_exact_and_used(ctx):
 
 @pytest.mark.parametrize("frames,p", [(32, 1369), (16, 777)], ids=["config2", "config4"])
 def test_assembly_full_size(ctx, frames, p):
-    """Configs 2 and 4's assembly (37 x 37 and 21 x 37 patches): f32 patches
+    """The assembly at S=32 x 37 x 37 and S=16 x 21 x 37 patches: f32 patches
     + bias + pos-embed -> f16 tokens, with camera/register variants for frame
     0 and the rest; bit-exact."""
     r = 4
@@ -193,8 +193,8 @@ def test_assembly_dino_layout_full_size(ctx):
     assert_bit_exact(g3[:, 1:1 + r], np.broadcast_to(host(storage), (frames, r, DIM)), "storage")
 
 
-def test_config3_frame_layout_rope(ctx):
-    """Config 3's qk-norm + RoPE2D leg: S=200 frames x 1374 tokens in the
+def test_s200_frame_layout_rope(ctx):
+    """The S=200 qk-norm + RoPE2D leg: S=200 frames x 1374 tokens in the
     frame-block layout (37 x 37 tables, prefix 5), q and k in one launch.
     Oracle on 4 whole frames (5,496 tokens); at full size RoPE preserves
     every pair norm of the normalised vectors and the 5 prefix tokens pass
@@ -236,7 +236,7 @@ def test_config3_frame_layout_rope(ctx):
 
 
 def test_global_block_long_sequence(ctx):
-    """Config 3: S=200 frames flattened to one 274,800-token sequence through
+    """S=200 frames flattened to one 274,800-token sequence through
     the global-block ops (no RoPE). Oracle on 512 sampled token rows; the
     split is checked bit-exact at full size; LN invariants at full size."""
     rows = 200 * 1374
