@@ -149,7 +149,7 @@ def test_non_square_tables_bit_exact_and_used(ctx):
     assert_bit_exact(got[:, :, :5], np.ascontiguousarray(xs[:, :5].transpose(0, 2, 1, 3)), "prefix")
 
 
-@pytest.mark.parametrize("frames,p", [(32, 1369), (16, 777)], ids=["config2", "config4"])
+@pytest.mark.parametrize("frames,p", [(32, 1369), (16, 777)], ids=["s32_37x37", "s16_21x37"])
 def test_assembly_full_size(ctx, frames, p):
     """The assembly at S=32 x 37 x 37 and S=16 x 21 x 37 patches: f32 patches
     + bias + pos-embed -> f16 tokens, with camera/register variants for frame

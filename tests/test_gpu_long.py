@@ -39,11 +39,11 @@ def max_scaled_err(got: torch.Tensor, ref: torch.Tensor) -> float:
     return worst
 
 
-def test_attention_config3(ctx):
+def test_attention_s200(ctx):
     """Global attention over 274,800 tokens, 16 heads of 64, written
     token-major: 64 sampled queries against float32 torch, 2 against the
     oracle, and constant V rows reproduced at every query."""
-    print(f"[config3 attention: t={ROWS}]", flush=True)
+    print(f"[s200 attention: t={ROWS}]", flush=True)
     q, k, v = (randn((1, H, ROWS, D), 300 + i) for i in range(3))
     got = ctx.attention_merged(q, k, v).view(ROWS, H, D)
     rows = np.sort(np.random.default_rng(3).choice(ROWS, 64, replace=False))
@@ -51,11 +51,11 @@ def test_attention_config3(ctx):
     s = torch.matmul(q[0][:, ri].float(), k[0].float().transpose(-1, -2).contiguous()) / 8.0
     ref = torch.matmul(torch.softmax(s, dim=-1), v[0].float())          # (H, 64, D)
     f16_close(back(got[ri].permute(1, 0, 2)).astype(np.float32), back(ref),
-              "config3 attention vs torch f32")
+              "s200 attention vs torch f32")
     idx = rows[[5, 40]].astype(np.int32)
     want = O.attention(back(q), back(k), back(v), q_idx=idx)            # (1, H, 2, D)
     f16_close(back(got[torch.from_numpy(idx).long().to("cuda:0")].permute(1, 0, 2)).astype(np.float32),
-              want[0].astype(np.float32), "config3 attention vs oracle")
+              want[0].astype(np.float32), "s200 attention vs oracle")
     vc = v[:, :, :1].expand(1, H, ROWS, D).contiguous()
     out = ctx.attention_merged(q, k, vc).view(ROWS, H, D)
     err = (out.float() - vc[0, :, 0].float().unsqueeze(0)).abs().max().item()
@@ -63,13 +63,13 @@ def test_attention_config3(ctx):
 
 
 @pytest.mark.parametrize("name", ["fc1", "fc2"])
-def test_linear_config3(ctx, name):
+def test_linear_s200(ctx, name):
     """fc1 + bias + GELU (274,800 x 1024 -> 4096) and fc2 + bias + LayerScale
     + residual (274,800 x 4096 -> 1024): every output against float32 torch
     of the reference sequence (the linear's output stored as f16, then the
     epilogue), 4 rows against the oracle."""
     n, k = (4096, 1024) if name == "fc1" else (1024, 4096)
-    print(f"[config3 {name}: m={ROWS} n={n} k={k}]", flush=True)
+    print(f"[s200 {name}: m={ROWS} n={n} k={k}]", flush=True)
     x = randn((ROWS, k), 11 + n)
     w = randn((n, k), 12 + n, 1.0 / k ** 0.5)
     b = (randn((n,), 13 + n).float() * 0.02)
@@ -84,7 +84,7 @@ def test_linear_config3(ctx, name):
         ref = res.float() + gam * y
     del y
     err = max_scaled_err(got, ref)
-    assert err <= 2e-3, f"config3 {name} vs torch f32: max scaled error {err:.3g}"
+    assert err <= 2e-3, f"s200 {name} vs torch f32: max scaled error {err:.3g}"
     rows = np.array([0, 70001, 199999, ROWS - 1])
     ri = torch.from_numpy(rows).to("cuda:0")
     xs, ws, bs = back(x[ri]), back(w), back(b)
@@ -92,10 +92,10 @@ def test_linear_config3(ctx, name):
         want = O.linear_gelu(xs, ws, bs)
     else:
         want = O.linear_ls_residual(xs, ws, back(gam), back(res[ri]), bs)
-    f16_close(back(got[ri]).astype(np.float32), want.astype(np.float32), f"config3 {name} vs oracle")
+    f16_close(back(got[ri]).astype(np.float32), want.astype(np.float32), f"s200 {name} vs oracle")
 
 
-def test_cache_build_config3(ctx):
+def test_cache_build_s200(ctx):
     """The head-input cache at 274,800 rows, (rows, 2048) f32: bit-exact
     against the concatenation of the widened halves."""
     a, b = randn((ROWS, 1024), 21), randn((ROWS, 1024), 22)
