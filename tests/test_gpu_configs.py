@@ -210,7 +210,7 @@ def test_s200_frame_layout_rope(ctx):
     kn = (torch.randn(HD, generator=g, device="cuda:0") * 0.02 + 1,
           torch.randn(HD, generator=g, device="cuda:0") * 0.02)
     sin, cos = tables((37, 37))
-    print(f"[config3 frame layout: rows={rows}]", flush=True)
+    print(f"[s200 frame layout: rows={rows}]", flush=True)
     qh, kh = ctx.qknorm_rope_pair(q, k, frames, t, HEADS, HD, qn=qn, kn=kn,
                                   rope=(sin, cos, prefix), eps=1e-6)
     O.set_num_threads(min(16, os.cpu_count() or 1))
@@ -219,7 +219,7 @@ def test_s200_frame_layout_rope(ctx):
             x_f = host(src[f * t:(f + 1) * t])
             want = O.qknorm_rope(x_f, host(nrm[0]), host(nrm[1]), host(sin), host(cos), 1, t,
                                  HEADS, HD, prefix, 1e-6)
-            gate(host(got[f]), want[0], f"config3 {name} frame {f}")
+            gate(host(got[f]), want[0], f"s200 {name} frame {f}")
     # full size: the same normalisation without RoPE ...
     qa, ka = ctx.qknorm_rope_pair(q, k, frames, t, HEADS, HD, qn=qn, kn=kn, rope=None, eps=1e-6)
     for name, rot, plain in (("q", qh, qa), ("k", kh, ka)):
@@ -230,7 +230,7 @@ def test_s200_frame_layout_rope(ctx):
         # moves its norm by at most 2^-11 of the norm (half an f16 ulp per
         # component), plus f32 rounding
         err = ((nr - np_).abs() / np_.clamp_min(1.0)).max().item()
-        assert err < 1e-3, f"config3 {name} pair norms moved by {err}"
+        assert err < 1e-3, f"s200 {name} pair norms moved by {err}"
         assert torch.equal(rot[:, :, :prefix], plain[:, :, :prefix]), f"{name} prefix passthrough"
         del r32, p32, nr, np_
 
@@ -242,7 +242,7 @@ def test_global_block_long_sequence(ctx):
     rows = 200 * 1374
     dtype = torch.float16
     io, p = make_block(ctx, rows, dtype, seed=11)
-    print(f"[config3 global block: rows={rows}]", flush=True)
+    print(f"[s200 global block: rows={rows}]", flush=True)
     run_block_ops(ctx, p, io, 1, rows, HEADS, HD, rope=None, eps=1e-6)
     torch.cuda.synchronize()
     rng = np.random.default_rng(0)
