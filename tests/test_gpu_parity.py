@@ -414,7 +414,10 @@ def test_tiled_add_and_copy_rows(ctx):
                                               (2, (3, 2), 4, 96, 1), (1, (1, 4), 0, 512, 2),
                                               # several waves per patch position, the last
                                               # partial; several workgroup rounds per position
-                                              (11, (2, 3), 4, 1024, 2), (37, (3, 3), 4, 256, 2)])
+                                              (11, (2, 3), 4, 1024, 2), (37, (3, 3), 4, 256, 2),
+                                              # rows of 2048: each wave takes two of a
+                                              # row's eight 1 KiB chunks
+                                              (5, (3, 4), 4, 2048, 2)])
 @pytest.mark.parametrize("bias,pos", [(True, True), (False, False), (True, False)])
 def test_assemble_tokens(ctx, out_dtype, patch_dtype, s, grid, r, d, n_var, bias, pos):
     p = grid[0] * grid[1]
