@@ -552,3 +552,47 @@ def test_every_op_accepts_empty_inputs(ctx):
                                      w.data_ptr(), None, e(0, 256).data_ptr(), 0, 256, 1024, 1e-6)
     assert rc == _lib.HS_OK, L.hs_last_error().decode()
     torch.cuda.synchronize()
+
+
+def test_every_op_f16_matches_f32(ctx):
+    """The reference's every_op_f16_matches_f32 (tests/f16_ops.rs:36-123) on
+    the HIP ops: each op's f16 variant against its f32 variant on the same
+    f16-exact inputs in [-1, 1) (its rvec), with its max-abs tolerances:
+    layernorm 2e-2, gelu 2e-3, residual_ls 2e-3, split_heads and attn_merge
+    1e-6 (exact), rope_apply 2e-3, concat_channels 1e-6 (exact)."""
+    s, h, t, d = 2, 4, 21, 64
+    c, rows = h * d, s * t
+
+    def both(a):
+        return (torch.from_numpy(a.astype(np.float32)).to("cuda:0"),
+                torch.from_numpy(a.astype(np.float16)).to("cuda:0"))
+
+    def close(got16, got32, tol, what):
+        a, b = back(got16).astype(np.float32), back(got32).astype(np.float32)
+        assert np.count_nonzero(b) > 0, f"{what}: f32 output is all zero"
+        assert np.count_nonzero(a) > 0, f"{what}: f16 output is all zero"
+        err = np.abs(a - b).max()
+        assert err < tol, f"{what}: max diff {err} >= {tol}"
+
+    x32, x16 = both(O.rvec_f16(1, rows * c).reshape(rows, c))
+    w = torch.from_numpy(O.rvec_f16(2, c)).to("cuda:0")
+    b = torch.from_numpy(O.rvec_f16(3, c)).to("cuda:0")
+    close(ctx.layernorm(x16, w, b), ctx.layernorm(x32, w, b), 2e-2, "layernorm")
+    close(ctx.gelu(x16), ctx.gelu(x32), 2e-3, "gelu")
+    r32, r16 = both(O.rvec_f16(4, rows * c).reshape(rows, c))
+    g = torch.from_numpy(O.rvec_f16(5, c)).to("cuda:0")
+    close(ctx.residual_ls(r16, x16, g), ctx.residual_ls(r32, x32, g), 2e-3, "residual_ls")
+    q32, q16 = both(O.rvec_f16(6, rows * c).reshape(rows, c))
+    hq32, hq16 = ctx.split_heads(q32, s, t, h, d), ctx.split_heads(q16, s, t, h, d)
+    close(hq16, hq32, 1e-6, "split_heads")
+    close(ctx.attn_merge(hq16), ctx.attn_merge(hq32), 1e-6, "attn_merge")
+    sin, cos = rope.tables(rope.periods(), 4, 4)
+    sin_t, cos_t = dev(sin), dev(cos)
+    prefix = t - 16
+    g32, g16 = both(O.rvec_f16(7, s * h * t * d).reshape(s, h, t, d))
+    ctx.rope_apply(g32, sin_t, cos_t, prefix)
+    ctx.rope_apply(g16, sin_t, cos_t, prefix)
+    close(g16, g32, 2e-3, "rope_apply")
+    a32, a16 = both(O.rvec_f16(8, rows * 8).reshape(rows, 8))
+    c32, c16 = both(O.rvec_f16(9, rows * 24).reshape(rows, 24))
+    close(ctx.concat_channels(a16, c16), ctx.concat_channels(a32, c32), 1e-6, "concat_channels")
