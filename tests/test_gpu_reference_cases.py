@@ -11,6 +11,11 @@ closed form or CPU routine that test uses.
   float64 erf form, 1e-5, and gelu(0) = 0, gelu(+-10) = 10 / 0;
 - rope_apply_matches_cpu (:149-182): (2, 3, 11, 64), prefix 5, 2 x 3 grid,
   each vector against rope::apply_cpu (the oracle's restatement), 1e-5;
+- linear_matches_cpu (:63-98): (m, k, n) = (37, 53, 29) f32, with and
+  without bias, 1e-4 against float64 sums;
+- linear_f16_and_wmma_match_cpu (:313-375): (37, 96, 128) f16 with bias,
+  1e-2, and n = 48 without bias, 2e-3, against float64 sums of the
+  f16-rounded inputs stored as f16;
 - split_heads_merge_roundtrip (:241-274): (2, 5, 4, 8), exact;
 - the concat part of im2col_and_concat (:300-310): (3, 2) ++ (3, 3), exact.
 """
@@ -102,3 +107,30 @@ def test_concat_channels(ctx):
     want = np.array([a[0], a[1], b[0], b[1], b[2], a[2], a[3], b[3], b[4], b[5], a[4], a[5],
                      b[6], b[7], b[8]], np.float32)
     assert_bit_exact(got, want, "concat")
+
+
+def test_linear_matches_cpu(ctx):
+    m, k, n = 37, 53, 29  # deliberately not multiples of any tile
+    v = O.rng_vec(2, m * k + n * k + n)
+    x = v[: m * k].reshape(m, k)
+    w = v[m * k: m * k + n * k].reshape(n, k)
+    b = v[m * k + n * k:]
+    want = (x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32) + b
+    assert_close(back(ctx.linear(dev(x), dev(w), dev(b))), want, 1e-4, "linear")
+    assert_close(back(ctx.linear(dev(x), dev(w), None)), want - b, 1e-4, "linear no bias")
+
+
+def test_linear_f16_matches_cpu(ctx):
+    m, k, n = 37, 96, 128
+    v = O.rng_vec(8, m * k + n * k + n)
+    x = O.to_f16(v[: m * k].reshape(m, k))
+    w = O.to_f16(v[m * k: m * k + n * k].reshape(n, k))
+    b = v[m * k + n * k:]
+    acc = x.astype(np.float64) @ w.astype(np.float64).T
+    want = (acc.astype(np.float32) + b).astype(np.float16).astype(np.float32)
+    got = back(ctx.linear(dev(x), dev(w), dev(b))).astype(np.float32)
+    assert_close(got, want, 1e-2, "linear f16")
+    n2 = 48
+    want2 = acc[:, :n2].astype(np.float32).astype(np.float16).astype(np.float32)
+    got2 = back(ctx.linear(dev(x), dev(np.ascontiguousarray(w[:n2])), None)).astype(np.float32)
+    assert_close(got2, want2, 2e-3, "linear f16 n=48")
