@@ -446,13 +446,20 @@ def rng_vec(seed: int, n: int) -> np.ndarray:
     return (v - np.float32(1.0)).astype(np.float32)
 
 
-def rvec_f16(seed: int, n: int) -> np.ndarray:
-    """``rvec(seed, n)`` of tests/f16_ops.rs:7-19: f16-exact values in [-1, 1)."""
+def rvec(seed: int, n: int) -> np.ndarray:
+    """``rvec(seed, n)`` of tests/dense_kernels.rs:6-17, bit for bit:
+    ``(z >> 40) as f32 / 2^24 * 2 - 1``, values in [-1, 1). That function
+    stops before SplitMix64's last ``z ^ (z >> 31)``, which leaves the top
+    24 bits unchanged, so the shared generator gives the same values."""
     top = (_splitmix_z(seed, n) >> np.uint64(40)).astype(np.float32)
     v = top / np.float32(1 << 24)
     v = v * np.float32(2.0)
-    v = (v - np.float32(1.0)).astype(np.float32)
-    return f16_to_f32(to_f16(v))
+    return (v - np.float32(1.0)).astype(np.float32)
+
+
+def rvec_f16(seed: int, n: int) -> np.ndarray:
+    """``rvec(seed, n)`` of tests/f16_ops.rs:7-19: f16-exact values in [-1, 1)."""
+    return f16_to_f32(to_f16(rvec(seed, n)))
 
 
 def normal(seed: int, shape, mean: float = 0.0, std: float = 1.0) -> np.ndarray:

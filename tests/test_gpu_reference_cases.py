@@ -17,7 +17,10 @@ closed form or CPU routine that test uses.
   1e-2, and n = 48 without bias, 2e-3, against float64 sums of the
   f16-rounded inputs stored as f16;
 - split_heads_merge_roundtrip (:241-274): (2, 5, 4, 8), exact;
-- the concat part of im2col_and_concat (:300-310): (3, 2) ++ (3, 3), exact.
+- the concat part of im2col_and_concat (:300-310): (3, 2) ++ (3, 3), exact;
+- tiled_add_broadcasts (tests/dense_kernels.rs:50-63): (3, 40) + a table
+  of 40 broadcast over rows, inputs from that file's rvec (:6-17), 1e-6
+  (one f32 add per element, so exact).
 """
 import math
 
@@ -134,3 +137,12 @@ def test_linear_f16_matches_cpu(ctx):
     want2 = acc[:, :n2].astype(np.float32).astype(np.float16).astype(np.float32)
     got2 = back(ctx.linear(dev(x), dev(np.ascontiguousarray(w[:n2])), None)).astype(np.float32)
     assert_close(got2, want2, 2e-3, "linear f16 n=48")
+
+
+def test_tiled_add_broadcasts(ctx):
+    n, block = 3, 40
+    x, t = O.rvec(2, n * block), O.rvec(3, block)
+    got = back(ctx.tiled_add(dev(x.reshape(n, block)), dev(t))).reshape(-1)
+    want = x + t[np.arange(n * block) % block]
+    assert_close(got, want, 1e-6, "tiled_add")
+    assert_bit_exact(got, want, "tiled_add (one f32 add)")

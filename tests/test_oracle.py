@@ -25,8 +25,10 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 
 # ------------------------------------------------------------------ inputs
 
-def _splitmix_py(seed, n, denom):
-    """SplitMix64 in plain Python ints (tests/kernels.rs:7-23)."""
+def _splitmix_py(seed, n, denom, last_xor=True):
+    """SplitMix64 in plain Python ints (tests/kernels.rs:7-23; with
+    ``last_xor=False`` the variant of tests/dense_kernels.rs:6-17, which
+    stops before ``z ^= z >> 31``)."""
     out, state = [], seed
     mask = (1 << 64) - 1
     for _ in range(n):
@@ -34,7 +36,8 @@ def _splitmix_py(seed, n, denom):
         z = state
         z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
         z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
-        z ^= z >> 31
+        if last_xor:
+            z ^= z >> 31
         v = np.float32(z >> 40) / np.float32(denom)
         out.append(np.float32(np.float32(v * np.float32(2.0)) - np.float32(1.0)))
     return np.array(out, np.float32)
@@ -48,6 +51,9 @@ def test_rng_matches_reference_splitmix():
     r = O.rvec_f16(7, 1000)
     want = _splitmix_py(7, 1000, 1 << 24).astype(np.float16).astype(np.float32)
     assert_bit_exact(r, want, "rvec f16")
+    d = O.rvec(2, 120)
+    assert_bit_exact(d, _splitmix_py(2, 120, 1 << 24, last_xor=False), "dense rvec")
+    assert d.min() >= -1.0 and d.max() < 1.0
 
 
 def test_normal_is_seeded_standard_normal():
