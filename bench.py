@@ -133,6 +133,11 @@ def parse():
     ap.add_argument("--counter-pair", action="store_true",
                     help="launch bias + GELU at this S (rows x 4096 f16) and its copy probe 8 "
                          "times each over rotating buffers, then exit (for rocprofv3 --pmc)")
+    ap.add_argument("--clock-trace", choices=["gelu", "pass"],
+                    help="sample the shader clock (a one-wave sampler on a second stream) "
+                         "during 16 bias + GELU launches at this S, 16 of its copy probe and 16 "
+                         "GELU again (gelu), or during 18 replays of the pass (pass); print "
+                         "per-launch times and the clock per phase, then exit")
     ap.add_argument("--summarize-pair", metavar="CSV", nargs="+",
                     help="print each counter's mean per dispatch for bias + GELU and its copy "
                          "probe, and their ratio, from --counter-pair counter_collection CSVs")
@@ -423,6 +428,8 @@ def load_ceiling():
     lib.hsc_run.restype = ctypes.c_int
     lib.hsc_run.argtypes = [ctypes.c_int, ctypes.c_int] + [ctypes.c_void_p] * 4 + \
         [ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p]
+    lib.hsc_clock.restype = ctypes.c_int
+    lib.hsc_clock.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
     return lib
 
 
@@ -1589,6 +1596,114 @@ def counter_pair(frames: int) -> None:
     print(json.dumps({"counter_pair": "done", "rows": rows, "cols": HIDDEN}), flush=True)
 
 
+def clock_trace(kind: str, frames: int) -> None:
+    """The shader clock while kernels run (bench_ceiling.hip's hsc_clock: a
+    one-wave sampler on a second stream records the shader-clock and 100 MHz
+    real-time counters every 10 us; one-sample markers on the kernels' own
+    stream delimit the phases). ``gelu``: bias + GELU on (frames * 1374,
+    4096) f16 launched 16 times, its copy probe (one vector per lane,
+    streaming) 16 times, GELU 16 times again, each launch between event
+    pairs; ``pass``: 18 replays of the fused-op pass's graph. Prints one JSON
+    line: per-phase launch times and clock (mean and minimum over 0.5 ms
+    windows) and the clock per window."""
+    import torch
+
+    from headshot_amd.context import HipContext
+
+    ctx = HipContext("cuda:0")
+    lib = load_ceiling()
+    dev = ctx.device
+    main = torch.cuda.current_stream()
+    step = 1000  # real-time ticks (10 us) between samples
+
+    def clock(buf, n, st, stp):
+        rc = lib.hsc_clock(buf.data_ptr(), n, stp, st.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"hsc_clock returned {rc}")
+
+    phases = []  # (label, thunk, launches)
+    if kind == "gelu":
+        rows = frames * (GRID[0] * GRID[1] + PREFIX)
+        nbytes = rows * HIDDEN * 4
+        g = torch.Generator(device="cpu").manual_seed(13)
+        sets = [(torch.randn((rows, HIDDEN), generator=g).half().to(dev),
+                 torch.empty((rows, HIDDEN), device=dev, dtype=torch.float16))
+                for _ in range(max(1, -(-ROTATE_BYTES // nbytes)))]
+        bias = (torch.randn(HIDDEN, generator=g) * 0.02).to(dev)
+        n16 = rows * HIDDEN * 2 // 16
+        count = [0]
+
+        def gelu():
+            x, o = sets[count[0] % len(sets)]
+            count[0] += 1
+            ctx.bias_gelu(x, bias, out=o)
+
+        def copy():
+            x, o = sets[count[0] % len(sets)]
+            count[0] += 1
+            rc = lib.hsc_run(KINDS["copy"], CEILING_SHAPES["streaming x1"], x.data_ptr(), None,
+                             o.data_ptr(), None, n16, 0, 0, main.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"hsc_run(copy) returned {rc}")
+
+        phases = [("bias_gelu", gelu, 16), ("copy probe", copy, 16), ("bias_gelu", gelu, 16)]
+        est_ms = 48 * nbytes / 4e9
+        what = {"rows": rows, "cols": HIDDEN, "bytes_per_launch": nbytes}
+    else:
+        b = Pass(ctx, frames, torch.float16, distinct=True)
+        b.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            b.run()
+        graph.replay()
+        torch.cuda.synchronize()
+        phases = [("pass", graph.replay, 18)]
+        est_ms = 18 * b.pass_bytes / 4e9
+        what = {"pass_bytes": b.pass_bytes}
+    for _, fn, _ in phases:
+        fn()
+    torch.cuda.synchronize()
+    n = int((est_ms + 20.0) * 100)  # samples, 10 us apart
+    samples = torch.zeros(2 * n, dtype=torch.int64, device=dev)
+    marks = torch.zeros(2 * (len(phases) + 1), dtype=torch.int64, device=dev)
+    side = torch.cuda.Stream(device=dev)
+    clock(samples, n, side, step)
+    torch.cuda._sleep(5_000_000)
+    events = []
+    for i, (label, fn, k) in enumerate(phases):
+        clock(marks[2 * i:], 1, main, 0)
+        evs = []
+        for _ in range(k):
+            a, e = KernelEvent(), KernelEvent()
+            a.record()
+            fn()
+            e.record()
+            evs.append((a, e))
+        events.append(evs)
+    clock(marks[2 * len(phases):], 1, main, 0)
+    torch.cuda.synchronize()
+    sm = samples.cpu().view(-1, 2).tolist()
+    mk = [r for _, r in marks.cpu().view(-1, 2).tolist()]
+    t0 = sm[0][1]
+    w = 50  # samples per 0.5 ms window
+    windows = []
+    for i in range(0, n - w, w):
+        (c0, r0), (c1, r1) = sm[i], sm[i + w]
+        windows.append(((r0 + r1) / 2, (c1 - c0) / ((r1 - r0) / 100.0)))
+    out_phases = []
+    for i, (label, _, k) in enumerate(phases):
+        inside = [mhz for r, mhz in windows if mk[i] <= r < mk[i + 1]]
+        us = [round(a.elapsed_time(e) * 1e3, 1) for a, e in events[i]]
+        out_phases.append({"phase": label, "launches": k, "start_ms": round((mk[i] - t0) / 1e5, 2),
+                           "end_ms": round((mk[i + 1] - t0) / 1e5, 2), "launch_us": us,
+                           "clock_mhz_mean": round(sum(inside) / len(inside)) if inside else None,
+                           "clock_mhz_min": round(min(inside)) if inside else None})
+    print(json.dumps({"clock_trace": kind, "frames": frames, **what, "phases": out_phases,
+                      "clock_mhz_per_0.5ms": [[round((r - t0) / 1e5, 2), round(m)]
+                                              for r, m in windows]}), flush=True)
+
+
 def summarize_pair(paths) -> None:
     """Mean per dispatch of every counter in the --counter-pair CSVs for the
     op and the probe, their ratio, and the kernel-trace duration; derived:
@@ -1638,6 +1753,9 @@ def main():
         return
     if args.summarize_pair:
         summarize_pair(args.summarize_pair)
+        return
+    if args.clock_trace:
+        clock_trace(args.clock_trace, args.frames)
         return
     if args.counter_pair:
         counter_pair(args.frames)

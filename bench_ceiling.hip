@@ -16,6 +16,9 @@
 //   inplace  1 read : 1 write of the same buffer   (rope_apply in place)
 //   add2w2 2 reads : 2 writes, contiguous          (bias_ls_residual_layernorm)
 //
+// Also a shader-clock sampler (hsc_clock) for timing kernels whose speed
+// follows the clock the chip's power management sets.
+//
 // Each kernel runs with non-temporal (streaming) or ordinary cached loads and
 // stores, the two policies the library's kernels use, and in two launch
 // shapes: four 16-byte vectors per lane (two whole rows per wave for heads)
@@ -277,9 +280,38 @@ int run(int kind, const void* a, const void* b, void* o, void* o2, int64_t n, in
     return static_cast<int>(hipGetLastError());
 }
 
+// Shader-clock samples: one wave records (s_memtime, s_memrealtime) n
+// times, each once the 100 MHz real-time counter has advanced by `step`
+// ticks since the previous sample, with vector stores from lane 0 (every
+// wait ends as the counter advances). On a second stream beside the kernels
+// under study, the two counters' advance between samples gives the shader
+// clock; with n = 1 and step = 0 on the kernels' own stream, one sample
+// marks a point of their sequence.
+__global__ __launch_bounds__(64) void clock_kernel(unsigned long long* out, int n, int step) {
+    for (int i = 0; i < n; i++) {
+        const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+        unsigned long long r = r0;
+        while (r - r0 < static_cast<unsigned long long>(step)) r = __builtin_amdgcn_s_memrealtime();
+        const unsigned long long c = __builtin_amdgcn_s_memtime();
+        if (threadIdx.x == 0) {
+            out[2 * i] = c;
+            out[2 * i + 1] = r;
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+// n samples of (shader clock count, 100 MHz real-time count) into out
+// (2n 64-bit values), step real-time ticks apart (clock_kernel). Returns 0,
+// -1 for an argument the kernel does not take, or the launch's HIP error.
+int hsc_clock(unsigned long long* out, int n, int step, hipStream_t stream) {
+    if (!out || n < 1 || step < 0) return -1;
+    clock_kernel<<<dim3(1), dim3(64), 0, stream>>>(out, n, step);
+    return static_cast<int>(hipGetLastError());
+}
 
 // kind 0 copy / 1 add2: n 16-byte vectors (a, b -> o). kind 2 heads: s
 // frames of t tokens, a and b -> o and o2. kind 3 cast: n f32 elements

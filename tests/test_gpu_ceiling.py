@@ -105,3 +105,22 @@ def test_kernel_event_times_what_torch_events_time():
         ms[name] = a.elapsed_time(b)
     assert ms["kernel"] > 0.5, ms  # a ~5 M-cycle wait is milliseconds long
     assert abs(ms["kernel"] - ms["torch"]) < 0.01 + 0.05 * ms["torch"], ms
+
+
+def test_clock_sampler(lib):
+    """hsc_clock's samples: the real-time counter advances by at least the
+    step between samples, the shader-clock counter advances too, and the
+    clock they imply lies between 0.3 and 5 GHz; bad arguments are refused."""
+    n, step = 64, 200  # 2 us apart
+    buf = torch.zeros(2 * n, dtype=torch.int64, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert lib.hsc_clock(buf.data_ptr(), n, step, st) == 0
+    torch.cuda.synchronize()
+    s = buf.cpu().view(-1, 2).tolist()
+    for (c0, r0), (c1, r1) in zip(s, s[1:]):
+        assert r1 - r0 >= step and c1 > c0
+    mhz = (s[-1][0] - s[0][0]) / ((s[-1][1] - s[0][1]) / 100.0)
+    assert 300 < mhz < 5000, mhz
+    assert lib.hsc_clock(buf.data_ptr(), 0, step, st) == -1
+    assert lib.hsc_clock(buf.data_ptr(), 1, -1, st) == -1
+    assert lib.hsc_clock(None, 1, 0, st) == -1
