@@ -133,11 +133,12 @@ def parse():
     ap.add_argument("--counter-pair", action="store_true",
                     help="launch bias + GELU at this S (rows x 4096 f16) and its copy probe 8 "
                          "times each over rotating buffers, then exit (for rocprofv3 --pmc)")
-    ap.add_argument("--clock-trace", choices=["gelu", "pass"],
+    ap.add_argument("--clock-trace", choices=["gelu", "pass", "matrix"],
                     help="sample the shader clock (a one-wave sampler on a second stream) "
                          "during 16 bias + GELU launches at this S, 16 of its copy probe and 16 "
-                         "GELU again (gelu), or during 18 replays of the pass (pass); print "
-                         "per-launch times and the clock per phase, then exit")
+                         "GELU again (gelu), during 18 replays of the pass (pass), or during "
+                         "this S's global and frame attention and fc1 with and without its GELU "
+                         "(matrix); print per-launch times and the clock per phase, then exit")
     ap.add_argument("--summarize-pair", metavar="CSV", nargs="+",
                     help="print each counter's mean per dispatch for bias + GELU and its copy "
                          "probe, and their ratio, from --counter-pair counter_collection CSVs")
@@ -1649,6 +1650,32 @@ def clock_trace(kind: str, frames: int) -> None:
         phases = [("bias_gelu", gelu, 16), ("copy probe", copy, 16), ("bias_gelu", gelu, 16)]
         est_ms = 48 * nbytes / 4e9
         what = {"rows": rows, "cols": HIDDEN, "bytes_per_launch": nbytes}
+    elif kind == "matrix":
+        t = GRID[0] * GRID[1] + PREFIX
+        g = torch.Generator(device="cpu").manual_seed(7)
+        att = {}
+        for name, (s_, tt) in {"global": (1, frames * t), "frame": (frames, t)}.items():
+            q, k, v = (torch.randn((s_, HEADS, tt, HEAD_DIM), generator=g).half().to(dev)
+                       for _ in range(3))
+            o = torch.empty((s_ * tt, HEADS * HEAD_DIM), dtype=torch.float16, device=dev)
+            ctx.attention_merged(q, k, v, out=o)
+            att[name] = (ctx.last_launch, 4.0 * tt * tt * HEAD_DIM * s_ * HEADS, (q, k, v, o))
+        m = frames * t
+        x = torch.randn((m, DIM), generator=g).half().to(dev)
+        w = (torch.randn((HIDDEN, DIM), generator=g) / DIM ** 0.5).half().to(dev)
+        bias = (torch.randn(HIDDEN, generator=g) * 0.02).to(dev)
+        o1 = torch.empty((m, HIDDEN), dtype=torch.float16, device=dev)
+        ctx.linear(x, w, bias, out=o1)
+        fc1 = ctx.last_launch
+        ctx.linear_gelu(x, w, bias, out=o1)
+        fc1_gelu = ctx.last_launch
+        lin_flops = 2.0 * m * HIDDEN * DIM
+        phases = [("global attention", att["global"][0], 6), ("frame attention", att["frame"][0], 40),
+                  ("fc1, bias", fc1, 40), ("fc1 + GELU", fc1_gelu, 40)]
+        flops = {"global attention": att["global"][1], "frame attention": att["frame"][1],
+                 "fc1, bias": lin_flops, "fc1 + GELU": lin_flops}
+        est_ms = 6 * 9.0 + 40 * 0.4 + 80 * 0.5
+        what = {"tokens": m}
     else:
         b = Pass(ctx, frames, torch.float16, distinct=True)
         b.run()
@@ -1695,10 +1722,19 @@ def clock_trace(kind: str, frames: int) -> None:
     for i, (label, _, k) in enumerate(phases):
         inside = [mhz for r, mhz in windows if mk[i] <= r < mk[i + 1]]
         us = [round(a.elapsed_time(e) * 1e3, 1) for a, e in events[i]]
-        out_phases.append({"phase": label, "launches": k, "start_ms": round((mk[i] - t0) / 1e5, 2),
-                           "end_ms": round((mk[i + 1] - t0) / 1e5, 2), "launch_us": us,
-                           "clock_mhz_mean": round(sum(inside) / len(inside)) if inside else None,
-                           "clock_mhz_min": round(min(inside)) if inside else None})
+        entry = {"phase": label, "launches": k, "start_ms": round((mk[i] - t0) / 1e5, 2),
+                 "end_ms": round((mk[i + 1] - t0) / 1e5, 2), "launch_us": us,
+                 "clock_mhz_mean": round(sum(inside) / len(inside)) if inside else None,
+                 "clock_mhz_min": round(min(inside)) if inside else None}
+        if kind == "matrix" and inside:
+            # the phase's rate against the dense f16 peak (quoted at 2.4
+            # GHz) and against that peak scaled to the clock it ran at
+            tf = flops[label] / (sum(us) / len(us) * 1e-6) / 1e12
+            at_clock = MFMA_PEAK_TFLOPS * entry["clock_mhz_mean"] / 2400.0
+            entry.update({"TFLOP/s": round(tf, 1), "frac": round(tf / MFMA_PEAK_TFLOPS, 4),
+                          "peak_at_clock_TFLOP/s": round(at_clock, 1),
+                          "frac_at_clock": round(tf / at_clock, 4)})
+        out_phases.append(entry)
     print(json.dumps({"clock_trace": kind, "frames": frames, **what, "phases": out_phases,
                       "clock_mhz_per_0.5ms": [[round((r - t0) / 1e5, 2), round(m)]
                                               for r, m in windows]}), flush=True)
