@@ -26,7 +26,13 @@ namespace {
 // thread (S=32: 117.3 us against 120.8 for 64 workgroups per CU, ~5
 // visits, and 118.0-119.7 for 96-176 workgroups per CU or three or four
 // visits; 130 for 256 per CU, 157 for one visit in a one-shot grid),
-// LayerScale with 32 workgroups per CU (~3 visits). GELU must keep
+// LayerScale with 32 workgroups per CU (~3 visits) while one of its
+// streams fits in half the 256 MB Infinity Cache (S=32: 90 MB), and with
+// two visits per thread beyond that: 32 workgroups per CU give a thread ~17
+// visits at S=200, and there the two-visit grid runs 268 against 332 us
+// (79% against 63% of peak; S=48 65 against 67 us, S=100 131 against 145,
+// S=140 184 against 214), while at S=32 it leaves the op's own time alone
+// and makes the pass 0.7% slower. GELU must keep
 // non-temporal stores, because with plain stores its output occupies the
 // cache and the LayerNorm after it slows by a third.
 #ifndef HS_GELU_U
@@ -51,7 +57,13 @@ namespace {
 #define HS_LS_BPC 32
 #endif
 #ifndef HS_LS_ITERS
-#define HS_LS_ITERS 0
+#define HS_LS_ITERS 0  // > 0: visits per thread at every size
+#endif
+#ifndef HS_LS_BIG_BYTES
+#define HS_LS_BIG_BYTES (int64_t{128} << 20)  // one stream's bytes above which...
+#endif
+#ifndef HS_LS_BIG_ITERS
+#define HS_LS_BIG_ITERS 2  // ...the grid gives each thread this many visits (0: never)
 #endif
 #ifndef HS_LS_NTS
 #define HS_LS_NTS (HS_NT != 0)  // non-temporal stores of the LayerScale + residual output
@@ -80,6 +92,10 @@ int64_t column_stationary_blocks(int64_t total, int64_t cols, int V, int U, int 
     int64_t blocks = want < cap ? want : cap;
     blocks = ceil_div(blocks, step) * step;
     if (blocks > 4 * cap) return 0;
+    // a launch holds fewer than 2^32 work-items; the grid-stride loop
+    // covers what a smaller grid leaves
+    const int64_t limit = ((int64_t{1} << 32) - 1) / kBlock;
+    if (blocks > limit) blocks = (limit / step) * step;
     return blocks;
 }
 
@@ -338,10 +354,14 @@ hs_status launch_ls(hipStream_t st, const void* res, const void* x, const float*
     const int64_t total = rows * cols;
     const bool vec_ok = cols % V == 0 && aligned16(res) && aligned16(x) && aligned16(out) &&
                         aligned16(gamma) && (!bias || aligned16(bias));
+    const int iters = HS_LS_ITERS > 0 ? HS_LS_ITERS
+                      : HS_LS_BIG_ITERS > 0 && total * static_cast<int64_t>(sizeof(T)) > HS_LS_BIG_BYTES
+                          ? HS_LS_BIG_ITERS
+                          : 0;
     const int64_t blocks =
         !vec_ok ? 0
-        : HS_LS_ITERS > 0 ? column_stationary_blocks(total, cols, V, U * HS_LS_ITERS, 1 << 16)
-                          : column_stationary_blocks(total, cols, V, U, HS_LS_BPC);
+        : iters > 0 ? column_stationary_blocks(total, cols, V, U * iters, 1 << 16)
+                    : column_stationary_blocks(total, cols, V, U, HS_LS_BPC);
     if (blocks > 0) {
         if (bias)
             bias_ls_kernel<T, true, U><<<dim3(static_cast<uint32_t>(blocks)), dim3(kBlock), 0, st>>>(

@@ -312,6 +312,30 @@ def test_bias_ls_residual(ctx, dtype, rows, dim, with_bias, gamma_kind):
     check(got, O.bias_ls_residual(res, x, b, g), f"bias_ls_residual {dtype} {rows}x{dim}")
 
 
+@pytest.mark.parametrize("dtype,rows", [(torch.float16, 70000), (torch.float32, 40000)])
+def test_bias_ls_residual_large_grid(ctx, dtype, rows):
+    """Above 128 MiB per stream the launch gives each thread two visits
+    instead of a fixed workgroup count per CU: the whole tensor (that grid)
+    equals its two halves (each below the threshold, the other grid) bit for
+    bit, and sampled rows match the oracle."""
+    print(f"[bias_ls_residual large grid: {dtype} rows={rows}]", flush=True)
+    dim = 1024
+    g = torch.Generator(device="cuda").manual_seed(rows)
+    res = torch.randn((rows, dim), device="cuda", generator=g).to(dtype)
+    x = torch.randn((rows, dim), device="cuda", generator=g).to(dtype)
+    gam = torch.randn(dim, device="cuda", generator=g)
+    b = torch.randn(dim, device="cuda", generator=g) * 0.02
+    whole = ctx.bias_ls_residual(res, x, gam, b)
+    h = rows // 2
+    halves = torch.cat([ctx.bias_ls_residual(res[:h], x[:h], gam, b),
+                        ctx.bias_ls_residual(res[h:], x[h:], gam, b)])
+    torch.cuda.synchronize()
+    assert torch.equal(whole, halves)
+    pick = torch.tensor([0, 1, h - 1, h, rows - 2, rows - 1], device="cuda")
+    want = O.bias_ls_residual(back(res[pick]), back(x[pick]), back(b), back(gam))
+    check(back(whole[pick]), want, f"bias_ls_residual large grid {dtype}")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_residual_ls_surface_in_place(ctx, dtype):
     res = host(O.normal(65, (40, 1024)), dtype)
