@@ -610,6 +610,42 @@ def ceiling_times(bench: Pass, op_warm: dict, op_cold: dict, flush, iters: int =
     return out
 
 
+def gelu_in_pass_probe_us(bench: Pass, passes: int) -> float | None:
+    """The copy probe (one 16-byte vector per lane, streaming: its fastest
+    shape) launched in place of every bias + GELU of the pass, on the same
+    fc1-output and activation buffers, timed as the ops are
+    (per_op_times): the op's ceiling in the op's own context (after the
+    same LayerNorm, before the same LayerScale), where the probe loop of
+    ceiling_times runs it back to back."""
+    if not os.path.exists(CEILING_LIB):
+        return None
+    import torch
+
+    lib = load_ceiling()
+    stream = torch.cuda.current_stream().cuda_stream
+    fp, act = bench.fp, bench.fp.io.act
+    esz = act.element_size()
+    seq, k = [], 0
+    for op, thunk in bench.seq:
+        if op == "bias_gelu":
+            x = fp.raws[k][3]
+            k += 1
+
+            def thunk(x=x, n16=x.numel() * esz // 16):
+                rc = lib.hsc_run(KINDS["copy"], CEILING_SHAPES["streaming x1"], x.data_ptr(), None,
+                                 act.data_ptr(), None, n16, 0, 0, stream)
+                if rc != 0:
+                    raise RuntimeError(f"hsc_run(copy) returned {rc}")
+        seq.append((op, thunk))
+    saved = bench.seq
+    bench.seq = seq
+    try:
+        t = per_op_times(bench, passes)
+    finally:
+        bench.seq = saved
+    return t["bias_gelu"] * 1e3
+
+
 def attention_times(ctx, frames: int, iters: int) -> dict:
     """The aggregator's attention calls at this S, fused with the head merge
     (hs_attention_merged, as model/block.rs:148-149 consumes it): frame
@@ -1859,6 +1895,12 @@ def main():
         per_op_cold = op_rates(bench, per_op_times(bench, args.op_passes, flush=flush))
         if not args.no_ceilings:
             ceilings = ceiling_times(bench, per_op, per_op_cold, flush)
+            if "bias_gelu" in ceilings:
+                pus = gelu_in_pass_probe_us(bench, args.op_passes)
+                if pus:
+                    ceilings["bias_gelu"]["in_pass_probe_us"] = round(pus, 2)
+                    ceilings["bias_gelu"]["op_frac_of_in_pass_probe"] = round(
+                        pus / per_op["bias_gelu"]["us"], 4)
         pass_cold = pass_from_ops(bench, per_op_cold)
         if not args.no_workloads:
             workloads = workload_legs(ctx, args.op_passes, flush)
