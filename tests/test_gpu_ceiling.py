@@ -124,3 +124,16 @@ def test_clock_sampler(lib):
     assert lib.hsc_clock(buf.data_ptr(), 0, step, st) == -1
     assert lib.hsc_clock(buf.data_ptr(), 1, -1, st) == -1
     assert lib.hsc_clock(None, 1, 0, st) == -1
+
+
+def test_gelu_in_pass_probe(ctx):
+    """bench.gelu_in_pass_probe_us swaps the copy probe in for every bias +
+    GELU of a pass, times it, and leaves the pass's own launch sequence in
+    place."""
+    b = bench.Pass(ctx, 2, torch.float16, distinct=True)
+    seq = b.seq
+    us = bench.gelu_in_pass_probe_us(b, 1)
+    assert us is not None and 0 < us < 1e4
+    assert b.seq is seq
+    b.run()
+    torch.cuda.synchronize()
