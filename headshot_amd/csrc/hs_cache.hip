@@ -194,6 +194,7 @@ extern "C" hs_status hs_cast_f16_to_f32(hs_stream_t stream, const void* x, float
                                         int64_t total) {
     using namespace hs;
     if (total < 0) return fail(HS_EINVAL, "cast_f16_to_f32: negative length");
+    if (total >= kMaxElems) return fail(HS_EINVAL, "cast_f16_to_f32: tensor too large");
     if (total == 0) return HS_OK;
     if (!x || !out) return fail(HS_EINVAL, "cast_f16_to_f32: null buffer");
     if (overlaps(out, total * 4, x, total * 2)) return fail(HS_EINVAL, "cast_f16_to_f32: out overlaps x");

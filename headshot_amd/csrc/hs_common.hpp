@@ -37,6 +37,11 @@ inline int64_t dtype_size(hs_dtype dt) { return dt == HS_F16 ? 2 : 4; }
 
 inline bool valid_dtype(hs_dtype dt) { return dt == HS_F32 || dt == HS_F16; }
 
+// Tensors of 2^40 elements or more are refused, so that byte counts and
+// offsets stay far inside int64_t (rows and cols non-negative).
+constexpr int64_t kMaxElems = int64_t{1} << 40;
+inline bool too_large(int64_t rows, int64_t cols) { return cols > 0 && rows >= kMaxElems / cols; }
+
 // ---------------------------------------------------------------------------
 // device: storage types and 16-byte vectors
 

@@ -395,6 +395,7 @@ hs_status hs_bias_gelu(hs_stream_t stream, hs_dtype dt, const void* x, const flo
     if (!valid_dtype(dt)) return fail(HS_EINVAL, "bias_gelu: unknown dtype %d", (int)dt);
     if (rows < 0 || cols <= 0)
         return fail(HS_EINVAL, "bias_gelu: rows %lld / cols %d", (long long)rows, cols);
+    if (too_large(rows, cols)) return fail(HS_EINVAL, "bias_gelu: tensor too large");
     if (rows == 0) return HS_OK;
     if (!x || !out) return fail(HS_EINVAL, "bias_gelu: null buffer");
     if (bad_alias(x, out, rows * cols * dtype_size(dt)))
@@ -420,6 +421,7 @@ hs_status hs_bias_ls_residual(hs_stream_t stream, hs_dtype dt, const void* res, 
     if (!valid_dtype(dt)) return fail(HS_EINVAL, "bias_ls_residual: unknown dtype %d", (int)dt);
     if (rows < 0 || dim <= 0)
         return fail(HS_EINVAL, "bias_ls_residual: rows %lld / dim %d", (long long)rows, dim);
+    if (too_large(rows, dim)) return fail(HS_EINVAL, "bias_ls_residual: tensor too large");
     if (rows == 0) return HS_OK;
     if (!res || !x || !gamma || !out) return fail(HS_EINVAL, "bias_ls_residual: null buffer");
     const int64_t bytes = rows * dim * dtype_size(dt);
@@ -443,6 +445,7 @@ hs_status hs_residual_ls(hs_stream_t stream, hs_dtype dt, const void* res, const
 hs_status hs_cast_f32_to_f16(hs_stream_t stream, const float* x, void* out, int64_t total) {
     using namespace hs;
     if (total < 0) return fail(HS_EINVAL, "cast_f32_to_f16: negative length");
+    if (total >= kMaxElems) return fail(HS_EINVAL, "cast_f32_to_f16: tensor too large");
     if (total == 0) return HS_OK;
     if (!x || !out) return fail(HS_EINVAL, "cast_f32_to_f16: null buffer");
     if (overlaps(x, total * 4, out, total * 2))
@@ -464,6 +467,7 @@ hs_status hs_tiled_add(hs_stream_t stream, const float* x, const float* table, f
                        int64_t total, int64_t block) {
     using namespace hs;
     if (total < 0 || block <= 0) return fail(HS_EINVAL, "tiled_add: total / block");
+    if (total >= kMaxElems) return fail(HS_EINVAL, "tiled_add: tensor too large");
     if (total % block != 0)
         return fail(HS_EINVAL, "tiled_add: table of %lld does not tile %lld elements",
                     (long long)block, (long long)total);

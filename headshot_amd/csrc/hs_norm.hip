@@ -478,6 +478,7 @@ extern "C" hs_status hs_layernorm(hs_stream_t stream, hs_dtype dt, const void* x
     if (!valid_dtype(dt)) return fail(HS_EINVAL, "layernorm: unknown dtype %d", (int)dt);
     if (rows < 0 || dim <= 0)
         return fail(HS_EINVAL, "layernorm: rows %lld / dim %d", (long long)rows, dim);
+    if (too_large(rows, dim)) return fail(HS_EINVAL, "layernorm: tensor too large");
     if (rows == 0) return HS_OK;
     if (!x || !w || !b || !out) return fail(HS_EINVAL, "layernorm: null buffer");
     const int64_t bytes = rows * dim * dtype_size(dt);
@@ -494,6 +495,7 @@ extern "C" hs_status hs_layernorm_stats(hs_stream_t stream, hs_dtype dt, const v
     if (!valid_dtype(dt)) return fail(HS_EINVAL, "layernorm_stats: unknown dtype %d", (int)dt);
     if (rows < 0 || dim <= 0)
         return fail(HS_EINVAL, "layernorm_stats: rows %lld / dim %d", (long long)rows, dim);
+    if (too_large(rows, dim)) return fail(HS_EINVAL, "layernorm_stats: tensor too large");
     if (rows == 0) return HS_OK;
     if (!x || !stats) return fail(HS_EINVAL, "layernorm_stats: null buffer");
     if (reinterpret_cast<uintptr_t>(stats) % 8 != 0)
@@ -514,6 +516,7 @@ extern "C" hs_status hs_bias_ls_residual_layernorm(hs_stream_t stream, hs_dtype 
     const char* op = "bias_ls_residual_layernorm";
     if (!valid_dtype(dt)) return fail(HS_EINVAL, "%s: unknown dtype %d", op, (int)dt);
     if (rows < 0 || dim <= 0) return fail(HS_EINVAL, "%s: rows %lld / dim %d", op, (long long)rows, dim);
+    if (too_large(rows, dim)) return fail(HS_EINVAL, "%s: tensor too large", op);
     if (rows == 0) return HS_OK;
     if (!res || !x || !gamma || !ln_w || !ln_b || !out || !normed)
         return fail(HS_EINVAL, "%s: null buffer", op);

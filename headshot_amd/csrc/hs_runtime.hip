@@ -66,6 +66,10 @@ hs_status hs_copy_rows(hs_stream_t stream, const void* src, int64_t src_row, voi
     if (n_rows < 0 || row_bytes < 0 || src_row < 0 || dst_row < 0)
         return hs::fail(HS_EINVAL, "copy_rows: negative row index, count or width");
     if (n_rows == 0 || row_bytes == 0) return HS_OK;
+    // every byte offset below stays under 2^50
+    const int64_t lim = (int64_t{1} << 49) / row_bytes;
+    if (n_rows > lim || src_row > lim || dst_row > lim)
+        return hs::fail(HS_EINVAL, "copy_rows: rows or width too large");
     if (!src || !dst) return hs::fail(HS_EINVAL, "copy_rows: null buffer");
     const int64_t bytes = n_rows * row_bytes;
     const char* s = static_cast<const char*>(src) + src_row * row_bytes;

@@ -125,6 +125,27 @@ def test_elementwise_contracts():
     assert L.hs_gelu(None, F16, None, None, 0) == _lib.HS_OK
 
 
+def test_size_limits():
+    """Tensors of 2^40 elements or more are refused before anything is
+    launched (byte counts and offsets then stay far inside 64 bits)."""
+    big = 1 << 31  # rows; x 1024 columns = 2^41 elements
+    _einval(L.hs_layernorm(None, F16, FAKE, FAKE, FAKE, FAKE2, big, 1024, 1e-5), "too large")
+    _einval(L.hs_layernorm_stats(None, F16, FAKE, FAKE2, big, 1024, 1e-5), "too large")
+    _einval(L.hs_bias_ls_residual_layernorm(None, F16, FAKE, FAKE, None, FAKE, FAKE, FAKE, FAKE2,
+                                            FAKE2, big, 1024, 1e-5), "too large")
+    _einval(L.hs_bias_gelu(None, F16, FAKE, None, FAKE2, big, 4096), "too large")
+    _einval(L.hs_gelu(None, F16, FAKE, FAKE2, 1 << 41), "too large")
+    _einval(L.hs_bias_ls_residual(None, F16, FAKE, FAKE, None, FAKE, FAKE2, big, 1024),
+            "too large")
+    _einval(L.hs_cast_f32_to_f16(None, FAKE, FAKE2, 1 << 40), "too large")
+    _einval(L.hs_cast_f16_to_f32(None, FAKE, FAKE2, 1 << 40), "too large")
+    _einval(L.hs_tiled_add(None, FAKE, FAKE2, FAKE, 1 << 40, 1024), "too large")
+    _einval(L.hs_copy_rows(None, FAKE, 0, FAKE2, 0, 1 << 40, 2048), "too large")
+    _einval(L.hs_copy_rows(None, FAKE, 1 << 40, FAKE2, 0, 4, 2048), "too large")
+    # just below the limit the checks pass on to the next one (null buffers)
+    _einval(L.hs_layernorm(None, F16, None, FAKE, FAKE, FAKE2, (1 << 30) - 1, 1024, 1e-5), "null")
+
+
 def test_assemble_contract():
     a = L.hs_assemble_tokens
     _einval(a(None, F16, FAKE, F32, None, None, FAKE2, FAKE2, FAKE, 2, 6, 4, 1024, 3), "n_var")
