@@ -27,6 +27,8 @@
  *    library does not implement. hs_last_error() gives the message. Nothing
  *    is enqueued when a call fails validation.
  *  - Zero-sized work (rows == 0, S == 0, ...) is a valid no-op.
+ *  - Tensors of 2^40 elements or more are refused with HS_EINVAL (several
+ *    entry points also keep row or token counts below 2^31, as noted).
  *  - Calls are reentrant; calls on one stream execute in order.
  */
 #ifndef HEADSHOT_HIP_H
