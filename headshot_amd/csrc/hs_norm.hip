@@ -164,6 +164,12 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
 #ifndef HS_LSLN_BPC
 #define HS_LSLN_BPC 0  // its workgroups per CU (a persistent grid); 0: one wave per U rows
 #endif
+// Above this many bytes per stream no reader finds out or res in the 256 MB
+// Infinity Cache anyway, and all four streams go non-temporal (S=200,
+// 563 MB per stream: 368-390 against 397-411 us in the four-op sequence).
+#ifndef HS_LSLN_BIG_BYTES
+#define HS_LSLN_BIG_BYTES (int64_t{128} << 20)
+#endif
 
 // LayerScale + residual, then the LayerNorm of its output
 // (hs_bias_ls_residual_layernorm): the pre-norm block stores x1 = res +
@@ -174,7 +180,7 @@ __global__ __launch_bounds__(kBlock) void ln_vec_kernel(const T* x, const float*
 // (rounded) values by the same moments and affine as ln_vec_kernel, so out
 // and normed are bit-identical to hs_bias_ls_residual then hs_layernorm.
 // Each row is read once (res and x) and written twice (out and normed).
-template <typename T, int CHUNKS, int U, bool BIAS>
+template <typename T, int CHUNKS, int U, bool BIAS, bool BIG>
 __global__ __launch_bounds__(kBlock) void ls_ln_kernel(const T* res, const T* x,
                                                        const float* __restrict__ bias,
                                                        const float* __restrict__ gamma,
@@ -213,8 +219,8 @@ __global__ __launch_bounds__(kBlock) void ls_ln_kernel(const T* res, const T* x,
                 const int64_t off = (r0 + u) * DIM + lane * V;
 #pragma unroll
                 for (int c = 0; c < CHUNKS; c++) {
-                    rr[u][c] = ld_stream<HS_LSLN_NT_RES != 0>(res + off + c * 64 * V);
-                    xr[u][c] = ld_stream<HS_LSLN_NT_X != 0>(x + off + c * 64 * V);
+                    rr[u][c] = ld_stream<BIG || HS_LSLN_NT_RES != 0>(res + off + c * 64 * V);
+                    xr[u][c] = ld_stream<BIG || HS_LSLN_NT_X != 0>(x + off + c * 64 * V);
                 }
             }
         }
@@ -235,7 +241,7 @@ __global__ __launch_bounds__(kBlock) void ls_ln_kernel(const T* res, const T* x,
                     fr[k] = ls_affine(fr[k], gr[c][k], v);
                 }
                 const u32x4 o = pack(fr, T{});
-                st_stream<HS_LSLN_NT_OUT != 0>(out + off + c * 64 * V, o);
+                st_stream<BIG || HS_LSLN_NT_OUT != 0>(out + off + c * 64 * V, o);
                 unpack(o, f[c], T{});  // the stored value, as hs_layernorm reads it
             }
             float mean, inv;
@@ -245,7 +251,7 @@ __global__ __launch_bounds__(kBlock) void ls_ln_kernel(const T* res, const T* x,
                 float y[V];
 #pragma unroll
                 for (int k = 0; k < V; k++) y[k] = ln_affine(f[c][k], mean, inv, wr[c][k], br[c][k]);
-                st_stream<HS_LSLN_NT_NORMED != 0>(normed + off + c * 64 * V, pack(y, T{}));
+                st_stream<BIG || HS_LSLN_NT_NORMED != 0>(normed + off + c * 64 * V, pack(y, T{}));
             }
         }
     }
@@ -431,15 +437,16 @@ bool launch_ls_ln(hipStream_t st, const void* res, const void* x, const float* b
     const T* X = static_cast<const T*>(x);
     T* O = static_cast<T*>(out);
     T* N = static_cast<T*>(normed);
-#define HS_LS_LN(C)                                                                               \
-    (bias ? (ls_ln_kernel<T, C, U, true><<<grid, dim3(kBlock), 0, st>>>(R, X, bias, gamma, w, b, O, \
-                                                                         N, rows, eps), 0)       \
-          : (ls_ln_kernel<T, C, U, false><<<grid, dim3(kBlock), 0, st>>>(R, X, bias, gamma, w, b, \
-                                                                          O, N, rows, eps), 0))
+    const bool big = rows * dim * static_cast<int64_t>(sizeof(T)) > HS_LSLN_BIG_BYTES;
+#define HS_LS_LN(C, G)                                                                            \
+    (bias ? (ls_ln_kernel<T, C, U, true, G><<<grid, dim3(kBlock), 0, st>>>(R, X, bias, gamma, w, b, \
+                                                                            O, N, rows, eps), 0)  \
+          : (ls_ln_kernel<T, C, U, false, G><<<grid, dim3(kBlock), 0, st>>>(R, X, bias, gamma, w, \
+                                                                             b, O, N, rows, eps), 0))
     switch (chunks) {
-        case 1: HS_LS_LN(1); break;
-        case 2: HS_LS_LN(2); break;
-        default: HS_LS_LN(4); break;
+        case 1: big ? HS_LS_LN(1, true) : HS_LS_LN(1, false); break;
+        case 2: big ? HS_LS_LN(2, true) : HS_LS_LN(2, false); break;
+        default: big ? HS_LS_LN(4, true) : HS_LS_LN(4, false); break;
     }
 #undef HS_LS_LN
     return true;

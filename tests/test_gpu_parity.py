@@ -377,6 +377,28 @@ def test_bias_ls_residual_layernorm(ctx, dtype, rows, dim, with_bias):
     check(back(normed), O.layernorm(want_x1, lw, lb, 1e-6), what + " chain vs oracle", stages=2)
 
 
+@pytest.mark.parametrize("dtype,rows", [(torch.float16, 70000), (torch.float32, 40000)])
+def test_bias_ls_residual_layernorm_large(ctx, dtype, rows):
+    """Above 128 MiB per stream the fused kernel streams all four tensors
+    (non-temporal loads and stores): still bit-identical to the two single
+    ops, which take their own large-tensor launch shapes."""
+    print(f"[bias_ls_residual_layernorm large: {dtype} rows={rows}]", flush=True)
+    dim = 1024
+    g = torch.Generator(device="cuda").manual_seed(rows + 1)
+    res = torch.randn((rows, dim), device="cuda", generator=g).to(dtype)
+    x = torch.randn((rows, dim), device="cuda", generator=g).to(dtype)
+    gam = torch.randn(dim, device="cuda", generator=g)
+    b = torch.randn(dim, device="cuda", generator=g) * 0.02
+    lw = 1.0 + 0.02 * torch.randn(dim, device="cuda", generator=g)
+    lb = 0.02 * torch.randn(dim, device="cuda", generator=g)
+    out, normed = ctx.bias_ls_residual_layernorm(res, x, gam, b, (lw, lb), eps=1e-6)
+    x1 = ctx.bias_ls_residual(res, x, gam, b)
+    n2 = ctx.layernorm(x1, lw, lb, eps=1e-6)
+    torch.cuda.synchronize()
+    assert torch.equal(out, x1)
+    assert torch.equal(normed, n2)
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_bias_ls_residual_layernorm_in_place(ctx, dtype):
     """out may be res (the residual stream updated in place)."""
