@@ -137,3 +137,21 @@ def test_gelu_in_pass_probe(ctx):
     assert b.seq is seq
     b.run()
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("kind", ["gelu", "matrix"])
+def test_clock_trace_runs(ctx, capsys, kind):
+    """bench.py --clock-trace at a small S: one JSON line with every phase,
+    its launch times and a shader clock between 0.3 and 5 GHz."""
+    import json
+
+    bench.clock_trace(kind, 2)
+    line = capsys.readouterr().out.strip().splitlines()[-1]
+    d = json.loads(line)
+    assert d["clock_trace"] == kind and d["frames"] == 2
+    assert len(d["phases"]) == (3 if kind == "gelu" else 4)
+    for p in d["phases"]:
+        assert len(p["launch_us"]) == p["launches"] and min(p["launch_us"]) > 0
+        assert p["end_ms"] >= p["start_ms"]
+    mhz = [m for _, m in d["clock_mhz_per_0.5ms"]]
+    assert mhz and 300 < min(mhz) and max(mhz) < 5000
