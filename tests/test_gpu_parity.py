@@ -312,14 +312,15 @@ def test_bias_ls_residual(ctx, dtype, rows, dim, with_bias, gamma_kind):
     check(got, O.bias_ls_residual(res, x, b, g), f"bias_ls_residual {dtype} {rows}x{dim}")
 
 
-@pytest.mark.parametrize("dtype,rows", [(torch.float16, 70000), (torch.float32, 40000)])
-def test_bias_ls_residual_large_grid(ctx, dtype, rows):
+@pytest.mark.parametrize("dtype,rows,dim", [(torch.float16, 70000, 1024), (torch.float32, 40000, 1024),
+                                            (torch.float16, 20000, 4096), (torch.float16, 90000, 768),
+                                            (torch.float32, 30000, 1200)])
+def test_bias_ls_residual_large_grid(ctx, dtype, rows, dim):
     """Above 128 MiB per stream the launch gives each thread two visits
     instead of a fixed workgroup count per CU: the whole tensor (that grid)
     equals its two halves (each below the threshold, the other grid) bit for
     bit, and sampled rows match the oracle."""
-    print(f"[bias_ls_residual large grid: {dtype} rows={rows}]", flush=True)
-    dim = 1024
+    print(f"[bias_ls_residual large grid: {dtype} rows={rows} dim={dim}]", flush=True)
     g = torch.Generator(device="cuda").manual_seed(rows)
     res = torch.randn((rows, dim), device="cuda", generator=g).to(dtype)
     x = torch.randn((rows, dim), device="cuda", generator=g).to(dtype)
