@@ -28,8 +28,13 @@
 // stores drain that burst faster than write-allocating ones (fc1 + GELU at
 // S=32: 494 us against 523).
 //
-// Generic path (f32, or shapes the fast path does not cover): a tiled
-// scalar kernel, f32 accumulation in K order.
+// f32 (N % 128 == 0, K % 32 == 0; every epilogue but the q|k|v split, with
+// or without the LayerNorm prologue): the same arrangement on the f32
+// matrix cores in 128 x 128 tiles, the epilogue stored straight from the
+// accumulators.
+//
+// Generic path (the shapes neither covers): a tiled scalar kernel, f32
+// accumulation in K order.
 #include <math.h>
 
 #include <initializer_list>
@@ -627,6 +632,276 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// f32 matrix-core path (f32, N % 128 == 0, K % 32 == 0): v_mfma_f32_32x32x2_f32
+// in the f16 kernel's arrangement. A workgroup of WAVES waves in 2 row
+// groups computes a (2 WROWS) x (32 WAVES) tile, each wave WROWS rows x 64
+// columns as out^T blocks of 32 x 32; K in stages of 32 floats through LDS,
+// double-buffered and filled by LDS-DMA. A stage row is 128 bytes (8
+// chunks of 4 floats) with the f16 kernel's swizzle: logical chunk c of row
+// r sits at physical chunk c ^ ((r / 2) % 8). In slice ks of a stage lane
+// (l32, hh) reads logical chunk 2 ks + hh (floats 8 ks + 4 hh .. + 4) of its
+// rows, and MFMA j of the slice takes element j of both operands: it sums
+// k = 8 ks + j (lanes hh = 0) and 8 ks + 4 + j (hh = 1), so the four MFMAs
+// of a slice cover its 8 k. The epilogue stores from the accumulators:
+// register quad r4 of lane (l32, hh) is 4 consecutive columns of one row
+// (16 bytes; the lane pair's quads are 32 contiguous bytes, and the wave's
+// four r4 complete the row's 128 bytes of the block).
+//
+// The shape used, F32Shape: 4 waves, 128 x 128 tiles, 64 KiB of LDS, two
+// workgroups per CU. It beats 8 waves in 256 x 256 tiles (128 KiB, one per
+// CU) at every trunk shape, by 6-9% at S=32 (43968 x 4096 x 1024: 2716 us
+// against 2873) and by 3x where 256 x 256 tiles are too few to fill the
+// chip (2748 x 1024 x 4096, 44 of them: 286 us against 925).
+template <int WAVES, int WROWS>
+struct F32Tile {
+    static constexpr int kWaves = WAVES, kThreads = 64 * WAVES;
+    static constexpr int kBM = 2 * WROWS, kBN = 32 * WAVES;
+    static constexpr int kBK = 32;                      // floats per stage row
+    static constexpr int kXI = kBM * 8 / 64 / WAVES;    // LDS-DMA instructions per wave, x stage
+    static constexpr int kWI = kBN * 8 / 64 / WAVES;    // w stage
+    static constexpr int kRB = WROWS / 32;              // 32-row blocks per wave
+    static constexpr int kWavesPerEu = 8 / WAVES;
+    static_assert(kXI * 64 * WAVES == kBM * 8 && kWI * 64 * WAVES == kBN * 8, "stage split");
+};
+using F32Shape = F32Tile<4, 64>;
+
+template <typename P>
+struct F32Smem {
+    float x[2][P::kBM * P::kBK];
+    float w[2][P::kBN * P::kBK];
+};
+static_assert(2 * sizeof(F32Smem<F32Shape>) <= 160 * 1024, "two workgroups per CU");
+
+// Per-lane byte offsets of a wave's stage loads (4 instructions each for
+// x and w): instruction i of wave wv brings rows
+// 8 (wv + waves i) .. + 8, lane L row + L / 8 at physical chunk L % 8; x
+// rows past M read row M - 1 (their outputs are masked).
+struct F32Offsets {
+    uint32_t x[4];
+    uint32_t w[4];
+};
+static_assert(F32Shape::kXI == 4 && F32Shape::kWI == 4, "four stage loads per wave and operand");
+
+__device__ __forceinline__ F32Offsets f32_offsets(int64_t m0, int M, int K, int waves, int wv,
+                                                  int lane) {
+    F32Offsets o;
+    const int prow = lane / 8, pc = lane % 8;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = 8 * (wv + waves * i) + prow;
+        const int lrow = static_cast<int>(min(m0 + row, static_cast<int64_t>(M) - 1) - m0);
+        o.x[i] = static_cast<uint32_t>(lrow * K * 4 + 16 * (pc ^ swz(row)));
+        o.w[i] = static_cast<uint32_t>(row * K * 4 + 16 * (pc ^ swz(row)));
+    }
+    return o;
+}
+
+// This wave's LDS-DMA loads of one stage into xdst / wdst (1 KiB, i.e. 8
+// rows of 32 floats, per instruction); koff = the stage's first column in
+// bytes.
+__device__ __forceinline__ void f32_issue(float* xdst, float* wdst, __amdgpu_buffer_rsrc_t xr,
+                                          __amdgpu_buffer_rsrc_t wr, int koff, const F32Offsets& o,
+                                          int waves, int wv) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(xdst + (wv + waves * i) * 256), 16,
+                                                 o.x[i], koff, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(wdst + (wv + waves * i) * 256), 16,
+                                                 o.w[i], koff, 0, 0);
+}
+
+// Operand chunk c (4 floats) of LDS row `row` (rows of 32 floats).
+__device__ __forceinline__ u32x4 f32_op(const float* buf, int row, int c) {
+    return ld16(buf + row * 32 + 4 * (c ^ swz(row)));
+}
+
+template <int EPI, typename P, bool LN>
+__global__ __launch_bounds__(P::kThreads, P::kWavesPerEu) void gemm_f32_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
+    const float* __restrict__ gamma, const float* res, float* out, int M, int N, int K,
+    int tiles_n, int ntiles, LnArgs la) {
+    constexpr int kRB = P::kRB;
+    __shared__ __align__(16) unsigned char smem_raw[sizeof(F32Smem<P>)];
+    F32Smem<P>& sm = *reinterpret_cast<F32Smem<P>*>(smem_raw);
+    const int lane = lane_id();
+    const int wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, hh = lane >> 5;
+#if HS_GEMM_XCD
+    // the f16 kernel's XCD-aware tile order
+    const int per = static_cast<int>(gridDim.x / 8);
+    const int tile = static_cast<int>(blockIdx.x % 8) * per + static_cast<int>(blockIdx.x / 8);
+    if (tile >= ntiles) return;  // padding, before any barrier
+#else
+    const int tile = static_cast<int>(blockIdx.x);
+#endif
+    const int64_t m0 = static_cast<int64_t>(tile / tiles_n) * P::kBM;
+    const int64_t n0 = static_cast<int64_t>(tile % tiles_n) * P::kBN;
+    const int wm = (wave / (P::kWaves / 2)) * (32 * kRB);
+    const int wn = (wave % (P::kWaves / 2)) * 64;
+
+    // acc[a][b]: register r of lane (l32, hh) is column wn + 32 a + 8 (r / 4)
+    // + 4 hh + r % 4, row wm + 32 b + l32 of the tile
+    f32x16 acc[2][kRB];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int b = 0; b < kRB; b++) acc[a][b] = f32x16{};
+
+    const int nsteps = K / P::kBK;
+    const int wv = wave_in_block();
+    const F32Offsets so = f32_offsets(m0, M, K, P::kWaves, wv, lane);
+    const int xrows = static_cast<int>(min(static_cast<int64_t>(P::kBM), M - m0));
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x + m0 * K), 0, xrows * K * 4, kRawBufferFlags);
+    const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(w + n0 * K), 0, P::kBN * K * 4, kRawBufferFlags);
+    constexpr int kStageFloats = P::kBK, kStageBytes = P::kBK * 4;
+    auto issue = [&](int buf, int koff) {
+        f32_issue(sm.x[buf], sm.w[buf], xr, wr, koff, so, P::kWaves, wv);
+    };
+    // The LayerNorm prologue (hs_linear_ln*): each lane normalises, in
+    // place, the x pieces that its own stage loads brought (instruction i:
+    // floats (wv + WAVES i) * 256 + 4 lane .. + 4 of the stage), once they
+    // have landed (vmcnt, no barrier) and before the barrier that opens the
+    // stage to every wave. The pieces' rows are fixed for the kernel, so
+    // their (mean, rstd) stay in registers; their logical chunk (lane % 8) ^
+    // swz(row) does not depend on i, so a stage needs 4 columns of ln_w and
+    // ln_b per lane, loaded one stage ahead. Each element becomes what
+    // hs_layernorm stores for it.
+    static_assert(P::kWaves % 2 == 0, "a lane's x pieces share one logical chunk");
+    f32x2 lst[4];
+    int lcol = 0;
+    float4 lw = {0.0f, 0.0f, 0.0f, 0.0f}, lb = lw;
+    if constexpr (LN) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = 8 * (wv + P::kWaves * i) + lane / 8;
+            // rows past M hold row M - 1 and take its statistics
+            const int64_t r = min(m0 + row, static_cast<int64_t>(M) - 1);
+            lst[i] = *reinterpret_cast<const f32x2*>(la.stats + 2 * r);
+        }
+        lcol = 4 * ((lane % 8) ^ swz(8 * wv + lane / 8));
+        lw = ld_f32x4(la.ln_w + lcol), lb = ld_f32x4(la.ln_b + lcol);
+    }
+    auto normalise = [&](int buf) {  // with the stage's parameters in lw, lb
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float* piece = sm.x[buf] + (wv + P::kWaves * i) * 256 + 4 * lane;
+            const u32x4 v = ld16(piece);
+            u32x4 o;
+            o[0] = f2u(ln_affine(u2f(v[0]), lst[i][0], lst[i][1], lw.x, lb.x));
+            o[1] = f2u(ln_affine(u2f(v[1]), lst[i][0], lst[i][1], lw.y, lb.y));
+            o[2] = f2u(ln_affine(u2f(v[2]), lst[i][0], lst[i][1], lw.z, lb.z));
+            o[3] = f2u(ln_affine(u2f(v[3]), lst[i][0], lst[i][1], lw.w, lb.w));
+            st16(piece, o);
+        }
+    };
+    issue(0, 0);
+    if (nsteps > 1) issue(1, kStageBytes);
+    if constexpr (LN) {
+        // stage 0 landed (stage 1's loads, the last issued, may be in flight)
+        if (nsteps > 1)
+            asm volatile("s_waitcnt vmcnt(%0)" ::"n"(P::kXI + P::kWI) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        normalise(0);
+        if (nsteps > 1) lw = ld_f32x4(la.ln_w + kStageFloats + lcol), lb = ld_f32x4(la.ln_b + kStageFloats + lcol);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    } else {
+        if (nsteps > 1)
+            asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(P::kXI + P::kWI) : "memory");
+        else
+            asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    // operand registers in two sets: the next slice is read from LDS while
+    // the current one multiplies, across stage boundaries too
+    u32x4 A[2][2], B[2][kRB];
+#pragma unroll
+    for (int a = 0; a < 2; a++) A[0][a] = f32_op(sm.w[0], wn + 32 * a + l32, hh);
+#pragma unroll
+    for (int b = 0; b < kRB; b++) B[0][b] = f32_op(sm.x[0], wm + 32 * b + l32, hh);
+    for (int s = 0; s < nsteps; s++) {
+        const int cur = s & 1;
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            const int p = ks & 1;
+            if (ks + 1 < 4) {
+                const int kc = 2 * (ks + 1) + hh;
+#pragma unroll
+                for (int a = 0; a < 2; a++) A[p ^ 1][a] = f32_op(sm.w[cur], wn + 32 * a + l32, kc);
+#pragma unroll
+                for (int b = 0; b < kRB; b++) B[p ^ 1][b] = f32_op(sm.x[cur], wm + 32 * b + l32, kc);
+            } else {
+                // every wave's reads of stage s are done and stage s + 1 has
+                // landed (and, with the prologue, is normalised); buffer cur
+                // is refilled with stage s + 2
+                if constexpr (LN) {
+                    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+                    if (s + 1 < nsteps) {
+                        normalise(cur ^ 1);
+                        if (s + 2 < nsteps) {
+                            const int c = (s + 2) * kStageFloats + lcol;
+                            lw = ld_f32x4(la.ln_w + c), lb = ld_f32x4(la.ln_b + c);
+                        }
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                } else {
+                    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                }
+                if (s + 2 < nsteps) issue(cur, (s + 2) * kStageBytes);
+                if (s + 1 < nsteps) {
+#pragma unroll
+                    for (int a = 0; a < 2; a++) A[p ^ 1][a] = f32_op(sm.w[cur ^ 1], wn + 32 * a + l32, hh);
+#pragma unroll
+                    for (int b = 0; b < kRB; b++) B[p ^ 1][b] = f32_op(sm.x[cur ^ 1], wm + 32 * b + l32, hh);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int a = 0; a < 2; a++)
+#pragma unroll
+                    for (int b = 0; b < kRB; b++)
+                        acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x2f32(u2f(A[p][a][j]), u2f(B[p][b][j]),
+                                                                         acc[a][b], 0, 0, 0);
+        }
+    }
+
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; r4++) {
+            const int64_t n = n0 + wn + 32 * a + 8 * r4 + 4 * hh;
+            const float4 bv = bias ? ld_f32x4(bias + n) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+            float4 gv = {0.0f, 0.0f, 0.0f, 0.0f};
+            if constexpr (EPI == EPI_LS) gv = ld_f32x4(gamma + n);
+#pragma unroll
+            for (int b = 0; b < kRB; b++) {
+                const int64_t m = m0 + wm + 32 * b + l32;
+                if (m >= M) continue;
+                float v[4] = {acc[a][b][4 * r4] + bv.x, acc[a][b][4 * r4 + 1] + bv.y,
+                              acc[a][b][4 * r4 + 2] + bv.z, acc[a][b][4 * r4 + 3] + bv.w};
+                if constexpr (EPI == EPI_GELU) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = gelu_f(v[e]);
+                }
+                if constexpr (EPI == EPI_LS) {
+                    // res + gamma * x, read and written by this lane only
+                    // (res may be out)
+                    const float4 rv = ld_f32x4(res + m * N + n);
+                    v[0] = rv.x + gv.x * v[0], v[1] = rv.y + gv.y * v[1];
+                    v[2] = rv.z + gv.z * v[2], v[3] = rv.w + gv.w * v[3];
+                }
+                u32x4 o;
+                o[0] = f2u(v[0]), o[1] = f2u(v[1]), o[2] = f2u(v[2]), o[3] = f2u(v[3]);
+                st16_nt(out + m * N + n, o);
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
 // generic path: 64 x 64 output tile per 256 threads, 4 x 4 per thread,
 // K in steps of 16 through LDS; f32 accumulation in K order.
 
@@ -707,10 +982,38 @@ bool takes_fast_path(hs_dtype dt, int N, int K, const void* x, const void* w, co
            (!LN || (aligned16(la.ln_w) && aligned16(la.ln_b)));
 }
 
+// f32 matrix-core eligibility: shape and alignment.
+bool f32_fast(hs_dtype dt, int N, int K, const void* x, const void* w, const float* bias,
+              const float* gamma, const void* out, const void* res) {
+    // K <= 2^19 keeps a tile's byte offsets (128 rows x K x 4) in 32 bits
+    return dt == HS_F32 && N % F32Shape::kBN == 0 && K > 0 && K % F32Shape::kBK == 0 &&
+           K <= (1 << 19) && aligned16(x) && aligned16(w) && (!bias || aligned16(bias)) &&
+           (!gamma || aligned16(gamma)) && aligned16(out) && (!res || aligned16(res));
+}
+
+template <int EPI, typename P, bool LN>
+void launch_f32(hipStream_t st, const void* x, const void* w, const float* bias, const float* gamma,
+                const void* res, void* out, int M, int N, int K, const LnArgs& la) {
+    const int tiles_n = N / P::kBN;
+    const int64_t ntiles = ceil_div(M, P::kBM) * tiles_n;
+    const int64_t blocks = HS_GEMM_XCD ? ceil_div(ntiles, 8) * 8 : ntiles;
+    gemm_f32_kernel<EPI, P, LN><<<dim3(static_cast<uint32_t>(blocks)), dim3(P::kThreads), 0, st>>>(
+        static_cast<const float*>(x), static_cast<const float*>(w), bias, gamma,
+        static_cast<const float*>(res), static_cast<float*>(out), M, N, K, tiles_n,
+        static_cast<int>(ntiles), la);
+}
+
 template <int EPI, bool LN = false>
 hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, const float* bias,
                  const float* gamma, const void* res, void* out, int M, int N, int K,
                  const char* op, const QkvArgs& qa = QkvArgs{}, const LnArgs& la = LnArgs{}) {
+    if constexpr (EPI != EPI_QKV) {
+        if (f32_fast(dt, N, K, x, w, bias, gamma, out, res) &&
+            (!LN || (aligned16(la.ln_w) && aligned16(la.ln_b)))) {
+            launch_f32<EPI, F32Shape, LN>(st, x, w, bias, gamma, res, out, M, N, K, la);
+            return check_launch(op);
+        }
+    }
     if (takes_fast_path<LN>(dt, N, K, x, w, bias, gamma, out, res, la)) {
         const int tiles_n = N / kBN;
         const int64_t ntiles = ceil_div(M, kBM) * tiles_n;

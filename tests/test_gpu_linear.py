@@ -144,6 +144,107 @@ def test_linear_epilogues_random_sweep(ctx, case):
               back(res.float() + gam * stored), what + " layerscale")
 
 
+# f32 shapes on the f32 matrix-core kernel (n % 128 == 0, k % 32 == 0; 128
+# x 128 tiles): a last row tile of 56 rows; of 19 rows; one k stage (k =
+# 32) with a last row tile of one row; an odd stage count; a single column
+# tile (n = 128) with 2 stages. The smaller shapes of the tests above with
+# n % 128 == 0 and k % 32 == 0 run on it too.
+F32_MATRIX = [(3000, 2048, 64), (6163, 1024, 96), (6145, 1024, 32), (24577, 256, 160),
+              (2815, 128, 64)]
+
+
+@pytest.mark.parametrize("m,n,k", F32_MATRIX)
+def test_linear_f32_matrix_core_epilogues(ctx, m, n, k):
+    x, w, b = operands(m + 11 * n + k, m, n, k, np.float32, scale=2.0)
+    rng = np.random.default_rng(m + k)
+    res = rng.standard_normal((m, n)).astype(np.float32)
+    g = (rng.standard_normal(n) * 0.5).astype(np.float32)
+    y = O.linear(x, w, b)
+    xd, wd, bd = dev(x), dev(w), dev(b)
+    check(back(ctx.linear(xd, wd, bd)), y, f"f32 linear {(m, n, k)}")
+    check(back(ctx.linear(xd, wd)), O.linear(x, w), f"f32 linear without bias {(m, n, k)}")
+    check(back(ctx.linear_gelu(xd, wd, bd)), O.gelu(y), f"f32 linear_gelu {(m, n, k)}")
+    want = O.residual_ls(res, y, g)
+    check(back(ctx.linear_ls_residual(xd, wd, dev(g), dev(res), bd)), want,
+          f"f32 linear_ls_residual {(m, n, k)}")
+    r = dev(res)
+    ctx.linear_ls_residual(xd, wd, dev(g), r, bd, out=r)
+    check(back(r), want, f"f32 linear_ls_residual in place {(m, n, k)}")
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_linear_f32_random_sweep(ctx, case):
+    """Seeded random f32 shapes on the f32 matrix-core kernel, each epilogue
+    against a float64 product on the device; m from 1 to 3000 covers every
+    remainder of the 128-row tile."""
+    rng = np.random.default_rng(900 + case)
+    m = int(rng.integers(1, 3001))
+    n = int(rng.choice([128, 256, 384, 640, 1024]))
+    k = int(rng.choice([32, 64, 96, 160, 512, 1024]))
+    g = torch.Generator(device="cpu").manual_seed(900 + case)
+    x = torch.randn((m, k), generator=g).to("cuda:0")
+    w = (torch.randn((n, k), generator=g) / k ** 0.5).to("cuda:0")
+    b = (torch.randn(n, generator=g) * 0.02).to("cuda:0")
+    res = torch.randn((m, n), generator=g).to("cuda:0")
+    gam = torch.randn(n, generator=g).to("cuda:0")
+    y = x.double() @ w.double().t().contiguous() + b.double()
+    what = f"f32 sweep case {case}: m={m} n={n} k={k}"
+    check(back(ctx.linear(x, w, b)), back(y), what + " bias")
+    check(back(ctx.linear_gelu(x, w, b)), back(torch.nn.functional.gelu(y)), what + " gelu")
+    check(back(ctx.linear_ls_residual(x, w, gam, res, b)), back(res.double() + gam.double() * y),
+          what + " layerscale")
+
+
+def test_linear_f32_integers_exact(ctx):
+    """Small-integer f32 operands on the f32 matrix-core kernel: every
+    product and partial sum is an integer below 2^24, so any summation order
+    gives the oracle's value exactly."""
+    m, n, k = 6000, 1024, 256
+    rng = np.random.default_rng(77)
+    x = rng.integers(-3, 4, (m, k)).astype(np.float32)
+    w = rng.integers(-3, 4, (n, k)).astype(np.float32)
+    assert_bit_exact(back(ctx.linear(dev(x), dev(w))), O.linear(x, w), "integer linear f32")
+
+
+@pytest.mark.parametrize("name", ["qkv", "fc1", "fc2"])
+def test_linear_f32_full_size(ctx, name):
+    """The trunk's f32 products at S=32 (43968 rows) on the f32 matrix-core
+    kernel against a float64 product on the device, and sampled rows
+    against the oracle."""
+    n, k = FULL[name]
+    n = n // 3 if name == "qkv" else n  # the f32 q|k|v runs one product per third
+    m = 32 * 1374
+    g = torch.Generator(device="cpu").manual_seed(n + k + 1)
+    x = torch.randn((m, k), generator=g).to("cuda:0")
+    w = (torch.randn((n, k), generator=g) / k ** 0.5).to("cuda:0")
+    b = (torch.randn(n, generator=g) * 0.02).to("cuda:0")
+    ref = x.double() @ w.double().t().contiguous() + b.double()
+    if name == "fc1":
+        got = ctx.linear_gelu(x, w, b)
+        ref = torch.nn.functional.gelu(ref)
+    elif name == "fc2":
+        res = torch.randn((m, n), generator=g).to("cuda:0")
+        gam = (torch.randn(n, generator=g) * 0.1).to("cuda:0")
+        got = ctx.linear_ls_residual(x, w, gam, res, b)
+        ref = res.double() + gam.double() * ref
+    else:
+        got = ctx.linear(x, w, b)
+    torch.cuda.synchronize()
+    err = ((got.double() - ref).abs() / (ref.abs() + 1)).max().item()
+    assert err < 4e-5, f"f32 full-size {name}: max relative error {err}"
+    rows = np.array([0, 1, 255, 256, 20000, m - 1])
+    xs, ws, bs = back(x), back(w), back(b)
+    y = O.linear(xs, ws, bs, rows)
+    if name == "fc1":
+        want = O.gelu(y)
+    elif name == "fc2":
+        want = O.residual_ls(back(res)[rows], y, back(gam))
+    else:
+        want = y
+    check(back(got)[rows], want, f"f32 full-size {name} vs oracle")
+    del ref
+
+
 def test_linear_contract(ctx):
     x = torch.zeros((4, 32), dtype=torch.float16, device="cuda:0")
     with pytest.raises(AssertionError):
