@@ -26,8 +26,12 @@
 // are ordered XCD-aware: all query tiles of one (frame, head) run on one
 // XCD, so its K/V stream through that XCD's L2.
 //
-// Generic path (f32, or D = 128): one thread per query over LDS-staged f32
-// K/V tiles, the reference's per-key online softmax in its operand order.
+// f32, D = 64 (16-byte aligned buffers): the same transposed flash scheme
+// on v_mfma_f32_32x32x2_f32 (flash_f32_kernel).
+//
+// Generic path (D = 128, or unaligned buffers): one thread per query over
+// LDS-staged f32 K/V tiles, the reference's per-key online softmax in its
+// operand order.
 #include <math.h>
 
 #include "hs_common.hpp"
@@ -563,6 +567,170 @@ __global__ __launch_bounds__(256) void merge_scalar_kernel(const T* __restrict__
     }
 }
 
+// ---------------------------------------------------------------------------
+// f32 flash attention, head_dim 64, on v_mfma_f32_32x32x2_f32. A workgroup
+// of kF32Waves waves takes kF32Q queries of one (frame, head), a wave 32 of
+// them; keys stream through LDS in tiles of kF32Keys: K row-major [key][dim]
+// and V transposed [dim][key], rows padded to kF32Pitch floats, written
+// from a register prefetch of the next tile issued while the current one
+// computes. Per tile and wave, in transposed form so that a lane's column is
+// its own query (its softmax statistics need only the lane pair's
+// exchange):
+//   S^T (keys x queries) = K Q^T: MFMA j of dim group g takes element j of
+//     lane (n, hh)'s 16-byte chunk 8 g + 4 hh of its K row and of query n
+//     (held in registers), i.e. sums dims 8 g + j and 8 g + 4 + j; register
+//     r of lane (n, hh) is then key 8 (r / 4) + 4 hh + r % 4 of the 32-key
+//     block, query n.
+//   online softmax in log2 units, as the f16 kernel: m = the running max of
+//     s c, weights exp2(s c - m), c = scale / ln 2.
+//   O^T (dims x queries) += V^T P^T: MFMA j = 4 qd + e takes, from lane (n,
+//     hh), element e of V^T row (dim) n's chunk at key 8 qd + 4 hh and the
+//     weight in score register j, which is that same key: the scores are
+//     the B operand as they stand.
+// The output (O / l) leaves from the accumulators: register quad r4 of lane
+// (n, hh) is dims 32 db + 8 r4 + 4 hh .. + 4 of query n, one 16-byte store.
+constexpr int kF32Waves = 4;
+constexpr int kF32Threads = 64 * kF32Waves;
+constexpr int kF32Q = 32 * kF32Waves;  // queries per workgroup
+constexpr int kF32Keys = 64;           // keys per LDS tile
+constexpr int kF32Pitch = 68;          // floats per LDS row (16-byte aligned, 4 banks apart)
+constexpr int kF32Loads = kF32Keys * kD / 4 / kF32Threads;  // 16-byte loads per thread, K or V
+static_assert(kF32Loads * kF32Threads * 4 == kF32Keys * kD, "tile split");
+
+struct alignas(16) F32FlashSmem {
+    float k[kF32Keys * kF32Pitch];  // [key][dim]
+    float vt[kD * kF32Pitch];       // [dim][key]
+};
+
+__global__ __launch_bounds__(kF32Threads, 2) void flash_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ out, int sh_count, int heads, int t, int qtiles, float c, int token_major) {
+    __shared__ F32FlashSmem sm;
+    // the f16 kernel's XCD-aware order: the query tiles of one (frame,
+    // head) run on one XCD and share its L2 copy of K and V
+    const int b = blockIdx.x;
+    const int slot = b / kXcds;
+    const int sh = (slot / qtiles) * kXcds + b % kXcds;
+    if (sh >= sh_count) return;  // workgroup-uniform, before any barrier
+    const int qt = slot % qtiles;
+    const int tid = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = tid >> 6;
+    const int n = lane & 31, hh = lane >> 5;
+    const int64_t base = static_cast<int64_t>(sh) * t * kD;
+    const float* kb = k + base;
+    const float* vb = v + base;
+
+    // query n of the wave (queries past T read row T - 1; not stored)
+    const int qi = qt * kF32Q + wave * 32 + n;
+    const float* qrow = q + base + static_cast<int64_t>(min(qi, t - 1)) * kD;
+    float4 qv[8];
+#pragma unroll
+    for (int g = 0; g < 8; g++) qv[g] = ld_f32x4(qrow + 8 * g + 4 * hh);
+
+    f32x16 o[2] = {f32x16{}, f32x16{}};
+    float m = -3.0e38f, l = 0.0f;
+
+    // staging: load i of thread tid is float4 f = tid + kF32Threads i of the
+    // tile, key f / 16, dims 4 (f % 16) .. + 4 (16 lanes per 256-byte row)
+    float4 kr[kF32Loads], vr[kF32Loads];
+    auto load = [&](int k0) {
+#pragma unroll
+        for (int i = 0; i < kF32Loads; i++) {
+            const int f = tid + kF32Threads * i;
+            const int64_t row = min(k0 + f / 16, t - 1);  // keys past T: masked below
+            kr[i] = ld_f32x4(kb + row * kD + 4 * (f % 16));
+            vr[i] = ld_f32x4(vb + row * kD + 4 * (f % 16));
+        }
+    };
+    auto stage = [&]() {
+#pragma unroll
+        for (int i = 0; i < kF32Loads; i++) {
+            const int f = tid + kF32Threads * i;
+            const int key = f / 16, d0 = 4 * (f % 16);
+            *reinterpret_cast<float4*>(sm.k + key * kF32Pitch + d0) = kr[i];
+            sm.vt[(d0 + 0) * kF32Pitch + key] = vr[i].x;
+            sm.vt[(d0 + 1) * kF32Pitch + key] = vr[i].y;
+            sm.vt[(d0 + 2) * kF32Pitch + key] = vr[i].z;
+            sm.vt[(d0 + 3) * kF32Pitch + key] = vr[i].w;
+        }
+    };
+    load(0);
+    for (int k0 = 0; k0 < t; k0 += kF32Keys) {
+        __syncthreads();  // every wave's reads of the previous tile are done
+        stage();
+        __syncthreads();
+        if (k0 + kF32Keys < t) load(k0 + kF32Keys);
+
+        f32x16 s[2] = {f32x16{}, f32x16{}};
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+            for (int g = 0; g < 8; g++) {
+                const float4 a =
+                    *reinterpret_cast<const float4*>(sm.k + (32 * kb2 + n) * kF32Pitch + 8 * g + 4 * hh);
+                s[kb2] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, qv[g].x, s[kb2], 0, 0, 0);
+                s[kb2] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, qv[g].y, s[kb2], 0, 0, 0);
+                s[kb2] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, qv[g].z, s[kb2], 0, 0, 0);
+                s[kb2] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, qv[g].w, s[kb2], 0, 0, 0);
+            }
+        if (k0 + kF32Keys > t) {
+#pragma unroll
+            for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    if (k0 + 32 * kb2 + 8 * (r / 4) + 4 * hh + r % 4 >= t) s[kb2][r] = -INFINITY;
+        }
+        float mx = s[0][0];
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[kb2][r]);
+        // every tile holds a key below T, so the pair's max is finite
+        const float m_new = fmaxf(m, halves_max(mx) * c);
+        const float corr = __builtin_amdgcn_exp2f(m - m_new);
+        float sum = 0.0f;
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(s[kb2][r], c, -m_new));
+                s[kb2][r] = p;
+                sum += p;
+            }
+        l = l * corr + halves_sum(sum);
+        m = m_new;
+        o[0] *= corr;
+        o[1] *= corr;
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+#pragma unroll
+            for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+                for (int qd = 0; qd < 4; qd++) {
+                    const float4 a = *reinterpret_cast<const float4*>(
+                        sm.vt + (32 * db + n) * kF32Pitch + 32 * kb2 + 8 * qd + 4 * hh);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.x, s[kb2][4 * qd + 0], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.y, s[kb2][4 * qd + 1], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.z, s[kb2][4 * qd + 2], o[db], 0, 0, 0);
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a.w, s[kb2][4 * qd + 3], o[db], 0, 0, 0);
+                }
+    }
+    if (qi >= t) return;  // after the last barrier
+    float* orow = token_major
+                      ? out + ((static_cast<int64_t>(sh / heads) * t + qi) * heads + sh % heads) * kD
+                      : out + base + static_cast<int64_t>(qi) * kD;
+#pragma unroll
+    for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; r4++) {
+            u32x4 w;
+#pragma unroll
+            for (int e = 0; e < 4; e++) w[e] = f2u(o[db][4 * r4 + e] / l);
+            st16(orow + 32 * db + 8 * r4 + 4 * hh, w);
+        }
+}
+
 int64_t grid_blocks(int64_t items) {
     const int64_t cap = static_cast<int64_t>(num_cus()) * 8;
     const int64_t blocks = ceil_div(items, 256);
@@ -616,6 +784,16 @@ hs_status launch_attention(hipStream_t st, hs_dtype dt, const void* q, const voi
                     static_cast<const f16*>(q), static_cast<const f16*>(k), static_cast<const f16*>(v),
                     static_cast<f16*>(out), sh, h, t, 1, c, token_major, qtiles - 1);
             }
+            return check_launch("attention");
+        }
+    }
+    if (dt == HS_F32 && d == kD && aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out)) {
+        const int qtiles = static_cast<int>(ceil_div(t, kF32Q));
+        const int64_t blocks = static_cast<int64_t>(kXcds) * ceil_div(sh, kXcds) * qtiles;
+        if (blocks < (int64_t{1} << 31) / kF32Threads) {
+            flash_f32_kernel<<<dim3(static_cast<uint32_t>(blocks)), dim3(kF32Threads), 0, st>>>(
+                static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+                static_cast<float*>(out), sh, h, t, qtiles, scale * 1.4426950408889634f, token_major);
             return check_launch("attention");
         }
     }

@@ -222,6 +222,78 @@ def test_attention_partial_tile_launch(ctx, t):
                      f"partial-tile launch merged t={t}")
 
 
+# ------------------------------------------- f32 head_dim 64 (matrix cores)
+
+@pytest.mark.parametrize("scale", [0.25, 4.0])
+def test_attention_f32_score_range(ctx, scale):
+    """Flat (scale 0.25) and peaked (scale 4: scores of std 16) softmax in
+    f32, against the oracle and the float64 softmax."""
+    rng = np.random.default_rng(78)
+    s, h, t = 2, 4, 300
+    q = (scale * rng.standard_normal((s, h, t, 64))).astype(np.float32)
+    k, v = (rng.standard_normal((s, h, t, 64)).astype(np.float32) for _ in range(2))
+    got = back(ctx.attention(dev(q), dev(k), dev(v)))
+    check(got, O.attention(q, k, v), f"f32 attention score scale {scale}")
+    assert np.abs(got - naive64(q, k, v)).max() < 1e-4
+
+
+@pytest.mark.parametrize("case", ["ramp", "falling", "spike"])
+def test_attention_f32_running_max(ctx, case):
+    """Scores that rise from one 64-key tile to the next by ~18 (log2
+    units), so every tile rescales what came before; that fall, so the first
+    tile's max holds; and one dominant key in the last tile."""
+    rng = np.random.default_rng(6)
+    s, h, t = 1, 2, 300
+    q = np.zeros((s, h, t, 64))
+    k = 0.5 * rng.standard_normal((s, h, t, 64))
+    v = rng.standard_normal((s, h, t, 64))
+    q[..., 0] = 8.0  # score = k[..., 0] (q.k / 8)
+    if case == "spike":
+        k[:, :, t - 3, 0] = 120.0
+    else:
+        k[..., 0] += (12.5 if case == "ramp" else -12.5) * (np.arange(t) // 64)
+    q, k, v = (a.astype(np.float32) for a in (q, k, v))
+    got = back(ctx.attention(dev(q), dev(k), dev(v)))
+    check(got, O.attention(q, k, v), f"f32 attention running max ({case})")
+    assert np.abs(got - naive64(q, k, v)).max() < 1e-4
+
+
+def test_attention_f32_unaligned_takes_generic(ctx):
+    """Inputs 4 bytes off 16-byte alignment take the generic kernel: the
+    same results within the f32 bar."""
+    rng = np.random.default_rng(79)
+    s, h, t = 1, 3, 100
+    q, k, v = (rng.standard_normal((s, h, t, 64)).astype(np.float32) for _ in range(3))
+    want = O.attention(q, k, v)
+    bufs = [torch.zeros(a.size + 1, dtype=torch.float32, device="cuda:0") for a in (q, k, v)]
+    views = []
+    for b_, a in zip(bufs, (q, k, v)):
+        b_[1:].copy_(torch.from_numpy(a.reshape(-1)))
+        views.append(b_[1:].view(s, h, t, 64))
+    assert views[0].data_ptr() % 16 != 0
+    check(back(ctx.attention(*views)), want, "f32 attention, unaligned inputs")
+
+
+@pytest.mark.parametrize("s,t", [(2, 1374), (1, 2748), (16, 782)])
+def test_attention_f32_block_shapes(ctx, s, t):
+    """The f32 block's frame and global attention at S=2 (2 x 1374 tokens)
+    and the 21x37 frame (782 tokens), 16 heads: every query against a
+    float64 softmax on the device, sampled queries against the oracle,
+    and the merged output bit-exact against the merge of the plain one."""
+    q, k, v = rand_qkv(s * 10000 + t, (s, 16, t, 64), torch.float32)
+    got = ctx.attention(q, k, v)
+    sc = torch.matmul(q.double(), k.double().transpose(-1, -2).contiguous()) / 8.0
+    ref = torch.matmul(torch.softmax(sc, dim=-1), v.double())
+    err = (got.double() - ref).abs().max().item()
+    assert err < 1e-4, f"f32 attention ({s}, 16, {t}): max error {err} against float64"
+    rows = np.array([0, 1, 31, 32, 127, 128, t - 1])
+    qs, ks, vs = back(q), back(k), back(v)
+    check(back(got)[:, :, rows], O.attention(qs, ks, vs, rows), f"f32 attention ({s}, 16, {t}) vs oracle")
+    assert_bit_exact(back(ctx.attention_merged(q, k, v)), back(ctx.attn_merge(got)),
+                     f"f32 attention merged ({s}, 16, {t})")
+    del sc, ref
+
+
 def test_attention_d128_f32(ctx):
     """The camera head's head_dim 128 (f32 only, engine/ops.rs:233-238)."""
     rng = np.random.default_rng(128)
