@@ -1032,6 +1032,92 @@ def block_times(ctx, frames: int, iters: int) -> dict:
     return out
 
 
+def f32_block_times(ctx, iters: int) -> dict:
+    """The reference's f32 path at S=2 x 1374 (its CPU-runnable case): one
+    frame block and one global block with every op on HIP in f32
+    (block_forward, random-init f32 weights), and the blocks' matrix kernels
+    in f32: attention fused with the head merge (hs_attention_merged), the
+    q|k|v projection with its head split, QK-norm and RoPE (three products
+    and the head ops in f32), proj and fc2 with LayerScale + residual, fc1
+    with GELU. Beside each, torch's library op (f32 scaled_dot_product_
+    attention, F.linear of the same shape; not part of this library). HIP
+    events around `iters` back-to-back calls; each figure the fastest of
+    three alternating rounds."""
+    import torch
+
+    from headshot_amd import rope as _rope
+    from headshot_amd.aggregator import BlockWeights, block_forward
+
+    frames = 2
+    t = GRID[0] * GRID[1] + PREFIX
+    m = frames * t
+    gen = torch.Generator(device=ctx.device).manual_seed(19)
+    wts = BlockWeights.random(DIM, HIDDEN, HEAD_DIM, torch.float32, ctx.device, gen)
+    p = wts.p
+    x = torch.randn((m, DIM), generator=gen, device=ctx.device)
+    sin, cos = (torch.from_numpy(a).to(ctx.device) for a in _rope.tables(_rope.periods(), *GRID))
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(iters):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / iters
+
+    out = {"shape": {"frames": frames, "tokens": t, "dim": DIM}}
+    blocks = {"frame": (frames, t, (sin, cos, PREFIX)), "global": (1, m, None)}
+    best = alternating_best({kind: (lambda s_=s_, tt=tt, r=r: block_forward(ctx, wts, x, s_, tt, rope=r,
+                                                                             eps=EPS))
+                             for kind, (s_, tt, r) in blocks.items()}, timed)
+    out["block_ms"] = {kind: round(ms, 3) for kind, ms in best.items()}
+
+    att = {}
+    g = torch.Generator(device="cpu").manual_seed(23)
+    for name, (s_, tt) in {"frame": (frames, t), "global": (1, m)}.items():
+        q, k, v = (torch.randn((s_, HEADS, tt, HEAD_DIM), generator=g).to(ctx.device) for _ in range(3))
+        o = torch.empty((s_ * tt, HEADS * HEAD_DIM), device=ctx.device)
+        ctx.attention_merged(q, k, v, out=o)
+        call = ctx.last_launch
+        b = alternating_best({"hip": call, "library": lambda: torch.nn.functional.
+                              scaled_dot_product_attention(q, k, v)}, timed)
+        flops = 4.0 * tt * tt * HEAD_DIM * s_ * HEADS
+        att[name] = {"shape_SHTD": [s_, HEADS, tt, HEAD_DIM], "ms": round(b["hip"], 3),
+                     "TFLOP/s": round(flops / (b["hip"] * 1e-3) / 1e12, 1),
+                     "library_sdpa_ms": round(b["library"], 3)}
+        del q, k, v, o
+    out["attention"] = att
+
+    lin = {}
+    xa = torch.randn((m, DIM), generator=g).to(ctx.device)
+    xh = torch.randn((m, HIDDEN), generator=g).to(ctx.device)
+    res = torch.randn((m, DIM), generator=g).to(ctx.device)
+    o_d = torch.empty((m, DIM), device=ctx.device)
+    o_h = torch.empty((m, HIDDEN), device=ctx.device)
+    layers = {
+        "qkv_heads": (lambda: ctx.linear_qkv_heads(xa, wts.qkv_w, wts.qkv_b, frames, t, HEADS,
+                                                   qn=p.qn, kn=p.kn, rope=(sin, cos, PREFIX), eps=EPS),
+                      lambda: torch.nn.functional.linear(xa, wts.qkv_w, wts.qkv_b), 3 * DIM, DIM),
+        "proj_ls": (lambda: ctx.linear_ls_residual(xa, wts.proj_w, p.ls1, res, p.proj_b, out=o_d),
+                    lambda: torch.nn.functional.linear(xa, wts.proj_w, p.proj_b), DIM, DIM),
+        "fc1_gelu": (lambda: ctx.linear_gelu(xa, wts.fc1_w, p.fc1_b, out=o_h),
+                     lambda: torch.nn.functional.linear(xa, wts.fc1_w, p.fc1_b), HIDDEN, DIM),
+        "fc2_ls": (lambda: ctx.linear_ls_residual(xh, wts.fc2_w, p.ls2, res, p.fc2_b, out=o_d),
+                   lambda: torch.nn.functional.linear(xh, wts.fc2_w, p.fc2_b), DIM, HIDDEN),
+    }
+    for name, (hip, library, n, k) in layers.items():
+        b = alternating_best({"hip": hip, "library": library}, timed)
+        flops = 2.0 * m * n * k
+        lin[name] = {"MNK": [m, n, k], "ms": round(b["hip"], 3),
+                     "TFLOP/s": round(flops / (b["hip"] * 1e-3) / 1e12, 1),
+                     "library_linear_ms": round(b["library"], 3)}
+    out["linear"] = lin
+    return out
+
+
 def trunk_times(ctx, frames: int, iters: int) -> dict:
     """One whole aggregator trunk forward at this S (model/trunk.rs:49-146)
     on HIP: token assembly from f32 DINO tokens (S x 37 x 37 patches, 17
@@ -1971,6 +2057,7 @@ def main():
         del flush
         line["linear"] = gemm_times(ctx, args.frames, args.attention_iters)
         line["block"] = block_times(ctx, args.frames, max(1, args.attention_iters // 2))
+        line["f32_s2"] = f32_block_times(ctx, args.attention_iters)
         trunk_iters = args.trunk_iters if args.trunk_iters >= 0 else max(1, args.attention_iters // 5)
         if trunk_iters > 0:
             line["trunk"] = trunk_times(ctx, args.frames, trunk_iters)

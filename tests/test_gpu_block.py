@@ -81,6 +81,35 @@ def test_block_small(ctx, kind):
     assert err.max() <= 1e-2, f"block {kind} vs float32: max scaled error {err.max():.3g}"
 
 
+@pytest.mark.parametrize("kind", ["frame", "global"])
+def test_block_f32_s2(ctx, kind):
+    """The reference's f32 path at S=2 x 1374 (37x37 grid, prefix 5): a
+    whole block in f32 (f32 linear layers and attention on the matrix cores)
+    against the reference's unfused sequence through the same library
+    (within 1e-5 * max(1, |e|): only summation orders differ) and against
+    the float32 torch restatement (within 1e-4 * max(1, |e|), the
+    reference's f32 gate)."""
+    g = torch.Generator(device="cpu").manual_seed(8)
+    grid = (37, 37)
+    t = PREFIX + grid[0] * grid[1]
+    if kind == "frame":
+        s = 2
+        sin, cos = (torch.from_numpy(a).to("cuda:0") for a in rp.tables(rp.periods(), *grid))
+        rope = (sin, cos, PREFIX)
+    else:
+        s, t, rope = 1, 2 * t, None
+    wts = BlockWeights.random(DIM, HIDDEN, 64, torch.float32, "cuda:0",
+                              torch.Generator(device="cuda:0").manual_seed(8), ls_init=0.1)
+    x = torch.randn((s * t, DIM), generator=g).to("cuda:0")
+    fused = back(block_forward(ctx, wts, x, s, t, rope=rope))
+    seq = back(block_forward_reference(ctx, wts, x, s, t, rope=rope))
+    err = np.abs(fused - seq) / np.maximum(1.0, np.abs(seq))
+    assert err.max() <= 1e-5, f"f32 block {kind} fused vs reference sequence: {err.max():.3g}"
+    ref = back(torch_block(wts, x, s, t, rope, 1e-6))
+    err = np.abs(fused - ref) / np.maximum(1.0, np.abs(ref))
+    assert err.max() <= 1e-4, f"f32 block {kind} vs float32 torch: max scaled error {err.max():.3g}"
+
+
 def test_block_full_size_frame(ctx):
     """A frame block at S=32 (32 x 1374 tokens, 37x37 grid, prefix 5)."""
     g = torch.Generator(device="cpu").manual_seed(6)
