@@ -647,11 +647,15 @@ __global__ __launch_bounds__(kThreads, 8 / kWaves) void gemm_f16_kernel(
 // (16 bytes; the lane pair's quads are 32 contiguous bytes, and the wave's
 // four r4 complete the row's 128 bytes of the block).
 //
-// The shape used, F32Shape: 4 waves, 128 x 128 tiles, 64 KiB of LDS, two
+// Shapes: F32Shape, 4 waves, 128 x 128 tiles, 64 KiB of LDS, two
 // workgroups per CU. It beats 8 waves in 256 x 256 tiles (128 KiB, one per
 // CU) at every trunk shape, by 6-9% at S=32 (43968 x 4096 x 1024: 2716 us
 // against 2873) and by 3x where 256 x 256 tiles are too few to fill the
-// chip (2748 x 1024 x 4096, 44 of them: 286 us against 925).
+// chip (2748 x 1024 x 4096, 44 of them: 286 us against 925). Below 512
+// tiles of 128 x 128 (the chip's slots at two per CU) F32Narrow, 4 waves
+// of 32 x 64 in 64 x 128 tiles (48 KiB, three per CU), doubles the tile
+// count: 6-23% faster there (2748 x 1024 x 1024: 74 us against 82; 5496 x
+// 1024 x 4096: 434 against 515), within 5% either way above.
 template <int WAVES, int WROWS>
 struct F32Tile {
     static constexpr int kWaves = WAVES, kThreads = 64 * WAVES;
@@ -664,13 +668,15 @@ struct F32Tile {
     static_assert(kXI * 64 * WAVES == kBM * 8 && kWI * 64 * WAVES == kBN * 8, "stage split");
 };
 using F32Shape = F32Tile<4, 64>;
+using F32Narrow = F32Tile<4, 32>;
 
 template <typename P>
 struct F32Smem {
     float x[2][P::kBM * P::kBK];
     float w[2][P::kBN * P::kBK];
 };
-static_assert(2 * sizeof(F32Smem<F32Shape>) <= 160 * 1024, "two workgroups per CU");
+static_assert(2 * sizeof(F32Smem<F32Shape>) <= 160 * 1024 && 3 * sizeof(F32Smem<F32Narrow>) <= 160 * 1024,
+              "workgroups per CU");
 
 // Per-lane byte offsets of a wave's stage loads (4 instructions each for
 // x and w): instruction i of wave wv brings rows
@@ -680,18 +686,20 @@ struct F32Offsets {
     uint32_t x[4];
     uint32_t w[4];
 };
-static_assert(F32Shape::kXI == 4 && F32Shape::kWI == 4, "four stage loads per wave and operand");
+static_assert(F32Shape::kXI <= 4 && F32Shape::kWI <= 4 && F32Narrow::kXI <= 4 && F32Narrow::kWI <= 4,
+              "at most four stage loads per wave and operand");
 
+// xi / wi: the loads per wave of an x / w stage (compile-time after inlining)
 __device__ __forceinline__ F32Offsets f32_offsets(int64_t m0, int M, int K, int waves, int wv,
-                                                  int lane) {
+                                                  int lane, int xi, int wi) {
     F32Offsets o;
     const int prow = lane / 8, pc = lane % 8;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = 8 * (wv + waves * i) + prow;
         const int lrow = static_cast<int>(min(m0 + row, static_cast<int64_t>(M) - 1) - m0);
-        o.x[i] = static_cast<uint32_t>(lrow * K * 4 + 16 * (pc ^ swz(row)));
-        o.w[i] = static_cast<uint32_t>(row * K * 4 + 16 * (pc ^ swz(row)));
+        o.x[i] = i < xi ? static_cast<uint32_t>(lrow * K * 4 + 16 * (pc ^ swz(row))) : 0u;
+        o.w[i] = i < wi ? static_cast<uint32_t>(row * K * 4 + 16 * (pc ^ swz(row))) : 0u;
     }
     return o;
 }
@@ -701,15 +709,17 @@ __device__ __forceinline__ F32Offsets f32_offsets(int64_t m0, int M, int K, int 
 // bytes.
 __device__ __forceinline__ void f32_issue(float* xdst, float* wdst, __amdgpu_buffer_rsrc_t xr,
                                           __amdgpu_buffer_rsrc_t wr, int koff, const F32Offsets& o,
-                                          int waves, int wv) {
+                                          int waves, int wv, int xi, int wi) {
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(xdst + (wv + waves * i) * 256), 16,
-                                                 o.x[i], koff, 0, 0);
+        if (i < xi)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(xdst + (wv + waves * i) * 256), 16,
+                                                     o.x[i], koff, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(wdst + (wv + waves * i) * 256), 16,
-                                                 o.w[i], koff, 0, 0);
+        if (i < wi)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(wr, (lds_void*)(wdst + (wv + waves * i) * 256), 16,
+                                                     o.w[i], koff, 0, 0);
 }
 
 // Operand chunk c (4 floats) of LDS row `row` (rows of 32 floats).
@@ -751,7 +761,7 @@ __global__ __launch_bounds__(P::kThreads, P::kWavesPerEu) void gemm_f32_kernel(
 
     const int nsteps = K / P::kBK;
     const int wv = wave_in_block();
-    const F32Offsets so = f32_offsets(m0, M, K, P::kWaves, wv, lane);
+    const F32Offsets so = f32_offsets(m0, M, K, P::kWaves, wv, lane, P::kXI, P::kWI);
     const int xrows = static_cast<int>(min(static_cast<int64_t>(P::kBM), M - m0));
     const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(x + m0 * K), 0, xrows * K * 4, kRawBufferFlags);
@@ -759,7 +769,7 @@ __global__ __launch_bounds__(P::kThreads, P::kWavesPerEu) void gemm_f32_kernel(
         const_cast<float*>(w + n0 * K), 0, P::kBN * K * 4, kRawBufferFlags);
     constexpr int kStageFloats = P::kBK, kStageBytes = P::kBK * 4;
     auto issue = [&](int buf, int koff) {
-        f32_issue(sm.x[buf], sm.w[buf], xr, wr, koff, so, P::kWaves, wv);
+        f32_issue(sm.x[buf], sm.w[buf], xr, wr, koff, so, P::kWaves, wv, P::kXI, P::kWI);
     };
     // The LayerNorm prologue (hs_linear_ln*): each lane normalises, in
     // place, the x pieces that its own stage loads brought (instruction i:
@@ -776,7 +786,7 @@ __global__ __launch_bounds__(P::kThreads, P::kWavesPerEu) void gemm_f32_kernel(
     float4 lw = {0.0f, 0.0f, 0.0f, 0.0f}, lb = lw;
     if constexpr (LN) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < P::kXI; i++) {
             const int row = 8 * (wv + P::kWaves * i) + lane / 8;
             // rows past M hold row M - 1 and take its statistics
             const int64_t r = min(m0 + row, static_cast<int64_t>(M) - 1);
@@ -787,7 +797,7 @@ __global__ __launch_bounds__(P::kThreads, P::kWavesPerEu) void gemm_f32_kernel(
     }
     auto normalise = [&](int buf) {  // with the stage's parameters in lw, lb
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < P::kXI; i++) {
             float* piece = sm.x[buf] + (wv + P::kWaves * i) * 256 + 4 * lane;
             const u32x4 v = ld16(piece);
             u32x4 o;
@@ -982,6 +992,10 @@ bool takes_fast_path(hs_dtype dt, int N, int K, const void* x, const void* w, co
            (!LN || (aligned16(la.ln_w) && aligned16(la.ln_b)));
 }
 
+#ifndef HS_GEMM_F32_NARROW_TILES
+#define HS_GEMM_F32_NARROW_TILES 512  // 128 x 128 tiles below which F32Narrow runs
+#endif
+
 // f32 matrix-core eligibility: shape and alignment.
 bool f32_fast(hs_dtype dt, int N, int K, const void* x, const void* w, const float* bias,
               const float* gamma, const void* out, const void* res) {
@@ -1010,7 +1024,10 @@ hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, cons
     if constexpr (EPI != EPI_QKV) {
         if (f32_fast(dt, N, K, x, w, bias, gamma, out, res) &&
             (!LN || (aligned16(la.ln_w) && aligned16(la.ln_b)))) {
-            launch_f32<EPI, F32Shape, LN>(st, x, w, bias, gamma, res, out, M, N, K, la);
+            if (ceil_div(M, F32Shape::kBM) * (N / F32Shape::kBN) < HS_GEMM_F32_NARROW_TILES)
+                launch_f32<EPI, F32Narrow, LN>(st, x, w, bias, gamma, res, out, M, N, K, la);
+            else
+                launch_f32<EPI, F32Shape, LN>(st, x, w, bias, gamma, res, out, M, N, K, la);
             return check_launch(op);
         }
     }

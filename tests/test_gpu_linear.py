@@ -144,13 +144,16 @@ def test_linear_epilogues_random_sweep(ctx, case):
               back(res.float() + gam * stored), what + " layerscale")
 
 
-# f32 shapes on the f32 matrix-core kernel (n % 128 == 0, k % 32 == 0; 128
-# x 128 tiles): a last row tile of 56 rows; of 19 rows; one k stage (k =
-# 32) with a last row tile of one row; an odd stage count; a single column
-# tile (n = 128) with 2 stages. The smaller shapes of the tests above with
-# n % 128 == 0 and k % 32 == 0 run on it too.
+# f32 shapes on the f32 matrix-core kernel (n % 128 == 0, k % 32 == 0): 64
+# x 128 tiles below 512 tiles of 128 x 128, 128 x 128 tiles from there.
+# Narrow: a last row tile of 56 rows; of 19 rows; one k stage (k = 32) with
+# a last row tile of one row; an odd stage count; a single column tile (n =
+# 128) with 2 stages (the smaller shapes of the tests above with n % 128 ==
+# 0 and k % 32 == 0 run on it too). 128 x 128: a last row tile of 57 rows
+# and 3 stages; one stage and a last row tile of one row; an odd stage
+# count and n = 1024.
 F32_MATRIX = [(3000, 2048, 64), (6163, 1024, 96), (6145, 1024, 32), (24577, 256, 160),
-              (2815, 128, 64)]
+              (2815, 128, 64), (12345, 768, 96), (8193, 1024, 32), (8300, 1024, 160)]
 
 
 @pytest.mark.parametrize("m,n,k", F32_MATRIX)

@@ -85,9 +85,10 @@ def test_layernorm_stats(ctx, rows, dim, dtype):
     assert_bit_exact(normed, mine, f"stats of hs_layernorm {rows}x{dim}")
 
 
-# (m, n, k): k = 64, 128, 192 run the matrix-core pipeline with 1, 2 and 3
-# stages (its peeled last steps alone), 1024 with 16; m = 1, 19, 257 and 300
-# leave partial row tiles; n = 48 and the f32 cases take the generic kernel.
+# (m, n, k): k = 64, 128, 192 run the f16 matrix-core pipeline with 1, 2
+# and 3 stages (its peeled last steps alone), 1024 with 16; m = 1, 19, 257
+# and 300 leave partial row tiles; n = 48 takes the generic kernel; f32
+# takes the f32 matrix-core kernel in 64 x 128 tiles (n % 128 == 0).
 SHAPES = [(1, 256, 1024), (19, 256, 1024), (257, 512, 1024), (300, 256, 64), (300, 256, 128),
           (300, 256, 192), (37, 48, 80), (1374, 1024, 1024), (600, 256, 2048)]
 
@@ -118,6 +119,25 @@ def test_linear_ln_gelu(ctx, m, n, k, dtype):
     assert_bit_exact(got, seq, what + " against layernorm then linear_gelu")
     # the reference's sequence: the linear's storage rounding, then gelu
     check(got, O.gelu(reference_ln_linear(x, g, be, w, b, 1e-6)), what)
+
+
+@pytest.mark.parametrize("m,n,k", [(8300, 1024, 256), (12345, 768, 96), (3000, 1024, 32)])
+def test_linear_ln_f32_tile_shapes(ctx, m, n, k):
+    """The f32 prologue in both tile shapes of the f32 matrix-core kernel:
+    128 x 128 tiles (at least 512 of them: 8300 and 12345 rows, last row
+    tiles of 108 and 57 rows) and 64 x 128 (3000 rows, one k stage), each
+    bit-exact against layernorm then the product and within the f32 bar of
+    the oracle's sequence."""
+    x, g, be, w, b = ln_operands(m + n + 3 * k, m, n, k, np.float32, 2.0)
+    xd, gd, bed, wd, bd = map(dev, (x, g, be, w, b))
+    normed = ctx.layernorm(xd, gd, bed, eps=1e-6)
+    got = back(ctx.linear_ln(xd, (gd, bed), wd, bd, eps=1e-6))
+    assert_bit_exact(got, back(ctx.linear(normed, wd, bd)), f"f32 linear_ln {(m, n, k)}")
+    got_g = back(ctx.linear_ln_gelu(xd, (gd, bed), wd, bd, eps=1e-6))
+    assert_bit_exact(got_g, back(ctx.linear_gelu(normed, wd, bd)), f"f32 linear_ln_gelu {(m, n, k)}")
+    rows = np.array([0, 1, 63, 64, 127, 128, m - 1])
+    want = O.linear(O.layernorm(x, g, be, 1e-6)[rows], w, b)
+    check(got[rows], want, f"f32 linear_ln {(m, n, k)} vs oracle")
 
 
 def test_linear_ln_without_bias(ctx):
