@@ -61,6 +61,16 @@ def _opt(t, n: int, what: str):
     return None if t is None else _param(t, n, what)
 
 
+def _qkv_fused(dtype, d: int, n3: int, k: int) -> bool:
+    """Shapes the fused q|k|v kernels cover: head dim 64, whole column tiles
+    (256 in f16, 128 in f32) and whole k stages (64 in f16, 32 in f32)."""
+    if d != 64:
+        return False
+    if dtype == F16:
+        return n3 % 256 == 0 and k % 64 == 0
+    return dtype == F32 and n3 % 128 == 0 and k % 32 == 0
+
+
 class HipContext:
     """One device's op surface. ``device`` is a torch device (default cuda:0)."""
 
@@ -339,7 +349,7 @@ class HipContext:
         d = n3 // (3 * h)
         assert x.numel() == s * t * k and x.dtype == w_qkv.dtype, "x shape/dtype"
         hd = h * d
-        if not (x.dtype == F16 and d == 64 and n3 % 256 == 0 and k % 64 == 0):
+        if not _qkv_fused(x.dtype, d, n3, k):
             outs = []
             for i, norm in enumerate((qn, kn, None)):
                 b = None if b_qkv is None else b_qkv[i * hd:(i + 1) * hd]
@@ -436,7 +446,7 @@ class HipContext:
         assert n3 % (3 * h) == 0, "w_qkv rows must be 3 * H * d"
         d = n3 // (3 * h)
         assert x.numel() == s * t * k and x.dtype == w_qkv.dtype, "x shape/dtype"
-        if not (x.dtype == F16 and d == 64 and n3 % 256 == 0 and k % 64 == 0):
+        if not _qkv_fused(x.dtype, d, n3, k):
             xn = self.layernorm(x, ln[0], ln[1], eps=eps)
             return self.linear_qkv_heads(xn, w_qkv, b_qkv, s, t, h, qn=qn, kn=kn, rope=rope,
                                          eps=eps, out=out)

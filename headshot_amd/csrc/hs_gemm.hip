@@ -55,7 +55,7 @@ enum Epi { EPI_BIAS = 0, EPI_GELU = 1, EPI_LS = 2, EPI_QKV = 3 };
 // T, 64) q, k, v; QK-norm weight / bias per q and k (null: none); RoPE
 // tables (T - prefix, 64) (null: none).
 struct QkvArgs {
-    f16* out[3];
+    void* out[3];  // f16 or f32, as the product
     const float* nw[2];
     const float* nb[2];
     const float* sin_tab;
@@ -310,7 +310,7 @@ __device__ __forceinline__ void qkv_heads_out(const f16* stage, const QkvArgs& q
         br[0] = b0.x, br[1] = b0.y, br[2] = b0.z, br[3] = b0.w;
         br[4] = b1.x, br[5] = b1.y, br[6] = b1.z, br[7] = b1.w;
     }
-    f16* obase = qa.out[which] + static_cast<int64_t>(head) * qa.seq * 64 + ch;
+    f16* obase = static_cast<f16*>(qa.out[which]) + static_cast<int64_t>(head) * qa.seq * 64 + ch;
     const float sg = upper ? 1.0f : -1.0f;
     // this lane's row: token m = s * seq + t (m < 2^31), advanced by 8 rows
     // per step
@@ -727,13 +727,83 @@ __device__ __forceinline__ u32x4 f32_op(const float* buf, int row, int c) {
     return ld16(buf + row * 32 + 4 * (c ^ swz(row)));
 }
 
+// The f32 q|k|v epilogue's staging: each wave's block (32 kRB token rows x
+// one head's 64 columns, acc + bias) in rows of kQkvPitch floats (16-byte
+// aligned, 4 banks apart), in the LDS the stages used.
+constexpr int kQkvPitch = 68;
+template <typename P>
+constexpr size_t f32_smem_bytes(int epi) {
+    const size_t loop = sizeof(F32Smem<P>);
+    const size_t qkv = epi == EPI_QKV ? size_t{4} * P::kWaves * 32 * P::kRB * kQkvPitch : 0;
+    return loop > qkv ? loop : qkv;
+}
+static_assert(2 * f32_smem_bytes<F32Shape>(EPI_QKV) <= 160 * 1024 &&
+                  3 * f32_smem_bytes<F32Narrow>(EPI_QKV) <= 160 * 1024,
+              "workgroups per CU with the q|k|v staging");
+
+// The f32 q|k|v epilogue's second phase: the wave's staged block is `rows`
+// token rows of one head of q, k or v. 16 lanes per row hold the head
+// vector in the lane layout of the standalone f32 QK-norm / RoPE op (piece
+// p < 8: channels 4 p .. + 4; p >= 8: 32 + 4 (15 - p) .. + 4), so each head
+// vector is normalised and rotated by the same code as there, and each
+// row's 256 bytes go to (frame, head, token) of the head-major output.
+__device__ __forceinline__ void qkv_heads_out_f32(const float* stage, const QkvArgs& qa, int64_t row0,
+                                                  int M, int64_t col, int lane, int rows) {
+    const int hd = qa.heads * 64;
+    const int which = static_cast<int>(col / hd);  // 0 q, 1 k, 2 v: wave-uniform
+    const int head = static_cast<int>(col - int64_t{which} * hd) / 64;
+    const int piece = lane & 15;
+    const bool upper = piece >= 8;
+    const int ch = upper ? 32 + (15 - piece) * 4 : piece * 4;
+    const float* nw = which < 2 ? qa.nw[which] : nullptr;
+    const float* nb = which < 2 ? qa.nb[which] : nullptr;
+    const bool norm = nw != nullptr;
+    const bool rope = which < 2 && qa.sin_tab != nullptr;
+    float wr[4] = {0.0f, 0.0f, 0.0f, 0.0f}, br[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (norm) {
+        const float4 w0 = ld_f32x4(nw + ch), b0 = ld_f32x4(nb + ch);
+        wr[0] = w0.x, wr[1] = w0.y, wr[2] = w0.z, wr[3] = w0.w;
+        br[0] = b0.x, br[1] = b0.y, br[2] = b0.z, br[3] = b0.w;
+    }
+    float* obase = static_cast<float*>(qa.out[which]) + static_cast<int64_t>(head) * qa.seq * 64 + ch;
+    const float sg = upper ? 1.0f : -1.0f;
+    // this lane's row: token m = s * seq + t (m < 2^31), advanced by 4 rows
+    // per step
+    int64_t m = row0 + (lane >> 4);
+    uint32_t s = static_cast<uint32_t>(m) / static_cast<uint32_t>(qa.seq);
+    int t = static_cast<int>(static_cast<uint32_t>(m) - s * static_cast<uint32_t>(qa.seq));
+    for (int rr = 0; rr < rows; rr += 4) {
+        if (m >= M) break;  // rows grow with rr: the rest are past M too
+        const u32x4 v = ld16(stage + (rr + (lane >> 4)) * kQkvPitch + ch);
+        float f[4] = {u2f(v[0]), u2f(v[1]), u2f(v[2]), u2f(v[3])};
+        const bool rot = rope && t >= qa.prefix;  // the same for the row's 16 lanes
+        float cs[4] = {0.0f, 0.0f, 0.0f, 0.0f}, sn[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (rot) {
+            const int64_t trow = static_cast<int64_t>(t - qa.prefix) * 64 + ch;
+            const float4 c4 = ld_f32x4(qa.cos_tab + trow), s4 = ld_f32x4(qa.sin_tab + trow);
+            cs[0] = c4.x, cs[1] = c4.y, cs[2] = c4.z, cs[3] = c4.w;
+            sn[0] = sg * s4.x, sn[1] = sg * s4.y, sn[2] = sg * s4.z, sn[3] = sg * s4.w;
+        }
+        if (norm)
+            qk_norm_rope_vec<float, 16, true>(f, wr, br, qa.eps, rot, cs, sn);
+        else
+            qk_norm_rope_vec<float, 16, false>(f, wr, br, qa.eps, rot, cs, sn);
+        u32x4 o;
+        o[0] = f2u(f[0]), o[1] = f2u(f[1]), o[2] = f2u(f[2]), o[3] = f2u(f[3]);
+        st16(obase + (static_cast<int64_t>(s) * qa.heads * qa.seq + t) * 64, o);
+        m += 4;
+        t += 4;
+        while (t >= qa.seq) t -= qa.seq, s++;
+    }
+}
+
 template <int EPI, typename P, bool LN>
 __global__ __launch_bounds__(P::kThreads, P::kWavesPerEu) void gemm_f32_kernel(
     const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ bias,
     const float* __restrict__ gamma, const float* res, float* out, int M, int N, int K,
-    int tiles_n, int ntiles, LnArgs la) {
+    int tiles_n, int ntiles, LnArgs la, QkvArgs qa) {
     constexpr int kRB = P::kRB;
-    __shared__ __align__(16) unsigned char smem_raw[sizeof(F32Smem<P>)];
+    __shared__ __align__(16) unsigned char smem_raw[f32_smem_bytes<P>(EPI)];
     F32Smem<P>& sm = *reinterpret_cast<F32Smem<P>*>(smem_raw);
     const int lane = lane_id();
     const int wave = threadIdx.x >> 6;
@@ -879,6 +949,32 @@ __global__ __launch_bounds__(P::kThreads, P::kWavesPerEu) void gemm_f32_kernel(
         }
     }
 
+    if constexpr (EPI == EPI_QKV) {
+        // every wave has left the main loop: the stages' LDS takes the
+        // waves' blocks
+        __syncthreads();
+        float* stage = reinterpret_cast<float*>(smem_raw) + wave * (32 * kRB * kQkvPitch);
+#pragma unroll
+        for (int a = 0; a < 2; a++)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; r4++) {
+                const int cl = 32 * a + 8 * r4 + 4 * hh;
+                const float4 bv = bias ? ld_f32x4(bias + n0 + wn + cl) : float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int b = 0; b < kRB; b++) {
+                    u32x4 o;
+                    o[0] = f2u(acc[a][b][4 * r4] + bv.x), o[1] = f2u(acc[a][b][4 * r4 + 1] + bv.y);
+                    o[2] = f2u(acc[a][b][4 * r4 + 2] + bv.z), o[3] = f2u(acc[a][b][4 * r4 + 3] + bv.w);
+                    st16(stage + (32 * b + l32) * kQkvPitch + cl, o);
+                }
+            }
+        // only this wave reads its block back: a wave-level fence suffices
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        qkv_heads_out_f32(stage, qa, m0 + wm, M, n0 + wn, lane, 32 * kRB);
+        return;
+    }
 #pragma unroll
     for (int a = 0; a < 2; a++)
 #pragma unroll
@@ -1007,29 +1103,27 @@ bool f32_fast(hs_dtype dt, int N, int K, const void* x, const void* w, const flo
 
 template <int EPI, typename P, bool LN>
 void launch_f32(hipStream_t st, const void* x, const void* w, const float* bias, const float* gamma,
-                const void* res, void* out, int M, int N, int K, const LnArgs& la) {
+                const void* res, void* out, int M, int N, int K, const LnArgs& la, const QkvArgs& qa) {
     const int tiles_n = N / P::kBN;
     const int64_t ntiles = ceil_div(M, P::kBM) * tiles_n;
     const int64_t blocks = HS_GEMM_XCD ? ceil_div(ntiles, 8) * 8 : ntiles;
     gemm_f32_kernel<EPI, P, LN><<<dim3(static_cast<uint32_t>(blocks)), dim3(P::kThreads), 0, st>>>(
         static_cast<const float*>(x), static_cast<const float*>(w), bias, gamma,
         static_cast<const float*>(res), static_cast<float*>(out), M, N, K, tiles_n,
-        static_cast<int>(ntiles), la);
+        static_cast<int>(ntiles), la, qa);
 }
 
 template <int EPI, bool LN = false>
 hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, const float* bias,
                  const float* gamma, const void* res, void* out, int M, int N, int K,
                  const char* op, const QkvArgs& qa = QkvArgs{}, const LnArgs& la = LnArgs{}) {
-    if constexpr (EPI != EPI_QKV) {
-        if (f32_fast(dt, N, K, x, w, bias, gamma, out, res) &&
-            (!LN || (aligned16(la.ln_w) && aligned16(la.ln_b)))) {
-            if (ceil_div(M, F32Shape::kBM) * (N / F32Shape::kBN) < HS_GEMM_F32_NARROW_TILES)
-                launch_f32<EPI, F32Narrow, LN>(st, x, w, bias, gamma, res, out, M, N, K, la);
-            else
-                launch_f32<EPI, F32Shape, LN>(st, x, w, bias, gamma, res, out, M, N, K, la);
-            return check_launch(op);
-        }
+    if (f32_fast(dt, N, K, x, w, bias, gamma, out, res) &&
+        (!LN || (aligned16(la.ln_w) && aligned16(la.ln_b)))) {
+        if (ceil_div(M, F32Shape::kBM) * (N / F32Shape::kBN) < HS_GEMM_F32_NARROW_TILES)
+            launch_f32<EPI, F32Narrow, LN>(st, x, w, bias, gamma, res, out, M, N, K, la, qa);
+        else
+            launch_f32<EPI, F32Shape, LN>(st, x, w, bias, gamma, res, out, M, N, K, la, qa);
+        return check_launch(op);
     }
     if (takes_fast_path<LN>(dt, N, K, x, w, bias, gamma, out, res, la)) {
         const int tiles_n = N / kBN;
@@ -1042,8 +1136,9 @@ hs_status launch(hipStream_t st, hs_dtype dt, const void* x, const void* w, cons
         return check_launch(op);
     }
     if constexpr (EPI == EPI_QKV) {
-        return fail(HS_EUNSUPPORTED, "%s: needs f16, K %% %d == 0 and 16-byte aligned buffers", op,
-                    kBK);
+        return fail(HS_EUNSUPPORTED,
+                    "%s: needs K %% %d == 0 (f16) or %% %d == 0 (f32) and 16-byte aligned buffers", op,
+                    kBK, F32Shape::kBK);
     } else {
         const int tiles_n = static_cast<int>(ceil_div(N, kGT));
         const int64_t blocks = ceil_div(M, kGT) * tiles_n;
@@ -1149,17 +1244,19 @@ hs_status qkv_setup(const char* op, hs_dtype dt, const void* x, const void* w_qk
             if (overlaps(outs[i], ob, outs[j], ob)) return fail(HS_EINVAL, "%s: outputs overlap", op);
     }
     // The fused epilogue needs one head per wave (64 columns) and whole
-    // 256-column tiles; other shapes run linear then qknorm_rope.
-    if (dt != HS_F16 || d != 64 || N % kBN != 0)
-        return fail(HS_EUNSUPPORTED, "%s: needs f16, head dim 64 and 3*H*64 %% %d == 0", op, kBN);
+    // column tiles (256 in f16, 128 in f32); other shapes run linear then
+    // qknorm_rope.
+    const int64_t tile_n = dt == HS_F16 ? kBN : F32Shape::kBN;
+    if (d != 64 || N % tile_n != 0)
+        return fail(HS_EUNSUPPORTED, "%s: needs head dim 64 and 3*H*64 %% %lld == 0", op,
+                    static_cast<long long>(tile_n));
     const float* params[6] = {qn_w, qn_b, kn_w, kn_b, sin_tab, cos_tab};
     for (const float* p : params)
         if (p && !aligned16(p)) return fail(HS_EUNSUPPORTED, "%s: parameters must be 16-byte aligned", op);
     if (!aligned16(k_out) || !aligned16(v_out))
         return fail(HS_EUNSUPPORTED, "%s: outputs must be 16-byte aligned", op);
     *qa = QkvArgs{};
-    qa->out[0] = static_cast<f16*>(q_out), qa->out[1] = static_cast<f16*>(k_out);
-    qa->out[2] = static_cast<f16*>(v_out);
+    qa->out[0] = q_out, qa->out[1] = k_out, qa->out[2] = v_out;
     qa->nw[0] = qn_w, qa->nb[0] = qn_b, qa->nw[1] = kn_w, qa->nb[1] = kn_b;
     qa->sin_tab = sin_tab, qa->cos_tab = cos_tab;
     qa->seq = T, qa->heads = H, qa->prefix = prefix, qa->eps = eps;
@@ -1278,9 +1375,13 @@ extern "C" hs_status hs_linear_ln_qkv_heads(hs_stream_t stream, hs_dtype dt, con
     const LnArgs la{workspace, ln_w, ln_b};
     // the q|k|v epilogue exists on the matrix-core path only: refuse other
     // calls before the statistics are enqueued
-    if (!takes_fast_path<true>(dt, static_cast<int>(N), k, x, w_qkv, b_qkv, nullptr, q_out,
-                               nullptr, la))
-        return fail(HS_EUNSUPPORTED, "%s: needs K %% %d == 0 and 16-byte aligned buffers", op, kBK);
+    const bool f32_ok = f32_fast(dt, static_cast<int>(N), k, x, w_qkv, b_qkv, nullptr, q_out, nullptr) &&
+                        aligned16(ln_w) && aligned16(ln_b);
+    if (!f32_ok && !takes_fast_path<true>(dt, static_cast<int>(N), k, x, w_qkv, b_qkv, nullptr, q_out,
+                                          nullptr, la))
+        return fail(HS_EUNSUPPORTED,
+                    "%s: needs K %% %d == 0 (f16) or %% %d == 0 (f32) and 16-byte aligned buffers", op,
+                    kBK, F32Shape::kBK);
     hipStream_t st = static_cast<hipStream_t>(stream);
     rc = hs_layernorm_stats(st, dt, x, workspace, M, k, eps);
     if (rc != HS_OK) return rc;

@@ -251,8 +251,9 @@ hs_status hs_linear_ls_residual(hs_stream_t stream, hs_dtype dt, const void* x, 
  * covers, whose head-vector code this shares), within one f16 ulp for
  * other H. qn_w/qn_b, kn_w/kn_b (d, f32) NULL = no QK-norm; sin/cos (T -
  * prefix, d) f32 NULL = no RoPE; b_qkv (3*H*d) f32 may be NULL. x is (S*T,
- * k). Fast path only: f16, d == 64, H % 4 == 0, k % 64 == 0, 16-byte aligned
- * buffers; other shapes return HS_EUNSUPPORTED (run hs_linear then
+ * k). Fused kernels only: d == 64 and 16-byte aligned buffers with, in f16,
+ * 3*H*64 % 256 == 0 and k % 64 == 0, in f32, 3*H*64 % 128 == 0 and k % 32
+ * == 0; other shapes return HS_EUNSUPPORTED (run hs_linear then
  * hs_qknorm_rope). Outputs must not overlap x, w_qkv or each other. */
 hs_status hs_linear_qkv_heads(hs_stream_t stream, hs_dtype dt, const void* x, const void* w_qkv,
                               const float* b_qkv, const float* qn_w, const float* qn_b,

@@ -32,6 +32,13 @@ enum class Dtype : int { F32 = HS_F32, F16 = HS_F16 };
 
 inline size_t dtype_size(Dtype dt) { return dt == Dtype::F16 ? 2 : 4; }
 
+// Shapes the fused q|k|v kernels cover: head dim 64, whole column tiles (256
+// in f16, 128 in f32) and whole k stages (64 in f16, 32 in f32).
+inline bool qkv_fused(Dtype dt, size_t d, size_t n3, size_t k) {
+    if (d != 64) return false;
+    return dt == Dtype::F16 ? n3 % 256 == 0 && k % 64 == 0 : n3 % 128 == 0 && k % 32 == 0;
+}
+
 struct ContractViolation : std::logic_error {
     using std::logic_error::logic_error;
 };
@@ -516,9 +523,9 @@ class HipContext {
 
     // The q|k|v projection with split_heads, QK-norm and RoPE
     // (model/block.rs:128-146) in one launch on the fused (3*h*d, k) weight.
-    // Returns head-major q, k, v. Shapes the fused kernel does not cover
-    // (f32, d != 64, 3*h*64 not a multiple of 256) run linear then
-    // qknorm_rope per third.
+    // Returns head-major q, k, v. Shapes the fused kernels do not cover
+    // (d != 64, 3*h*64 not a multiple of 256 in f16 or 128 in f32) run
+    // linear then qknorm_rope per third.
     struct Qkv {
         HipTensor q, k, v;
     };
@@ -529,7 +536,7 @@ class HipContext {
         const size_t n3 = w_qkv.shape()[0], k = w_qkv.shape()[1], d = n3 / (3 * h), hd = h * d;
         HS_REQUIRE(x.len() == s * t * k && x.dtype() == w_qkv.dtype(), "x shape/dtype");
         HS_REQUIRE(!b_qkv || (b_qkv->dtype() == Dtype::F32 && b_qkv->len() == n3), "qkv bias");
-        const bool fused = x.dtype() == Dtype::F16 && d == 64 && n3 % 256 == 0 && k % 64 == 0;
+        const bool fused = qkv_fused(x.dtype(), d, n3, k);
         if (!fused) {
             Qkv out;
             HipTensor* dst[3] = {&out.q, &out.k, &out.v};
@@ -589,8 +596,8 @@ class HipContext {
         return ln_call(x, norm, w, bias, eps, true);
     }
     // LN1 and the q|k|v projection with heads, QK-norm and RoPE
-    // (model/block.rs:128-146) in one product. Shapes the fused kernel does
-    // not cover (f32, d != 64) run layernorm then linear_qkv_heads.
+    // (model/block.rs:128-146) in one product. Shapes the fused kernels do
+    // not cover (see qkv_fused) run layernorm then linear_qkv_heads.
     Qkv linear_ln_qkv_heads(const HipTensor& x, const Norm& norm, const HipTensor& w_qkv,
                             const HipTensor* b_qkv, size_t s, size_t t, size_t h, const Norm* qn,
                             const Norm* kn, const Rope* rope, float eps = 1e-5f) const {
@@ -599,7 +606,7 @@ class HipContext {
         HS_REQUIRE(x.len() == s * t * k && x.dtype() == w_qkv.dtype(), "x shape/dtype");
         HS_REQUIRE(!b_qkv || (b_qkv->dtype() == Dtype::F32 && b_qkv->len() == n3), "qkv bias");
         ln_params(norm, k);
-        if (!(x.dtype() == Dtype::F16 && d == 64 && n3 % 256 == 0 && k % 64 == 0))
+        if (!qkv_fused(x.dtype(), d, n3, k))
             return linear_qkv_heads(layernorm(x, *norm.weight, *norm.bias, eps), w_qkv, b_qkv, s, t,
                                     h, qn, kn, rope, eps);
         const float *qw = nullptr, *qb = nullptr, *kw = nullptr, *kb = nullptr;

@@ -229,10 +229,14 @@ def test_linear_qkv_heads_contract():
     _einval(call(x=None), "null")
     _einval(call(k=ctypes.c_void_p(0x3000000 + 64)), "outputs overlap")
     _einval(call(v=ctypes.c_void_p(0x1000000 + 64)), "overlaps x or w")
-    assert call(dt=_lib.HS_F32) == _lib.HS_EUNSUPPORTED
+    # f32 with an odd H (3 * 3 * 64 = 576 columns, not whole 128-column tiles)
+    assert call(dt=_lib.HS_F32, H=3) == _lib.HS_EUNSUPPORTED
     # each output is (S*T, H*d), not (S*T, 3*H*d): w may start right after q
-    # (f32 stops with HS_EUNSUPPORTED after the overlap checks, before any launch)
-    assert call(dt=_lib.HS_F32, w=ctypes.c_void_p(0x3000000 + 2 * 8 * 4 * 64 * 4)) == _lib.HS_EUNSUPPORTED
+    # (that f32 shape stops with HS_EUNSUPPORTED after the overlap checks,
+    # before any launch)
+    assert call(dt=_lib.HS_F32, H=3,
+                w=ctypes.c_void_p(0x3000000 + 2 * 8 * 3 * 64 * 4)) == _lib.HS_EUNSUPPORTED
+    assert call(dt=_lib.HS_F32, kk=48) == _lib.HS_EUNSUPPORTED  # f32 k stages of 32
     assert call(d=32) == _lib.HS_EUNSUPPORTED
     assert call(H=2) == _lib.HS_EUNSUPPORTED            # 3 * 2 * 64 = 384 columns
     assert call(S=0) == _lib.HS_OK                      # zero tokens: no-op

@@ -342,16 +342,58 @@ def test_linear_qkv_heads_full_size_frame(ctx):
         assert torch.equal(a, e), f"full-size {name}"
 
 
-def test_linear_qkv_heads_fallback_f32(ctx):
-    """f32 (and head dims other than 64) run the unfused sequence."""
-    x, w, b, qn, kn, rope = qkv_case(3, 2, 41, 4, 64, True, 5)
+@pytest.mark.parametrize("s,t,h,k,norm,prefix", QKV_CASES)
+def test_linear_qkv_heads_f32_is_the_sequence(ctx, s, t, h, k, norm, prefix):
+    """The f32 q|k|v epilogue (f32 matrix-core kernel) against hs_linear +
+    hs_qknorm_rope per third: bit-exact where hs_qknorm_rope runs its row
+    kernel (8, 16 or 32 heads: the same head-vector code in the same lane
+    layout), within 1e-6 relative where it runs its generic kernel (another
+    reduction order); q against the oracle's reference sequence within the
+    f32 bar."""
+    x, w, b, qn, kn, rope = qkv_case(s * 1000 + t + 1, s, t, h, k, norm, prefix)
     x, w = x.float(), w.float()
-    got = ctx.linear_qkv_heads(x, w, b, 2, 41, 4, qn=qn, kn=kn, rope=rope)
-    want = qkv_sequence(ctx, x, w, b, 2, 41, 4, qn, kn, rope, 1e-5)
+    got = ctx.linear_qkv_heads(x, w, b, s, t, h, qn=qn, kn=kn, rope=rope, eps=1e-5)
+    want = qkv_sequence(ctx, x, w, b, s, t, h, qn, kn, rope, 1e-5)
+    for name, a, e in zip("qkv", got, want):
+        assert tuple(a.shape) == (s, h, t, 64) and a.dtype == torch.float32
+        what = f"f32 {name} {(s, t, h, k, norm, prefix)}"
+        if h in (8, 16, 32) or name == "v":
+            assert_bit_exact(back(a), back(e), what)
+        else:
+            assert_close(back(a), back(e), 1e-6, what)
+    qproj = O.linear(back(x), back(w[:h * 64]), back(b[:h * 64]))
+    tabs = (None, None, 0) if rope is None else (back(rope[0]), back(rope[1]), prefix)
+    qo = O.qknorm_rope(qproj, *(tuple(back(a) for a in qn) if qn else (None, None)),
+                       tabs[0], tabs[1], s, t, h, 64, tabs[2], 1e-5)
+    check(back(got[0]), qo, "f32 q vs oracle")
+
+
+def test_linear_qkv_heads_f32_block_shape(ctx):
+    """The S=2 f32 frame block's projection (2 x 1374 tokens, 37x37 grid,
+    prefix 5, 16 heads, dim 1024: 64 x 128 tiles) and the same at 8 frames
+    (128 x 128 tiles), bit-exact against the unfused sequence."""
+    from headshot_amd import rope as rp
+    sin, cos = (torch.from_numpy(a).to("cuda:0") for a in rp.tables(rp.periods(), 37, 37))
+    for s in (2, 8):
+        x, w, b, qn, kn, _ = qkv_case(77 + s, s, 1374, 16, 1024, True, None)
+        x, w = x.float(), w.float()
+        got = ctx.linear_qkv_heads(x, w, b, s, 1374, 16, qn=qn, kn=kn, rope=(sin, cos, 5), eps=1e-6)
+        want = qkv_sequence(ctx, x, w, b, s, 1374, 16, qn, kn, (sin, cos, 5), 1e-6)
+        for name, a, e in zip("qkv", got, want):
+            assert_bit_exact(back(a), back(e), f"f32 {name} at S={s}")
+
+
+def test_linear_qkv_heads_fallback_f32(ctx):
+    """f32 shapes the fused kernel does not cover (3 * H * 64 not a multiple
+    of 128: H odd) run the unfused sequence; the C entry point refuses them."""
+    x, w, b, qn, kn, rope = qkv_case(3, 2, 41, 3, 64, True, 5)
+    x, w = x.float(), w.float()
+    got = ctx.linear_qkv_heads(x, w, b, 2, 41, 3, qn=qn, kn=kn, rope=rope)
+    want = qkv_sequence(ctx, x, w, b, 2, 41, 3, qn, kn, rope, 1e-5)
     for a, e in zip(got, want):
         assert torch.equal(a, e)
     with pytest.raises(_lib.HsError):
         _lib.check(ctx.lib.hs_linear_qkv_heads(
             torch.cuda.current_stream().cuda_stream, _lib.HS_F32, x.data_ptr(), w.data_ptr(),
             None, None, None, None, None, None, None, got[0].data_ptr(), got[1].data_ptr(),
-            got[2].data_ptr(), 2, 41, 4, 64, 64, 0, 1e-5), "linear_qkv_heads")
+            got[2].data_ptr(), 2, 41, 3, 64, 64, 0, 1e-5), "linear_qkv_heads")

@@ -157,12 +157,13 @@ def qk_norms(d, seed=5):
 @pytest.mark.parametrize("frames,grid,heads,rope_on", [(2, (37, 37), 16, True),
                                                        (1, (8, 8), 16, False),
                                                        (3, (4, 6), 8, True)])
-def test_linear_ln_qkv_heads(ctx, frames, grid, heads, rope_on):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_linear_ln_qkv_heads(ctx, frames, grid, heads, rope_on, dtype):
     prefix = 5
     t = grid[0] * grid[1] + prefix
     d, dim = 64, heads * 64
     m = frames * t
-    x, g, be, w, b = ln_operands(frames * 31 + heads, m, 3 * dim, dim, np.float16)
+    x, g, be, w, b = ln_operands(frames * 31 + heads, m, 3 * dim, dim, NP[dtype])
     qn, kn = qk_norms(d)
     sin, cos = rope.tables(rope.periods(), *grid)
     rp = (dev(sin), dev(cos), prefix) if rope_on else None
@@ -181,7 +182,7 @@ def test_linear_ln_qkv_heads(ctx, frames, grid, heads, rope_on):
         third = np.ascontiguousarray(proj[:, i * dim:(i + 1) * dim])
         want = O.qknorm_rope(third, nw, nb, sin if use_rope else None, cos if use_rope else None,
                              frames, t, heads, d, prefix if use_rope else 0, 1e-6)
-        f16_close(back(mine).astype(np.float32), want.astype(np.float32), what)
+        check(back(mine), want, what)
 
 
 @pytest.mark.parametrize("name", ["qkv", "fc1"])
