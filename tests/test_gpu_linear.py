@@ -151,9 +151,11 @@ def test_linear_epilogues_random_sweep(ctx, case):
 # 128) with 2 stages (the smaller shapes of the tests above with n % 128 ==
 # 0 and k % 32 == 0 run on it too). 128 x 128: a last row tile of 57 rows
 # and 3 stages; one stage and a last row tile of one row; an odd stage
-# count and n = 1024.
+# count and n = 1024. Long k on few tiles: 16 x 8 tiles at k = 2048; 5 x 2
+# tiles at k = 2080 (65 stages).
 F32_MATRIX = [(3000, 2048, 64), (6163, 1024, 96), (6145, 1024, 32), (24577, 256, 160),
-              (2815, 128, 64), (12345, 768, 96), (8193, 1024, 32), (8300, 1024, 160)]
+              (2815, 128, 64), (12345, 768, 96), (8193, 1024, 32), (8300, 1024, 160),
+              (1000, 1024, 2048), (301, 256, 2080)]
 
 
 @pytest.mark.parametrize("m,n,k", F32_MATRIX)

@@ -121,7 +121,8 @@ def test_linear_ln_gelu(ctx, m, n, k, dtype):
     check(got, O.gelu(reference_ln_linear(x, g, be, w, b, 1e-6)), what)
 
 
-@pytest.mark.parametrize("m,n,k", [(8300, 1024, 256), (12345, 768, 96), (3000, 1024, 32)])
+@pytest.mark.parametrize("m,n,k", [(8300, 1024, 256), (12345, 768, 96), (3000, 1024, 32),
+                                   (700, 512, 2048)])
 def test_linear_ln_f32_tile_shapes(ctx, m, n, k):
     """The f32 prologue in both tile shapes of the f32 matrix-core kernel:
     128 x 128 tiles (at least 512 of them: 8300 and 12345 rows, last row
